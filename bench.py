@@ -1,0 +1,233 @@
+#!/usr/bin/env python3
+"""Benchmark of the TESM forward hot path on one MI355X; prints ONE JSON line.
+
+Workload: one TESM_SISO prefill forward at base() dims with the
+BASELINE overrides d_state=256, window=16 (d_model 768, ent_rank 64, thr 0.08, scale 0.2,
+decay_init_bias 2.0), batch 4 x seq 2048, bf16 activations, INT2 weights, random init from
+seed 0, synthetic input already resident in HBM.  A step is one layer forward (8192 tokens).
+
+Besides the headline tokens/s the line carries:
+  roofline      the dominant kernel (the in_proj int8-MFMA GEMM, M=8192 K=768 N=2432), timed
+                per launch with HIP events on the stream it runs on;
+  kernels       the isolated-op measurements of configs[1] and configs[2] (GEMV/GEMM, scan,
+                entanglement) with rotating buffers so the 256 MB Infinity Cache cannot serve
+                repeats;
+  cpu_baseline  the oracle (torch restatement of the reference's torch path) timed on this
+                host's cores on the same workload, bf16, repeated for about --cpu-seconds.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "TESM-layer tokens/s at base() shape; INT2 BitLinear GB/s as % of HBM peak"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+LAYER = dict(d_model=768, d_state=256, ent_rank=64, entanglement_window=16, entanglement_threshold=0.08,
+             entanglement_scale=0.2, decay_init_bias=2.0, max_seq_len=2048, state_scan_chunk_size=16)
+B, L = 4, 2048
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel measurements")
+    p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
+    return p.parse_args()
+
+
+def busy(torch, ms: float = 20.0):
+    """Queue a spin kernel so later launches are enqueued ahead of the GPU (events then time kernels,
+    not host launch latency)."""
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(int(ms * 2.0e6))
+
+
+def time_launches(torch, fn, n: int, warm: int = 3):
+    """Average device duration of fn() over n launches, one event pair per launch on the current stream."""
+    for _ in range(warm):
+        fn(0)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    busy(torch)
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / n * 1e-3  # seconds
+
+
+def packed_codes(torch, N, ldw, device, gen):
+    c = [torch.randint(0, 3, (N, ldw), dtype=torch.uint8, device=device, generator=gen) for _ in range(4)]
+    return c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6)
+
+
+def measure_kernels(torch, only):
+    from tesm_amd import hip_ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    res = {}
+    want = set(only.split(",")) if only else None
+
+    def sel(name):
+        return want is None or name in want
+
+    # BitLinear GEMV (M=1) and GEMM (M=2048), fp32 output
+    for (M, K, N) in [(1, 4096, 4096), (1, 4096, 11008), (2048, 4096, 4096)]:
+        name = f"bitlinear_M{M}_K{K}_N{N}"
+        if not sel(name):
+            continue
+        ldw = hip_ops.kpad(K) // 4
+        wbytes = N * ldw
+        nrot = max(1, min(128, (512 << 20) // wbytes)) if M == 1 else 1
+        packs = [packed_codes(torch, N, ldw, dev, gen) for _ in range(nrot)]
+        x = torch.randn(M, K, device=dev, generator=gen)
+        q, s, rs = hip_ops.quant_act(x)
+        c_w = torch.full((1,), 0.05, device=dev)
+        out = torch.empty(M, N, device=dev)
+        t = time_launches(torch, lambda i: hip_ops.bitlinear(q, s, rs, packs[i % nrot], c_w, N, K, torch.float32,
+                                                             out=out), 200 if M == 1 else 50)
+        if M == 1:
+            nbytes = N * K // 4 + M * K + M * N * 4 + 8 * M + 4
+            res[name] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
+                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
+        else:
+            ops = 2 * M * N * K
+            res[name] = {"us": t * 1e6, "bound": "mfma", "achieved": ops / t / 1e12, "unit": "TOP/s (int8)",
+                         "frac": ops / t / 1e12 / INT8_PEAK_TOPS, "ops": ops}
+        del packs
+    # SISO scan + local entanglement at small() dims, W=16, B8 x L512, bf16
+    Bs, Ls, D, R, W = 8, 512, 256, 48, 16
+    if sel("scan_small"):
+        nrot = 80
+        sets = [(torch.sigmoid(torch.randn(Bs, Ls, D, device=dev, generator=gen)).to(torch.bfloat16),
+                 torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
+        t = time_launches(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100)
+        nbytes = Bs * Ls * D * (2 + 2 + 2)
+        res["scan_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
+                             "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
+        del sets
+    if sel("local_ent_small"):
+        nrot = 80
+        rope = hip_ops.rope_table(Ls, R, torch.bfloat16, dev)
+        bias = torch.randn(W, device=dev, generator=gen) * 0.3
+        sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
+                 torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
+                 torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
+        t = time_launches(torch, lambda i: hip_ops.local_ent(sets[i % nrot][0], sets[i % nrot][1], rope,
+                                                             sets[i % nrot][2], bias, W, 0.08, 0.2), 100)
+        nbytes = Bs * Ls * (2 * R + 2 * D) * 2
+        res["local_ent_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
+                                  "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
+        del sets
+    return res
+
+
+def cpu_baseline(torch, seconds: float):
+    """The oracle's torch path (restating the reference's kernel_backend='torch') on host cores."""
+    from oracle import tesm_torch as ot
+
+    torch.manual_seed(0)
+    m = ot.TESM_SISO(**LAYER).eval().to(torch.bfloat16)
+    u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    with torch.no_grad():
+        m(u)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            m(u)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    return {"value": n * B * L / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle TESM_SISO.forward (torch restatement of the reference torch path), bf16, "
+                      f"{B}x{L} tokens, {n} forwards in {el:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is "
+              f"design-only", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from tesm_amd import TESM_SISO, hip_ops
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    m = TESM_SISO(**LAYER).to(dev).to(torch.bfloat16).eval()
+    u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            m(u)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            m(u)
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+        ms = e0.elapsed_time(e1) / args.steps
+
+        # dominant kernel: the in_proj GEMM of the same layer on the same stream
+        M, K = B * L, LAYER["d_model"]
+        N = m.in_proj.out_features
+        pw = m.in_proj.packed_weight()
+        q, s, rs = hip_ops.quant_act(u.reshape(M, K))
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        t_gemm = time_launches(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K, torch.bfloat16,
+                                                                  out=out), 50)
+        ops = 2 * M * N * K
+        kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
+        if args.only:
+            print(json.dumps({"kernels": kernels}))
+            return
+
+    value = B * L / (ms * 1e-3)
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "wall_ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn input, random-init weights from seed 0)",
+        "config": {"workload": "TESM_SISO prefill forward, base() dims with d_state=256 window=16 (configs[3])",
+                   "batch": B, "seq_len": L, "d_model": 768, "d_state": 256, "ent_rank": 64, "window": 16,
+                   "weights": "INT2 ternary", "activations": "bf16"},
+        "roofline": {"kernel": "in_proj INT2xINT8 MFMA GEMM (M=8192, K=768, N=2432)", "bound": "mfma",
+                     "achieved": ops / t_gemm / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": ops / t_gemm / 1e12 / INT8_PEAK_TOPS, "traffic": None, "us": t_gemm * 1e6,
+                     "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak"},
+        "kernels": kernels,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,151 @@
+/*
+ * tesm_hip.h -- C-ABI of libtesm_hip.so, the gfx950 (MI355X) kernels behind kernel_backend='hip'.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers unless noted; every output and workspace is allocated by the
+ *     caller.  No entry point allocates device memory or synchronises with the host.
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is queued asynchronously on it.
+ *   - Element types: 0 = float32, 1 = bfloat16 (TESM_DT_*).  Sizes and leading dimensions are in
+ *     elements unless named *_bytes.
+ *   - Return 0 on success or a TESM_ERR_* code; tesm_hip_last_error() then describes the failure
+ *     (thread-local, valid until the next call on the same thread).
+ *   - Activation-code buffers are int8 (rows, ldq) with ldq a multiple of 16 and >= kpad(K); packed
+ *     weights are uint8 (N, ldw) with ldw a multiple of 16 and >= kpad(K)/4 for the products.
+ *     kpad(K) = tesm_hip_kpad(K) rounds K up to the 128-code GEMM tile; pad codes are 0 in
+ *     activations and code 1 (value 0) in weights.
+ *
+ * Reference = WANGLILIN360/tesm.  Each declaration names the reference interface it replaces.
+ */
+#ifndef TESM_HIP_H_
+#define TESM_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TESM_HIP_ABI_VERSION 1
+
+#define TESM_DT_F32 0
+#define TESM_DT_BF16 1
+
+#define TESM_OK 0
+#define TESM_ERR_INVALID_ARG 1
+#define TESM_ERR_ALIGNMENT 2
+#define TESM_ERR_UNSUPPORTED 3
+#define TESM_ERR_LAUNCH 4
+#define TESM_ERR_WORKSPACE 5
+
+/* Library identity.  No reference counterpart (the reference loads a pybind11 module,
+ * tesm_ssm/ops/cuda/__init__.py:19-48). */
+int tesm_hip_abi_version(void);
+const char* tesm_hip_last_error(void);
+int64_t tesm_hip_kpad(int64_t K);
+
+/* Per-token int8 activation codes.  Replaces BitLinear.quantized_input
+ * (tesm_ssm/modules/tesm.py:206-209): s_x[m] = 127 / max(amax_k |x[m,k]|, eps) evaluated as
+ * reciprocal()*127 with the module dtype's rounding, q = clamp(rne(x * s_x), -128, 127).
+ * layout 0 writes codes row-major; layout 1 writes them in the order the INT2 products read
+ * (within each group of 16 codes, byte 4s+j holds code 4j+s).  rowsum[m] = sum_k q[m,k] (nullable). */
+int tesm_hip_quant_act_i8(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout,
+                          int8_t* q, int64_t ldq, float* s_x, int32_t* rowsum, void* stream);
+
+/* Per-tensor absmean ternary scale.  Replaces the scale of BitLinear.quantized_weight
+ * (tesm.py:212): s_w = 1 / max(mean|w|, eps) in the weight dtype; c_w = 1 / s_w (the dequantised
+ * value of a +1 code, tesm.py:215).  ws: tesm_hip_absmean_ws_bytes() bytes of device scratch. */
+int64_t tesm_hip_absmean_ws_bytes(void);
+int tesm_hip_absmean_scale(const void* w, int dt, int64_t n, float eps, void* ws, float* s_w, float* c_w,
+                           void* stream);
+
+/* Ternary codes clamp(rne(w * s_w), -1, 1) packed four per byte (code+1 in bits 2i..2i+1 of byte
+ * k/4, i = k%4).  Replaces pack_ternary_to_int2 (tesm_ssm/utils/int2_quantization.py:21-58) fed by
+ * BitLinear.quantized_weight's codes (tesm.py:213-214).  s_w is a device scalar, or (N) if
+ * per_row.  Bytes past ceil(K/4) up to ldp hold code 1. */
+int tesm_hip_pack_w_i2(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
+                       uint8_t* packed, int64_t ldp, void* stream);
+
+/* Inverse of the packing.  Replaces unpack_int2_to_ternary (int2_quantization.py:68-93). */
+int tesm_hip_unpack_w_i2(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
+                         void* stream);
+
+/* INT2 x INT8 BitLinear product out[m,n] = (sum_k q[m,k] * code[n,k]) / s_x[m] * c_w (+ bias[n]).
+ * Replaces BitLinear._project_quantized / F.linear on the dequantised operands
+ * (tesm.py:238-290) and the cuda_quantized_linear op (tesm_ssm/ops/cuda/__init__.py:128-139).
+ * q: layout-1 codes (M, ldq), kpad(K) wide; packed: (N, ldw).  c_w: device scalar or (N) if
+ * c_w_per_row.  bias: (N) in out_dt or NULL.  acc_dump: optional (M, N) exact int32 accumulators.
+ * M <= 4 runs the bandwidth-bound GEMV; larger M the int8-MFMA GEMM. */
+int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const int32_t* rowsum,
+                          const uint8_t* packed, int64_t ldw, const float* c_w, int c_w_per_row, const void* bias,
+                          int64_t M, int64_t N, int64_t K, void* out, int out_dt, int64_t ldo, int32_t* acc_dump,
+                          void* stream);
+
+/* State scan h_t = d_t h_{t-1} + u_t over (B, L, C), C contiguous.  Replaces
+ * TESM_SISO._parallel_state_scan (tesm.py:1091-1164, torch branch; chunk_size = state_scan_chunk_size
+ * reproduces its 1e-12 clamp semantics) and chunk_state_scan (ops/cuda/__init__.py:140-150).
+ * decay/update: element (b,t,c) at ptr[(b*L+t)*ld + c], dt; states likewise in out_dt.
+ * h0, h_final: (B, C) float64, nullable.  ws: tesm_hip_scan_ws_bytes() bytes. */
+int64_t tesm_hip_scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t chunk_size);
+int tesm_hip_scan(const void* decay, int64_t ld_decay, const void* update, int64_t ld_update, int dt, int64_t B,
+                  int64_t L, int64_t C, int64_t chunk_size, const double* h0, void* states, int64_t ld_states,
+                  int out_dt, double* h_final, void* ws, int64_t ws_bytes, void* stream);
+
+/* RoPE cos/sin table for positions pos_offset..pos_offset+L-1: tab[t*(R/2)+i] = (cos, sin) of
+ * pos * (1 / base**(2i/R)), rounded to dt.  Replaces the table built inside TESM_SISO._apply_rope
+ * (tesm.py:783-793).  tab: (L, R/2) float2 (8 bytes each). */
+int tesm_hip_rope_table(void* tab, int64_t L, int64_t R, int64_t pos_offset, double base, int dt, void* stream);
+
+/* Causal local-window ternary entanglement + mix.  Replaces TESM_SISO._compute_local_entanglement
+ * (tesm.py:853-952, torch branch) and the mix of TESM_SISO.forward (tesm.py:1231-1232, 1256), and
+ * (mimo = 1) TESMMIMO_Optimized._compute_local_entanglement_mimo (tesm_mimo.py:394-588).
+ * q, k: raw (pre-RoPE) queries/keys, element (b,t,h,r) at ptr[(b*L+t)*ld + h*R + r]; rope: table of
+ * tesm_hip_rope_table for positions 0..L-1; q_add: optional cross-layer query bias added after
+ * RoPE; bias: (H, W) float32 holding dt-rounded values; thr: threshold rounded to dt.
+ * S: states, element (b,t,h,d) at S[(b*L+t)*ld_s + h*D + d].  Outputs (each nullable) share ld_out:
+ * avg (window average), e_out (E = S + scale*(avg - S)), c_out (E - S), e_tanh (tanh E).
+ * tern: optional int8 ternary map (B, L, H, W_eff).  ws: tesm_hip_local_ent_ws_bytes() bytes. */
+int64_t tesm_hip_local_ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W);
+int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k, const void* rope, const void* q_add,
+                       int64_t ld_qadd, const float* bias, const void* S, int64_t ld_s, int dt, int mimo, int64_t B,
+                       int64_t L, int64_t H, int64_t R, int64_t D, int64_t W, float thr, float ent_scale, void* avg,
+                       void* e_out, void* c_out, void* e_tanh, int64_t ld_out, int8_t* tern, void* ws,
+                       int64_t ws_bytes, void* stream);
+
+/* One packed BitLinear as the fused layer drivers consume it. */
+typedef struct tesm_hip_linear {
+  const uint8_t* packed; /* (N, ldw) */
+  int64_t ldw;
+  const float* c_w;      /* device scalar (or (N) if c_w_per_row) */
+  int c_w_per_row;
+} tesm_hip_linear;
+
+/* Whole TESM_SISO prefill forward (eval, no grad).  Replaces TESM_SISO.forward
+ * (tesm.py:1175-1272) for L > 1 without an inference cache: in_proj, gates, RoPE, cross-layer
+ * query bias, state scan, local entanglement, mix, state_proj/ent_proj with the output gate
+ * y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(E - S), out_proj. */
+typedef struct tesm_hip_siso_layer {
+  int dt;                     /* activations / module dtype */
+  int64_t B, L, d_model, d_state, ent_rank, window, chunk_size;
+  float bit_eps, thr, ent_scale;
+  const void* u;              /* (B, L, d_model), contiguous */
+  tesm_hip_linear in_proj, state_proj, ent_proj, out_proj, cross_q_proj;
+  const void* decay_bias;     /* (d_state) in dt */
+  const float* local_bias;    /* (window) float32 holding dt values */
+  const void* rope;           /* tesm_hip_rope_table(L, ent_rank, 0) */
+  const void* cross_state;    /* optional (B, L, d_state) in dt (previous layer's states) */
+  const double* h0;           /* optional (B, d_state) */
+  void* y;                    /* (B, L, d_model) */
+  void* states;               /* (B, L, d_state) in dt */
+  double* h_final;            /* optional (B, d_state) */
+  void* proj_out;             /* optional (B, L, N_in) copy target; NULL = workspace only */
+} tesm_hip_siso_layer;
+
+int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p);
+int tesm_hip_siso_prefill(const tesm_hip_siso_layer* p, void* ws, int64_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TESM_HIP_H_ */

@@ -1,0 +1,114 @@
+"""ctypes binding of ``libtesm_hip.so`` (C-ABI declared in ``include/tesm_hip.h``).
+
+The library is built in-tree by ``tesm_amd.build`` into ``tesm_amd/_build/``;
+``TESM_HIP_LIB`` overrides the path.  Loading never falls back to anything: a
+missing or mismatched library raises ``HipBackendUnavailable`` (a
+``RuntimeError``), mirroring the reference's strict-backend errors
+(tesm_ssm/modules/tesm.py:278-285, tesm_ssm/ops/cuda/__init__.py:41-48).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+ABI_VERSION = 1
+_DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int
+F32 = ctypes.c_float
+F64 = ctypes.c_double
+
+
+class HipBackendUnavailable(RuntimeError):
+    pass
+
+
+class Linear(ctypes.Structure):
+    """``tesm_hip_linear``."""
+    _fields_ = [("packed", P), ("ldw", I64), ("c_w", P), ("c_w_per_row", I32)]
+
+
+class SisoLayer(ctypes.Structure):
+    """``tesm_hip_siso_layer``."""
+    _fields_ = [
+        ("dt", I32),
+        ("B", I64), ("L", I64), ("d_model", I64), ("d_state", I64), ("ent_rank", I64), ("window", I64),
+        ("chunk_size", I64),
+        ("bit_eps", F32), ("thr", F32), ("ent_scale", F32),
+        ("u", P),
+        ("in_proj", Linear), ("state_proj", Linear), ("ent_proj", Linear), ("out_proj", Linear),
+        ("cross_q_proj", Linear),
+        ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P), ("h0", P),
+        ("y", P), ("states", P), ("h_final", P), ("proj_out", P),
+    ]
+
+
+_SIGNATURES = {
+    "tesm_hip_abi_version": ([], I32),
+    "tesm_hip_last_error": ([], ctypes.c_char_p),
+    "tesm_hip_kpad": ([I64], I64),
+    "tesm_hip_quant_act_i8": ([P, I32, I64, I64, I64, F32, I32, P, I64, P, P, P], I32),
+    "tesm_hip_absmean_ws_bytes": ([], I64),
+    "tesm_hip_absmean_scale": ([P, I32, I64, F32, P, P, P, P], I32),
+    "tesm_hip_pack_w_i2": ([P, I32, I64, I64, I64, P, I32, P, I64, P], I32),
+    "tesm_hip_unpack_w_i2": ([P, I64, I64, I64, P, I64, P], I32),
+    "tesm_hip_bitlinear_i2": ([P, I64, P, P, P, I64, P, I32, P, I64, I64, I64, P, I32, I64, P, P], I32),
+    "tesm_hip_scan_ws_bytes": ([I64, I64, I64, I64], I64),
+    "tesm_hip_scan": ([P, I64, P, I64, I32, I64, I64, I64, I64, P, P, I64, I32, P, P, I64, P], I32),
+    "tesm_hip_rope_table": ([P, I64, I64, I64, F64, I32, P], I32),
+    "tesm_hip_local_ent_ws_bytes": ([I64, I64, I64, I64], I64),
+    "tesm_hip_local_ent": ([P, I64, P, I64, P, P, I64, P, P, I64, I32, I32, I64, I64, I64, I64, I64, I64, F32, F32,
+                            P, P, P, P, I64, P, P, I64, P], I32),
+    "tesm_hip_siso_prefill_ws_bytes": ([ctypes.POINTER(SisoLayer)], I64),
+    "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib_path() -> str:
+    return os.environ.get("TESM_HIP_LIB", _DEFAULT)
+
+
+def exported_symbols():
+    """Names the binding expects the library to export."""
+    return sorted(_SIGNATURES)
+
+
+def load():
+    """Load and type the library once; raise HipBackendUnavailable if it cannot be used."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = lib_path()
+        if not os.path.exists(path):
+            raise HipBackendUnavailable(
+                f"libtesm_hip.so not found at {path}; build it with `python -m tesm_amd.build`")
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as e:
+            raise HipBackendUnavailable(f"cannot load {path}: {e}") from e
+        for name, (args, res) in _SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as e:
+                raise HipBackendUnavailable(f"{path} does not export {name}") from e
+            fn.argtypes, fn.restype = args, res
+        ver = lib.tesm_hip_abi_version()
+        if ver != ABI_VERSION:
+            raise HipBackendUnavailable(f"{path} has ABI version {ver}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = _lib.tesm_hip_last_error().decode(errors="replace") if _lib is not None else "unknown error"
+        raise RuntimeError(f"tesm_hip error {rc}: {msg}")

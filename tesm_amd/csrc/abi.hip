@@ -1,0 +1,389 @@
+// extern "C" entry points of libtesm_hip.so (declared in include/tesm_hip.h) and the fused
+// layer drivers.  The drivers only queue kernels on the caller's stream; every buffer comes
+// from the caller (outputs) or from one caller-provided workspace carved up here.
+#include <cstring>
+#include <string>
+
+#include "entangle.h"
+#include "scan.h"
+#include "tesm_hip_internal.h"
+#include "../../include/tesm_hip.h"
+
+namespace tesm {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(kErrLaunch, std::string(what) + ": launch failed: " + hipGetErrorString(e));
+  return kOk;
+}
+
+namespace {
+
+// Bump allocator over the caller's workspace (256-byte aligned pieces).
+struct Carve {
+  char* base;
+  int64_t off = 0;
+  explicit Carve(void* p) : base(static_cast<char*>(p)) {}
+  template <class T>
+  T* take(int64_t bytes) {
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off += round_up(std::max<int64_t>(bytes, 1), 256);
+    return p;
+  }
+};
+
+struct CodeBuf {
+  int8_t* q;
+  float* s;
+  int32_t* rs;
+  int64_t ldq;
+};
+
+CodeBuf take_codes(Carve& c, int64_t M, int64_t K) {
+  CodeBuf b;
+  b.ldq = kpad(K);
+  b.q = c.take<int8_t>(M * b.ldq);
+  b.s = c.take<float>(M * 4);
+  b.rs = c.take<int32_t>(M * 4);
+  return b;
+}
+
+LinearOperand operand(const CodeBuf& x, const tesm_hip_linear& w) {
+  LinearOperand o;
+  o.q = x.q;
+  o.ldq = x.ldq;
+  o.s_x = x.s;
+  o.rowsum = x.rs;
+  o.w = w.packed;
+  o.ldw = w.ldw;
+  o.c_w = w.c_w;
+  o.c_w_per_row = w.c_w_per_row;
+  return o;
+}
+
+int esize(int dt) { return dt == kBF16 ? 2 : 4; }
+
+// Workspace layout of the SISO prefill; with base == nullptr it only measures.
+struct SisoPlan {
+  CodeBuf xu, xe, xc, xy, xs;
+  void* proj;
+  void* scan_ws;
+  int64_t scan_bytes;
+  float* wts;
+  void* e_tanh;
+  void* c_mix;
+  void* yg;
+  void* cq;
+  int64_t total;
+};
+
+SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
+  Carve c(base);
+  SisoPlan s;
+  const int64_t M = p.B * p.L;
+  const int64_t n_in = 2 * p.d_model + 3 * p.d_state + 2 * p.ent_rank;
+  const int es = esize(p.dt);
+  s.xu = take_codes(c, M, p.d_model);
+  s.proj = c.take<void>(M * n_in * es);
+  s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
+  s.scan_ws = c.take<void>(s.scan_bytes);
+  s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
+  s.e_tanh = c.take<void>(M * p.d_state * es);
+  s.c_mix = c.take<void>(M * p.d_state * es);
+  s.xe = take_codes(c, M, p.d_state);
+  s.xc = take_codes(c, M, p.d_state);
+  s.yg = c.take<void>(M * p.d_model * es);
+  s.xy = take_codes(c, M, p.d_model);
+  if (p.cross_state) {
+    s.xs = take_codes(c, M, p.d_state);
+    s.cq = c.take<void>(M * p.ent_rank * es);
+  } else {
+    s.xs = CodeBuf{nullptr, nullptr, nullptr, 0};
+    s.cq = nullptr;
+  }
+  s.total = c.off;
+  return s;
+}
+
+int check_linear(const tesm_hip_linear& w, int64_t K, const char* name) {
+  TESM_REQUIRE(w.packed && w.c_w, kErrInvalidArg, std::string("siso layer: null ") + name);
+  TESM_REQUIRE(w.ldw >= kpad(K) / 4 && w.ldw % 16 == 0, kErrInvalidArg,
+               std::string("siso layer: ") + name + " ldw must be >= kpad(K)/4 and a multiple of 16");
+  return kOk;
+}
+
+int run_linear(const CodeBuf& x, const tesm_hip_linear& w, int64_t M, int64_t N, int64_t K, void* out, int dt,
+               int64_t ldo, hipStream_t st) {
+  LinearArgs a;
+  a.op[0] = operand(x, w);
+  a.M = M;
+  a.N = N;
+  a.Kp = kpad(K);
+  a.out = out;
+  a.out_dt = dt;
+  a.ldo = ldo;
+  return launch_linear(a, st);
+}
+
+}  // namespace
+}  // namespace tesm
+
+using namespace tesm;
+
+extern "C" {
+
+int tesm_hip_abi_version(void) { return TESM_HIP_ABI_VERSION; }
+
+const char* tesm_hip_last_error(void) { return g_last_error.c_str(); }
+
+int64_t tesm_hip_kpad(int64_t K) { return kpad(K); }
+
+int tesm_hip_quant_act_i8(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
+                          int64_t ldq, float* s_x, int32_t* rowsum, void* stream) {
+  return launch_quant_act(x, dt, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, static_cast<hipStream_t>(stream));
+}
+
+int64_t tesm_hip_absmean_ws_bytes(void) { return 512 * static_cast<int64_t>(sizeof(double)); }
+
+int tesm_hip_absmean_scale(const void* w, int dt, int64_t n, float eps, void* ws, float* s_w, float* c_w,
+                           void* stream) {
+  return launch_absmean(w, dt, n, eps, static_cast<double*>(ws), s_w, c_w, static_cast<hipStream_t>(stream));
+}
+
+int tesm_hip_pack_w_i2(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
+                       uint8_t* packed, int64_t ldp, void* stream) {
+  return launch_pack(w, dt, N, K, ldw, s_w, per_row, packed, ldp, static_cast<hipStream_t>(stream));
+}
+
+int tesm_hip_unpack_w_i2(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
+                         void* stream) {
+  return launch_unpack(packed, N, K, ldp, codes, ldc, static_cast<hipStream_t>(stream));
+}
+
+int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const int32_t* rowsum,
+                          const uint8_t* packed, int64_t ldw, const float* c_w, int c_w_per_row, const void* bias,
+                          int64_t M, int64_t N, int64_t K, void* out, int out_dt, int64_t ldo, int32_t* acc_dump,
+                          void* stream) {
+  TESM_REQUIRE(K >= 1, kErrInvalidArg, "bitlinear: K must be >= 1");
+  LinearArgs a;
+  a.op[0].q = q;
+  a.op[0].ldq = ldq;
+  a.op[0].s_x = s_x;
+  a.op[0].rowsum = rowsum;
+  a.op[0].w = packed;
+  a.op[0].ldw = ldw;
+  a.op[0].c_w = c_w;
+  a.op[0].c_w_per_row = c_w_per_row;
+  a.M = M;
+  a.N = N;
+  a.Kp = kpad(K);
+  a.bias = bias;
+  a.out = out;
+  a.out_dt = out_dt;
+  a.ldo = ldo;
+  a.acc_dump = acc_dump;
+  return launch_linear(a, static_cast<hipStream_t>(stream));
+}
+
+int64_t tesm_hip_scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t chunk_size) {
+  return scan_ws_bytes(B, L, C, chunk_size);
+}
+
+int tesm_hip_scan(const void* decay, int64_t ld_decay, const void* update, int64_t ld_update, int dt, int64_t B,
+                  int64_t L, int64_t C, int64_t chunk_size, const double* h0, void* states, int64_t ld_states,
+                  int out_dt, double* h_final, void* ws, int64_t ws_bytes, void* stream) {
+  ScanArgs a;
+  a.mode = 0;
+  a.dt = dt;
+  a.out_dt = out_dt;
+  a.clamp = 1;
+  a.B = B;
+  a.L = L;
+  a.C = C;
+  a.cs = chunk_size;
+  a.decay = decay;
+  a.ld_decay = ld_decay;
+  a.update = update;
+  a.ld_update = ld_update;
+  a.h0 = h0;
+  a.states = states;
+  a.ld_states = ld_states;
+  a.h_final = h_final;
+  return launch_scan(a, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+int tesm_hip_rope_table(void* tab, int64_t L, int64_t R, int64_t pos_offset, double base, int dt, void* stream) {
+  return launch_rope_table(static_cast<float2*>(tab), L, R, pos_offset, base, dt, static_cast<hipStream_t>(stream));
+}
+
+int64_t tesm_hip_local_ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W) { return ent_ws_bytes(B, L, H, W); }
+
+int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k, const void* rope, const void* q_add,
+                       int64_t ld_qadd, const float* bias, const void* S, int64_t ld_s, int dt, int mimo, int64_t B,
+                       int64_t L, int64_t H, int64_t R, int64_t D, int64_t W, float thr, float ent_scale, void* avg,
+                       void* e_out, void* c_out, void* e_tanh, int64_t ld_out, int8_t* tern, void* ws,
+                       int64_t ws_bytes, void* stream) {
+  EntArgs a;
+  a.dt = dt;
+  a.mimo = mimo;
+  a.B = B;
+  a.L = L;
+  a.H = H;
+  a.R = R;
+  a.D = D;
+  a.W = W;
+  a.q = q;
+  a.ld_q = ld_q;
+  a.k = k;
+  a.ld_k = ld_k;
+  a.rope = static_cast<const float2*>(rope);
+  a.q_add = q_add;
+  a.ld_qadd = ld_qadd;
+  a.bias = bias;
+  a.thr = thr;
+  a.ent_scale = ent_scale;
+  a.S = S;
+  a.ld_s = ld_s;
+  a.avg = avg;
+  a.e_out = e_out;
+  a.c_out = c_out;
+  a.e_tanh = e_tanh;
+  a.ld_out = ld_out;
+  a.tern = tern;
+  a.wts = static_cast<float*>(ws);
+  const int64_t weff = mimo ? W : std::min(W, L);
+  TESM_REQUIRE(ws && ws_bytes >= ent_ws_bytes(B, L, H, weff), kErrWorkspace, "local_ent: workspace too small");
+  return launch_local_ent(a, static_cast<hipStream_t>(stream));
+}
+
+int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p) {
+  if (!p) return -1;
+  return plan_siso(*p, nullptr).total;
+}
+
+int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso layer: null descriptor");
+  const tesm_hip_siso_layer& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso layer: dtype must be 0 or 1");
+  TESM_REQUIRE(p.B >= 1 && p.L >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.ent_rank >= 2 && p.ent_rank % 2 == 0 &&
+                   p.window >= 1 && p.window <= 64 && p.chunk_size >= 1,
+               kErrInvalidArg, "siso layer: bad sizes (need even ent_rank, 1 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.y && p.states, kErrInvalidArg,
+               "siso layer: null pointer");
+  if (int rc = check_linear(p.in_proj, p.d_model, "in_proj")) return rc;
+  if (int rc = check_linear(p.state_proj, p.d_state, "state_proj")) return rc;
+  if (int rc = check_linear(p.ent_proj, p.d_state, "ent_proj")) return rc;
+  if (int rc = check_linear(p.out_proj, p.d_model, "out_proj")) return rc;
+  if (p.cross_state)
+    if (int rc = check_linear(p.cross_q_proj, p.d_state, "cross_q_proj")) return rc;
+  const SisoPlan s = plan_siso(p, ws);
+  TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "siso layer: workspace too small");
+
+  const int dt = p.dt;
+  const int es = esize(dt);
+  const int64_t M = p.B * p.L, dm = p.d_model, D = p.d_state, R = p.ent_rank;
+  const int64_t n_in = 2 * dm + 3 * D + 2 * R;
+  char* proj = static_cast<char*>(s.proj);
+  // slice offsets of the in_proj output (tesm.py:1197-1201)
+  const int64_t o_local = 0, o_sv = dm, o_decay = dm + D, o_write = dm + 2 * D, o_gate = dm + 3 * D,
+                o_q = 2 * dm + 3 * D, o_k = 2 * dm + 3 * D + R;
+  int rc;
+  // 1. in_proj
+  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
+  if (p.proj_out) {
+    if (hipMemcpyAsync(p.proj_out, proj, M * n_in * es, hipMemcpyDeviceToDevice, st) != hipSuccess)
+      return fail(kErrLaunch, "siso layer: proj copy failed");
+  }
+  // 2. cross-layer query bias (tesm.py:1213-1218)
+  if (p.cross_state) {
+    if ((rc = launch_quant_act(p.cross_state, dt, M, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs, st)))
+      return rc;
+    if ((rc = run_linear(s.xs, p.cross_q_proj, M, R, D, s.cq, dt, R, st))) return rc;
+  }
+  // 3. gates + state scan (tesm.py:1202-1205, 1222-1223)
+  ScanArgs sa;
+  sa.mode = 1;
+  sa.dt = dt;
+  sa.out_dt = dt;
+  sa.clamp = 1;
+  sa.round_update = 1;
+  sa.B = p.B;
+  sa.L = p.L;
+  sa.C = D;
+  sa.cs = p.chunk_size;
+  sa.decay = proj + o_decay * es;
+  sa.ld_decay = n_in;
+  sa.update = proj + o_write * es;
+  sa.ld_update = n_in;
+  sa.sv = proj + o_sv * es;
+  sa.ld_sv = n_in;
+  sa.decay_bias = p.decay_bias;
+  sa.h0 = p.h0;
+  sa.states = p.states;
+  sa.ld_states = D;
+  sa.h_final = p.h_final;
+  if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
+  // 4. local entanglement + mix (tesm.py:853-952, 1231-1232)
+  EntArgs ea;
+  ea.dt = dt;
+  ea.mimo = 0;
+  ea.B = p.B;
+  ea.L = p.L;
+  ea.H = 1;
+  ea.R = R;
+  ea.D = D;
+  ea.W = p.window;
+  ea.q = proj + o_q * es;
+  ea.ld_q = n_in;
+  ea.k = proj + o_k * es;
+  ea.ld_k = n_in;
+  ea.rope = static_cast<const float2*>(p.rope);
+  ea.q_add = s.cq;
+  ea.ld_qadd = R;
+  ea.bias = p.local_bias;
+  ea.thr = p.thr;
+  ea.ent_scale = p.ent_scale;
+  ea.S = p.states;
+  ea.ld_s = D;
+  ea.e_tanh = s.e_tanh;
+  ea.c_out = s.c_mix;
+  ea.ld_out = D;
+  ea.wts = s.wts;
+  if ((rc = launch_local_ent(ea, st))) return rc;
+  // 5. state_proj(tanh E), ent_proj(C) and the output gate (tesm.py:1256-1260)
+  if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
+  if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  LinearArgs ga;
+  ga.op[0] = operand(s.xe, p.state_proj);
+  ga.op[1] = operand(s.xc, p.ent_proj);
+  ga.M = M;
+  ga.N = dm;
+  ga.Kp = kpad(D);
+  ga.out = s.yg;
+  ga.ldo = dm;
+  ga.out_dt = dt;
+  ga.epilogue = kEpiOutputGate;
+  ga.local = proj + o_local * es;
+  ga.ld_local = n_in;
+  ga.gate = proj + o_gate * es;
+  ga.ld_gate = n_in;
+  if ((rc = launch_linear(ga, st))) return rc;
+  // 6. out_proj (tesm.py:1261; dropout is identity in eval)
+  if ((rc = launch_quant_act(s.yg, dt, M, dm, dm, p.bit_eps, 1, s.xy.q, s.xy.ldq, s.xy.s, s.xy.rs, st))) return rc;
+  return run_linear(s.xy, p.out_proj, M, dm, dm, p.y, dt, dm, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,366 @@
+// INT2 x INT8 BitLinear products for gfx950.
+//
+// Reference semantics (tesm_ssm/modules/tesm.py:238-290, torch branch):
+//   y = F.linear(q_x / s_x, q_w / s_w) with q_x int8 per-token codes and q_w ternary codes.
+// Here the contraction is done exactly in int32 on the codes and scaled once:
+//   acc = sum_k q_x[m,k] * q_w[n,k];   y = acc / s_x[m] * c_w     (c_w = 1 / s_w rounded)
+// Weights arrive packed (code + 1 in {0,1,2}, four per byte), so the kernels form
+//   acc = sum_k q_x * u_w - sum_k q_x      (u = code + 1)
+// and the per-row sum of activation codes (from the quantization kernel) removes the offset.
+//
+// Two kernels:
+//   * gemv_kernel  (M <= 4): bandwidth-bound decode path.  Each lane streams 16-byte packed
+//     chunks (64 codes) with one 128-bit load, unpacks in registers with shift/and and
+//     multiplies with v_dot4_i32_i8 against activation codes held in registers.
+//   * mfma_kernel  (M > 4): LDS-tiled int8 MFMA (v_mfma_i32_16x16x64_i8).  Packed weight tiles
+//     are unpacked to int8 while being staged in LDS; A and B fragments are stored in MFMA
+//     lane order so every ds_read_b128 of a wave is one contiguous 1 KiB block.
+#include "tesm_hip_internal.h"
+
+namespace tesm {
+
+namespace {
+
+__device__ __forceinline__ uint32_t unpack_u(uint32_t w, int s) { return (w >> (2 * s)) & 0x03030303u; }
+
+template <int OUT_DT>
+__device__ __forceinline__ void store_plain(const LinearArgs& a, int64_t m, int64_t n, float v) {
+  if (a.bias) v = v + ld<OUT_DT>(a.bias, n);
+  st<OUT_DT>(a.out, m * a.ldo + n, v);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV
+// ---------------------------------------------------------------------------
+template <int LPR, int MR, int NCH, int OUT_DT>
+__global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
+  constexpr int RPG = 4;          // output rows per lane group (independent loads in flight)
+  constexpr int GPW = 64 / LPR;   // lane groups per wave
+  const LinearOperand& o = a.op[0];
+  const int lane = threadIdx.x & 63;
+  const int g = lane & (LPR - 1);
+  const int64_t group = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * GPW + lane / LPR;
+  const int64_t n0 = group * RPG;
+  if (n0 >= a.N) return;
+  const int64_t nch = a.Kp / 64;
+
+  uint4 W[RPG][NCH];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    const int64_t n = n0 + r;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int64_t c = g + LPR * i;
+      W[r][i] = (n < a.N && c < nch) ? *reinterpret_cast<const uint4*>(o.w + n * o.ldw + 16 * c)
+                                     : make_uint4(0, 0, 0, 0);
+    }
+  }
+  uint32_t X[MR][NCH][16];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int64_t c = g + LPR * i;
+      const bool ok = m < a.M && c < nch;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint4 v = ok ? *reinterpret_cast<const uint4*>(o.q + m * o.ldq + 64 * c + 16 * d)
+                           : make_uint4(0, 0, 0, 0);
+        X[m][i][4 * d + 0] = v.x;
+        X[m][i][4 * d + 1] = v.y;
+        X[m][i][4 * d + 2] = v.z;
+        X[m][i][4 * d + 3] = v.w;
+      }
+    }
+  }
+  int acc[RPG][MR];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[r][m] = 0;
+
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const uint32_t wd[4] = {W[r][i].x, W[r][i].y, W[r][i].z, W[r][i].w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int u = static_cast<int>(unpack_u(wd[d], s));
+#pragma unroll
+          for (int m = 0; m < MR; ++m)
+            acc[r][m] = __builtin_amdgcn_sdot4(u, static_cast<int>(X[m][i][4 * d + s]), acc[r][m], false);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPG; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      int v = acc[r][m];
+#pragma unroll
+      for (int mask = LPR / 2; mask > 0; mask >>= 1) v += __shfl_xor(v, mask, 64);
+      acc[r][m] = v;
+    }
+  if (g != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= a.M) break;
+    const float inv = 1.0f / o.s_x[m];
+    const int32_t rs = o.rowsum[m];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) {
+      const int64_t n = n0 + r;
+      if (n >= a.N) break;
+      const int32_t av = acc[r][m] - rs;
+      if (a.acc_dump) a.acc_dump[m * a.N + n] = av;
+      const float cw = o.c_w_per_row ? o.c_w[n] : o.c_w[0];
+      store_plain<OUT_DT>(a, m, n, (static_cast<float>(av) * inv) * cw);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM
+// ---------------------------------------------------------------------------
+template <int WM, int WN, int TM, int TN>
+struct Cfg {
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int BM = WM * TM * 16, BN = WN * TN * 16, BK = 128;
+  static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_CHUNKS = BM * BK / 16;  // 16-byte code chunks per K tile
+  static constexpr int B_CHUNKS = BN * BK / 64;  // 16-byte packed chunks per K tile
+  static constexpr int A_PT = (A_CHUNKS + NT - 1) / NT;
+  static constexpr int B_PT = (B_CHUNKS + NT - 1) / NT;
+};
+
+// LDS fragment order: fragment (tile t of 16 rows, k-step ks of 64 codes) is 1 KiB; lane L holds
+// the 16 bytes of row 16t + L%16, code group 4ks + L/16 (16 codes).  The same order for A rows and
+// B columns makes lane L's A and B operands cover the same 16 codes.
+__device__ __forceinline__ int frag_off(int r, int kg) {
+  return (((r >> 4) * 2 + (kg >> 2)) << 10) + (((r & 15) + 16 * (kg & 3)) << 4);
+}
+
+template <class C, int TM, int TN>
+__device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
+                                              int64_t Kp, v4i (&acc)[TM][TN], char* smem) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w / (C::BN / (TN * 16)), wn = w % (C::BN / (TN * 16));
+  uint4 ra[C::A_PT], rb[C::B_PT];
+
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int p = 0; p < C::A_PT; ++p) {
+      const int c = t + p * C::NT;
+      if (c < C::A_CHUNKS) {
+        const int64_t m = m0 + (c >> 3);
+        ra[p] = m < M ? *reinterpret_cast<const uint4*>(o.q + m * o.ldq + k0 + 16 * (c & 7))
+                      : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < C::B_PT; ++p) {
+      const int c = t + p * C::NT;
+      if (c < C::B_CHUNKS) {
+        const int64_t n = n0 + (c >> 1);
+        rb[p] = n < N ? *reinterpret_cast<const uint4*>(o.w + n * o.ldw + k0 / 4 + 16 * (c & 1))
+                      : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  auto sstore = [&](char* stage) {
+#pragma unroll
+    for (int p = 0; p < C::A_PT; ++p) {
+      const int c = t + p * C::NT;
+      if (c < C::A_CHUNKS) *reinterpret_cast<uint4*>(stage + frag_off(c >> 3, c & 7)) = ra[p];
+    }
+    char* sb = stage + C::A_BYTES;
+#pragma unroll
+    for (int p = 0; p < C::B_PT; ++p) {
+      const int c = t + p * C::NT;
+      if (c < C::B_CHUNKS) {
+        const int r = c >> 1, h = c & 1;
+        const uint32_t wd[4] = {rb[p].x, rb[p].y, rb[p].z, rb[p].w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint4 u = make_uint4(unpack_u(wd[d], 0), unpack_u(wd[d], 1), unpack_u(wd[d], 2), unpack_u(wd[d], 3));
+          *reinterpret_cast<uint4*>(sb + frag_off(r, 4 * h + d)) = u;
+        }
+      }
+    }
+  };
+
+  const int64_t nk = Kp / C::BK;
+  gload(0);
+  sstore(smem);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const char* cur = smem + (kt & 1) * C::STAGE;
+    if (kt + 1 < nk) gload((kt + 1) * C::BK);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      v4i af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const v4i*>(cur + ((((wm * TM + i) * 2 + ks)) << 10) + lane * 16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const v4i*>(cur + C::A_BYTES + ((((wn * TN + j) * 2 + ks)) << 10) + lane * 16);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * C::STAGE);
+    __syncthreads();
+  }
+}
+
+// Accumulator layout of v_mfma_i32_16x16x64_i8: lane L, element r -> row 4*(L/16) + r, column L%16.
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
+__global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
+  using C = Cfg<WM, WN, TM, TN>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
+  v4i acc0[TM][TN], acc1[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc0[i][j] = v4i{0, 0, 0, 0};
+      acc1[i][j] = v4i{0, 0, 0, 0};
+    }
+  mfma_mainloop<C, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w / WN, wn = w % WN;
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    int64_t mr[4];
+    float inv0[4], inv1[4];
+    int32_t rs0[4], rs1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      mr[r] = m0 + (wm * TM + i) * 16 + 4 * (lane >> 4) + r;
+      const bool ok = mr[r] < a.M;
+      inv0[r] = ok ? 1.0f / o0.s_x[mr[r]] : 0.0f;
+      rs0[r] = ok ? o0.rowsum[mr[r]] : 0;
+      if constexpr (EPI == kEpiOutputGate) {
+        inv1[r] = ok ? 1.0f / o1.s_x[mr[r]] : 0.0f;
+        rs1[r] = ok ? o1.rowsum[mr[r]] : 0;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + (wn * TN + j) * 16 + (lane & 15);
+      if (n >= a.N) continue;
+      const float cw0 = o0.c_w_per_row ? o0.c_w[n] : o0.c_w[0];
+      float cw1 = 0.0f;
+      if constexpr (EPI == kEpiOutputGate) cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = mr[r];
+        if (m >= a.M) continue;
+        const int32_t a0 = acc0[i][j][r] - rs0[r];
+        if (a.acc_dump) a.acc_dump[m * a.N + n] = a0;
+        const float v0 = (static_cast<float>(a0) * inv0[r]) * cw0;
+        if constexpr (EPI == kEpiStore) {
+          store_plain<OUT_DT>(a, m, n, v0);
+        } else {
+          const float sp = rnd<OUT_DT>(v0);
+          const float ep = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1[r]) * inv1[r]) * cw1);
+          const float gt = rnd<OUT_DT>(sigmoidf_(ld<OUT_DT>(a.gate, m * a.ld_gate + n)));
+          const float lo = ld<OUT_DT>(a.local, m * a.ld_local + n);
+          const float y = rnd<OUT_DT>(lo + rnd<OUT_DT>(gt * sp));
+          st<OUT_DT>(a.out, m * a.ldo + n, y + ep);
+        }
+      }
+    }
+  }
+}
+
+template <int WM, int WN, int TM, int TN, int EPI>
+int run_mfma(const LinearArgs& a, hipStream_t st) {
+  using C = Cfg<WM, WN, TM, TN>;
+  dim3 grid(static_cast<unsigned>((a.N + C::BN - 1) / C::BN), static_cast<unsigned>((a.M + C::BM - 1) / C::BM));
+  if (a.out_dt == kBF16)
+    mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
+  else
+    mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
+  return check_launch("bitlinear mfma");
+}
+
+template <int LPR, int MR, int NCH>
+int run_gemv(const LinearArgs& a, hipStream_t st) {
+  constexpr int GPW = 64 / LPR;
+  const int64_t groups = (a.N + 3) / 4;
+  const int64_t waves = (groups + GPW - 1) / GPW;
+  const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
+  if (a.out_dt == kBF16)
+    gemv_kernel<LPR, MR, NCH, kBF16><<<blocks, 256, 0, st>>>(a);
+  else
+    gemv_kernel<LPR, MR, NCH, kF32><<<blocks, 256, 0, st>>>(a);
+  return check_launch("bitlinear gemv");
+}
+
+template <int MR>
+int dispatch_gemv(const LinearArgs& a, int64_t nch, hipStream_t st) {
+  if (nch <= 4) return run_gemv<4, MR, 1>(a, st);
+  if (nch <= 8) return run_gemv<8, MR, 1>(a, st);
+  if (nch <= 16) return run_gemv<16, MR, 1>(a, st);
+  if (nch <= 32) return run_gemv<32, MR, 1>(a, st);
+  if (nch <= 64) return run_gemv<64, MR, 1>(a, st);
+  if (nch <= 128) return run_gemv<64, MR, 2>(a, st);
+  return run_gemv<64, MR, 4>(a, st);
+}
+
+int check_operand(const LinearOperand& o, int64_t Kp, const char* which) {
+  std::string p = std::string("bitlinear ") + which + ": ";
+  TESM_REQUIRE(o.q && o.s_x && o.rowsum && o.w && o.c_w, kErrInvalidArg, p + "null pointer");
+  TESM_REQUIRE(o.ldq >= Kp && o.ldq % 16 == 0, kErrInvalidArg, p + "ldq must be >= Kp and a multiple of 16");
+  TESM_REQUIRE(o.ldw >= Kp / 4 && o.ldw % 16 == 0, kErrInvalidArg, p + "ldw must be >= Kp/4 and a multiple of 16");
+  TESM_REQUIRE(aligned(o.q, 16) && aligned(o.w, 16), kErrAlignment, p + "codes and packed weights must be 16-byte aligned");
+  return kOk;
+}
+
+}  // namespace
+
+int launch_linear(const LinearArgs& a, hipStream_t st) {
+  TESM_REQUIRE(a.M >= 0 && a.N >= 0, kErrInvalidArg, "bitlinear: negative size");
+  TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "bitlinear: Kp must be a positive multiple of 128");
+  TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "bitlinear: out dtype must be 0 or 1");
+  TESM_REQUIRE(a.epilogue == kEpiStore || a.epilogue == kEpiOutputGate, kErrInvalidArg, "bitlinear: bad epilogue");
+  if (a.M == 0 || a.N == 0) return kOk;
+  TESM_REQUIRE(a.out && a.ldo >= a.N, kErrInvalidArg, "bitlinear: need out and ldo >= N");
+  if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
+  if (a.epilogue == kEpiOutputGate) {
+    if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
+    TESM_REQUIRE(a.local && a.gate && a.ld_local >= a.N && a.ld_gate >= a.N, kErrInvalidArg,
+                 "bitlinear output gate: need local and gate operands");
+    TESM_REQUIRE(a.bias == nullptr, kErrInvalidArg, "bitlinear output gate: bias unsupported");
+  }
+  const int64_t nch = a.Kp / 64;
+  if (a.epilogue == kEpiStore && a.M <= 4 && nch <= 256) {
+    if (a.M == 1) return dispatch_gemv<1>(a, nch, st);
+    if (a.M == 2) return dispatch_gemv<2>(a, nch, st);
+    return dispatch_gemv<4>(a, nch, st);
+  }
+  if (a.epilogue == kEpiStore) {
+    if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
+    if (a.M <= 64) return run_mfma<1, 4, 4, 1, kEpiStore>(a, st);
+    return run_mfma<2, 2, 4, 4, kEpiStore>(a, st);
+  }
+  if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
+  if (a.M <= 64) return run_mfma<1, 4, 4, 1, kEpiOutputGate>(a, st);
+  return run_mfma<2, 2, 4, 4, kEpiOutputGate>(a, st);
+}
+
+}  // namespace tesm

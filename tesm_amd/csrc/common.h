@@ -1,0 +1,130 @@
+// Shared device/host helpers for the TESM gfx950 kernels.
+//
+// Element types at the C-ABI are tagged by an int: 0 = float32, 1 = bfloat16
+// (raw 16-bit patterns, round-to-nearest-even on every store).  Every float
+// operation that the reference's torch path rounds to the module dtype is
+// rounded here at the same point (`rnd<DT>`), so that bf16 results follow the
+// reference op by op.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace tesm {
+
+enum Dtype : int { kF32 = 0, kBF16 = 1 };
+
+// ---------------------------------------------------------------------------
+// bf16 <-> f32
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Round a float to the nearest value of the storage dtype (identity for f32).
+template <int DT>
+__device__ __forceinline__ float rnd(float f) {
+  if constexpr (DT == kBF16) {
+    return bf16_to_f32(f32_to_bf16(f));
+  } else {
+    return f;
+  }
+}
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<kF32> {
+  using T = float;
+};
+template <>
+struct Elem<kBF16> {
+  using T = uint16_t;
+};
+
+template <int DT>
+__device__ __forceinline__ float ld(const void* p, int64_t i) {
+  if constexpr (DT == kBF16) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  } else {
+    return static_cast<const float*>(p)[i];
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void st(void* p, int64_t i, float v) {
+  if constexpr (DT == kBF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  } else {
+    static_cast<float*>(p)[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// transcendental helpers (IEEE float32 in, float32 out; libm-accurate ocml calls)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WIDTH));
+  return v;
+}
+
+template <int WIDTH = 64>
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
+  return v;
+}
+
+template <int WIDTH = 64>
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing (thread-local last error, returned codes)
+// ---------------------------------------------------------------------------
+enum Status : int {
+  kOk = 0,
+  kErrInvalidArg = 1,
+  kErrAlignment = 2,
+  kErrUnsupported = 3,
+  kErrLaunch = 4,
+  kErrWorkspace = 5,
+};
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// K padding used by every int8-code and packed-INT2 buffer of the BitLinear path:
+// one GEMM K tile is 128 codes.
+constexpr int64_t kKTile = 128;
+inline int64_t kpad(int64_t K) { return round_up(K < 1 ? 1 : K, kKTile); }
+
+}  // namespace tesm
+
+#define TESM_REQUIRE(cond, code, msg)        \
+  do {                                       \
+    if (!(cond)) return ::tesm::fail((code), (msg)); \
+  } while (0)

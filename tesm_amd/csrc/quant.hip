@@ -1,0 +1,243 @@
+// BitLinear quantization kernels for gfx950:
+//   * per-token int8 activation codes      (reference tesm_ssm/modules/tesm.py:206-209)
+//   * per-tensor absmean ternary scale      (tesm.py:211-212)
+//   * ternary codes packed 4 per byte       (tesm.py:213-214 + tesm_ssm/utils/int2_quantization.py:21-58)
+//   * unpacking back to signed codes        (int2_quantization.py:68-93)
+//
+// Code buffers feed the INT2 x INT8 GEMV/GEMM, which unpacks a packed dword
+// W (16 codes, code k = 4j + s of the group in bits 8j+2s) as the four dwords
+// (W >> 2s) & 0x03030303.  Byte j of dword s then holds code 4j + s, so the
+// activation codes are written in the matching order ("layout 1"): within each
+// group of 16, byte 4s + j holds x[4j + s].  Layout 0 is plain row-major.
+#include "tesm_hip_internal.h"
+
+namespace tesm {
+
+// One wave per row; 4 rows per 256-thread workgroup.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__ x, int64_t M, int64_t K,
+                                                        int64_t ldx, float eps, int layout, int8_t* __restrict__ q,
+                                                        int64_t ldq, float* __restrict__ s_out,
+                                                        int32_t* __restrict__ rowsum) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int64_t base = row * ldx;
+
+  float amax = 0.0f;
+  for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(ld<DT>(x, base + k)));
+  amax = wave_max(amax);
+
+  // scale = 127 / amax.clamp_min(eps), evaluated by torch as reciprocal() * 127
+  float sc;
+  if constexpr (DT == kBF16) {
+    const float e = rnd<DT>(eps);
+    const float d = amax < e ? e : amax;
+    sc = rnd<DT>(rnd<DT>(1.0f / d) * 127.0f);
+  } else {
+    const float d = amax < eps ? eps : amax;
+    sc = (1.0f / d) * 127.0f;
+  }
+
+  int32_t rs = 0;
+  const int64_t ngroups = ldq / 16;
+  for (int64_t g = lane; g < ngroups; g += 64) {
+    float v[16];
+    const int64_t k0 = g * 16;
+    if (VEC && k0 + 16 <= K) {
+      if constexpr (DT == kBF16) {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + k0);
+        const uint4 a = p[0], b = p[1];
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          v[2 * i] = __uint_as_float(w[i] << 16);
+          v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+      } else {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + k0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 f = p[i];
+          v[4 * i] = f.x;
+          v[4 * i + 1] = f.y;
+          v[4 * i + 2] = f.z;
+          v[4 * i + 3] = f.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = (k0 + i < K) ? ld<DT>(x, base + k0 + i) : 0.0f;
+    }
+    uint32_t c[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float r = rintf(rnd<DT>(v[i] * sc));
+      r = fminf(fmaxf(r, -128.0f), 127.0f);
+      const int ci = static_cast<int>(r);
+      rs += ci;
+      c[i] = static_cast<uint32_t>(ci) & 0xffu;
+    }
+    uint4 out;
+    if (layout == 1) {
+      out.x = c[0] | (c[4] << 8) | (c[8] << 16) | (c[12] << 24);
+      out.y = c[1] | (c[5] << 8) | (c[9] << 16) | (c[13] << 24);
+      out.z = c[2] | (c[6] << 8) | (c[10] << 16) | (c[14] << 24);
+      out.w = c[3] | (c[7] << 8) | (c[11] << 16) | (c[15] << 24);
+    } else {
+      out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+      out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+      out.z = c[8] | (c[9] << 8) | (c[10] << 16) | (c[11] << 24);
+      out.w = c[12] | (c[13] << 8) | (c[14] << 16) | (c[15] << 24);
+    }
+    *reinterpret_cast<uint4*>(q + row * ldq + k0) = out;
+  }
+  rs = wave_sum_i(rs);
+  if (lane == 0) {
+    s_out[row] = sc;
+    if (rowsum) rowsum[row] = rs;
+  }
+}
+
+int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
+                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st) {
+  TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "quant_act: dtype must be 0 (f32) or 1 (bf16)");
+  TESM_REQUIRE(M >= 0 && K >= 1 && ldx >= K, kErrInvalidArg, "quant_act: need M >= 0, K >= 1, ldx >= K");
+  TESM_REQUIRE(ldq >= K && ldq % 16 == 0, kErrInvalidArg, "quant_act: ldq must be >= K and a multiple of 16");
+  TESM_REQUIRE(layout == 0 || layout == 1, kErrInvalidArg, "quant_act: layout must be 0 or 1");
+  TESM_REQUIRE(M == 0 || (x && q && s_x), kErrInvalidArg, "quant_act: null pointer");
+  TESM_REQUIRE(aligned(q, 16), kErrAlignment, "quant_act: code buffer must be 16-byte aligned");
+  if (M == 0) return kOk;
+  const int esz = dt == kBF16 ? 2 : 4;
+  const bool vec = aligned(x, 16) && (ldx * esz) % 16 == 0;
+  dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  if (dt == kBF16) {
+    if (vec)
+      quant_act_kernel<kBF16, true><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+    else
+      quant_act_kernel<kBF16, false><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+  } else {
+    if (vec)
+      quant_act_kernel<kF32, true><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+    else
+      quant_act_kernel<kF32, false><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+  }
+  return check_launch("quant_act");
+}
+
+// ---------------------------------------------------------------------------
+// absmean weight scale: s_w = 1 / max(mean|w|, eps), c_w = 1 / s_w (the value of a
+// dequantized +1 code).  Deterministic: fixed grid, fixed reduction order, fp64 sums.
+// ---------------------------------------------------------------------------
+constexpr int kAbsmeanBlocks = 512;
+
+template <int DT>
+__global__ __launch_bounds__(256) void absmean_partial_kernel(const void* __restrict__ w, int64_t n,
+                                                              double* __restrict__ partial) {
+  __shared__ double red[4];
+  double acc = 0.0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    acc += fabs(static_cast<double>(ld<DT>(w, i)));
+  acc = wave_sum_d(acc);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <int DT>
+__global__ __launch_bounds__(64) void absmean_final_kernel(const double* __restrict__ partial, int np, int64_t n,
+                                                           float eps, float* __restrict__ s_w,
+                                                           float* __restrict__ c_w) {
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < np; i += 64) acc += partial[i];
+  acc = wave_sum_d(acc);
+  if (threadIdx.x == 0) {
+    float m = rnd<DT>(static_cast<float>(acc / static_cast<double>(n)));
+    const float e = rnd<DT>(eps);
+    m = m < e ? e : m;
+    const float s = rnd<DT>(1.0f / m);
+    s_w[0] = s;
+    c_w[0] = rnd<DT>(1.0f / s);
+  }
+}
+
+int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, float* s_w, float* c_w, hipStream_t st) {
+  TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "absmean: dtype must be 0 (f32) or 1 (bf16)");
+  TESM_REQUIRE(n >= 1 && w && ws && s_w && c_w, kErrInvalidArg, "absmean: need n >= 1 and non-null pointers");
+  const int nb = static_cast<int>(std::min<int64_t>(kAbsmeanBlocks, (n + 255) / 256));
+  if (dt == kBF16) {
+    absmean_partial_kernel<kBF16><<<nb, 256, 0, st>>>(w, n, ws);
+    absmean_final_kernel<kBF16><<<1, 64, 0, st>>>(ws, nb, n, eps, s_w, c_w);
+  } else {
+    absmean_partial_kernel<kF32><<<nb, 256, 0, st>>>(w, n, ws);
+    absmean_final_kernel<kF32><<<1, 64, 0, st>>>(ws, nb, n, eps, s_w, c_w);
+  }
+  return check_launch("absmean");
+}
+
+// ---------------------------------------------------------------------------
+// INT2 packing: code = clamp(rne(w * s_w), -1, 1) + 1, four codes per byte, code of
+// k = 4j + i in bits 2i..2i+1 of byte j, bytes past ceil(K/4) and codes past K hold
+// code 1 (value 0).  One thread per packed byte.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void pack_kernel(const void* __restrict__ w, int64_t N, int64_t K, int64_t ldw,
+                                                   const float* __restrict__ s_w, int per_row,
+                                                   uint8_t* __restrict__ packed, int64_t ldp) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= N * ldp) return;
+  const int64_t n = idx / ldp, j = idx - n * ldp;
+  const float s = per_row ? s_w[n] : s_w[0];
+  uint32_t byte = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t k = 4 * j + i;
+    uint32_t u = 1;
+    if (k < K) {
+      float r = rintf(rnd<DT>(ld<DT>(w, n * ldw + k) * s));
+      r = fminf(fmaxf(r, -1.0f), 1.0f);
+      u = static_cast<uint32_t>(static_cast<int>(r) + 1);
+    }
+    byte |= u << (2 * i);
+  }
+  packed[idx] = static_cast<uint8_t>(byte);
+}
+
+int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
+                uint8_t* packed, int64_t ldp, hipStream_t st) {
+  TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "pack_w_i2: dtype must be 0 (f32) or 1 (bf16)");
+  TESM_REQUIRE(N >= 0 && K >= 1 && ldw >= K && ldp >= (K + 3) / 4, kErrInvalidArg,
+               "pack_w_i2: need K >= 1, ldw >= K, ldp >= ceil(K/4)");
+  TESM_REQUIRE(N == 0 || (w && s_w && packed), kErrInvalidArg, "pack_w_i2: null pointer");
+  if (N == 0) return kOk;
+  const int64_t total = N * ldp;
+  const unsigned nb = static_cast<unsigned>((total + 255) / 256);
+  if (dt == kBF16)
+    pack_kernel<kBF16><<<nb, 256, 0, st>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
+  else
+    pack_kernel<kF32><<<nb, 256, 0, st>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
+  return check_launch("pack_w_i2");
+}
+
+__global__ __launch_bounds__(256) void unpack_kernel(const uint8_t* __restrict__ packed, int64_t N, int64_t K,
+                                                     int64_t ldp, int8_t* __restrict__ codes, int64_t ldc) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= N * K) return;
+  const int64_t n = idx / K, k = idx - n * K;
+  const int u = (packed[n * ldp + k / 4] >> (2 * (k & 3))) & 3;
+  codes[n * ldc + k] = static_cast<int8_t>(u - 1);
+}
+
+int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
+                  hipStream_t st) {
+  TESM_REQUIRE(N >= 0 && K >= 1 && ldp >= (K + 3) / 4 && ldc >= K, kErrInvalidArg,
+               "unpack_w_i2: need K >= 1, ldp >= ceil(K/4), ldc >= K");
+  TESM_REQUIRE(N == 0 || (packed && codes), kErrInvalidArg, "unpack_w_i2: null pointer");
+  if (N == 0) return kOk;
+  const unsigned nb = static_cast<unsigned>((N * K + 255) / 256);
+  unpack_kernel<<<nb, 256, 0, st>>>(packed, N, K, ldp, codes, ldc);
+  return check_launch("unpack_w_i2");
+}
+
+}  // namespace tesm

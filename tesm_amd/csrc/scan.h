@@ -1,0 +1,35 @@
+// State-scan arguments shared by the scan kernels and the fused layer drivers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tesm {
+
+struct ScanArgs {
+  int mode = 0;        // 0: decay/update given; 1: gates from raw projection slices
+  int dt = 0;          // input dtype (0 f32, 1 bf16)
+  int out_dt = 0;      // states dtype
+  int clamp = 1;       // 1: SISO closed-form clamp semantics (1e-12); 0: plain recurrence (MIMO)
+  int round_update = 1;  // mode 1: round write*tanh(sv) to dt (SISO) or keep fp32 (MIMO)
+  int64_t B = 0, L = 0, C = 0;
+  int64_t cs = 16;     // reference chunk size (state_scan_chunk_size)
+  // token-major inputs: element (b, t, c) at ptr[(b*L + t)*ld + c]
+  const void* decay = nullptr;   // mode 0: decay; mode 1: raw decay slice
+  int64_t ld_decay = 0;
+  const void* update = nullptr;  // mode 0: update; mode 1: raw write slice
+  int64_t ld_update = 0;
+  const void* sv = nullptr;      // mode 1: raw state_value slice
+  int64_t ld_sv = 0;
+  const void* decay_bias = nullptr;  // mode 1: (C) in dt
+  const double* h0 = nullptr;    // (B, C) initial state or null
+  void* states = nullptr;        // (b, t, c) at states[(b*L + t)*ld_states + c], out_dt
+  int64_t ld_states = 0;
+  double* h_final = nullptr;     // (B, C) final state or null
+};
+
+int64_t scan_chunk_len(int64_t L, int64_t cs);
+int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs);
+int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st);
+
+}  // namespace tesm

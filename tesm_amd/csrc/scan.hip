@@ -1,0 +1,153 @@
+// Chunked parallel state scan for gfx950:  h_t = d_t * h_{t-1} + g_t * u_t  over (B, L, C).
+//
+// Reference (torch branch): tesm_ssm/modules/tesm.py:1065-1164 (SISO) and
+// tesm_ssm/modules/tesm_mimo.py:375-392 (MIMO, sequential, no clamps).
+// The SISO reference evaluates each chunk of `state_scan_chunk_size` positions in closed form,
+//   A = cumprod(max(d, 1e-12)),  s = A * (h0 + cumsum(u / max(A, 1e-12))),
+// which is the recurrence above with g_t = A_t / max(A_t, 1e-12) (A_t = product of the clamped
+// decays since the start of the reference chunk).  g_t = 1 except when a within-chunk product
+// falls below 1e-12; the kernels reproduce that factor ("clamp" mode) and run the recurrence in
+// fp32 registers.
+//
+// Three launches, all channel-parallel (one lane per channel, coalesced along C):
+//   1. summary: each (b, chunk of T positions, channel) scans its chunk from h = 0 and stores
+//      (prod d, h_end);
+//   2. carry:   each (b, channel) folds the chunk summaries in order -> carry into every chunk
+//      and the final state (fp64 at the API);
+//   3. apply:   each (b, chunk, channel) rescans its chunk from its carry and writes the states.
+// Gate fusion ("mode 1") reads the raw in_proj slices and evaluates
+//   d = sigmoid(decay_raw + decay_bias), u = sigmoid(write_raw) * tanh(sv_raw)
+// with the reference's rounding points (tesm.py:1202-1205, 1222).
+#include "tesm_hip_internal.h"
+#include "scan.h"
+
+namespace tesm {
+
+namespace {
+
+constexpr float kScanEps = 1e-12f;
+
+template <int DT, int MODE>
+struct ScanIn {
+  const ScanArgs& a;
+  __device__ __forceinline__ void at(int64_t b, int64_t t, int64_t ch, float& d, float& u) const {
+    const int64_t tok = b * a.L + t;
+    if constexpr (MODE == 0) {
+      d = ld<DT>(a.decay, tok * a.ld_decay + ch);
+      u = ld<DT>(a.update, tok * a.ld_update + ch);
+    } else {
+      const float sv = rnd<DT>(tanhf(ld<DT>(a.sv, tok * a.ld_sv + ch)));
+      d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(a.decay, tok * a.ld_decay + ch) + ld<DT>(a.decay_bias, ch))));
+      const float w = rnd<DT>(sigmoidf_(ld<DT>(a.update, tok * a.ld_update + ch)));
+      u = a.round_update ? rnd<DT>(w * sv) : w * sv;
+    }
+  }
+};
+
+// PHASE 1: write chunk summary; PHASE 3: rescan from the carry and store states.
+template <int DT, int OUT_DT, int MODE, int PHASE>
+__global__ __launch_bounds__(64) void scan_chunk_kernel(ScanArgs a, int64_t T, int64_t nc, float* __restrict__ summ,
+                                                        const float* __restrict__ carry) {
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t c = blockIdx.y, b = blockIdx.z;
+  if (ch >= a.C) return;
+  const ScanIn<DT, MODE> in{a};
+  const int64_t t0 = c * T, t1 = (t0 + T < a.L) ? t0 + T : a.L;
+  const int64_t sidx = (b * nc + c) * a.C + ch;
+  float h = (PHASE == 1) ? 0.0f : carry[sidx];
+  float P = 1.0f, A = 1.0f;
+  for (int64_t t = t0; t < t1; ++t) {
+    float d, u;
+    in.at(b, t, ch, d, u);
+    float g = 1.0f;
+    if (a.clamp) {
+      d = fmaxf(d, kScanEps);
+      A = ((t % a.cs) == 0) ? d : A * d;
+      if (A < kScanEps) g = A / kScanEps;
+    }
+    h = d * h + g * u;
+    if (PHASE == 1) {
+      P *= d;
+    } else {
+      st<OUT_DT>(a.states, (b * a.L + t) * a.ld_states + ch, h);
+    }
+  }
+  if (PHASE == 1) {
+    summ[2 * sidx] = P;
+    summ[2 * sidx + 1] = h;
+  }
+}
+
+__global__ __launch_bounds__(64) void scan_carry_kernel(ScanArgs a, int64_t nc, const float* __restrict__ summ,
+                                                        float* __restrict__ carry) {
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (ch >= a.C) return;
+  float h = a.h0 ? static_cast<float>(a.h0[b * a.C + ch]) : 0.0f;
+  for (int64_t c = 0; c < nc; ++c) {
+    const int64_t sidx = (b * nc + c) * a.C + ch;
+    carry[sidx] = h;
+    h = summ[2 * sidx] * h + summ[2 * sidx + 1];
+  }
+  if (a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(h);
+}
+
+template <int DT, int OUT_DT, int MODE>
+int run_scan(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
+  dim3 g3(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(nc), static_cast<unsigned>(a.B));
+  scan_chunk_kernel<DT, OUT_DT, MODE, 1><<<g3, 64, 0, st>>>(a, T, nc, summ, carry);
+  dim3 g2(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.B));
+  scan_carry_kernel<<<g2, 64, 0, st>>>(a, nc, summ, carry);
+  scan_chunk_kernel<DT, OUT_DT, MODE, 3><<<g3, 64, 0, st>>>(a, T, nc, summ, carry);
+  return check_launch("scan");
+}
+
+}  // namespace
+
+int64_t scan_chunk_len(int64_t L, int64_t cs) {
+  const int64_t cse = std::max<int64_t>(1, std::min(cs, L));
+  return cse >= 32 ? cse : cse * (32 / cse);
+}
+
+int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
+  if (L <= 0) return 0;
+  const int64_t T = scan_chunk_len(L, cs);
+  const int64_t nc = (L + T - 1) / T;
+  return round_up(B * nc * C * 3 * static_cast<int64_t>(sizeof(float)), 256);
+}
+
+int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
+  TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "scan: input dtype must be 0 or 1");
+  TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "scan: output dtype must be 0 or 1");
+  TESM_REQUIRE(a.mode == 0 || a.mode == 1, kErrInvalidArg, "scan: mode must be 0 (decay/update) or 1 (gates)");
+  TESM_REQUIRE(a.B >= 0 && a.L >= 0 && a.C >= 1 && a.cs >= 1, kErrInvalidArg, "scan: bad sizes");
+  if (a.B == 0 || a.L == 0) return kOk;
+  TESM_REQUIRE(a.decay && a.update && a.states, kErrInvalidArg, "scan: null pointer");
+  TESM_REQUIRE(a.ld_decay >= a.C && a.ld_update >= a.C && a.ld_states >= a.C, kErrInvalidArg, "scan: ld < C");
+  if (a.mode == 1)
+    TESM_REQUIRE(a.sv && a.decay_bias && a.ld_sv >= a.C, kErrInvalidArg, "scan mode 1: need sv and decay_bias");
+  const int64_t need = scan_ws_bytes(a.B, a.L, a.C, a.cs);
+  TESM_REQUIRE(ws && ws_bytes >= need, kErrWorkspace, "scan: workspace too small");
+  const int64_t T = scan_chunk_len(a.L, a.cs);
+  const int64_t nc = (a.L + T - 1) / T;
+  TESM_REQUIRE(nc <= 65535 && a.B <= 65535, kErrUnsupported, "scan: too many chunks or batch rows");
+  float* summ = static_cast<float*>(ws);
+  float* carry = summ + 2 * a.B * nc * a.C;
+  // the reference chunk grid starts at 0 with chunk = min(cs, L); pass the effective value
+  ScanArgs e = a;
+  e.cs = std::max<int64_t>(1, std::min(a.cs, a.L));
+  const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
+  switch (key) {
+    case 0: return run_scan<kF32, kF32, 0>(e, T, nc, summ, carry, st);
+    case 1: return run_scan<kF32, kF32, 1>(e, T, nc, summ, carry, st);
+    case 110: return run_scan<kBF16, kBF16, 0>(e, T, nc, summ, carry, st);
+    case 111: return run_scan<kBF16, kBF16, 1>(e, T, nc, summ, carry, st);
+    case 100: return run_scan<kBF16, kF32, 0>(e, T, nc, summ, carry, st);
+    case 101: return run_scan<kBF16, kF32, 1>(e, T, nc, summ, carry, st);
+    case 10: return run_scan<kF32, kBF16, 0>(e, T, nc, summ, carry, st);
+    case 11: return run_scan<kF32, kBF16, 1>(e, T, nc, summ, carry, st);
+    default: return fail(kErrInvalidArg, "scan: unsupported dtype combination");
+  }
+}
+
+}  // namespace tesm

@@ -1,0 +1,55 @@
+// Internal launchers shared between the kernel sources and the C-ABI layer.
+#pragma once
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace tesm {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
+                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st);
+int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, float* s_w, float* c_w, hipStream_t st);
+int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
+                uint8_t* packed, int64_t ldp, hipStream_t st);
+int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
+                  hipStream_t st);
+
+// One INT2 x INT8 product  out = (A_codes . W_codes) / s_x * c_w (+ bias).
+struct LinearOperand {
+  const int8_t* q = nullptr;     // (M, ldq) activation codes, layout 1, zero padded to Kp
+  int64_t ldq = 0;
+  const float* s_x = nullptr;    // (M) activation scales
+  const int32_t* rowsum = nullptr;  // (M) sum of activation codes
+  const uint8_t* w = nullptr;    // (N, ldw) packed INT2 weights, padded with code 1 to Kp
+  int64_t ldw = 0;
+  const float* c_w = nullptr;    // dequantized +1 weight value: scalar, or (N) if c_w_per_row
+  int c_w_per_row = 0;
+};
+
+// Epilogues of the GEMM/GEMV.
+enum Epilogue : int {
+  kEpiStore = 0,       // out = rnd(v (+ bias))
+  kEpiOutputGate = 1,  // out = rnd(rnd(local + rnd(sigmoid(gate) * sp)) + ep), two products (sp, ep)
+};
+
+struct LinearArgs {
+  LinearOperand op[2];  // op[1] used only by kEpiOutputGate
+  int64_t M = 0, N = 0, Kp = 0;
+  const void* bias = nullptr;  // (N) in out dtype, kEpiStore only
+  void* out = nullptr;
+  int64_t ldo = 0;
+  int out_dt = 0;
+  int epilogue = kEpiStore;
+  const void* local = nullptr;  // kEpiOutputGate: (M, ld_local) and raw gate (M, ld_gate), out dtype
+  int64_t ld_local = 0;
+  const void* gate = nullptr;
+  int64_t ld_gate = 0;
+  int32_t* acc_dump = nullptr;  // optional (M, N) signed int32 accumulators of op[0]
+};
+
+int launch_linear(const LinearArgs& a, hipStream_t st);
+
+}  // namespace tesm

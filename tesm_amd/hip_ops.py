@@ -1,0 +1,214 @@
+"""Tensor-level wrappers over the C-ABI (device memory and streams come from torch).
+
+Every function queues HIP kernels on the current torch stream of the tensors'
+device and returns torch tensors allocated here.  Nothing computes on the host
+and nothing falls back to torch ops: a missing library raises.
+
+Row-major 2-D operands may have a row stride (``x.stride(0)``) larger than their
+width as long as the last dimension is contiguous, so slices of a wider
+projection output are passed without copies.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DT = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def dt_code(dtype: torch.dtype) -> int:
+    try:
+        return _DT[dtype]
+    except KeyError:
+        raise TypeError(f"hip backend supports float32 and bfloat16, got {dtype}") from None
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """2-D view with a contiguous last dimension (copies only if needed)."""
+    if x.dim() != 2:
+        raise ValueError("expected a 2-D tensor")
+    if x.stride(1) != 1 or x.stride(0) < x.shape[1]:
+        x = x.contiguous()
+    return x
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("hip backend ops need tensors on a ROCm device")
+
+
+def kpad(K: int) -> int:
+    return int(_lib.load().tesm_hip_kpad(K))
+
+
+def round_dtype(v: float, dtype: torch.dtype) -> float:
+    """The float value that torch uses for a Python scalar compared against a ``dtype`` tensor."""
+    return float(torch.tensor(v, dtype=torch.float32).to(dtype).float())
+
+
+# ---------------------------------------------------------------------------
+# BitLinear pieces
+# ---------------------------------------------------------------------------
+def quant_act(x: torch.Tensor, eps: float = 1e-5, layout: int = 1, ldq: Optional[int] = None):
+    """Per-token int8 codes of ``x`` (M, K): returns (codes (M, ldq), s_x (M), rowsum (M))."""
+    lib = _lib.load()
+    x = _rows(x)
+    _require_cuda(x)
+    M, K = x.shape
+    ldq = kpad(K) if ldq is None else ldq
+    q = torch.empty((M, ldq), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rs = torch.empty((M,), dtype=torch.int32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(lib.tesm_hip_quant_act_i8(_p(x), dt_code(x.dtype), M, K, x.stride(0), eps, layout, _p(q), ldq,
+                                             _p(s), _p(rs), _stream(x)))
+    return q, s, rs
+
+
+def absmean_scale(w: torch.Tensor, eps: float = 1e-5):
+    """(s_w, c_w) device scalars: s_w = 1/max(mean|w|, eps), c_w = 1/s_w, rounded to w's dtype."""
+    lib = _lib.load()
+    w = w.contiguous()
+    _require_cuda(w)
+    ws = torch.empty((int(lib.tesm_hip_absmean_ws_bytes()),), dtype=torch.uint8, device=w.device)
+    s_w = torch.empty((1,), dtype=torch.float32, device=w.device)
+    c_w = torch.empty((1,), dtype=torch.float32, device=w.device)
+    with torch.cuda.device(w.device):
+        _lib.check(lib.tesm_hip_absmean_scale(_p(w), dt_code(w.dtype), w.numel(), eps, _p(ws), _p(s_w), _p(c_w),
+                                              _stream(w)))
+    return s_w, c_w
+
+
+def pack_weight(w: torch.Tensor, s_w: torch.Tensor, per_row: bool = False, ldp: Optional[int] = None):
+    """Ternary codes of ``w`` (N, K) at scale ``s_w`` packed 4 per byte: (N, ldp) uint8.
+
+    ``ldp`` defaults to kpad(K)/4 (the layout the products read); pass
+    ``ldp=ceil(K/4)`` for the canonical export layout.
+    """
+    lib = _lib.load()
+    w = _rows(w)
+    _require_cuda(w, s_w)
+    N, K = w.shape
+    ldp = kpad(K) // 4 if ldp is None else ldp
+    packed = torch.empty((N, ldp), dtype=torch.uint8, device=w.device)
+    s_w = s_w.to(torch.float32).contiguous()
+    with torch.cuda.device(w.device):
+        _lib.check(lib.tesm_hip_pack_w_i2(_p(w), dt_code(w.dtype), N, K, w.stride(0), _p(s_w), int(per_row),
+                                          _p(packed), ldp, _stream(w)))
+    return packed
+
+
+def unpack_weight(packed: torch.Tensor, K: int):
+    lib = _lib.load()
+    packed = _rows(packed)
+    _require_cuda(packed)
+    N = packed.shape[0]
+    codes = torch.empty((N, K), dtype=torch.int8, device=packed.device)
+    with torch.cuda.device(packed.device):
+        _lib.check(lib.tesm_hip_unpack_w_i2(_p(packed), N, K, packed.stride(0), _p(codes), K, _stream(packed)))
+    return codes
+
+
+def bitlinear(q, s_x, rowsum, packed, c_w, N: int, K: int, out_dtype: torch.dtype, bias=None,
+              c_w_per_row: bool = False, acc_dump: bool = False, out: Optional[torch.Tensor] = None):
+    """out (M, N) = (q . codes) / s_x * c_w (+ bias); optionally also the int32 accumulators."""
+    lib = _lib.load()
+    _require_cuda(q, packed)
+    M = q.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=q.device)
+    acc = torch.empty((M, N), dtype=torch.int32, device=q.device) if acc_dump else None
+    with torch.cuda.device(q.device):
+        _lib.check(lib.tesm_hip_bitlinear_i2(_p(q), q.stride(0), _p(s_x), _p(rowsum), _p(packed), packed.stride(0),
+                                             _p(c_w), int(c_w_per_row), _p(bias), M, N, K, _p(out),
+                                             dt_code(out.dtype), out.stride(0), _p(acc), _stream(q)))
+    return (out, acc) if acc_dump else out
+
+
+# ---------------------------------------------------------------------------
+# scan / RoPE / entanglement
+# ---------------------------------------------------------------------------
+def scan(decay: torch.Tensor, update: torch.Tensor, chunk_size: int = 16, h0: Optional[torch.Tensor] = None,
+         out_dtype: Optional[torch.dtype] = None):
+    """States of h_t = d_t h_{t-1} + u_t for (B, L, C) inputs; returns (states, h_final fp64)."""
+    lib = _lib.load()
+    if decay.shape != update.shape or decay.dim() != 3:
+        raise ValueError("decay and update must both be (B, L, C)")
+    if decay.dtype != update.dtype:
+        raise TypeError("decay and update must share a dtype")
+    decay, update = decay.contiguous(), update.contiguous()
+    _require_cuda(decay, update)
+    B, L, C = decay.shape
+    out_dtype = out_dtype or decay.dtype
+    states = torch.empty((B, L, C), dtype=out_dtype, device=decay.device)
+    h_final = torch.empty((B, C), dtype=torch.float64, device=decay.device)
+    if h0 is not None:
+        h0 = h0.to(device=decay.device, dtype=torch.float64).contiguous()
+    nbytes = int(lib.tesm_hip_scan_ws_bytes(B, L, C, chunk_size))
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=decay.device)
+    with torch.cuda.device(decay.device):
+        _lib.check(lib.tesm_hip_scan(_p(decay), C, _p(update), C, dt_code(decay.dtype), B, L, C, chunk_size, _p(h0),
+                                     _p(states), C, dt_code(out_dtype), _p(h_final), _p(ws), nbytes, _stream(decay)))
+    return states, h_final
+
+
+def rope_table(L: int, R: int, dtype: torch.dtype, device, base: float = 10000.0, pos_offset: int = 0):
+    """(L, R/2, 2) float32 (cos, sin) of positions pos_offset..pos_offset+L-1, rounded to ``dtype``."""
+    lib = _lib.load()
+    tab = torch.empty((max(L, 1), R // 2, 2), dtype=torch.float32, device=device)
+    with torch.cuda.device(tab.device):
+        _lib.check(lib.tesm_hip_rope_table(_p(tab), L, R, pos_offset, float(base), dt_code(dtype), _stream(tab)))
+    return tab
+
+
+def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=None, mimo: bool = False, H: int = 1,
+              outputs=("avg",), want_tern: bool = False):
+    """Window entanglement over (B, L, H*R) queries/keys and (B, L, H*D) states.
+
+    ``bias`` is (H, W) (or (W,)) in any float dtype; it is rounded to the states' dtype.
+    ``thr`` is rounded to that dtype too.  Returns a dict of the requested outputs
+    among ``avg``, ``e``, ``c``, ``e_tanh`` (and ``tern`` if ``want_tern``).
+    """
+    lib = _lib.load()
+    B, L, HR = q.shape
+    D = S.shape[-1] // H
+    R = HR // H
+    dt = S.dtype
+    q = q.reshape(B * L, HR)
+    k = k.reshape(B * L, HR)
+    q, k = _rows(q), _rows(k)
+    S2 = _rows(S.reshape(B * L, H * D))
+    qa = _rows(q_add.reshape(B * L, HR)) if q_add is not None else None
+    bias_f = bias.reshape(H, W).to(dt).to(torch.float32).contiguous()
+    weff = W if mimo else min(W, L)
+    outs = {name: torch.empty((B, L, H * D), dtype=dt, device=S.device) for name in outputs}
+    tern = torch.empty((B, L, H, weff), dtype=torch.int8, device=S.device) if want_tern else None
+    nbytes = int(lib.tesm_hip_local_ent_ws_bytes(B, L, H, weff))
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=S.device)
+    with torch.cuda.device(S.device):
+        _lib.check(lib.tesm_hip_local_ent(
+            _p(q), q.stride(0), _p(k), k.stride(0), _p(rope), _p(qa), qa.stride(0) if qa is not None else 0,
+            _p(bias_f), _p(S2), S2.stride(0), dt_code(dt), int(mimo), B, L, H, R, D, W, round_dtype(thr, dt),
+            float(ent_scale), _p(outs.get("avg")), _p(outs.get("e")), _p(outs.get("c")), _p(outs.get("e_tanh")),
+            H * D, _p(tern), _p(ws), nbytes, _stream(S)))
+    if want_tern:
+        outs["tern"] = tern
+    return outs
+
+
+def sqrt_rank(R: int) -> float:
+    return math.sqrt(R)

@@ -1,0 +1,238 @@
+"""TESM_SISO with ``kernel_backend='hip'``.
+
+Constructor, parameter names, initialisation order and forward signature follow
+the reference's TESM_SISO (tesm_ssm/modules/tesm.py:456-1272), so a module built
+under the same seed holds the same parameters and ``MixerModel``-style callers
+run it unchanged.  The prefill forward is one call into the C-ABI driver
+``tesm_hip_siso_prefill``, which queues the layer's kernels on the current
+stream: in_proj, gates + state scan, RoPE'd local-window ternary entanglement,
+mix, state_proj/ent_proj with the fused output gate, out_proj.
+
+Like the reference's CUDA fast path, eval runs leave ``last_entanglement_map``
+and ``last_entanglement_stats`` at ``None`` (tesm.py:902-904).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _lib, hip_ops
+from .bitlinear import BitLinear, backend_error, check_hip_call
+
+_WORKSPACES = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-(device, stream) scratch buffer, grown on demand; reused across calls on that stream."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty((max(nbytes, 256),), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+class TESM_SISO(nn.Module):
+    def __init__(self, d_model, d_state=256, expand=2, ent_rank=64, entanglement_scale=0.2,
+                 entanglement_threshold=0.1, max_seq_len=2048, dropout=0.0, bit_eps=1e-5, bit_threshold=0.5,
+                 layer_idx=None, device=None, dtype=None, annealing_enabled=True, T_start=10.0, T_end=0.1,
+                 annealing_steps=1000, annealing_schedule="cosine", quantum_tunneling_enabled=False,
+                 tunneling_strength=0.1, num_tunnel_paths=4, energy_landscape="entropy",
+                 tunneling_schedule="adaptive", **kwargs):
+        super().__init__()
+        self.d_model = d_model
+        self.d_state = d_state
+        self.expand = expand
+        for name, v in (("d_state", d_state), ("d_model", d_model), ("ent_rank", ent_rank),
+                        ("max_seq_len", max_seq_len)):
+            if v <= 0:  # tesm.py:492-499
+                raise ValueError(f"{name} must be positive, got {v}")
+        if quantum_tunneling_enabled:
+            raise NotImplementedError("quantum tunnelling is a training-time option; the hip backend is eval-only")
+        self.ent_rank = ent_rank
+        self.entanglement_scale = entanglement_scale
+        self.entanglement_threshold = entanglement_threshold
+        self.entanglement_init = kwargs.get("entanglement_init", 0.3)
+        self.entanglement_window = int(kwargs.get("entanglement_window", 0) or 0)
+        self.entanglement_block_size = int(kwargs.get("entanglement_block_size", 256) or 256)
+        self.state_scan_chunk_size = int(kwargs.get("state_scan_chunk_size", 16) or 16)
+        self.use_triton_kernels = False
+        self.kernel_backend = str(kwargs.get("kernel_backend", "hip"))
+        self.kernel_mode = "precise" if str(kwargs.get("kernel_mode", "fast")) == "precise" else "fast"
+        self.max_seq_len = max_seq_len
+        self.layer_idx = layer_idx
+        self.annealing_enabled = annealing_enabled
+        self.T_start, self.T_end = T_start, T_end
+        self.annealing_steps = annealing_steps
+        self.annealing_schedule = annealing_schedule
+        self.register_buffer("annealing_step", torch.tensor(0))
+        self.quantum_tunneling_enabled = False
+        self.quantum_tunneler = None
+
+        bl = dict(bias=False, bit_eps=bit_eps, bit_threshold=bit_threshold, kernel_backend=self.kernel_backend,
+                  kernel_mode=self.kernel_mode, device=device, dtype=dtype)
+        total_proj = 2 * d_model + 3 * d_state + 2 * ent_rank  # tesm.py:533
+        self.in_proj = BitLinear(d_model, total_proj, **bl)
+        self.state_proj = BitLinear(d_state, d_model, **bl)
+        self.ent_proj = BitLinear(d_state, d_model, **bl)
+        self.out_proj = BitLinear(d_model, d_model, **bl)
+        self.dropout = nn.Dropout(dropout)
+        decay_init = float(kwargs.get("decay_init_bias", 3.0))
+        self.decay_bias = nn.Parameter(torch.full((d_state,), decay_init, device=device, dtype=torch.float32))
+        if self.entanglement_window > 0:  # tesm.py:543-551
+            self.register_parameter("entanglement", None)
+            self.local_entanglement_bias = nn.Parameter(
+                torch.randn(self.entanglement_window, device=device, dtype=torch.float32) * self.entanglement_init)
+        else:  # tesm.py:553-570: global entanglement parameters (same RNG use)
+            self.register_parameter("local_entanglement_bias", None)
+            self.global_rel_pos_scale = nn.Parameter(torch.ones(1, device=device, dtype=torch.float32))
+            self.global_rel_pos_bias = nn.Parameter(torch.zeros(1, device=device, dtype=torch.float32))
+            self.global_rel_pos_dim = int(kwargs.get("global_rel_pos_dim", 64))
+            self.global_rel_pos_embed = nn.Parameter(
+                torch.randn(self.global_rel_pos_dim, device=device, dtype=torch.float32) * 0.02)
+            self.register_parameter("entanglement", None)
+        self.rope_base = float(kwargs.get("rope_base", 10000.0))
+        self.cross_layer_q_proj = BitLinear(d_state, ent_rank, **bl)
+        self.last_entanglement_map = None
+        self.last_entanglement_stats = None
+        self._last_cross_layer_state = None
+        self._last_scan_state_f64 = None
+        self._rope = {}
+        self._bias_cache = None
+
+    # -- cached device constants ---------------------------------------------------
+    def rope_table(self, L: int, dtype: torch.dtype, device: torch.device, pos_offset: int = 0) -> torch.Tensor:
+        key = (dtype, device, pos_offset)
+        tab = self._rope.get(key)
+        if tab is None or tab.shape[0] < L:
+            n = max(L, min(self.max_seq_len, 2 * L))
+            tab = hip_ops.rope_table(n, self.ent_rank, dtype, device, self.rope_base, pos_offset)
+            self._rope[key] = tab
+        return tab
+
+    def _local_bias_f32(self, dtype: torch.dtype) -> torch.Tensor:
+        """``local_entanglement_bias`` rounded to the layer dtype (tesm.py:925), as float32.
+
+        The kernels use its last ``min(W, L)`` entries, as the reference does."""
+        p = self.local_entanglement_bias
+        key = (p._version, p.data_ptr(), dtype)
+        if self._bias_cache is None or self._bias_cache[0] != key:
+            with torch.no_grad():
+                v = p.detach().to(dtype).to(torch.float32).contiguous()
+            self._bias_cache = (key, v)
+        return self._bias_cache[1]
+
+    def _decay_bias_dt(self, dtype):
+        if self.decay_bias.dtype != dtype:
+            raise RuntimeError(
+                f"decay_bias is {self.decay_bias.dtype} but activations are {dtype}: convert the whole module with "
+                f"module.to({dtype}) (building with dtype= leaves decay_bias float32)")
+        return self.decay_bias.detach()
+
+    # -- forward ---------------------------------------------------------------------
+    def forward(self, u, inference_params=None, cross_layer_state=None, prev_state=None, **kwargs):
+        batch, seqlen, _ = u.shape
+        if seqlen > self.max_seq_len:  # tesm.py:1180-1181
+            raise ValueError(f"Sequence length {seqlen} exceeds max_seq_len {self.max_seq_len}")
+        if seqlen == 0:  # tesm.py:1184-1185
+            return u, None
+        check_hip_call(self.kernel_backend, "TESM", self, u)
+        if inference_params is not None and seqlen == 1:
+            cache = inference_params.get("state_cache")
+            if cache is not None and "state" in cache:
+                return self._forward_incremental(u, inference_params, cross_layer_state)
+        if self.entanglement_window <= 0:
+            raise backend_error(self.kernel_backend, "global entanglement",
+                                "entanglement_window=0 is not implemented by the hip backend yet")
+        y, states, h_final = self._prefill(u, cross_layer_state, prev_state)
+        if inference_params is not None:  # tesm.py:1235-1253
+            cache = inference_params.get("state_cache")
+            if cache is not None and "state" in cache:
+                self._write_prefill_cache(cache, u, states, h_final)
+        self._last_cross_layer_state = states
+        self._last_scan_state_f64 = h_final
+        self.last_entanglement_map = None
+        self.last_entanglement_stats = None
+        return y, h_final
+
+    def _prefill(self, u, cross_layer_state, prev_state):
+        lib = _lib.load()
+        dt = u.dtype
+        B, L, dm = u.shape
+        D, R = self.d_state, self.ent_rank
+        u = u.contiguous()
+        dev = u.device
+        y = torch.empty((B, L, dm), dtype=dt, device=dev)
+        states = torch.empty((B, L, D), dtype=dt, device=dev)
+        h_final = torch.empty((B, D), dtype=torch.float64, device=dev)
+        for p in (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj):
+            if p.weight.dtype != dt:
+                raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
+        cs = None
+        if cross_layer_state is not None:
+            cs = cross_layer_state
+            if cs.dim() == 2:
+                cs = cs.unsqueeze(1).expand(B, L, D)
+            cs = cs.to(dt).contiguous()
+        h0 = prev_state.to(device=dev, dtype=torch.float64).contiguous() if prev_state is not None else None
+        decay_bias = self._decay_bias_dt(dt)
+        local_bias = self._local_bias_f32(dt)
+        rope = self.rope_table(L, dt, dev)
+        desc = _lib.SisoLayer()
+        desc.dt = hip_ops.dt_code(dt)
+        desc.B, desc.L, desc.d_model, desc.d_state, desc.ent_rank = B, L, dm, D, R
+        desc.window, desc.chunk_size = self.entanglement_window, self.state_scan_chunk_size
+        desc.bit_eps = self.in_proj.bit_eps
+        desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
+        desc.ent_scale = float(self.entanglement_scale)
+        desc.u = u.data_ptr()
+        desc.in_proj = self.in_proj.linear_desc()
+        desc.state_proj = self.state_proj.linear_desc()
+        desc.ent_proj = self.ent_proj.linear_desc()
+        desc.out_proj = self.out_proj.linear_desc()
+        if cs is not None:
+            desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
+            desc.cross_state = cs.data_ptr()
+        desc.decay_bias = decay_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr()
+        desc.rope = rope.data_ptr()
+        desc.h0 = h0.data_ptr() if h0 is not None else None
+        desc.y = y.data_ptr()
+        desc.states = states.data_ptr()
+        desc.h_final = h_final.data_ptr()
+        nbytes = int(lib.tesm_hip_siso_prefill_ws_bytes(ctypes.byref(desc)))
+        with torch.cuda.device(dev):
+            ws = workspace(dev, nbytes)
+            _lib.check(lib.tesm_hip_siso_prefill(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                                 ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        return y, states, h_final
+
+    # -- inference cache (tesm.py:620-670, 1235-1253) -----------------------------------
+    def allocate_inference_cache(self, batch_size, max_seqlen, dtype=None, **kwargs):
+        dev = self.out_proj.weight.device
+        cdt = dtype or torch.float32
+        W = max(self.entanglement_window, 1)
+        if kwargs.get("use_paged_cache", False) and max_seqlen > 1024:
+            raise NotImplementedError("paged state cache is not supported by the hip backend")
+        return {
+            "use_paged": False,
+            "state": torch.zeros(batch_size, self.d_state, device=dev, dtype=torch.float64),
+            "seq_pos": 0,
+            "ent_k_cache": torch.zeros(batch_size, W, self.ent_rank, device=dev, dtype=cdt),
+            "ent_v_cache": torch.zeros(batch_size, W, self.d_state, device=dev, dtype=cdt),
+            "cache_idx": 0,
+            "cache_filled": False,
+        }
+
+    def _write_prefill_cache(self, cache, u, states, h_final):
+        raise backend_error(self.kernel_backend, "TESM prefill-with-cache", "decode caches are not wired yet")
+
+    def _forward_incremental(self, u, inference_params, cross_layer_state=None):
+        raise backend_error(self.kernel_backend, "TESM decode", "the incremental decode step is not wired yet")
+
+
+TESM = TESM_SISO

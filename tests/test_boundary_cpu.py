@@ -1,0 +1,89 @@
+"""CPU checks of the drop-in boundary: the C-ABI library, the host mirror of the reference API,
+and the strict-backend error contract (tesm_ssm/modules/tesm.py:278-285; the reference's own
+test_torch_only.py:101-104 expects RuntimeError matching "kernel_backend")."""
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+from oracle import tesm_torch as ot
+from tesm_amd import BitLinear, TESM, TESM_SISO, _lib
+
+
+def _declared_functions():
+    with open(os.path.join(ROOT, "include", "tesm_hip.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tesm_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"libtesm_hip.so does not export {name}"
+    assert sorted(_lib.exported_symbols()) == declared
+    assert lib.tesm_hip_abi_version() == _lib.ABI_VERSION
+    assert lib.tesm_hip_kpad(1) == 128 and lib.tesm_hip_kpad(768) == 768 and lib.tesm_hip_kpad(769) == 896
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setenv("TESM_HIP_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.HipBackendUnavailable, match="not found"):
+        _lib.load()
+
+
+def test_struct_layout_matches_header():
+    # pointer-aligned fields: tesm_hip_linear is 32 bytes; the layer descriptor packs 5 of them
+    assert torch.tensor(0).element_size() == 8
+    import ctypes
+    assert ctypes.sizeof(_lib.Linear) == 32
+    assert _lib.SisoLayer.in_proj.offset % 8 == 0
+    assert ctypes.sizeof(_lib.SisoLayer) == _lib.SisoLayer.proj_out.offset + 8
+
+
+def test_seeded_construction_matches_reference_parameters():
+    kw = dict(d_model=64, d_state=32, ent_rank=8, entanglement_window=8, decay_init_bias=1.0, max_seq_len=64)
+    torch.manual_seed(3)
+    ref = ot.TESM_SISO(**kw)
+    torch.manual_seed(3)
+    mine = TESM_SISO(**kw)
+    rs, ms = ref.state_dict(), mine.state_dict()
+    assert set(rs) == set(ms)
+    for k in rs:
+        assert torch.equal(rs[k], ms[k]), k
+    assert TESM is TESM_SISO
+
+
+def test_global_window_construction_matches_reference():
+    torch.manual_seed(1)
+    ref = ot.TESM_SISO(d_model=32, d_state=16, ent_rank=8, entanglement_window=0)
+    torch.manual_seed(1)
+    mine = TESM_SISO(d_model=32, d_state=16, ent_rank=8, entanglement_window=0)
+    for k, v in ref.state_dict().items():
+        assert torch.equal(v, mine.state_dict()[k]), k
+
+
+def test_strict_backend_errors_on_cpu():
+    bl = BitLinear(16, 4).eval()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="kernel_backend"):
+        bl(torch.randn(2, 16))
+    m = TESM_SISO(d_model=16, d_state=8, ent_rank=4, entanglement_window=4, max_seq_len=8).eval()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="kernel_backend"):
+        m(torch.randn(1, 3, 16))
+    with torch.no_grad(), pytest.raises(ValueError, match="exceeds max_seq_len"):
+        m(torch.randn(1, 9, 16))
+    with pytest.raises(ValueError, match="d_state must be positive"):
+        TESM_SISO(d_model=16, d_state=0)
+
+
+def test_empty_sequence_returns_input():
+    m = TESM_SISO(d_model=16, d_state=8, ent_rank=4, entanglement_window=4, max_seq_len=8).eval()
+    u = torch.randn(2, 0, 16)
+    with torch.no_grad():
+        out, fin = m(u)
+    assert out is u and fin is None
