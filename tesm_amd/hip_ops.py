@@ -11,7 +11,6 @@ projection output are passed without copies.
 from __future__ import annotations
 
 import ctypes
-import math
 from typing import Optional
 
 import torch
@@ -45,10 +44,19 @@ def _rows(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
-def _require_cuda(*ts):
+def require_device(*ts):
+    """Every tensor handed to a kernel must live on one ROCm device: a host pointer would be
+    dereferenced by the GPU."""
+    dev = None
     for t in ts:
-        if t is not None and not t.is_cuda:
-            raise RuntimeError("hip backend ops need tensors on a ROCm device")
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"hip backend ops need tensors on a ROCm device, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"hip backend ops need all tensors on one device, got {dev} and {t.device}")
 
 
 def kpad(K: int) -> int:
@@ -67,7 +75,7 @@ def quant_act(x: torch.Tensor, eps: float = 1e-5, layout: int = 1, ldq: Optional
     """Per-token int8 codes of ``x`` (M, K): returns (codes (M, ldq), s_x (M), rowsum (M))."""
     lib = _lib.load()
     x = _rows(x)
-    _require_cuda(x)
+    require_device(x)
     M, K = x.shape
     ldq = kpad(K) if ldq is None else ldq
     q = torch.empty((M, ldq), dtype=torch.int8, device=x.device)
@@ -83,7 +91,7 @@ def absmean_scale(w: torch.Tensor, eps: float = 1e-5):
     """(s_w, c_w) device scalars: s_w = 1/max(mean|w|, eps), c_w = 1/s_w, rounded to w's dtype."""
     lib = _lib.load()
     w = w.contiguous()
-    _require_cuda(w)
+    require_device(w)
     ws = torch.empty((int(lib.tesm_hip_absmean_ws_bytes()),), dtype=torch.uint8, device=w.device)
     s_w = torch.empty((1,), dtype=torch.float32, device=w.device)
     c_w = torch.empty((1,), dtype=torch.float32, device=w.device)
@@ -101,7 +109,7 @@ def pack_weight(w: torch.Tensor, s_w: torch.Tensor, per_row: bool = False, ldp: 
     """
     lib = _lib.load()
     w = _rows(w)
-    _require_cuda(w, s_w)
+    require_device(w, s_w)
     N, K = w.shape
     ldp = kpad(K) // 4 if ldp is None else ldp
     packed = torch.empty((N, ldp), dtype=torch.uint8, device=w.device)
@@ -115,7 +123,7 @@ def pack_weight(w: torch.Tensor, s_w: torch.Tensor, per_row: bool = False, ldp: 
 def unpack_weight(packed: torch.Tensor, K: int):
     lib = _lib.load()
     packed = _rows(packed)
-    _require_cuda(packed)
+    require_device(packed)
     N = packed.shape[0]
     codes = torch.empty((N, K), dtype=torch.int8, device=packed.device)
     with torch.cuda.device(packed.device):
@@ -127,11 +135,11 @@ def bitlinear(q, s_x, rowsum, packed, c_w, N: int, K: int, out_dtype: torch.dtyp
               c_w_per_row: bool = False, acc_dump: bool = False, out: Optional[torch.Tensor] = None):
     """out (M, N) = (q . codes) / s_x * c_w (+ bias); optionally also the int32 accumulators."""
     lib = _lib.load()
-    _require_cuda(q, packed)
     M = q.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=q.device)
     acc = torch.empty((M, N), dtype=torch.int32, device=q.device) if acc_dump else None
+    require_device(q, s_x, rowsum, packed, c_w, bias, out, acc)
     with torch.cuda.device(q.device):
         _lib.check(lib.tesm_hip_bitlinear_i2(_p(q), q.stride(0), _p(s_x), _p(rowsum), _p(packed), packed.stride(0),
                                              _p(c_w), int(c_w_per_row), _p(bias), M, N, K, _p(out),
@@ -151,13 +159,13 @@ def scan(decay: torch.Tensor, update: torch.Tensor, chunk_size: int = 16, h0: Op
     if decay.dtype != update.dtype:
         raise TypeError("decay and update must share a dtype")
     decay, update = decay.contiguous(), update.contiguous()
-    _require_cuda(decay, update)
+    require_device(decay, update, h0)
     B, L, C = decay.shape
     out_dtype = out_dtype or decay.dtype
     states = torch.empty((B, L, C), dtype=out_dtype, device=decay.device)
     h_final = torch.empty((B, C), dtype=torch.float64, device=decay.device)
     if h0 is not None:
-        h0 = h0.to(device=decay.device, dtype=torch.float64).contiguous()
+        h0 = h0.to(dtype=torch.float64).contiguous()
     nbytes = int(lib.tesm_hip_scan_ws_bytes(B, L, C, chunk_size))
     ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=decay.device)
     with torch.cuda.device(decay.device):
@@ -193,12 +201,14 @@ def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=N
     q, k = _rows(q), _rows(k)
     S2 = _rows(S.reshape(B * L, H * D))
     qa = _rows(q_add.reshape(B * L, HR)) if q_add is not None else None
-    bias_f = bias.reshape(H, W).to(dt).to(torch.float32).contiguous()
+    # small parameter: accepted from any device, copied next to the states
+    bias_f = bias.reshape(H, W).to(device=S.device, dtype=dt).to(torch.float32).contiguous()
     weff = W if mimo else min(W, L)
     outs = {name: torch.empty((B, L, H * D), dtype=dt, device=S.device) for name in outputs}
     tern = torch.empty((B, L, H, weff), dtype=torch.int8, device=S.device) if want_tern else None
     nbytes = int(lib.tesm_hip_local_ent_ws_bytes(B, L, H, weff))
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=S.device)
+    require_device(q, k, rope, qa, bias_f, S2, tern, ws, *outs.values())
     with torch.cuda.device(S.device):
         _lib.check(lib.tesm_hip_local_ent(
             _p(q), q.stride(0), _p(k), k.stride(0), _p(rope), _p(qa), qa.stride(0) if qa is not None else 0,
@@ -209,6 +219,3 @@ def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=N
         outs["tern"] = tern
     return outs
 
-
-def sqrt_rank(R: int) -> float:
-    return math.sqrt(R)

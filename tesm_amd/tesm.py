@@ -182,6 +182,7 @@ class TESM_SISO(nn.Module):
         decay_bias = self._decay_bias_dt(dt)
         local_bias = self._local_bias_f32(dt)
         rope = self.rope_table(L, dt, dev)
+        hip_ops.require_device(u, cs, h0, decay_bias, local_bias, rope, y, states, h_final)
         desc = _lib.SisoLayer()
         desc.dt = hip_ops.dt_code(dt)
         desc.B, desc.L, desc.d_model, desc.d_state, desc.ent_rank = B, L, dm, D, R

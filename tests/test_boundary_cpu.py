@@ -87,3 +87,15 @@ def test_empty_sequence_returns_input():
     with torch.no_grad():
         out, fin = m(u)
     assert out is u and fin is None
+
+
+def test_host_tensors_are_rejected_before_any_launch():
+    """A CPU tensor's address must never reach a kernel (it would be dereferenced by the GPU)."""
+    from tesm_amd import hip_ops
+    q = torch.randn(1, 4, 8)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        hip_ops.local_ent(q, q, torch.zeros(4, 4, 2), torch.randn(1, 4, 16), torch.zeros(4), 4, 0.1, 0.2)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        hip_ops.scan(torch.rand(1, 4, 8), torch.rand(1, 4, 8))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        hip_ops.quant_act(torch.randn(2, 8))
