@@ -112,6 +112,41 @@ int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k,
                        void* e_out, void* c_out, void* e_tanh, int64_t ld_out, int8_t* tern, void* ws,
                        int64_t ws_bytes, void* stream);
 
+/* Local-window entanglement fused with the per-token int8 quantization of its two consumers'
+ * inputs: tanh(E) (state_proj) and C = E - S (ent_proj).  Replaces, in one kernel,
+ * TESM_SISO._compute_local_entanglement (tesm.py:853-952), the mix (tesm.py:1231-1232, 1256) and
+ * BitLinear.quantized_input of state_proj / ent_proj (tesm.py:206-209).  SISO only, d_state <= 512.
+ * Operand conventions as tesm_hip_local_ent (H = 1); codes are layout 1 with row stride ldq >=
+ * kpad(D).  e_tanh / c_out (ld_out) optionally receive the float values as well. */
+typedef struct tesm_hip_ent_quant {
+  int dt;
+  int64_t B, L, R, D, W;
+  float thr, ent_scale, eps;
+  const void* q;
+  int64_t ld_q;
+  const void* k;
+  int64_t ld_k;
+  const void* rope;
+  const void* q_add;
+  int64_t ld_qadd;
+  const float* bias;          /* (W) float32 holding dt values */
+  const void* S;
+  int64_t ld_s;
+  int8_t* q_te;
+  float* s_te;
+  int32_t* rs_te;
+  int8_t* q_c;
+  float* s_c;
+  int32_t* rs_c;
+  int64_t ldq;
+  void* e_tanh;               /* optional */
+  void* c_out;                /* optional */
+  int64_t ld_out;
+  int8_t* tern;               /* optional (B, L, min(W, L)) ternary map */
+} tesm_hip_ent_quant;
+
+int tesm_hip_local_ent_quant(const tesm_hip_ent_quant* p, void* stream);
+
 /* One packed BitLinear as the fused layer drivers consume it. */
 typedef struct tesm_hip_linear {
   const uint8_t* packed; /* (N, ldw) */
@@ -119,6 +154,38 @@ typedef struct tesm_hip_linear {
   const float* c_w;      /* device scalar (or (N) if c_w_per_row) */
   int c_w_per_row;
 } tesm_hip_linear;
+
+/* Output gate y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(E - S) from the codes of
+ * tanh(E) and C.  Replaces tesm.py:1256-1260 (state_proj/ent_proj BitLinears and the gate) and,
+ * when q_y is given, BitLinear.quantized_input of out_proj (tesm.py:206-209): the kernel then owns
+ * whole rows (d_model <= 1024) and writes y's layout-1 codes (and y itself only if y != NULL).
+ * local / gate: raw in_proj slices (dt), element (m, n) at ptr[m*ld + n]. */
+typedef struct tesm_hip_output_gate {
+  int dt;
+  int64_t M, d_model, d_state;
+  float eps;
+  const int8_t* q_te;
+  int64_t ldq_te;
+  const float* s_te;
+  const int32_t* rs_te;
+  const int8_t* q_c;
+  int64_t ldq_c;
+  const float* s_c;
+  const int32_t* rs_c;
+  tesm_hip_linear state_proj, ent_proj;
+  const void* local;
+  int64_t ld_local;
+  const void* gate;
+  int64_t ld_gate;
+  void* y;                    /* (M, ld_y) in dt; required when q_y is NULL */
+  int64_t ld_y;
+  int8_t* q_y;                /* optional (M, ldq_y) codes for out_proj */
+  int64_t ldq_y;
+  float* s_y;
+  int32_t* rs_y;
+} tesm_hip_output_gate;
+
+int tesm_hip_output_gate_i2(const tesm_hip_output_gate* p, void* stream);
 
 /* Whole TESM_SISO prefill forward (eval, no grad).  Replaces TESM_SISO.forward
  * (tesm.py:1175-1272) for L > 1 without an inference cache: in_proj, gates, RoPE, cross-layer

@@ -31,6 +31,34 @@ class Linear(ctypes.Structure):
     _fields_ = [("packed", P), ("ldw", I64), ("c_w", P), ("c_w_per_row", I32)]
 
 
+class EntQuant(ctypes.Structure):
+    """``tesm_hip_ent_quant``."""
+    _fields_ = [
+        ("dt", I32),
+        ("B", I64), ("L", I64), ("R", I64), ("D", I64), ("W", I64),
+        ("thr", F32), ("ent_scale", F32), ("eps", F32),
+        ("q", P), ("ld_q", I64), ("k", P), ("ld_k", I64), ("rope", P), ("q_add", P), ("ld_qadd", I64),
+        ("bias", P), ("S", P), ("ld_s", I64),
+        ("q_te", P), ("s_te", P), ("rs_te", P), ("q_c", P), ("s_c", P), ("rs_c", P), ("ldq", I64),
+        ("e_tanh", P), ("c_out", P), ("ld_out", I64), ("tern", P),
+    ]
+
+
+class OutputGate(ctypes.Structure):
+    """``tesm_hip_output_gate``."""
+    _fields_ = [
+        ("dt", I32),
+        ("M", I64), ("d_model", I64), ("d_state", I64),
+        ("eps", F32),
+        ("q_te", P), ("ldq_te", I64), ("s_te", P), ("rs_te", P),
+        ("q_c", P), ("ldq_c", I64), ("s_c", P), ("rs_c", P),
+        ("state_proj", Linear), ("ent_proj", Linear),
+        ("local", P), ("ld_local", I64), ("gate", P), ("ld_gate", I64),
+        ("y", P), ("ld_y", I64),
+        ("q_y", P), ("ldq_y", I64), ("s_y", P), ("rs_y", P),
+    ]
+
+
 class SisoLayer(ctypes.Structure):
     """``tesm_hip_siso_layer``."""
     _fields_ = [
@@ -62,6 +90,8 @@ _SIGNATURES = {
     "tesm_hip_local_ent_ws_bytes": ([I64, I64, I64, I64], I64),
     "tesm_hip_local_ent": ([P, I64, P, I64, P, P, I64, P, P, I64, I32, I32, I64, I64, I64, I64, I64, I64, F32, F32,
                             P, P, P, P, I64, P, P, I64, P], I32),
+    "tesm_hip_local_ent_quant": ([ctypes.POINTER(EntQuant), P], I32),
+    "tesm_hip_output_gate_i2": ([ctypes.POINTER(OutputGate), P], I32),
     "tesm_hip_siso_prefill_ws_bytes": ([ctypes.POINTER(SisoLayer)], I64),
     "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
 }

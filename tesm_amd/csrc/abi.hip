@@ -76,6 +76,8 @@ int esize(int dt) { return dt == kBF16 ? 2 : 4; }
 
 // Workspace layout of the SISO prefill; with base == nullptr it only measures.
 struct SisoPlan {
+  bool fuse_ent;  // entanglement kernel also quantizes tanh(E) and C
+  bool rowq;      // output gate kernel also quantizes y (d_model <= 1024)
   CodeBuf xu, xe, xc, xy, xs;
   void* proj;
   void* scan_ws;
@@ -88,22 +90,42 @@ struct SisoPlan {
   int64_t total;
 };
 
+EntArgs siso_ent_shape(const tesm_hip_siso_layer& p) {
+  EntArgs e;
+  e.dt = p.dt;
+  e.mimo = 0;
+  e.B = p.B;
+  e.L = p.L;
+  e.H = 1;
+  e.R = p.ent_rank;
+  e.D = p.d_state;
+  e.W = p.window;
+  e.ldq = kpad(p.d_state);
+  return e;
+}
+
 SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   Carve c(base);
   SisoPlan s;
   const int64_t M = p.B * p.L;
   const int64_t n_in = 2 * p.d_model + 3 * p.d_state + 2 * p.ent_rank;
   const int es = esize(p.dt);
+  s.fuse_ent = ent_fused_ok(siso_ent_shape(p));
+  s.rowq = p.d_model <= 1024;
   s.xu = take_codes(c, M, p.d_model);
   s.proj = c.take<void>(M * n_in * es);
   s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
   s.scan_ws = c.take<void>(s.scan_bytes);
-  s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
-  s.e_tanh = c.take<void>(M * p.d_state * es);
-  s.c_mix = c.take<void>(M * p.d_state * es);
+  s.wts = nullptr;
+  s.e_tanh = s.c_mix = nullptr;
+  if (!s.fuse_ent) {
+    s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
+    s.e_tanh = c.take<void>(M * p.d_state * es);
+    s.c_mix = c.take<void>(M * p.d_state * es);
+  }
   s.xe = take_codes(c, M, p.d_state);
   s.xc = take_codes(c, M, p.d_state);
-  s.yg = c.take<void>(M * p.d_model * es);
+  s.yg = s.rowq ? nullptr : c.take<void>(M * p.d_model * es);
   s.xy = take_codes(c, M, p.d_model);
   if (p.cross_state) {
     s.xs = take_codes(c, M, p.d_state);
@@ -267,6 +289,79 @@ int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k,
   return launch_local_ent(a, static_cast<hipStream_t>(stream));
 }
 
+int tesm_hip_local_ent_quant(const tesm_hip_ent_quant* p, void* stream) {
+  TESM_REQUIRE(p != nullptr, kErrInvalidArg, "local_ent_quant: null descriptor");
+  EntArgs a;
+  a.dt = p->dt;
+  a.mimo = 0;
+  a.B = p->B;
+  a.L = p->L;
+  a.H = 1;
+  a.R = p->R;
+  a.D = p->D;
+  a.W = p->W;
+  a.q = p->q;
+  a.ld_q = p->ld_q;
+  a.k = p->k;
+  a.ld_k = p->ld_k;
+  a.rope = static_cast<const float2*>(p->rope);
+  a.q_add = p->q_add;
+  a.ld_qadd = p->ld_qadd;
+  a.bias = p->bias;
+  a.thr = p->thr;
+  a.ent_scale = p->ent_scale;
+  a.S = p->S;
+  a.ld_s = p->ld_s;
+  a.e_tanh = p->e_tanh;
+  a.c_out = p->c_out;
+  a.ld_out = p->ld_out;
+  a.tern = p->tern;
+  a.q_te = p->q_te;
+  a.s_te = p->s_te;
+  a.rs_te = p->rs_te;
+  a.q_c = p->q_c;
+  a.s_c = p->s_c;
+  a.rs_c = p->rs_c;
+  a.ldq = p->ldq;
+  a.eps = p->eps;
+  TESM_REQUIRE(a.q_te != nullptr, kErrInvalidArg, "local_ent_quant: q_te is required");
+  return launch_local_ent(a, static_cast<hipStream_t>(stream));
+}
+
+int tesm_hip_output_gate_i2(const tesm_hip_output_gate* p, void* stream) {
+  TESM_REQUIRE(p != nullptr, kErrInvalidArg, "output_gate: null descriptor");
+  CodeBuf te{const_cast<int8_t*>(p->q_te), const_cast<float*>(p->s_te), const_cast<int32_t*>(p->rs_te), p->ldq_te};
+  CodeBuf cc{const_cast<int8_t*>(p->q_c), const_cast<float*>(p->s_c), const_cast<int32_t*>(p->rs_c), p->ldq_c};
+  LinearArgs ga;
+  ga.op[0] = operand(te, p->state_proj);
+  ga.op[1] = operand(cc, p->ent_proj);
+  ga.M = p->M;
+  ga.N = p->d_model;
+  ga.Kp = kpad(p->d_state);
+  ga.out_dt = p->dt;
+  ga.epilogue = kEpiOutputGate;
+  ga.local = p->local;
+  ga.ld_local = p->ld_local;
+  ga.gate = p->gate;
+  ga.ld_gate = p->ld_gate;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p->q_y) {
+    RowQuant rq;
+    rq.q = p->q_y;
+    rq.ldq = p->ldq_y;
+    rq.s = p->s_y;
+    rq.rs = p->rs_y;
+    rq.eps = p->eps;
+    rq.y = p->y;
+    rq.ldy = p->ld_y;
+    return launch_gate_rowq(ga, rq, st);
+  }
+  TESM_REQUIRE(p->y != nullptr, kErrInvalidArg, "output_gate: need y or q_y");
+  ga.out = p->y;
+  ga.ldo = p->ld_y;
+  return launch_linear(ga, st);
+}
+
 int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p) {
   if (!p) return -1;
   return plan_siso(*p, nullptr).total;
@@ -336,16 +431,8 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   sa.ld_states = D;
   sa.h_final = p.h_final;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
-  // 4. local entanglement + mix (tesm.py:853-952, 1231-1232)
-  EntArgs ea;
-  ea.dt = dt;
-  ea.mimo = 0;
-  ea.B = p.B;
-  ea.L = p.L;
-  ea.H = 1;
-  ea.R = R;
-  ea.D = D;
-  ea.W = p.window;
+  // 4. local entanglement + mix (tesm.py:853-952, 1231-1232), quantized for state_proj / ent_proj
+  EntArgs ea = siso_ent_shape(p);
   ea.q = proj + o_q * es;
   ea.ld_q = n_in;
   ea.k = proj + o_k * es;
@@ -358,31 +445,55 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   ea.ent_scale = p.ent_scale;
   ea.S = p.states;
   ea.ld_s = D;
-  ea.e_tanh = s.e_tanh;
-  ea.c_out = s.c_mix;
-  ea.ld_out = D;
-  ea.wts = s.wts;
-  if ((rc = launch_local_ent(ea, st))) return rc;
-  // 5. state_proj(tanh E), ent_proj(C) and the output gate (tesm.py:1256-1260)
-  if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
-  if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  ea.eps = p.bit_eps;
+  if (s.fuse_ent) {
+    ea.q_te = s.xe.q;
+    ea.s_te = s.xe.s;
+    ea.rs_te = s.xe.rs;
+    ea.q_c = s.xc.q;
+    ea.s_c = s.xc.s;
+    ea.rs_c = s.xc.rs;
+    ea.ldq = s.xe.ldq;
+    if ((rc = launch_local_ent(ea, st))) return rc;
+  } else {
+    ea.e_tanh = s.e_tanh;
+    ea.c_out = s.c_mix;
+    ea.ld_out = D;
+    ea.wts = s.wts;
+    if ((rc = launch_local_ent(ea, st))) return rc;
+    if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
+      return rc;
+    if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
+      return rc;
+  }
+  // 5. state_proj(tanh E), ent_proj(C) and the output gate (tesm.py:1256-1260), quantized for out_proj
   LinearArgs ga;
   ga.op[0] = operand(s.xe, p.state_proj);
   ga.op[1] = operand(s.xc, p.ent_proj);
   ga.M = M;
   ga.N = dm;
   ga.Kp = kpad(D);
-  ga.out = s.yg;
-  ga.ldo = dm;
   ga.out_dt = dt;
   ga.epilogue = kEpiOutputGate;
   ga.local = proj + o_local * es;
   ga.ld_local = n_in;
   ga.gate = proj + o_gate * es;
   ga.ld_gate = n_in;
-  if ((rc = launch_linear(ga, st))) return rc;
+  if (s.rowq) {
+    RowQuant rq;
+    rq.q = s.xy.q;
+    rq.ldq = s.xy.ldq;
+    rq.s = s.xy.s;
+    rq.rs = s.xy.rs;
+    rq.eps = p.bit_eps;
+    if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
+  } else {
+    ga.out = s.yg;
+    ga.ldo = dm;
+    if ((rc = launch_linear(ga, st))) return rc;
+    if ((rc = launch_quant_act(s.yg, dt, M, dm, dm, p.bit_eps, 1, s.xy.q, s.xy.ldq, s.xy.s, s.xy.rs, st))) return rc;
+  }
   // 6. out_proj (tesm.py:1261; dropout is identity in eval)
-  if ((rc = launch_quant_act(s.yg, dt, M, dm, dm, p.bit_eps, 1, s.xy.q, s.xy.ldq, s.xy.s, s.xy.rs, st))) return rc;
   return run_linear(s.xy, p.out_proj, M, dm, dm, p.y, dt, dm, st);
 }
 

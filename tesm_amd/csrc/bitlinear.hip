@@ -130,7 +130,8 @@ template <int WM, int WN, int TM, int TN>
 struct Cfg {
   static constexpr int NT = WM * WN * 64;
   static constexpr int BM = WM * TM * 16, BN = WN * TN * 16, BK = 128;
-  static constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  static constexpr int A_BYTES = BM * BK;        // int8 codes, fragment order
+  static constexpr int B_BYTES = BN * BK / 4;    // packed INT2, fragment order (one dword per lane)
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_CHUNKS = BM * BK / 16;  // 16-byte code chunks per K tile
   static constexpr int B_CHUNKS = BN * BK / 64;  // 16-byte packed chunks per K tile
@@ -138,18 +139,27 @@ struct Cfg {
   static constexpr int B_PT = (B_CHUNKS + NT - 1) / NT;
 };
 
-// LDS fragment order: fragment (tile t of 16 rows, k-step ks of 64 codes) is 1 KiB; lane L holds
-// the 16 bytes of row 16t + L%16, code group 4ks + L/16 (16 codes).  The same order for A rows and
-// B columns makes lane L's A and B operands cover the same 16 codes.
-__device__ __forceinline__ int frag_off(int r, int kg) {
+// LDS fragment order.  A: fragment (tile t of 16 rows, k-step ks of 64 codes) is 1 KiB; lane L holds
+// the 16 code bytes of row 16t + L%16, code group 4ks + L/16.  B: fragment (tile t of 16 columns,
+// ks) is 256 bytes; lane L holds the packed dword (16 codes) of column 16t + L%16, group 4ks + L/16.
+// Lane L's A and B operands therefore cover the same 16 codes, in the order the unpack produces.
+__device__ __forceinline__ int a_frag_off(int r, int kg) {
   return (((r >> 4) * 2 + (kg >> 2)) << 10) + (((r & 15) + 16 * (kg & 3)) << 4);
 }
+__device__ __forceinline__ int b_frag_off(int r, int kg) {
+  return (((r >> 4) * 2 + (kg >> 2)) << 8) + (((r & 15) + 16 * (kg & 3)) << 2);
+}
 
-template <class C, int TM, int TN>
+__device__ __forceinline__ v4i unpack_frag(uint32_t w) {
+  return v4i{static_cast<int>(unpack_u(w, 0)), static_cast<int>(unpack_u(w, 1)), static_cast<int>(unpack_u(w, 2)),
+             static_cast<int>(unpack_u(w, 3))};
+}
+
+template <class C, int WN, int TM, int TN>
 __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
                                               int64_t Kp, v4i (&acc)[TM][TN], char* smem) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int wm = w / (C::BN / (TN * 16)), wn = w % (C::BN / (TN * 16));
+  const int wm = w / WN, wn = w % WN;
   uint4 ra[C::A_PT], rb[C::B_PT];
 
   auto gload = [&](int64_t k0) {
@@ -176,7 +186,7 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
 #pragma unroll
     for (int p = 0; p < C::A_PT; ++p) {
       const int c = t + p * C::NT;
-      if (c < C::A_CHUNKS) *reinterpret_cast<uint4*>(stage + frag_off(c >> 3, c & 7)) = ra[p];
+      if (c < C::A_CHUNKS) *reinterpret_cast<uint4*>(stage + a_frag_off(c >> 3, c & 7)) = ra[p];
     }
     char* sb = stage + C::A_BYTES;
 #pragma unroll
@@ -186,10 +196,7 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
         const int r = c >> 1, h = c & 1;
         const uint32_t wd[4] = {rb[p].x, rb[p].y, rb[p].z, rb[p].w};
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const uint4 u = make_uint4(unpack_u(wd[d], 0), unpack_u(wd[d], 1), unpack_u(wd[d], 2), unpack_u(wd[d], 3));
-          *reinterpret_cast<uint4*>(sb + frag_off(r, 4 * h + d)) = u;
-        }
+        for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(sb + b_frag_off(r, 4 * h + d)) = wd[d];
       }
     }
   };
@@ -203,21 +210,37 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
     if (kt + 1 < nk) gload((kt + 1) * C::BK);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      v4i af[TM], bf[TN];
+      v4i af[TM];
+      uint32_t bw[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(cur + ((((wm * TM + i) * 2 + ks)) << 10) + lane * 16);
+        af[i] = *reinterpret_cast<const v4i*>(cur + (((wm * TM + i) * 2 + ks) << 10) + lane * 16);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const v4i*>(cur + C::A_BYTES + ((((wn * TN + j) * 2 + ks)) << 10) + lane * 16);
+        bw[j] = *reinterpret_cast<const uint32_t*>(cur + C::A_BYTES + (((wn * TN + j) * 2 + ks) << 8) + lane * 4);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TN; ++j) {
+        const v4i bf = unpack_frag(bw[j]);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, acc[i][j], 0, 0, 0);
+      }
     }
     if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * C::STAGE);
     __syncthreads();
   }
+}
+
+// Tile order for a 1-D grid: workgroups are handed to the 8 XCDs round-robin by id, so id is
+// mapped to a tile such that each XCD gets a contiguous run of tiles (row-major over
+// (M tile, N tile)); consecutive tiles of one XCD share A rows in that XCD's L2.
+__device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
+  constexpr int64_t kXcd = 8;
+  const int64_t total = ntm * ntn, pid = blockIdx.x;
+  const int64_t x = pid % kXcd, i = pid / kXcd;
+  const int64_t q = total / kXcd, r = total % kXcd;
+  const int64_t tile = x * q + (x < r ? x : r) + i;
+  tm = tile / ntn;
+  tn = tile - tm * ntn;
 }
 
 // Accumulator layout of v_mfma_i32_16x16x64_i8: lane L, element r -> row 4*(L/16) + r, column L%16.
@@ -225,8 +248,10 @@ template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
 __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   using C = Cfg<WM, WN, TM, TN>;
   __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
+  int64_t tm, tn;
+  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
+  const int64_t m0 = tm * C::BM;
+  const int64_t n0 = tn * C::BN;
   v4i acc0[TM][TN], acc1[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -235,8 +260,8 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
       acc0[i][j] = v4i{0, 0, 0, 0};
       acc1[i][j] = v4i{0, 0, 0, 0};
     }
-  mfma_mainloop<C, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+  mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w / WN, wn = w % WN;
@@ -287,15 +312,171 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Output gate over whole rows: a workgroup owns 16 rows and all N = d_model columns (4 waves side by
+// side, NCT 16-column tiles each), so after y = local + sigmoid(gate)*state_proj + ent_proj it can
+// quantize y per token for out_proj without writing y.  Operands stream from global/L2 into
+// registers (A: 16 code rows; B: one packed dword per lane per tile), double buffered per k-step.
+// ---------------------------------------------------------------------------
+template <int NCT, int DT>
+__global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o) {
+  extern __shared__ __attribute__((aligned(16))) char lds_rowq[];
+  int8_t* codes = reinterpret_cast<int8_t*>(lds_rowq);                              // [16][ldq]
+  float* red = reinterpret_cast<float*>(lds_rowq + 16 * o.ldq);                     // [16 rows][4 waves]
+  int32_t* redi = reinterpret_cast<int32_t*>(lds_rowq + 16 * o.ldq + 16 * 4 * 4);   // [16 rows][4 waves]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t col0 = static_cast<int64_t>(w) * NCT * 16;
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+  const int64_t ma = m0 + (lane & 15);
+  const bool mok = ma < a.M;
+  const int64_t nks = a.Kp / 64;
+
+  for (int64_t i = tid; i < 16 * o.ldq / 16; i += 256) reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
+
+  v4i acc0[NCT], acc1[NCT];
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    acc0[j] = v4i{0, 0, 0, 0};
+    acc1[j] = v4i{0, 0, 0, 0};
+  }
+  v4i xa0, xa1, na0, na1;
+  uint32_t bw0[NCT], bw1[NCT], nb0[NCT], nb1[NCT];
+  auto load = [&](int64_t ks, v4i& r0, v4i& r1, uint32_t (&w0)[NCT], uint32_t (&w1)[NCT]) {
+    const int64_t ko = 64 * ks + 16 * (lane >> 4);
+    r0 = mok ? *reinterpret_cast<const v4i*>(o0.q + ma * o0.ldq + ko) : v4i{0, 0, 0, 0};
+    r1 = mok ? *reinterpret_cast<const v4i*>(o1.q + ma * o1.ldq + ko) : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < NCT; ++j) {
+      const int64_t n = col0 + 16 * j + (lane & 15);
+      w0[j] = n < a.N ? *reinterpret_cast<const uint32_t*>(o0.w + n * o0.ldw + ko / 4) : 0u;
+      w1[j] = n < a.N ? *reinterpret_cast<const uint32_t*>(o1.w + n * o1.ldw + ko / 4) : 0u;
+    }
+  };
+  load(0, xa0, xa1, bw0, bw1);
+  for (int64_t ks = 0; ks < nks; ++ks) {
+    if (ks + 1 < nks) load(ks + 1, na0, na1, nb0, nb1);
+#pragma unroll
+    for (int j = 0; j < NCT; ++j) {
+      acc0[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa0, unpack_frag(bw0[j]), acc0[j], 0, 0, 0);
+      acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa1, unpack_frag(bw1[j]), acc1[j], 0, 0, 0);
+    }
+    if (ks + 1 < nks) {
+      xa0 = na0;
+      xa1 = na1;
+#pragma unroll
+      for (int j = 0; j < NCT; ++j) {
+        bw0[j] = nb0[j];
+        bw1[j] = nb1[j];
+      }
+    }
+  }
+
+  // epilogue: y in registers, then the per-row amax across the 4 waves
+  float y[NCT][4];
+  float inv0[4], inv1[4];
+  int32_t rs0[4], rs1[4];
+  int64_t mr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mr[r] = m0 + 4 * (lane >> 4) + r;
+    const bool ok = mr[r] < a.M;
+    inv0[r] = ok ? 1.0f / o0.s_x[mr[r]] : 0.0f;
+    inv1[r] = ok ? 1.0f / o1.s_x[mr[r]] : 0.0f;
+    rs0[r] = ok ? o0.rowsum[mr[r]] : 0;
+    rs1[r] = ok ? o1.rowsum[mr[r]] : 0;
+  }
+  const float cws0 = o0.c_w[0], cws1 = o1.c_w[0];
+  float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int64_t n = col0 + 16 * j + (lane & 15);
+    const float cw0 = o0.c_w_per_row ? (n < a.N ? o0.c_w[n] : 0.0f) : cws0;
+    const float cw1 = o1.c_w_per_row ? (n < a.N ? o1.c_w[n] : 0.0f) : cws1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      y[j][r] = 0.0f;
+      const int64_t m = mr[r];
+      if (m >= a.M || n >= a.N) continue;
+      const float sp = rnd<DT>((static_cast<float>(acc0[j][r] - rs0[r]) * inv0[r]) * cw0);
+      const float ep = rnd<DT>((static_cast<float>(acc1[j][r] - rs1[r]) * inv1[r]) * cw1);
+      const float gt = rnd<DT>(sigmoidf_(ld<DT>(a.gate, m * a.ld_gate + n)));
+      const float lo = ld<DT>(a.local, m * a.ld_local + n);
+      const float v = rnd<DT>(rnd<DT>(lo + rnd<DT>(gt * sp)) + ep);
+      y[j][r] = v;
+      mx[r] = fmaxf(mx[r], fabsf(v));
+      if (o.y) st<DT>(o.y, m * o.ldy + n, v);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mx[r] = wave_max<16>(mx[r]);
+    if ((lane & 15) == 0) red[(4 * (lane >> 4) + r) * 4 + w] = mx[r];
+  }
+  __syncthreads();
+  float sc[4];
+  int sum[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float* rr = red + (4 * (lane >> 4) + r) * 4;
+    sc[r] = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
+  }
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int64_t n = col0 + 16 * j + (lane & 15);
+    if (n >= a.N) continue;
+    const int64_t pos = (n & ~15) + layout1_pos(static_cast<int>(n & 15));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (mr[r] >= a.M) continue;
+      const int q = act_code<DT>(y[j][r], sc[r]);
+      codes[(4 * (lane >> 4) + r) * o.ldq + pos] = static_cast<int8_t>(q);
+      sum[r] += q;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    sum[r] = wave_sum_i<16>(sum[r]);
+    if ((lane & 15) == 0) redi[(4 * (lane >> 4) + r) * 4 + w] = sum[r];
+  }
+  __syncthreads();
+  if (tid < 16 && m0 + tid < a.M) {
+    const float* rr = red + tid * 4;
+    const int32_t* ri = redi + tid * 4;
+    o.s[m0 + tid] = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
+    o.rs[m0 + tid] = (ri[0] + ri[1]) + (ri[2] + ri[3]);
+  }
+  const int64_t chunks = o.ldq / 16;
+  for (int64_t i = tid; i < 16 * chunks; i += 256) {
+    const int64_t r = i / chunks, ck = i - r * chunks;
+    if (m0 + r >= a.M) continue;
+    *reinterpret_cast<uint4*>(o.q + (m0 + r) * o.ldq + 16 * ck) = reinterpret_cast<const uint4*>(codes + r * o.ldq)[ck];
+  }
+}
+
 template <int WM, int WN, int TM, int TN, int EPI>
 int run_mfma(const LinearArgs& a, hipStream_t st) {
   using C = Cfg<WM, WN, TM, TN>;
-  dim3 grid(static_cast<unsigned>((a.N + C::BN - 1) / C::BN), static_cast<unsigned>((a.M + C::BM - 1) / C::BM));
+  const int64_t tiles = ((a.N + C::BN - 1) / C::BN) * ((a.M + C::BM - 1) / C::BM);
+  TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
+  const unsigned grid = static_cast<unsigned>(tiles);
   if (a.out_dt == kBF16)
     mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
   else
     mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
   return check_launch("bitlinear mfma");
+}
+
+template <int NCT>
+int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(16 * o.ldq + 2 * 16 * 4 * 4);
+  const unsigned grid = static_cast<unsigned>((a.M + 15) / 16);
+  if (a.out_dt == kBF16)
+    gate_rowq_kernel<NCT, kBF16><<<grid, 256, lds, st>>>(a, o);
+  else
+    gate_rowq_kernel<NCT, kF32><<<grid, 256, lds, st>>>(a, o);
+  return check_launch("output gate rowq");
 }
 
 template <int LPR, int MR, int NCH>
@@ -361,6 +542,30 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
   if (a.M <= 64) return run_mfma<1, 4, 4, 1, kEpiOutputGate>(a, st);
   return run_mfma<2, 2, 4, 4, kEpiOutputGate>(a, st);
+}
+
+int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
+  TESM_REQUIRE(a.epilogue == kEpiOutputGate, kErrInvalidArg, "gate_rowq: needs the output-gate operands");
+  TESM_REQUIRE(a.M >= 0 && a.N >= 1 && a.N <= 1024, kErrUnsupported, "gate_rowq: needs 1 <= d_model <= 1024");
+  TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "gate_rowq: Kp must be a multiple of 128");
+  TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "gate_rowq: dtype must be 0 or 1");
+  if (a.M == 0) return kOk;
+  if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
+  if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
+  TESM_REQUIRE(a.local && a.gate && a.ld_local >= a.N && a.ld_gate >= a.N, kErrInvalidArg,
+               "gate_rowq: need local and gate operands");
+  TESM_REQUIRE(o.q && o.s && o.rs && o.ldq >= a.N && o.ldq % 16 == 0 && aligned(o.q, 16), kErrInvalidArg,
+               "gate_rowq: bad code outputs");
+  TESM_REQUIRE(!o.y || o.ldy >= a.N, kErrInvalidArg, "gate_rowq: bad y output");
+  const int64_t nct = (a.N + 63) / 64;
+  if (nct <= 1) return run_rowq<1>(a, o, st);
+  if (nct <= 2) return run_rowq<2>(a, o, st);
+  if (nct <= 3) return run_rowq<3>(a, o, st);
+  if (nct <= 4) return run_rowq<4>(a, o, st);
+  if (nct <= 6) return run_rowq<6>(a, o, st);
+  if (nct <= 8) return run_rowq<8>(a, o, st);
+  if (nct <= 12) return run_rowq<12>(a, o, st);
+  return run_rowq<16>(a, o, st);
 }
 
 }  // namespace tesm

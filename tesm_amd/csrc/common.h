@@ -75,6 +75,35 @@ __device__ __forceinline__ void st(void* p, int64_t i, float v) {
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------------------
+// per-token int8 activation quantization (reference tesm.py:206-209)
+//   scale = 127 / max(amax, eps), evaluated by torch as reciprocal() * 127
+//   code  = clamp(rne(x * scale), -128, 127)
+// with every op rounded to the activation dtype.
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float act_scale(float amax, float eps) {
+  if constexpr (DT == kBF16) {
+    const float e = rnd<DT>(eps);
+    const float d = amax < e ? e : amax;
+    return rnd<DT>(rnd<DT>(1.0f / d) * 127.0f);
+  } else {
+    const float d = amax < eps ? eps : amax;
+    return (1.0f / d) * 127.0f;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ int act_code(float v, float scale) {
+  float r = rintf(rnd<DT>(v * scale));
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return static_cast<int>(r);
+}
+
+// Byte position of code e (0..15) inside its 16-code group in "layout 1", the order the INT2
+// products read: byte 4s + j holds code 4j + s.
+__device__ __forceinline__ int layout1_pos(int e) { return 4 * (e & 3) + (e >> 2); }
+
+// ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------
 template <int WIDTH = 64>
@@ -86,6 +115,13 @@ __device__ __forceinline__ float wave_max(float v) {
 
 template <int WIDTH = 64>
 __device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
+  return v;
+}
+
+template <int WIDTH = 64>
+__device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
   for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
   return v;

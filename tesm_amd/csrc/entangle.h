@@ -36,7 +36,20 @@ struct EntArgs {
   int64_t ld_out = 0;
   int8_t* tern = nullptr;  // optional ternary map (b, t, h, w) over the effective window
   float* wts = nullptr;    // workspace (B, L, H, W_eff) floats: normalised window weights
+  // fused per-token int8 quantization of tanh(E) and C (the state_proj / ent_proj inputs);
+  // codes in layout 1, rows of ldq = kpad(H*D) bytes.  Used when q_te != nullptr.
+  int8_t* q_te = nullptr;
+  float* s_te = nullptr;
+  int32_t* rs_te = nullptr;
+  int8_t* q_c = nullptr;
+  float* s_c = nullptr;
+  int32_t* rs_c = nullptr;
+  int64_t ldq = 0;
+  float eps = 1e-5f;
 };
+
+// True when launch_local_ent can produce the quantized outputs in one fused kernel.
+bool ent_fused_ok(const EntArgs& a);
 
 int64_t ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W);
 int launch_local_ent(const EntArgs& a, hipStream_t st);

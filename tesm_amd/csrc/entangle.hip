@@ -115,10 +115,10 @@ constexpr int kMixDS = 64;  // channels per workgroup
 
 template <int DT>
 __global__ __launch_bounds__(256) void ent_mix_kernel(EntArgs a, int64_t weff) {
-  extern __shared__ float lds[];
+  extern __shared__ float lds_mix[];
   const int64_t rows = kMixTP + weff - 1;
-  float* srow = lds;                    // [rows][kMixDS]
-  float* wt = lds + rows * kMixDS;      // [kMixTP][weff]
+  float* srow = lds_mix;                // [rows][kMixDS]
+  float* wt = lds_mix + rows * kMixDS;  // [kMixTP][weff]
   const int64_t bh = blockIdx.z;        // b * H + h
   const int64_t b = bh / a.H, h = bh - b * a.H;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kMixTP;
@@ -154,6 +154,234 @@ __global__ __launch_bounds__(256) void ent_mix_kernel(EntArgs a, int64_t weff) {
     if (a.e_out) st<DT>(a.e_out, o, e);
     if (a.c_out) st<DT>(a.c_out, o, e - s);
     if (a.e_tanh) st<DT>(a.e_tanh, o, tanhf(e));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused SISO kernel: a workgroup per (batch row, kFusedTP positions) with all D channels, so the
+// per-token quantization of tanh(E) and C happens in place.  The arithmetic of each value is the
+// same sequence of float operations as in ent_scores_kernel + ent_mix_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kFusedTP = 16;
+constexpr int kFusedMaxCPD = 2;  // channels per thread: D <= 512
+
+struct FusedLds {
+  int64_t kr, qr, wt, wn, sx, red, total;  // byte offsets
+  int64_t krs;                             // row stride of kr / qr in floats (R + 1: no bank conflicts)
+};
+
+__host__ __device__ inline FusedLds fused_lds(int64_t R, int64_t D, int64_t weff, int64_t ldq, int esz) {
+  FusedLds f;
+  const int64_t rows = kFusedTP + weff - 1;
+  f.krs = R + 1;
+  f.kr = 0;
+  f.qr = f.kr + rows * f.krs * 4;
+  const int64_t scores_end = f.qr + kFusedTP * f.krs * 4;
+  const int64_t codes_end = 2 * kFusedTP * ldq;  // code staging reuses the kr/qr region
+  int64_t off = ((scores_end > codes_end ? scores_end : codes_end) + 15) / 16 * 16;
+  f.wt = off;
+  off += kFusedTP * weff * 4;
+  f.wn = off;
+  off += kFusedTP * weff * 4;
+  f.red = off;
+  off += 2 * 2 * kFusedTP * 4 * 4;  // [amax|sum][te|c][TP][4 waves]
+  off = (off + 15) / 16 * 16;
+  f.sx = off;
+  off += rows * D * esz;
+  f.total = (off + 15) / 16 * 16;
+  return f;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff, FusedLds f) {
+  using T = typename Elem<DT>::T;
+  extern __shared__ __attribute__((aligned(16))) char lds_fused[];
+  char* lds = lds_fused;
+  float* kr = reinterpret_cast<float*>(lds + f.kr);
+  float* qr = reinterpret_cast<float*>(lds + f.qr);
+  float* wt = reinterpret_cast<float*>(lds + f.wt);
+  float* wn = reinterpret_cast<float*>(lds + f.wn);
+  float* red = reinterpret_cast<float*>(lds + f.red);
+  T* sx = reinterpret_cast<T*>(lds + f.sx);
+  int8_t* codes = reinterpret_cast<int8_t*>(lds);  // after the scores: [2][TP][ldq]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kFusedTP;
+  const int64_t half = a.R / 2, R = a.R, D = a.D;
+  const int64_t rows = kFusedTP + weff - 1;
+  const int64_t tk0 = t0 - (weff - 1);  // position of key row 0
+
+  // 1. RoPE'd keys and queries (tesm.py:783-793, 1209-1218)
+  for (int64_t i = tid; i < rows * half; i += 256) {
+    const int64_t r = i / half, c = i - r * half;
+    const int64_t t = tk0 + r;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (t >= 0 && t < a.L) {
+      const int64_t ko = (b * a.L + t) * a.ld_k;
+      rope_pair<DT>(ld<DT>(a.k, ko + c), ld<DT>(a.k, ko + half + c), a.rope[t * half + c], o1, o2);
+    }
+    kr[r * f.krs + c] = o1;
+    kr[r * f.krs + half + c] = o2;
+  }
+  for (int64_t i = tid; i < kFusedTP * half; i += 256) {
+    const int64_t p = i / half, c = i - p * half;
+    const int64_t t = t0 + p;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (t < a.L) {
+      const int64_t qo = (b * a.L + t) * a.ld_q;
+      rope_pair<DT>(ld<DT>(a.q, qo + c), ld<DT>(a.q, qo + half + c), a.rope[t * half + c], o1, o2);
+      if (a.q_add) {
+        const int64_t ao = (b * a.L + t) * a.ld_qadd;
+        o1 = rnd<DT>(o1 + ld<DT>(a.q_add, ao + c));
+        o2 = rnd<DT>(o2 + ld<DT>(a.q_add, ao + half + c));
+      }
+    }
+    qr[p * f.krs + c] = o1;
+    qr[p * f.krs + half + c] = o2;
+  }
+  // 2. state halo rows, raw dtype
+  const T* S = static_cast<const T*>(a.S);
+  for (int64_t i = tid; i < rows * D; i += 256) {
+    const int64_t r = i / D, c = i - r * D;
+    const int64_t t = tk0 + r;
+    sx[i] = (t >= 0 && t < a.L) ? S[(b * a.L + t) * a.ld_s + c] : T(0);
+  }
+  __syncthreads();
+
+  // 3. window scores and ternary decisions (same float sequence as ent_scores_kernel)
+  const float sq = static_cast<float>(sqrt(static_cast<double>(R)));
+  for (int64_t i = tid; i < kFusedTP * weff; i += 256) {
+    const int64_t p = i / weff, w = i - p * weff;
+    const int64_t t = t0 + p, j = t - (weff - 1) + w;
+    float tern = 0.0f;
+    if (t < a.L && j >= 0) {
+      const float* qp = qr + p * f.krs;
+      const float* kp = kr + (p + w) * f.krs;
+      float dot = 0.0f;
+      for (int64_t c = 0; c < half; ++c) {
+        dot += qp[c] * kp[c];
+        dot += qp[half + c] * kp[half + c];
+      }
+      float s = rnd<DT>(rnd<DT>(dot) / sq);
+      s = rnd<DT>(s + a.bias[a.W - weff + w]);
+      tern = s > a.thr ? 1.0f : (s < -a.thr ? -1.0f : 0.0f);
+    }
+    wt[i] = tern;
+    if (a.tern && t < a.L) a.tern[(b * a.L + t) * weff + w] = static_cast<int8_t>(tern);
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < kFusedTP * weff; i += 256) {
+    const int64_t p = i / weff;
+    float n = 0.0f;
+    for (int64_t w = 0; w < weff; ++w) n += fabsf(wt[p * weff + w]);
+    n = fmaxf(n, 1.0f);
+    wn[i] = rnd<DT>(wt[i] / n);
+  }
+  // zero the code staging area (it overlays kr/qr, free after the scores)
+  for (int64_t i = tid; i < 2 * kFusedTP * a.ldq / 16; i += 256)
+    reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+
+  // 4. window average, mix, tanh (ent_mix_kernel arithmetic), held in registers
+  float te[kFusedTP][kFusedMaxCPD], cc[kFusedTP][kFusedMaxCPD];
+  float mx_te[kFusedTP], mx_c[kFusedTP];
+#pragma unroll
+  for (int p = 0; p < kFusedTP; ++p) {
+    mx_te[p] = 0.0f;
+    mx_c[p] = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < kFusedMaxCPD; ++jj) {
+      te[p][jj] = 0.0f;
+      cc[p][jj] = 0.0f;
+      const int64_t c = tid + 256 * jj;
+      const int64_t t = t0 + p;
+      if (c >= D || t >= a.L) continue;
+      float acc = 0.0f;
+      for (int64_t w = 0; w < weff; ++w) acc += wn[p * weff + w] * ld<DT>(sx, (p + w) * D + c);
+      const float avg = rnd<DT>(acc);
+      const float s = ld<DT>(sx, (p + weff - 1) * D + c);
+      const float e = rnd<DT>(s + rnd<DT>(a.ent_scale * rnd<DT>(avg - s)));
+      const float cv = rnd<DT>(e - s);
+      const float tv = rnd<DT>(tanhf(e));
+      const int64_t o = (b * a.L + t) * a.ld_out + c;
+      if (a.avg) st<DT>(a.avg, o, avg);
+      if (a.e_out) st<DT>(a.e_out, o, e);
+      if (a.c_out) st<DT>(a.c_out, o, cv);
+      if (a.e_tanh) st<DT>(a.e_tanh, o, tv);
+      te[p][jj] = tv;
+      cc[p][jj] = cv;
+      mx_te[p] = fmaxf(mx_te[p], fabsf(tv));
+      mx_c[p] = fmaxf(mx_c[p], fabsf(cv));
+    }
+  }
+  // 5. per-token scales (tesm.py:206-209) over the D channels of the workgroup
+#pragma unroll
+  for (int p = 0; p < kFusedTP; ++p) {
+    const float m1 = wave_max(mx_te[p]), m2 = wave_max(mx_c[p]);
+    if (lane == 0) {
+      red[(0 * kFusedTP + p) * 4 + wave] = m1;
+      red[(1 * kFusedTP + p) * 4 + wave] = m2;
+    }
+  }
+  __syncthreads();
+  float sc_te[kFusedTP], sc_c[kFusedTP];
+#pragma unroll
+  for (int p = 0; p < kFusedTP; ++p) {
+    const float* r0 = red + (0 * kFusedTP + p) * 4;
+    const float* r1 = red + (1 * kFusedTP + p) * 4;
+    sc_te[p] = act_scale<DT>(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])), a.eps);
+    sc_c[p] = act_scale<DT>(fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])), a.eps);
+  }
+  // 6. codes into the staging rows, row sums of the codes
+  int32_t* redi = reinterpret_cast<int32_t*>(red + 2 * kFusedTP * 4);
+  __syncthreads();  // everyone has read red[] before it is reused for the sums
+#pragma unroll
+  for (int p = 0; p < kFusedTP; ++p) {
+    int s1 = 0, s2 = 0;
+#pragma unroll
+    for (int jj = 0; jj < kFusedMaxCPD; ++jj) {
+      const int64_t c = tid + 256 * jj;
+      if (c >= D || t0 + p >= a.L) continue;
+      const int q1 = act_code<DT>(te[p][jj], sc_te[p]);
+      const int q2 = act_code<DT>(cc[p][jj], sc_c[p]);
+      const int64_t pos = (c & ~15) + layout1_pos(static_cast<int>(c & 15));
+      codes[(0 * kFusedTP + p) * a.ldq + pos] = static_cast<int8_t>(q1);
+      codes[(1 * kFusedTP + p) * a.ldq + pos] = static_cast<int8_t>(q2);
+      s1 += q1;
+      s2 += q2;
+    }
+    s1 = wave_sum_i(s1);
+    s2 = wave_sum_i(s2);
+    if (lane == 0) {
+      redi[(0 * kFusedTP + p) * 4 + wave] = s1;
+      redi[(1 * kFusedTP + p) * 4 + wave] = s2;
+    }
+  }
+  __syncthreads();
+  if (tid < 2 * kFusedTP) {
+    const int which = tid / kFusedTP, p = tid % kFusedTP;
+    const int64_t t = t0 + p;
+    if (t < a.L) {
+      const int32_t* r = redi + (which * kFusedTP + p) * 4;
+      const int64_t row = b * a.L + t;
+      if (which == 0) {
+        a.s_te[row] = sc_te[p];
+        a.rs_te[row] = (r[0] + r[1]) + (r[2] + r[3]);
+      } else {
+        a.s_c[row] = sc_c[p];
+        a.rs_c[row] = (r[0] + r[1]) + (r[2] + r[3]);
+      }
+    }
+  }
+  const int64_t chunks = a.ldq / 16;
+  for (int64_t i = tid; i < 2 * kFusedTP * chunks; i += 256) {
+    const int64_t rr = i / chunks, ck = i - rr * chunks;
+    const int which = static_cast<int>(rr / kFusedTP), p = static_cast<int>(rr % kFusedTP);
+    const int64_t t = t0 + p;
+    if (t >= a.L) continue;
+    int8_t* dst = (which == 0 ? a.q_te : a.q_c) + (b * a.L + t) * a.ldq + 16 * ck;
+    *reinterpret_cast<uint4*>(dst) = reinterpret_cast<const uint4*>(codes + rr * a.ldq)[ck];
   }
 }
 
@@ -195,6 +423,13 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
 
+bool ent_fused_ok(const EntArgs& a) {
+  if (a.mimo || a.H != 1 || a.D > 256 * kFusedMaxCPD) return false;
+  const int64_t weff = eff_window(a);
+  const int64_t ldq = a.ldq > 0 ? a.ldq : kpad(a.D);
+  return fused_lds(a.R, a.D, weff, ldq, a.dt == kBF16 ? 2 : 4).total <= 64 * 1024;
+}
+
 int64_t ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W) {
   return round_up(std::max<int64_t>(1, B * L * H * W) * static_cast<int64_t>(sizeof(float)), 256);
 }
@@ -212,6 +447,20 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
                "local_ent: bad ld_out");
   TESM_REQUIRE(a.B * a.H <= 65535 && (a.L + kMixTP - 1) / kMixTP <= 65535, kErrUnsupported, "local_ent: grid too large");
   const int64_t weff = eff_window(a);
+  if (a.q_te) {
+    TESM_REQUIRE(ent_fused_ok(a), kErrUnsupported,
+                 "local_ent: fused quantization needs SISO, D <= 512 and a small enough window/rank");
+    TESM_REQUIRE(a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c && a.ldq >= a.D && a.ldq % 16 == 0 &&
+                     aligned(a.q_te, 16) && aligned(a.q_c, 16),
+                 kErrInvalidArg, "local_ent: bad quantized outputs");
+    const FusedLds f = fused_lds(a.R, a.D, weff, a.ldq, a.dt == kBF16 ? 2 : 4);
+    dim3 grid(static_cast<unsigned>((a.L + kFusedTP - 1) / kFusedTP), static_cast<unsigned>(a.B));
+    if (a.dt == kBF16)
+      ent_fused_kernel<kBF16><<<grid, 256, f.total, st>>>(a, weff, f);
+    else
+      ent_fused_kernel<kF32><<<grid, 256, f.total, st>>>(a, weff, f);
+    return check_launch("entanglement fused");
+  }
   int rc;
   if (a.dt == kBF16)
     rc = a.mimo ? run_scores<kBF16, 1>(a, weff, st) : run_scores<kBF16, 0>(a, weff, st);

@@ -13,90 +13,144 @@
 
 namespace tesm {
 
-// One wave per row; 4 rows per 256-thread workgroup.
+// Load the 16 values of code group g (codes 16g..16g+15) of one row, zero past K.
 template <int DT, bool VEC>
+__device__ __forceinline__ void load_group(const void* __restrict__ x, int64_t base, int64_t K, int64_t g,
+                                           float (&v)[16]) {
+  const int64_t k0 = g * 16;
+  if (VEC && k0 + 16 <= K) {
+    if constexpr (DT == kBF16) {
+      const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + k0);
+      const uint4 a = p[0], b = p[1];
+      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      }
+    } else {
+      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + k0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 f = p[i];
+        v[4 * i] = f.x;
+        v[4 * i + 1] = f.y;
+        v[4 * i + 2] = f.z;
+        v[4 * i + 3] = f.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (k0 + i < K) ? ld<DT>(x, base + k0 + i) : 0.0f;
+  }
+}
+
+// Codes of one group, packed in the requested layout; adds the codes to rs.
+template <int DT>
+__device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int layout, int32_t& rs) {
+  uint32_t c[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int ci = act_code<DT>(v[i], sc);
+    rs += ci;
+    c[i] = static_cast<uint32_t>(ci) & 0xffu;
+  }
+  uint4 out;
+  if (layout == 1) {
+    out.x = c[0] | (c[4] << 8) | (c[8] << 16) | (c[12] << 24);
+    out.y = c[1] | (c[5] << 8) | (c[9] << 16) | (c[13] << 24);
+    out.z = c[2] | (c[6] << 8) | (c[10] << 16) | (c[14] << 24);
+    out.w = c[3] | (c[7] << 8) | (c[11] << 16) | (c[15] << 24);
+  } else {
+    out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    out.z = c[8] | (c[9] << 8) | (c[10] << 16) | (c[11] << 24);
+    out.w = c[12] | (c[13] << 8) | (c[14] << 16) | (c[15] << 24);
+  }
+  return out;
+}
+
+// LPR lanes per row (64 / LPR rows per wave, 4 waves per workgroup).  Each lane owns code groups
+// lane, lane + LPR, ... ; with G > 0 its G groups stay in registers between the amax and the code
+// pass, with G == 0 (very wide rows) the row is read twice.
+template <int DT, bool VEC, int LPR, int G>
 __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__ x, int64_t M, int64_t K,
                                                         int64_t ldx, float eps, int layout, int8_t* __restrict__ q,
                                                         int64_t ldq, float* __restrict__ s_out,
                                                         int32_t* __restrict__ rowsum) {
+  constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
+  const int g0 = lane & (LPR - 1);
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  if (row >= M) return;  // whole lane groups leave together
   const int64_t base = row * ldx;
+  const int64_t ngroups = ldq / 16;
 
   float amax = 0.0f;
-  for (int64_t k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(ld<DT>(x, base + k)));
-  amax = wave_max(amax);
-
-  // scale = 127 / amax.clamp_min(eps), evaluated by torch as reciprocal() * 127
-  float sc;
-  if constexpr (DT == kBF16) {
-    const float e = rnd<DT>(eps);
-    const float d = amax < e ? e : amax;
-    sc = rnd<DT>(rnd<DT>(1.0f / d) * 127.0f);
-  } else {
-    const float d = amax < eps ? eps : amax;
-    sc = (1.0f / d) * 127.0f;
-  }
-
   int32_t rs = 0;
-  const int64_t ngroups = ldq / 16;
-  for (int64_t g = lane; g < ngroups; g += 64) {
-    float v[16];
-    const int64_t k0 = g * 16;
-    if (VEC && k0 + 16 <= K) {
-      if constexpr (DT == kBF16) {
-        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + k0);
-        const uint4 a = p[0], b = p[1];
-        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if constexpr (G > 0) {
+    float v[G][16];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v[2 * i] = __uint_as_float(w[i] << 16);
-          v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
+    for (int gi = 0; gi < G; ++gi) {
+      const int64_t g = g0 + LPR * gi;
+      if (g < ngroups) {
+        load_group<DT, VEC>(x, base, K, g, v[gi]);
       } else {
-        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + k0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float4 f = p[i];
-          v[4 * i] = f.x;
-          v[4 * i + 1] = f.y;
-          v[4 * i + 2] = f.z;
-          v[4 * i + 3] = f.w;
-        }
+        for (int i = 0; i < 16; ++i) v[gi][i] = 0.0f;
       }
-    } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = (k0 + i < K) ? ld<DT>(x, base + k0 + i) : 0.0f;
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[gi][i]));
     }
-    uint32_t c[16];
+    amax = wave_max<LPR>(amax);
+    const float sc = act_scale<DT>(amax, eps);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float r = rintf(rnd<DT>(v[i] * sc));
-      r = fminf(fmaxf(r, -128.0f), 127.0f);
-      const int ci = static_cast<int>(r);
-      rs += ci;
-      c[i] = static_cast<uint32_t>(ci) & 0xffu;
+    for (int gi = 0; gi < G; ++gi) {
+      const int64_t g = g0 + LPR * gi;
+      if (g < ngroups) *reinterpret_cast<uint4*>(q + row * ldq + 16 * g) = group_codes<DT>(v[gi], sc, layout, rs);
     }
-    uint4 out;
-    if (layout == 1) {
-      out.x = c[0] | (c[4] << 8) | (c[8] << 16) | (c[12] << 24);
-      out.y = c[1] | (c[5] << 8) | (c[9] << 16) | (c[13] << 24);
-      out.z = c[2] | (c[6] << 8) | (c[10] << 16) | (c[14] << 24);
-      out.w = c[3] | (c[7] << 8) | (c[11] << 16) | (c[15] << 24);
-    } else {
-      out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-      out.z = c[8] | (c[9] << 8) | (c[10] << 16) | (c[11] << 24);
-      out.w = c[12] | (c[13] << 8) | (c[14] << 16) | (c[15] << 24);
+    if (g0 == 0) s_out[row] = sc;
+  } else {
+    for (int64_t g = g0; g < ngroups; g += LPR) {
+      float v[16];
+      load_group<DT, VEC>(x, base, K, g, v);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
     }
-    *reinterpret_cast<uint4*>(q + row * ldq + k0) = out;
+    amax = wave_max<LPR>(amax);
+    const float sc = act_scale<DT>(amax, eps);
+    for (int64_t g = g0; g < ngroups; g += LPR) {
+      float v[16];
+      load_group<DT, VEC>(x, base, K, g, v);
+      *reinterpret_cast<uint4*>(q + row * ldq + 16 * g) = group_codes<DT>(v, sc, layout, rs);
+    }
+    if (g0 == 0) s_out[row] = sc;
   }
-  rs = wave_sum_i(rs);
-  if (lane == 0) {
-    s_out[row] = sc;
-    if (rowsum) rowsum[row] = rs;
-  }
+  rs = wave_sum_i<LPR>(rs);
+  if (g0 == 0 && rowsum) rowsum[row] = rs;
+}
+
+template <int DT, bool VEC, int LPR, int G>
+void run_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
+               float* s_x, int32_t* rowsum, hipStream_t st) {
+  constexpr int RPB = 4 * (64 / LPR);
+  const unsigned nb = static_cast<unsigned>((M + RPB - 1) / RPB);
+  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+}
+
+template <int DT, bool VEC>
+void dispatch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
+                    float* s_x, int32_t* rowsum, hipStream_t st) {
+  const int64_t ng = ldq / 16;
+  if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 8) return run_quant<DT, VEC, 8, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 16) return run_quant<DT, VEC, 16, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 32) return run_quant<DT, VEC, 32, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 64) return run_quant<DT, VEC, 64, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 128) return run_quant<DT, VEC, 64, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 256) return run_quant<DT, VEC, 64, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 512) return run_quant<DT, VEC, 64, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  return run_quant<DT, VEC, 64, 0>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
 }
 
 int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
@@ -110,17 +164,12 @@ int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, f
   if (M == 0) return kOk;
   const int esz = dt == kBF16 ? 2 : 4;
   const bool vec = aligned(x, 16) && (ldx * esz) % 16 == 0;
-  dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
   if (dt == kBF16) {
-    if (vec)
-      quant_act_kernel<kBF16, true><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
-    else
-      quant_act_kernel<kBF16, false><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+    if (vec) dispatch_quant<kBF16, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+    else dispatch_quant<kBF16, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
   } else {
-    if (vec)
-      quant_act_kernel<kF32, true><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
-    else
-      quant_act_kernel<kF32, false><<<grid, block, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+    if (vec) dispatch_quant<kF32, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+    else dispatch_quant<kF32, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
   }
   return check_launch("quant_act");
 }

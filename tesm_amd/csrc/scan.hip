@@ -9,7 +9,7 @@
 // falls below 1e-12; the kernels reproduce that factor ("clamp" mode) and run the recurrence in
 // fp32 registers.
 //
-// Three launches, all channel-parallel (one lane per channel, coalesced along C):
+// Three launches, all channel-parallel (lanes along C, coalesced):
 //   1. summary: each (b, chunk of T positions, channel) scans its chunk from h = 0 and stores
 //      (prod d, h_end);
 //   2. carry:   each (b, channel) folds the chunk summaries in order -> carry into every chunk
@@ -92,6 +92,168 @@ __global__ __launch_bounds__(64) void scan_carry_kernel(ScanArgs a, int64_t nc, 
   if (a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(h);
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: TM positions per thread-chunk fully unrolled (all loads issued before the
+// recurrence), CPT adjacent channels per thread (bf16 pairs -> 4-byte loads and stores).
+// ---------------------------------------------------------------------------
+template <int DT, int CPT>
+struct Vec;
+template <>
+struct Vec<kBF16, 2> {
+  __device__ static __forceinline__ void load(const void* p, int64_t i, float (&v)[2]) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(w << 16);
+    v[1] = __uint_as_float(w & 0xffff0000u);
+  }
+};
+template <int DT>
+struct Vec<DT, 1> {
+  __device__ static __forceinline__ void load(const void* p, int64_t i, float (&v)[1]) { v[0] = ld<DT>(p, i); }
+};
+
+template <int DT, int OUT_DT, int MODE, int PHASE, int TM, int CPT>
+__global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, int64_t nc, float* __restrict__ summ,
+                                                        const float* __restrict__ carry) {
+  const int64_t ng = a.C / CPT;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= a.B * nc * ng) return;
+  const int64_t gq = idx % ng, rest = idx / ng;
+  const int64_t c = rest % nc, b = rest / nc;
+  const int64_t ch = gq * CPT;
+  const int64_t t0 = c * T;
+  const int n = static_cast<int>((t0 + T < a.L ? t0 + T : a.L) - t0);
+
+  float d[TM][CPT], u[TM][CPT], bias[CPT];
+  if constexpr (MODE == 1) Vec<DT, CPT>::load(a.decay_bias, ch, bias);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    if (i < n) {
+      const int64_t tok = b * a.L + t0 + i;
+      float x0[CPT], x1[CPT];
+      Vec<DT, CPT>::load(a.decay, tok * a.ld_decay + ch, x0);
+      Vec<DT, CPT>::load(a.update, tok * a.ld_update + ch, x1);
+      if constexpr (MODE == 0) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+          d[i][j] = x0[j];
+          u[i][j] = x1[j];
+        }
+      } else {
+        float x2[CPT];
+        Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+          const float sv = rnd<DT>(tanhf(x2[j]));
+          d[i][j] = rnd<DT>(sigmoidf_(rnd<DT>(x0[j] + bias[j])));
+          const float w = rnd<DT>(sigmoidf_(x1[j]));
+          u[i][j] = a.round_update ? rnd<DT>(w * sv) : w * sv;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        d[i][j] = 1.0f;
+        u[i][j] = 0.0f;
+      }
+    }
+  }
+  const int64_t sidx = (b * nc + c) * a.C + ch;
+  const int cs = static_cast<int>(a.cs);  // the thread-chunk start is a multiple of cs
+  float h[CPT], P[CPT], A[CPT];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    h[j] = (PHASE == 1) ? 0.0f : carry[sidx + j];
+    P[j] = 1.0f;
+    A[j] = 1.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    if (i < n) {
+      const bool reset = (i % cs) == 0;
+      float out[CPT];
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        float dd = d[i][j], g = 1.0f;
+        if (a.clamp) {
+          dd = fmaxf(dd, kScanEps);
+          A[j] = reset ? dd : A[j] * dd;
+          if (A[j] < kScanEps) g = A[j] / kScanEps;
+        }
+        h[j] = dd * h[j] + g * u[i][j];
+        P[j] *= dd;
+        out[j] = h[j];
+      }
+      if (PHASE == 3) {
+        const int64_t o = (b * a.L + t0 + i) * a.ld_states + ch;
+        if constexpr (OUT_DT == kBF16 && CPT == 2) {
+          const uint32_t w = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
+          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.states) + o) = w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < CPT; ++j) st<OUT_DT>(a.states, o + j, out[j]);
+        }
+      }
+    }
+  }
+  if (PHASE == 1) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      summ[2 * (sidx + j)] = P[j];
+      summ[2 * (sidx + j) + 1] = h[j];
+    }
+  }
+}
+
+// Carry propagation over the chunk summaries: a workgroup per (batch row, 64 channels) with
+// NSEG waves, each folding a contiguous run of chunks; the runs are combined through LDS.
+template <int NSEG>
+__global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, int64_t nc,
+                                                                   const float* __restrict__ summ,
+                                                                   float* __restrict__ carry) {
+  __shared__ float segP[NSEG][64], segH[NSEG][64];
+  const int lane = threadIdx.x & 63, seg = threadIdx.x >> 6;
+  const int64_t ch = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  const int64_t b = blockIdx.y;
+  const bool ok = ch < a.C;
+  const int64_t per = (nc + NSEG - 1) / NSEG;
+  const int64_t c0 = seg * per, c1 = (c0 + per < nc) ? c0 + per : nc;
+  float Ps = 1.0f, Hs = 0.0f;
+  if (ok) {
+    for (int64_t c = c0; c < c1; ++c) {
+      const int64_t sidx = (b * nc + c) * a.C + ch;
+      const float P = summ[2 * sidx], H = summ[2 * sidx + 1];
+      Hs = P * Hs + H;
+      Ps *= P;
+    }
+  }
+  segP[seg][lane] = Ps;
+  segH[seg][lane] = Hs;
+  __syncthreads();
+  if (!ok) return;
+  float h = a.h0 ? static_cast<float>(a.h0[b * a.C + ch]) : 0.0f;
+  for (int s2 = 0; s2 < seg; ++s2) h = segP[s2][lane] * h + segH[s2][lane];
+  for (int64_t c = c0; c < c1; ++c) {
+    const int64_t sidx = (b * nc + c) * a.C + ch;
+    carry[sidx] = h;
+    h = summ[2 * sidx] * h + summ[2 * sidx + 1];
+  }
+  if (seg == NSEG - 1 && a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(h);
+}
+
+template <int DT, int OUT_DT, int MODE, int TM, int CPT>
+int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
+  const int64_t threads = a.B * nc * (a.C / CPT);
+  const unsigned nb = static_cast<unsigned>((threads + 255) / 256);
+  scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+  dim3 g2(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.B));
+  if (nc >= 64)
+    scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, st>>>(a, nc, summ, carry);
+  else
+    scan_carry_seg_kernel<4><<<g2, 4 * 64, 0, st>>>(a, nc, summ, carry);
+  scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+  return check_launch("scan");
+}
+
 template <int DT, int OUT_DT, int MODE>
 int run_scan(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
   dim3 g3(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(nc), static_cast<unsigned>(a.B));
@@ -104,9 +266,11 @@ int run_scan(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry
 
 }  // namespace
 
+// Thread-chunk length: a multiple of the reference chunk (so the clamp's running product restarts
+// inside a thread) of at most 16 positions when possible.
 int64_t scan_chunk_len(int64_t L, int64_t cs) {
   const int64_t cse = std::max<int64_t>(1, std::min(cs, L));
-  return cse >= 32 ? cse : cse * (32 / cse);
+  return cse >= 16 ? cse : cse * (16 / cse);
 }
 
 int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
@@ -136,6 +300,33 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   // the reference chunk grid starts at 0 with chunk = min(cs, L); pass the effective value
   ScanArgs e = a;
   e.cs = std::max<int64_t>(1, std::min(a.cs, a.L));
+  const bool pairs = a.dt == kBF16 && a.C % 2 == 0 && a.ld_decay % 2 == 0 && a.ld_update % 2 == 0 &&
+                     (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
+                     aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
+                     aligned(a.states, 4);
+  if (T <= 32) {
+    const int key = a.dt * 1000 + a.out_dt * 100 + a.mode * 10 + (T <= 16 ? 1 : 2);
+    switch (key) {
+      case 1: return run_scan_fast<kF32, kF32, 0, 16, 1>(e, T, nc, summ, carry, st);
+      case 2: return run_scan_fast<kF32, kF32, 0, 32, 1>(e, T, nc, summ, carry, st);
+      case 11: return run_scan_fast<kF32, kF32, 1, 16, 1>(e, T, nc, summ, carry, st);
+      case 12: return run_scan_fast<kF32, kF32, 1, 32, 1>(e, T, nc, summ, carry, st);
+      case 1101:
+        return pairs ? run_scan_fast<kBF16, kBF16, 0, 16, 2>(e, T, nc, summ, carry, st)
+                     : run_scan_fast<kBF16, kBF16, 0, 16, 1>(e, T, nc, summ, carry, st);
+      case 1102:
+        return pairs ? run_scan_fast<kBF16, kBF16, 0, 32, 2>(e, T, nc, summ, carry, st)
+                     : run_scan_fast<kBF16, kBF16, 0, 32, 1>(e, T, nc, summ, carry, st);
+      case 1111:
+        return pairs ? run_scan_fast<kBF16, kBF16, 1, 16, 2>(e, T, nc, summ, carry, st)
+                     : run_scan_fast<kBF16, kBF16, 1, 16, 1>(e, T, nc, summ, carry, st);
+      case 1112:
+        return pairs ? run_scan_fast<kBF16, kBF16, 1, 32, 2>(e, T, nc, summ, carry, st)
+                     : run_scan_fast<kBF16, kBF16, 1, 32, 1>(e, T, nc, summ, carry, st);
+      default:
+        break;  // mixed dtypes: generic kernels below
+    }
+  }
   const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
   switch (key) {
     case 0: return run_scan<kF32, kF32, 0>(e, T, nc, summ, carry, st);

@@ -52,4 +52,18 @@ struct LinearArgs {
 
 int launch_linear(const LinearArgs& a, hipStream_t st);
 
+// Per-token int8 codes of the output-gate result y (the out_proj input), written instead of y.
+struct RowQuant {
+  int8_t* q = nullptr;   // (M, ldq) layout-1 codes
+  int64_t ldq = 0;
+  float* s = nullptr;    // (M) scales
+  int32_t* rs = nullptr; // (M) code sums
+  float eps = 1e-5f;
+  void* y = nullptr;     // optional (M, ldy) y itself, in the output dtype
+  int64_t ldy = 0;
+};
+
+// Output gate (kEpiOutputGate operands) with the whole row per workgroup; N <= 1024.
+int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st);
+
 }  // namespace tesm

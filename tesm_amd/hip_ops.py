@@ -219,3 +219,88 @@ def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=N
         outs["tern"] = tern
     return outs
 
+
+
+def local_ent_quant(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, eps: float = 1e-5, q_add=None,
+                    want_floats: bool = False, want_tern: bool = False):
+    """Fused SISO entanglement + int8 codes of tanh(E) and C (the state_proj / ent_proj inputs).
+
+    Returns a dict with ``te`` and ``c`` = (codes (M, kpad(D)) layout 1, scales (M), rowsums (M)),
+    plus ``e_tanh`` / ``c_float`` / ``tern`` when asked for.
+    """
+    lib = _lib.load()
+    B, L, R = q.shape
+    D = S.shape[-1]
+    dt = S.dtype
+    q2, k2 = _rows(q.reshape(B * L, R)), _rows(k.reshape(B * L, R))
+    S2 = _rows(S.reshape(B * L, D))
+    qa = _rows(q_add.reshape(B * L, R)) if q_add is not None else None
+    bias_f = bias.reshape(W).to(device=S.device, dtype=dt).to(torch.float32).contiguous()
+    M, ldq = B * L, kpad(D)
+    dev = S.device
+    te = (torch.empty((M, ldq), dtype=torch.int8, device=dev), torch.empty(M, device=dev),
+          torch.empty(M, dtype=torch.int32, device=dev))
+    cc = (torch.empty((M, ldq), dtype=torch.int8, device=dev), torch.empty(M, device=dev),
+          torch.empty(M, dtype=torch.int32, device=dev))
+    et = torch.empty((B, L, D), dtype=dt, device=dev) if want_floats else None
+    cf = torch.empty((B, L, D), dtype=dt, device=dev) if want_floats else None
+    tern = torch.empty((B, L, min(W, L)), dtype=torch.int8, device=dev) if want_tern else None
+    require_device(q2, k2, rope, qa, bias_f, S2, *te, *cc, et, cf, tern)
+    d = _lib.EntQuant()
+    d.dt = dt_code(dt)
+    d.B, d.L, d.R, d.D, d.W = B, L, R, D, W
+    d.thr, d.ent_scale, d.eps = round_dtype(thr, dt), float(ent_scale), float(eps)
+    d.q, d.ld_q, d.k, d.ld_k = q2.data_ptr(), q2.stride(0), k2.data_ptr(), k2.stride(0)
+    d.rope = rope.data_ptr()
+    d.q_add, d.ld_qadd = (qa.data_ptr(), qa.stride(0)) if qa is not None else (None, 0)
+    d.bias, d.S, d.ld_s = bias_f.data_ptr(), S2.data_ptr(), S2.stride(0)
+    d.q_te, d.s_te, d.rs_te = (t.data_ptr() for t in te)
+    d.q_c, d.s_c, d.rs_c = (t.data_ptr() for t in cc)
+    d.ldq = ldq
+    d.e_tanh = et.data_ptr() if et is not None else None
+    d.c_out = cf.data_ptr() if cf is not None else None
+    d.ld_out = D
+    d.tern = tern.data_ptr() if tern is not None else None
+    with torch.cuda.device(dev):
+        _lib.check(lib.tesm_hip_local_ent_quant(ctypes.byref(d), _stream(S)))
+    out = {"te": te, "c": cc}
+    if want_floats:
+        out["e_tanh"], out["c_float"] = et, cf
+    if want_tern:
+        out["tern"] = tern
+    return out
+
+
+def output_gate(te, cc, sp_packed, sp_cw, ep_packed, ep_cw, local, gate, d_state: int, eps: float = 1e-5,
+                quantize: bool = True, want_y: bool = True):
+    """y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(C) from code triples ``te``/``cc``.
+
+    ``local``/``gate`` are (M, d_model) views (row stride allowed).  With ``quantize`` the kernel
+    also returns y's out_proj codes (codes, scales, rowsums).
+    """
+    lib = _lib.load()
+    local, gate = _rows(local), _rows(gate)
+    M, dm = local.shape
+    dt = local.dtype
+    dev = local.device
+    y = torch.empty((M, dm), dtype=dt, device=dev) if (want_y or not quantize) else None
+    qy = None
+    if quantize:
+        ldq = kpad(dm)
+        qy = (torch.empty((M, ldq), dtype=torch.int8, device=dev), torch.empty(M, device=dev),
+              torch.empty(M, dtype=torch.int32, device=dev))
+    require_device(*te, *cc, sp_packed, sp_cw, ep_packed, ep_cw, local, gate, y, *(qy or ()))
+    d = _lib.OutputGate()
+    d.dt = dt_code(dt)
+    d.M, d.d_model, d.d_state, d.eps = M, dm, d_state, float(eps)
+    d.q_te, d.ldq_te, d.s_te, d.rs_te = te[0].data_ptr(), te[0].stride(0), te[1].data_ptr(), te[2].data_ptr()
+    d.q_c, d.ldq_c, d.s_c, d.rs_c = cc[0].data_ptr(), cc[0].stride(0), cc[1].data_ptr(), cc[2].data_ptr()
+    d.state_proj = _lib.Linear(sp_packed.data_ptr(), sp_packed.stride(0), sp_cw.data_ptr(), 0)
+    d.ent_proj = _lib.Linear(ep_packed.data_ptr(), ep_packed.stride(0), ep_cw.data_ptr(), 0)
+    d.local, d.ld_local, d.gate, d.ld_gate = local.data_ptr(), local.stride(0), gate.data_ptr(), gate.stride(0)
+    d.y, d.ld_y = (y.data_ptr(), dm) if y is not None else (None, 0)
+    if qy is not None:
+        d.q_y, d.ldq_y, d.s_y, d.rs_y = qy[0].data_ptr(), qy[0].stride(0), qy[1].data_ptr(), qy[2].data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(lib.tesm_hip_output_gate_i2(ctypes.byref(d), _stream(local)))
+    return y, qy

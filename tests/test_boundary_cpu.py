@@ -37,13 +37,46 @@ def test_missing_library_raises(monkeypatch, tmp_path):
         _lib.load()
 
 
-def test_struct_layout_matches_header():
-    # pointer-aligned fields: tesm_hip_linear is 32 bytes; the layer descriptor packs 5 of them
-    assert torch.tensor(0).element_size() == 8
+def _c_struct_fields(header_text, name):
+    body = re.search(r"typedef struct " + name + r" \{(.*?)\} " + name + ";", header_text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = decl.split(None, 1)[1] if not decl.startswith("const ") else decl.split(None, 2)[2]
+        for nm in names.split(","):
+            fields.append(nm.strip().lstrip("*").strip())
+    return fields
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """Every ctypes descriptor has the C struct's field names, offsets and size (compiled with gcc)."""
     import ctypes
-    assert ctypes.sizeof(_lib.Linear) == 32
-    assert _lib.SisoLayer.in_proj.offset % 8 == 0
-    assert ctypes.sizeof(_lib.SisoLayer) == _lib.SisoLayer.proj_out.offset + 8
+    import subprocess
+    with open(os.path.join(ROOT, "include", "tesm_hip.h")) as f:
+        text = f.read()
+    structs = {"tesm_hip_linear": _lib.Linear, "tesm_hip_ent_quant": _lib.EntQuant,
+               "tesm_hip_output_gate": _lib.OutputGate, "tesm_hip_siso_layer": _lib.SisoLayer}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "tesm_hip.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        fields = _c_struct_fields(text, cname)
+        assert fields == [f[0] for f in py._fields_], cname
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fld in fields:
+            lines.append(f'printf("{cname} {fld} %zu\\n", offsetof({cname}, {fld}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l.strip()}
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fld, _ in py._fields_:
+            assert got[(cname, fld)] == getattr(py, fld).offset, (cname, fld)
 
 
 def test_seeded_construction_matches_reference_parameters():

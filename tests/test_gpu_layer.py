@@ -107,3 +107,19 @@ def test_siso_prefill_errors():
         assert out is u0 and fin is None
     with pytest.raises(RuntimeError, match="kernel_backend"):
         m(torch.randn(1, 4, 64, device=DEV))  # grad enabled
+
+
+def test_siso_prefill_unfused_fallbacks_vs_oracle():
+    """d_model > 1024 and d_state > 512 take the unfused output-gate and entanglement paths."""
+    cfg = dict(d_model=1100, d_state=520, ent_rank=8, entanglement_window=4, entanglement_threshold=0.08,
+               entanglement_scale=0.2, decay_init_bias=1.0, max_seq_len=64)
+    torch.manual_seed(5)
+    ref = ot.TESM_SISO(**cfg).eval()
+    torch.manual_seed(5)
+    m = TESM_SISO(**cfg).to(DEV).eval()
+    u = torch.randn(1, 20, 1100, generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        yr, fr = ref(u)
+        y, f = m(u.to(DEV))
+    flip_aware(to_np(y), to_np(yr), row_tol=1e-5, max_flip_frac=0.1, bound=1e-2)
+    np.testing.assert_allclose(f.cpu().numpy(), fr.numpy(), rtol=1e-4, atol=1e-5)
