@@ -132,6 +132,21 @@ def measure_kernels(torch, only):
         res["local_ent_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
                                   "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
         del sets
+    if sel("local_ent_quant_small"):
+        nrot = 80
+        rope = hip_ops.rope_table(Ls, R, torch.bfloat16, dev)
+        bias = torch.randn(W, device=dev, generator=gen) * 0.3
+        sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
+                 torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
+                 torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
+        t = time_launches(torch, lambda i: hip_ops.local_ent_quant(sets[i % nrot][0], sets[i % nrot][1], rope,
+                                                                   sets[i % nrot][2], bias, W, 0.08, 0.2), 100)
+        # q, k, states in; int8 codes + scale + rowsum of tanh(E) and C out
+        nbytes = Bs * Ls * (2 * R * 2 + D * 2 + 2 * (D + 8))
+        res["local_ent_quant_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
+                                        "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes,
+                                        "rotating_buffers": nrot}
+        del sets
     return res
 
 
