@@ -440,7 +440,8 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.R >= 2 && a.R % 2 == 0, kErrInvalidArg, "local_ent: ent_rank must be even (RoPE halves)");
   TESM_REQUIRE(a.W >= 1 && a.W <= 64, kErrUnsupported, "local_ent: window must be in [1, 64]");
   if (a.B == 0 || a.L == 0) return kOk;
-  TESM_REQUIRE(a.q && a.k && a.rope && a.bias && a.S && a.wts, kErrInvalidArg, "local_ent: null pointer");
+  TESM_REQUIRE(a.q && a.k && a.rope && a.bias && a.S, kErrInvalidArg, "local_ent: null pointer");
+  TESM_REQUIRE(a.q_te || a.wts, kErrWorkspace, "local_ent: missing window-weight workspace");
   TESM_REQUIRE(a.ld_q >= a.H * a.R && a.ld_k >= a.H * a.R && a.ld_s >= a.H * a.D, kErrInvalidArg, "local_ent: bad ld");
   TESM_REQUIRE(!a.q_add || a.ld_qadd >= a.H * a.R, kErrInvalidArg, "local_ent: bad ld_qadd");
   TESM_REQUIRE(!(a.avg || a.e_tanh || a.c_out || a.e_out) || a.ld_out >= a.H * a.D, kErrInvalidArg,
