@@ -221,8 +221,10 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const v4i bf = unpack_frag(bw[j]);
+        // weights as the MFMA's A operand: the accumulator comes out transposed, so each lane holds
+        // 4 consecutive output columns of one row (vector stores in the epilogue)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf, acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[i], acc[i][j], 0, 0, 0);
       }
     }
     if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * C::STAGE);
@@ -243,7 +245,53 @@ __device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, 
   tn = tile - tm * ntn;
 }
 
-// Accumulator layout of v_mfma_i32_16x16x64_i8: lane L, element r -> row 4*(L/16) + r, column L%16.
+// With the weights as the A operand, element r of lane L's accumulator is output row L%16 and
+// output column 4*(L/16) + r of the 16 x 16 tile.
+template <int OUT_DT>
+__device__ __forceinline__ void store4(void* out, int64_t idx, const float (&v)[4], bool vec) {
+  if (vec) {
+    if constexpr (OUT_DT == kBF16) {
+      const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+      const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + idx) = make_uint2(lo, hi);
+    } else {
+      *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st<OUT_DT>(out, idx + r, v[r]);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void load4(const void* p, int64_t idx, bool vec, float (&v)[4]) {
+  if (vec) {
+    if constexpr (DT == kBF16) {
+      const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + idx);
+      v[0] = __uint_as_float(w.x << 16);
+      v[1] = __uint_as_float(w.x & 0xffff0000u);
+      v[2] = __uint_as_float(w.y << 16);
+      v[3] = __uint_as_float(w.y & 0xffff0000u);
+    } else {
+      const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + idx);
+      v[0] = f.x;
+      v[1] = f.y;
+      v[2] = f.z;
+      v[3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = ld<DT>(p, idx + r);
+  }
+}
+
+// 4-element vector access at element (m * ld + n) is aligned for every m and every n % 4 == 0.
+template <int DT>
+__device__ __forceinline__ bool vec4_ok(const void* p, int64_t ld) {
+  constexpr int64_t bytes = DT == kBF16 ? 8 : 16;
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (DT == kBF16 ? 2 : 4)) % bytes == 0;
+}
+
 template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
 __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   using C = Cfg<WM, WN, TM, TN>;
@@ -267,46 +315,61 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   const int wm = w / WN, wn = w % WN;
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
+  const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+  bool vin = false;
+  if constexpr (EPI == kEpiOutputGate) vin = vec4_ok<OUT_DT>(a.local, a.ld_local) && vec4_ok<OUT_DT>(a.gate, a.ld_gate);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    int64_t mr[4];
-    float inv0[4], inv1[4];
-    int32_t rs0[4], rs1[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      mr[r] = m0 + (wm * TM + i) * 16 + 4 * (lane >> 4) + r;
-      const bool ok = mr[r] < a.M;
-      inv0[r] = ok ? 1.0f / o0.s_x[mr[r]] : 0.0f;
-      rs0[r] = ok ? o0.rowsum[mr[r]] : 0;
-      if constexpr (EPI == kEpiOutputGate) {
-        inv1[r] = ok ? 1.0f / o1.s_x[mr[r]] : 0.0f;
-        rs1[r] = ok ? o1.rowsum[mr[r]] : 0;
-      }
+    const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
+    if (m >= a.M) continue;
+    const float inv0 = 1.0f / o0.s_x[m];
+    const int32_t rs0 = o0.rowsum[m];
+    float inv1 = 0.0f;
+    int32_t rs1 = 0;
+    if constexpr (EPI == kEpiOutputGate) {
+      inv1 = 1.0f / o1.s_x[m];
+      rs1 = o1.rowsum[m];
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + (wn * TN + j) * 16 + (lane & 15);
-      if (n >= a.N) continue;
-      const float cw0 = o0.c_w_per_row ? o0.c_w[n] : o0.c_w[0];
-      float cw1 = 0.0f;
-      if constexpr (EPI == kEpiOutputGate) cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
+      const int64_t nb = n0 + (wn * TN + j) * 16 + 4 * (lane >> 4);
+      if (nb >= a.N) continue;
+      const bool full = nb + 3 < a.N;
+      float v[4], lo[4], gt[4];
+      if constexpr (EPI == kEpiOutputGate) {
+        if (full) {
+          load4<OUT_DT>(a.local, m * a.ld_local + nb, vin, lo);
+          load4<OUT_DT>(a.gate, m * a.ld_gate + nb, vin, gt);
+        } else {
+          for (int r = 0; r < 4; ++r) {
+            lo[r] = nb + r < a.N ? ld<OUT_DT>(a.local, m * a.ld_local + nb + r) : 0.0f;
+            gt[r] = nb + r < a.N ? ld<OUT_DT>(a.gate, m * a.ld_gate + nb + r) : 0.0f;
+          }
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t m = mr[r];
-        if (m >= a.M) continue;
-        const int32_t a0 = acc0[i][j][r] - rs0[r];
+        const int64_t n = nb + r;
+        v[r] = 0.0f;
+        if (n >= a.N) continue;
+        const float cw0 = o0.c_w_per_row ? o0.c_w[n] : o0.c_w[0];
+        const int32_t a0 = acc0[i][j][r] - rs0;
         if (a.acc_dump) a.acc_dump[m * a.N + n] = a0;
-        const float v0 = (static_cast<float>(a0) * inv0[r]) * cw0;
+        const float v0 = (static_cast<float>(a0) * inv0) * cw0;
         if constexpr (EPI == kEpiStore) {
-          store_plain<OUT_DT>(a, m, n, v0);
+          v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n) : v0;
         } else {
+          const float cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
           const float sp = rnd<OUT_DT>(v0);
-          const float ep = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1[r]) * inv1[r]) * cw1);
-          const float gt = rnd<OUT_DT>(sigmoidf_(ld<OUT_DT>(a.gate, m * a.ld_gate + n)));
-          const float lo = ld<OUT_DT>(a.local, m * a.ld_local + n);
-          const float y = rnd<OUT_DT>(lo + rnd<OUT_DT>(gt * sp));
-          st<OUT_DT>(a.out, m * a.ldo + n, y + ep);
+          const float ep = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1) * inv1) * cw1);
+          const float g = rnd<OUT_DT>(sigmoidf_(gt[r]));
+          v[r] = rnd<OUT_DT>(rnd<OUT_DT>(lo[r] + rnd<OUT_DT>(g * sp)) + ep);
         }
+      }
+      if (full) {
+        store4<OUT_DT>(a.out, m * a.ldo + nb, v, vout);
+      } else {
+        for (int r = 0; r < 4 && nb + r < a.N; ++r) st<OUT_DT>(a.out, m * a.ldo + nb + r, v[r]);
       }
     }
   }
@@ -329,8 +392,9 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
   const int64_t col0 = static_cast<int64_t>(w) * NCT * 16;
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
-  const int64_t ma = m0 + (lane & 15);
-  const bool mok = ma < a.M;
+  const int row = lane & 15;            // the activation row this lane feeds and the output row it holds
+  const int64_t m = m0 + row;
+  const bool mok = m < a.M;
   const int64_t nks = a.Kp / 64;
 
   for (int64_t i = tid; i < 16 * o.ldq / 16; i += 256) reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
@@ -345,8 +409,8 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
   uint32_t bw0[NCT], bw1[NCT], nb0[NCT], nb1[NCT];
   auto load = [&](int64_t ks, v4i& r0, v4i& r1, uint32_t (&w0)[NCT], uint32_t (&w1)[NCT]) {
     const int64_t ko = 64 * ks + 16 * (lane >> 4);
-    r0 = mok ? *reinterpret_cast<const v4i*>(o0.q + ma * o0.ldq + ko) : v4i{0, 0, 0, 0};
-    r1 = mok ? *reinterpret_cast<const v4i*>(o1.q + ma * o1.ldq + ko) : v4i{0, 0, 0, 0};
+    r0 = mok ? *reinterpret_cast<const v4i*>(o0.q + m * o0.ldq + ko) : v4i{0, 0, 0, 0};
+    r1 = mok ? *reinterpret_cast<const v4i*>(o1.q + m * o1.ldq + ko) : v4i{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < NCT; ++j) {
       const int64_t n = col0 + 16 * j + (lane & 15);
@@ -359,8 +423,8 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
     if (ks + 1 < nks) load(ks + 1, na0, na1, nb0, nb1);
 #pragma unroll
     for (int j = 0; j < NCT; ++j) {
-      acc0[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa0, unpack_frag(bw0[j]), acc0[j], 0, 0, 0);
-      acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa1, unpack_frag(bw1[j]), acc1[j], 0, 0, 0);
+      acc0[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(bw0[j]), xa0, acc0[j], 0, 0, 0);
+      acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(bw1[j]), xa1, acc1[j], 0, 0, 0);
     }
     if (ks + 1 < nks) {
       xa0 = na0;
@@ -373,85 +437,86 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
     }
   }
 
-  // epilogue: y in registers, then the per-row amax across the 4 waves
-  float y[NCT][4];
-  float inv0[4], inv1[4];
-  int32_t rs0[4], rs1[4];
-  int64_t mr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mr[r] = m0 + 4 * (lane >> 4) + r;
-    const bool ok = mr[r] < a.M;
-    inv0[r] = ok ? 1.0f / o0.s_x[mr[r]] : 0.0f;
-    inv1[r] = ok ? 1.0f / o1.s_x[mr[r]] : 0.0f;
-    rs0[r] = ok ? o0.rowsum[mr[r]] : 0;
-    rs1[r] = ok ? o1.rowsum[mr[r]] : 0;
-  }
+  // epilogue: lane holds row m, columns col0 + 16j + 4*(lane/16) + r
+  const float inv0 = mok ? 1.0f / o0.s_x[m] : 0.0f, inv1 = mok ? 1.0f / o1.s_x[m] : 0.0f;
+  const int32_t rs0 = mok ? o0.rowsum[m] : 0, rs1 = mok ? o1.rowsum[m] : 0;
   const float cws0 = o0.c_w[0], cws1 = o1.c_w[0];
-  float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const bool vin = vec4_ok<DT>(a.local, a.ld_local) && vec4_ok<DT>(a.gate, a.ld_gate);
+  float y[NCT][4];
+  float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < NCT; ++j) {
-    const int64_t n = col0 + 16 * j + (lane & 15);
-    const float cw0 = o0.c_w_per_row ? (n < a.N ? o0.c_w[n] : 0.0f) : cws0;
-    const float cw1 = o1.c_w_per_row ? (n < a.N ? o1.c_w[n] : 0.0f) : cws1;
+    const int64_t nb = col0 + 16 * j + 4 * (lane >> 4);
+    float lo[4], gt[4];
+    const bool full = nb + 3 < a.N;
+    if (mok && full) {
+      load4<DT>(a.local, m * a.ld_local + nb, vin, lo);
+      load4<DT>(a.gate, m * a.ld_gate + nb, vin, gt);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = mok && nb + r < a.N;
+        lo[r] = ok ? ld<DT>(a.local, m * a.ld_local + nb + r) : 0.0f;
+        gt[r] = ok ? ld<DT>(a.gate, m * a.ld_gate + nb + r) : 0.0f;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      const int64_t n = nb + r;
       y[j][r] = 0.0f;
-      const int64_t m = mr[r];
-      if (m >= a.M || n >= a.N) continue;
-      const float sp = rnd<DT>((static_cast<float>(acc0[j][r] - rs0[r]) * inv0[r]) * cw0);
-      const float ep = rnd<DT>((static_cast<float>(acc1[j][r] - rs1[r]) * inv1[r]) * cw1);
-      const float gt = rnd<DT>(sigmoidf_(ld<DT>(a.gate, m * a.ld_gate + n)));
-      const float lo = ld<DT>(a.local, m * a.ld_local + n);
-      const float v = rnd<DT>(rnd<DT>(lo + rnd<DT>(gt * sp)) + ep);
+      if (!mok || n >= a.N) continue;
+      const float cw0 = o0.c_w_per_row ? o0.c_w[n] : cws0;
+      const float cw1 = o1.c_w_per_row ? o1.c_w[n] : cws1;
+      const float sp = rnd<DT>((static_cast<float>(acc0[j][r] - rs0) * inv0) * cw0);
+      const float ep = rnd<DT>((static_cast<float>(acc1[j][r] - rs1) * inv1) * cw1);
+      const float g = rnd<DT>(sigmoidf_(gt[r]));
+      const float v = rnd<DT>(rnd<DT>(lo[r] + rnd<DT>(g * sp)) + ep);
       y[j][r] = v;
-      mx[r] = fmaxf(mx[r], fabsf(v));
-      if (o.y) st<DT>(o.y, m * o.ldy + n, v);
+      mx = fmaxf(mx, fabsf(v));
+    }
+    if (o.y && mok) {
+      if (full) {
+        store4<DT>(o.y, m * o.ldy + nb, y[j], vec4_ok<DT>(o.y, o.ldy));
+      } else {
+        for (int r = 0; r < 4 && nb + r < a.N; ++r) st<DT>(o.y, m * o.ldy + nb + r, y[j][r]);
+      }
     }
   }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mx[r] = wave_max<16>(mx[r]);
-    if ((lane & 15) == 0) red[(4 * (lane >> 4) + r) * 4 + w] = mx[r];
-  }
+  // row max over the 4 lanes sharing the row, then over the 4 waves
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (lane < 16) red[row * 4 + w] = mx;
   __syncthreads();
-  float sc[4];
-  int sum[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float* rr = red + (4 * (lane >> 4) + r) * 4;
-    sc[r] = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
-  }
+  const float* rr = red + row * 4;
+  const float sc = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
+  int sum = 0;
 #pragma unroll
   for (int j = 0; j < NCT; ++j) {
-    const int64_t n = col0 + 16 * j + (lane & 15);
-    if (n >= a.N) continue;
-    const int64_t pos = (n & ~15) + layout1_pos(static_cast<int>(n & 15));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (mr[r] >= a.M) continue;
-      const int q = act_code<DT>(y[j][r], sc[r]);
-      codes[(4 * (lane >> 4) + r) * o.ldq + pos] = static_cast<int8_t>(q);
-      sum[r] += q;
+      const int64_t n = col0 + 16 * j + 4 * (lane >> 4) + r;
+      if (!mok || n >= a.N) continue;
+      const int q = act_code<DT>(y[j][r], sc);
+      // layout 1: element e = n % 16 = 4 * (lane / 16) + r sits at byte 4 * r + lane / 16 of its group
+      codes[row * o.ldq + (n & ~static_cast<int64_t>(15)) + 4 * r + (lane >> 4)] = static_cast<int8_t>(q);
+      sum += q;
     }
   }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    sum[r] = wave_sum_i<16>(sum[r]);
-    if ((lane & 15) == 0) redi[(4 * (lane >> 4) + r) * 4 + w] = sum[r];
-  }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  if (lane < 16) redi[row * 4 + w] = sum;
   __syncthreads();
   if (tid < 16 && m0 + tid < a.M) {
-    const float* rr = red + tid * 4;
     const int32_t* ri = redi + tid * 4;
-    o.s[m0 + tid] = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
+    const float* rm = red + tid * 4;
+    o.s[m0 + tid] = act_scale<DT>(fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3])), o.eps);
     o.rs[m0 + tid] = (ri[0] + ri[1]) + (ri[2] + ri[3]);
   }
   const int64_t chunks = o.ldq / 16;
-  for (int64_t i = tid; i < 16 * chunks; i += 256) {
-    const int64_t r = i / chunks, ck = i - r * chunks;
+  for (int r = w; r < 16; r += 4) {
     if (m0 + r >= a.M) continue;
-    *reinterpret_cast<uint4*>(o.q + (m0 + r) * o.ldq + 16 * ck) = reinterpret_cast<const uint4*>(codes + r * o.ldq)[ck];
+    for (int64_t ck = lane; ck < chunks; ck += 64)
+      reinterpret_cast<uint4*>(o.q + (m0 + r) * o.ldq)[ck] = reinterpret_cast<const uint4*>(codes + r * o.ldq)[ck];
   }
 }
 

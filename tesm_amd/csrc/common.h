@@ -70,9 +70,34 @@ __device__ __forceinline__ void st(void* p, int64_t i, float v) {
 }
 
 // ---------------------------------------------------------------------------
-// transcendental helpers (IEEE float32 in, float32 out; libm-accurate ocml calls)
+// Branch-free float32 transcendentals for the gates (a few ulp; every result that the reference
+// rounds to bf16 is rounded again afterwards).  Built on the hardware exp2 / reciprocal.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// e^x = 2^(x log2 e), with x * log2 e split into a rounded product and its error term so that
+// the argument error stays below an ulp of 2^t for |x| up to ~88.
+__device__ __forceinline__ float fast_exp(float x) {
+  constexpr float kL2e = 1.44269504088896340736f;
+  const float t = x * kL2e;
+  const float err = __builtin_fmaf(x, kL2e, -t) + x * 1.925963033500e-8f;  // log2(e) - kL2e
+  const float r = __builtin_amdgcn_exp2f(t);
+  return __builtin_fmaf(r, err * 0.69314718055994531f, r);
+}
+
+// 1 / (1 + e^-x); saturates to 0 / 1 without NaN for large |x|.
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + fast_exp(-x)); }
+
+// tanh: odd Taylor polynomial below |x| = 0.25 (truncation < 1e-8 relative), otherwise
+// sign(x) * (1 - 2 / (e^{2|x|} + 1)).
+__device__ __forceinline__ float tanhf_(float x) {
+  const float ax = fabsf(x);
+  const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(fast_exp(2.0f * ax) + 1.0f);
+  const float x2 = x * x;
+  float p = __builtin_fmaf(x2, 62.0f / 2835.0f, -17.0f / 315.0f);
+  p = __builtin_fmaf(x2, p, 2.0f / 15.0f);
+  p = __builtin_fmaf(x2, p, -1.0f / 3.0f);
+  const float small = __builtin_fmaf(x * x2, p, x);
+  return ax < 0.25f ? small : __builtin_copysignf(big, x);
+}
 
 // ---------------------------------------------------------------------------
 // per-token int8 activation quantization (reference tesm.py:206-209)

@@ -153,235 +153,273 @@ __global__ __launch_bounds__(256) void ent_mix_kernel(EntArgs a, int64_t weff) {
     if (a.avg) st<DT>(a.avg, o, avg);
     if (a.e_out) st<DT>(a.e_out, o, e);
     if (a.c_out) st<DT>(a.c_out, o, e - s);
-    if (a.e_tanh) st<DT>(a.e_tanh, o, tanhf(e));
+    if (a.e_tanh) st<DT>(a.e_tanh, o, tanhf_(e));
   }
 }
 
 // ---------------------------------------------------------------------------
 // Fused SISO kernel: a workgroup per (batch row, kFusedTP positions) with all D channels, so the
-// per-token quantization of tanh(E) and C happens in place.  The arithmetic of each value is the
-// same sequence of float operations as in ent_scores_kernel + ent_mix_kernel.
+// per-token quantization of tanh(E) and C happens in place.  Thread (p, g) owns position p and
+// 16-channel groups g, g + 16, ...: its window weights, window sums, mix and the 16 int8 codes of
+// a group (one 16-byte store) stay in registers; row maxima and code sums reduce over the 16
+// lanes of a position.  Every value is the same sequence of float operations as in
+// ent_scores_kernel + ent_mix_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kFusedTP = 16;
-constexpr int kFusedMaxCPD = 2;  // channels per thread: D <= 512
+constexpr int kFusedMaxGPT = 2;  // channel groups per thread: D <= 16 * 16 * 2 = 512
 
 struct FusedLds {
-  int64_t kr, qr, wt, wn, sx, red, total;  // byte offsets
-  int64_t krs;                             // row stride of kr / qr in floats (R + 1: no bank conflicts)
+  int64_t kr, qr, wn, sx, total;  // byte offsets
+  int64_t krs;                    // row stride of kr / qr in floats
+  int64_t dp;                     // row stride of sx in elements (D rounded up to 16)
 };
 
-__host__ __device__ inline FusedLds fused_lds(int64_t R, int64_t D, int64_t weff, int64_t ldq, int esz) {
+__host__ __device__ inline FusedLds fused_lds(int64_t R, int64_t D, int64_t weff, int esz) {
   FusedLds f;
   const int64_t rows = kFusedTP + weff - 1;
-  f.krs = R + 1;
+  f.krs = R + 4;
+  f.dp = (D + 15) / 16 * 16;
   f.kr = 0;
   f.qr = f.kr + rows * f.krs * 4;
-  const int64_t scores_end = f.qr + kFusedTP * f.krs * 4;
-  const int64_t codes_end = 2 * kFusedTP * ldq;  // code staging reuses the kr/qr region
-  int64_t off = ((scores_end > codes_end ? scores_end : codes_end) + 15) / 16 * 16;
-  f.wt = off;
-  off += kFusedTP * weff * 4;
-  f.wn = off;
-  off += kFusedTP * weff * 4;
-  f.red = off;
-  off += 2 * 2 * kFusedTP * 4 * 4;  // [amax|sum][te|c][TP][4 waves]
-  off = (off + 15) / 16 * 16;
-  f.sx = off;
-  off += rows * D * esz;
-  f.total = (off + 15) / 16 * 16;
+  f.wn = f.qr + kFusedTP * f.krs * 4;
+  f.sx = (f.wn + kFusedTP * weff * 4 + 15) / 16 * 16;
+  f.total = (f.sx + rows * f.dp * esz + 15) / 16 * 16;
   return f;
+}
+
+// 16 channels of one staged state row as floats.
+template <int DT>
+__device__ __forceinline__ void lds_row16(const void* base, float (&x)[16]) {
+  if constexpr (DT == kBF16) {
+    const uint4 a = reinterpret_cast<const uint4*>(base)[0], b = reinterpret_cast<const uint4*>(base)[1];
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 v = reinterpret_cast<const float4*>(base)[i];
+      x[4 * i] = v.x;
+      x[4 * i + 1] = v.y;
+      x[4 * i + 2] = v.z;
+      x[4 * i + 3] = v.w;
+    }
+  }
 }
 
 template <int DT>
 __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff, FusedLds f) {
   using T = typename Elem<DT>::T;
   extern __shared__ __attribute__((aligned(16))) char lds_fused[];
-  char* lds = lds_fused;
-  float* kr = reinterpret_cast<float*>(lds + f.kr);
-  float* qr = reinterpret_cast<float*>(lds + f.qr);
-  float* wt = reinterpret_cast<float*>(lds + f.wt);
-  float* wn = reinterpret_cast<float*>(lds + f.wn);
-  float* red = reinterpret_cast<float*>(lds + f.red);
-  T* sx = reinterpret_cast<T*>(lds + f.sx);
-  int8_t* codes = reinterpret_cast<int8_t*>(lds);  // after the scores: [2][TP][ldq]
+  float* kr = reinterpret_cast<float*>(lds_fused + f.kr);
+  float* qr = reinterpret_cast<float*>(lds_fused + f.qr);
+  float* wn = reinterpret_cast<float*>(lds_fused + f.wn);
+  T* sx = reinterpret_cast<T*>(lds_fused + f.sx);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.y;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kFusedTP;
-  const int64_t half = a.R / 2, R = a.R, D = a.D;
-  const int64_t rows = kFusedTP + weff - 1;
-  const int64_t tk0 = t0 - (weff - 1);  // position of key row 0
+  const int half = static_cast<int>(a.R / 2), D = static_cast<int>(a.D), W = static_cast<int>(weff);
+  const int krs = static_cast<int>(f.krs), dp = static_cast<int>(f.dp);
+  const int rows = kFusedTP + W - 1;
+  const int64_t tk0 = t0 - (W - 1);  // position of key row 0
 
-  // 1. RoPE'd keys and queries (tesm.py:783-793, 1209-1218)
-  for (int64_t i = tid; i < rows * half; i += 256) {
-    const int64_t r = i / half, c = i - r * half;
+  // 1. RoPE'd keys and queries (tesm.py:783-793, 1209-1218): rows over waves, pairs over lanes
+  for (int r = wave; r < rows; r += 4) {
     const int64_t t = tk0 + r;
-    float o1 = 0.0f, o2 = 0.0f;
-    if (t >= 0 && t < a.L) {
-      const int64_t ko = (b * a.L + t) * a.ld_k;
-      rope_pair<DT>(ld<DT>(a.k, ko + c), ld<DT>(a.k, ko + half + c), a.rope[t * half + c], o1, o2);
+    const bool ok = t >= 0 && t < a.L;
+    const int64_t ko = (b * a.L + t) * a.ld_k;
+    for (int c = lane; c < half; c += 64) {
+      float o1 = 0.0f, o2 = 0.0f;
+      if (ok) rope_pair<DT>(ld<DT>(a.k, ko + c), ld<DT>(a.k, ko + half + c), a.rope[t * half + c], o1, o2);
+      kr[r * krs + c] = o1;
+      kr[r * krs + half + c] = o2;
     }
-    kr[r * f.krs + c] = o1;
-    kr[r * f.krs + half + c] = o2;
   }
-  for (int64_t i = tid; i < kFusedTP * half; i += 256) {
-    const int64_t p = i / half, c = i - p * half;
+  for (int p = wave; p < kFusedTP; p += 4) {
     const int64_t t = t0 + p;
-    float o1 = 0.0f, o2 = 0.0f;
-    if (t < a.L) {
-      const int64_t qo = (b * a.L + t) * a.ld_q;
-      rope_pair<DT>(ld<DT>(a.q, qo + c), ld<DT>(a.q, qo + half + c), a.rope[t * half + c], o1, o2);
-      if (a.q_add) {
-        const int64_t ao = (b * a.L + t) * a.ld_qadd;
-        o1 = rnd<DT>(o1 + ld<DT>(a.q_add, ao + c));
-        o2 = rnd<DT>(o2 + ld<DT>(a.q_add, ao + half + c));
+    const bool ok = t < a.L;
+    const int64_t qo = (b * a.L + t) * a.ld_q;
+    const int64_t ao = (b * a.L + t) * a.ld_qadd;
+    for (int c = lane; c < half; c += 64) {
+      float o1 = 0.0f, o2 = 0.0f;
+      if (ok) {
+        rope_pair<DT>(ld<DT>(a.q, qo + c), ld<DT>(a.q, qo + half + c), a.rope[t * half + c], o1, o2);
+        if (a.q_add) {
+          o1 = rnd<DT>(o1 + ld<DT>(a.q_add, ao + c));
+          o2 = rnd<DT>(o2 + ld<DT>(a.q_add, ao + half + c));
+        }
       }
+      qr[p * krs + c] = o1;
+      qr[p * krs + half + c] = o2;
     }
-    qr[p * f.krs + c] = o1;
-    qr[p * f.krs + half + c] = o2;
   }
-  // 2. state halo rows, raw dtype
+  // 2. state halo rows in the raw dtype, channels padded with zeros to a multiple of 16
   const T* S = static_cast<const T*>(a.S);
-  for (int64_t i = tid; i < rows * D; i += 256) {
-    const int64_t r = i / D, c = i - r * D;
+  constexpr int kVec = 16 / sizeof(T);
+  const bool vec = (D % kVec) == 0 && (a.ld_s % kVec) == 0 && (reinterpret_cast<uintptr_t>(S) % 16) == 0;
+  for (int r = wave; r < rows; r += 4) {
     const int64_t t = tk0 + r;
-    sx[i] = (t >= 0 && t < a.L) ? S[(b * a.L + t) * a.ld_s + c] : T(0);
+    const bool ok = t >= 0 && t < a.L;
+    const T* src = S + (b * a.L + t) * a.ld_s;
+    T* dst = sx + static_cast<int64_t>(r) * dp;
+    if (vec) {
+      for (int c = lane * kVec; c < dp; c += 64 * kVec)
+        *reinterpret_cast<uint4*>(dst + c) =
+            (ok && c < D) ? *reinterpret_cast<const uint4*>(src + c) : make_uint4(0, 0, 0, 0);
+    } else {
+      for (int c = lane; c < dp; c += 64) dst[c] = (ok && c < D) ? src[c] : T(0);
+    }
   }
   __syncthreads();
 
-  // 3. window scores and ternary decisions (same float sequence as ent_scores_kernel)
-  const float sq = static_cast<float>(sqrt(static_cast<double>(R)));
-  for (int64_t i = tid; i < kFusedTP * weff; i += 256) {
-    const int64_t p = i / weff, w = i - p * weff;
-    const int64_t t = t0 + p, j = t - (weff - 1) + w;
-    float tern = 0.0f;
-    if (t < a.L && j >= 0) {
-      const float* qp = qr + p * f.krs;
-      const float* kp = kr + (p + w) * f.krs;
-      float dot = 0.0f;
-      for (int64_t c = 0; c < half; ++c) {
-        dot += qp[c] * kp[c];
-        dot += qp[half + c] * kp[half + c];
-      }
-      float s = rnd<DT>(rnd<DT>(dot) / sq);
-      s = rnd<DT>(s + a.bias[a.W - weff + w]);
-      tern = s > a.thr ? 1.0f : (s < -a.thr ? -1.0f : 0.0f);
-    }
-    wt[i] = tern;
-    if (a.tern && t < a.L) a.tern[(b * a.L + t) * weff + w] = static_cast<int8_t>(tern);
-  }
-  __syncthreads();
-  for (int64_t i = tid; i < kFusedTP * weff; i += 256) {
-    const int64_t p = i / weff;
+  const int p = tid >> 4, g0 = tid & 15;
+  const int64_t t = t0 + p;
+  const bool tok = t < a.L;
+  // 3. window scores, ternary decisions and their normalisation (ent_scores_kernel arithmetic)
+  {
+    const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
+    // float4 LDS reads need 16-byte aligned rows and halves: R % 8 == 0 (krs = R + 4)
+    const int half4 = (half % 4 == 0) ? half : 0;
+    float tern[4];  // W <= 64: slots w0, w0 + 16, ...
     float n = 0.0f;
-    for (int64_t w = 0; w < weff; ++w) n += fabsf(wt[p * weff + w]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = g0 + 16 * i;
+      tern[i] = 0.0f;
+      if (w >= W) continue;
+      const int64_t j = t - (W - 1) + w;
+      if (tok && j >= 0) {
+        const float* qp = qr + p * krs;
+        const float* kp = kr + (p + w) * krs;
+        float dot = 0.0f;
+        for (int c = 0; c < half4; c += 4) {
+          const float4 qa = *reinterpret_cast<const float4*>(qp + c);
+          const float4 ka = *reinterpret_cast<const float4*>(kp + c);
+          const float4 qb = *reinterpret_cast<const float4*>(qp + half + c);
+          const float4 kb = *reinterpret_cast<const float4*>(kp + half + c);
+          dot += qa.x * ka.x;
+          dot += qb.x * kb.x;
+          dot += qa.y * ka.y;
+          dot += qb.y * kb.y;
+          dot += qa.z * ka.z;
+          dot += qb.z * kb.z;
+          dot += qa.w * ka.w;
+          dot += qb.w * kb.w;
+        }
+        for (int c = half4; c < half; ++c) {
+          dot += qp[c] * kp[c];
+          dot += qp[half + c] * kp[half + c];
+        }
+        float sc = rnd<DT>(rnd<DT>(dot) / sq);
+        sc = rnd<DT>(sc + a.bias[a.W - W + w]);
+        tern[i] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
+      }
+      n += fabsf(tern[i]);
+      if (a.tern && tok) a.tern[(b * a.L + t) * W + w] = static_cast<int8_t>(tern[i]);
+    }
+    n = wave_sum_f<16>(n);
     n = fmaxf(n, 1.0f);
-    wn[i] = rnd<DT>(wt[i] / n);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = g0 + 16 * i;
+      if (w < W) wn[p * W + w] = rnd<DT>(tern[i] / n);
+    }
   }
-  // zero the code staging area (it overlays kr/qr, free after the scores)
-  for (int64_t i = tid; i < 2 * kFusedTP * a.ldq / 16; i += 256)
-    reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
   __syncthreads();
 
-  // 4. window average, mix, tanh (ent_mix_kernel arithmetic), held in registers
-  float te[kFusedTP][kFusedMaxCPD], cc[kFusedTP][kFusedMaxCPD];
-  float mx_te[kFusedTP], mx_c[kFusedTP];
+  // 4. window sums, mix and tanh for the thread's channel groups (ent_mix_kernel arithmetic)
+  const int groups = dp / 16;
+  float tv[kFusedMaxGPT][16], cv[kFusedMaxGPT][16];
+  float mx_t = 0.0f, mx_c = 0.0f;
 #pragma unroll
-  for (int p = 0; p < kFusedTP; ++p) {
-    mx_te[p] = 0.0f;
-    mx_c[p] = 0.0f;
+  for (int gi = 0; gi < kFusedMaxGPT; ++gi) {
+    const int g = g0 + 16 * gi;
 #pragma unroll
-    for (int jj = 0; jj < kFusedMaxCPD; ++jj) {
-      te[p][jj] = 0.0f;
-      cc[p][jj] = 0.0f;
-      const int64_t c = tid + 256 * jj;
-      const int64_t t = t0 + p;
-      if (c >= D || t >= a.L) continue;
-      float acc = 0.0f;
-      for (int64_t w = 0; w < weff; ++w) acc += wn[p * weff + w] * ld<DT>(sx, (p + w) * D + c);
-      const float avg = rnd<DT>(acc);
-      const float s = ld<DT>(sx, (p + weff - 1) * D + c);
-      const float e = rnd<DT>(s + rnd<DT>(a.ent_scale * rnd<DT>(avg - s)));
-      const float cv = rnd<DT>(e - s);
-      const float tv = rnd<DT>(tanhf(e));
-      const int64_t o = (b * a.L + t) * a.ld_out + c;
-      if (a.avg) st<DT>(a.avg, o, avg);
-      if (a.e_out) st<DT>(a.e_out, o, e);
-      if (a.c_out) st<DT>(a.c_out, o, cv);
-      if (a.e_tanh) st<DT>(a.e_tanh, o, tv);
-      te[p][jj] = tv;
-      cc[p][jj] = cv;
-      mx_te[p] = fmaxf(mx_te[p], fabsf(tv));
-      mx_c[p] = fmaxf(mx_c[p], fabsf(cv));
+    for (int e = 0; e < 16; ++e) {
+      tv[gi][e] = 0.0f;
+      cv[gi][e] = 0.0f;
     }
-  }
-  // 5. per-token scales (tesm.py:206-209) over the D channels of the workgroup
+    if (g >= groups || !tok) continue;
+    float acc[16];
 #pragma unroll
-  for (int p = 0; p < kFusedTP; ++p) {
-    const float m1 = wave_max(mx_te[p]), m2 = wave_max(mx_c[p]);
-    if (lane == 0) {
-      red[(0 * kFusedTP + p) * 4 + wave] = m1;
-      red[(1 * kFusedTP + p) * 4 + wave] = m2;
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    for (int w = 0; w < W; ++w) {
+      float x[16];
+      lds_row16<DT>(sx + static_cast<int64_t>(p + w) * dp + 16 * g, x);
+      const float wt = wn[p * W + w];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] += wt * x[e];
     }
-  }
-  __syncthreads();
-  float sc_te[kFusedTP], sc_c[kFusedTP];
+    float sv[16];
+    lds_row16<DT>(sx + static_cast<int64_t>(p + W - 1) * dp + 16 * g, sv);
 #pragma unroll
-  for (int p = 0; p < kFusedTP; ++p) {
-    const float* r0 = red + (0 * kFusedTP + p) * 4;
-    const float* r1 = red + (1 * kFusedTP + p) * 4;
-    sc_te[p] = act_scale<DT>(fmaxf(fmaxf(r0[0], r0[1]), fmaxf(r0[2], r0[3])), a.eps);
-    sc_c[p] = act_scale<DT>(fmaxf(fmaxf(r1[0], r1[1]), fmaxf(r1[2], r1[3])), a.eps);
-  }
-  // 6. codes into the staging rows, row sums of the codes
-  int32_t* redi = reinterpret_cast<int32_t*>(red + 2 * kFusedTP * 4);
-  __syncthreads();  // everyone has read red[] before it is reused for the sums
-#pragma unroll
-  for (int p = 0; p < kFusedTP; ++p) {
-    int s1 = 0, s2 = 0;
-#pragma unroll
-    for (int jj = 0; jj < kFusedMaxCPD; ++jj) {
-      const int64_t c = tid + 256 * jj;
-      if (c >= D || t0 + p >= a.L) continue;
-      const int q1 = act_code<DT>(te[p][jj], sc_te[p]);
-      const int q2 = act_code<DT>(cc[p][jj], sc_c[p]);
-      const int64_t pos = (c & ~15) + layout1_pos(static_cast<int>(c & 15));
-      codes[(0 * kFusedTP + p) * a.ldq + pos] = static_cast<int8_t>(q1);
-      codes[(1 * kFusedTP + p) * a.ldq + pos] = static_cast<int8_t>(q2);
-      s1 += q1;
-      s2 += q2;
-    }
-    s1 = wave_sum_i(s1);
-    s2 = wave_sum_i(s2);
-    if (lane == 0) {
-      redi[(0 * kFusedTP + p) * 4 + wave] = s1;
-      redi[(1 * kFusedTP + p) * 4 + wave] = s2;
-    }
-  }
-  __syncthreads();
-  if (tid < 2 * kFusedTP) {
-    const int which = tid / kFusedTP, p = tid % kFusedTP;
-    const int64_t t = t0 + p;
-    if (t < a.L) {
-      const int32_t* r = redi + (which * kFusedTP + p) * 4;
-      const int64_t row = b * a.L + t;
-      if (which == 0) {
-        a.s_te[row] = sc_te[p];
-        a.rs_te[row] = (r[0] + r[1]) + (r[2] + r[3]);
-      } else {
-        a.s_c[row] = sc_c[p];
-        a.rs_c[row] = (r[0] + r[1]) + (r[2] + r[3]);
+    for (int e = 0; e < 16; ++e) {
+      const int c = 16 * g + e;
+      if (c >= D) continue;
+      const float avg = rnd<DT>(acc[e]);
+      const float s = sv[e];
+      const float ev = rnd<DT>(s + rnd<DT>(a.ent_scale * rnd<DT>(avg - s)));
+      cv[gi][e] = rnd<DT>(ev - s);
+      tv[gi][e] = rnd<DT>(tanhf_(ev));
+      mx_t = fmaxf(mx_t, fabsf(tv[gi][e]));
+      mx_c = fmaxf(mx_c, fabsf(cv[gi][e]));
+      if (a.e_tanh || a.c_out) {
+        const int64_t o = (b * a.L + t) * a.ld_out + c;
+        if (a.c_out) st<DT>(a.c_out, o, cv[gi][e]);
+        if (a.e_tanh) st<DT>(a.e_tanh, o, tv[gi][e]);
       }
     }
   }
-  const int64_t chunks = a.ldq / 16;
-  for (int64_t i = tid; i < 2 * kFusedTP * chunks; i += 256) {
-    const int64_t rr = i / chunks, ck = i - rr * chunks;
-    const int which = static_cast<int>(rr / kFusedTP), p = static_cast<int>(rr % kFusedTP);
-    const int64_t t = t0 + p;
-    if (t >= a.L) continue;
-    int8_t* dst = (which == 0 ? a.q_te : a.q_c) + (b * a.L + t) * a.ldq + 16 * ck;
-    *reinterpret_cast<uint4*>(dst) = reinterpret_cast<const uint4*>(codes + rr * a.ldq)[ck];
+  // 5. per-token scales and codes (tesm.py:206-209); a position's 16 lanes share its row
+  mx_t = wave_max<16>(mx_t);
+  mx_c = wave_max<16>(mx_c);
+  const float sc_t = act_scale<DT>(mx_t, a.eps);
+  const float sc_c = act_scale<DT>(mx_c, a.eps);
+  int sum_t = 0, sum_c = 0;
+  const int64_t row = b * a.L + t;
+  const int ngq = static_cast<int>(a.ldq / 16);
+#pragma unroll
+  for (int gi = 0; gi < kFusedMaxGPT; ++gi) {
+    const int g = g0 + 16 * gi;
+    if (!tok || g >= ngq) continue;
+    uint32_t qt[16], qc[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int c1 = (g < groups) ? act_code<DT>(tv[gi][e], sc_t) : 0;
+      const int c2 = (g < groups) ? act_code<DT>(cv[gi][e], sc_c) : 0;
+      sum_t += c1;
+      sum_c += c2;
+      qt[e] = static_cast<uint32_t>(c1) & 0xffu;
+      qc[e] = static_cast<uint32_t>(c2) & 0xffu;
+    }
+    // layout 1: byte 4s + j of the group holds code 4j + s
+    const uint4 ot = make_uint4(qt[0] | (qt[4] << 8) | (qt[8] << 16) | (qt[12] << 24),
+                                qt[1] | (qt[5] << 8) | (qt[9] << 16) | (qt[13] << 24),
+                                qt[2] | (qt[6] << 8) | (qt[10] << 16) | (qt[14] << 24),
+                                qt[3] | (qt[7] << 8) | (qt[11] << 16) | (qt[15] << 24));
+    const uint4 oc = make_uint4(qc[0] | (qc[4] << 8) | (qc[8] << 16) | (qc[12] << 24),
+                                qc[1] | (qc[5] << 8) | (qc[9] << 16) | (qc[13] << 24),
+                                qc[2] | (qc[6] << 8) | (qc[10] << 16) | (qc[14] << 24),
+                                qc[3] | (qc[7] << 8) | (qc[11] << 16) | (qc[15] << 24));
+    reinterpret_cast<uint4*>(a.q_te + row * a.ldq)[g] = ot;
+    reinterpret_cast<uint4*>(a.q_c + row * a.ldq)[g] = oc;
+  }
+  // code groups of the padding past the thread's range (ldq > 512) are zero as well
+  for (int g = g0 + 16 * kFusedMaxGPT; tok && g < ngq; g += 16) {
+    reinterpret_cast<uint4*>(a.q_te + row * a.ldq)[g] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(a.q_c + row * a.ldq)[g] = make_uint4(0, 0, 0, 0);
+  }
+  sum_t = wave_sum_i<16>(sum_t);
+  sum_c = wave_sum_i<16>(sum_c);
+  if (tok && g0 == 0) {
+    a.s_te[row] = sc_t;
+    a.rs_te[row] = sum_t;
+    a.s_c[row] = sc_c;
+    a.rs_c[row] = sum_c;
   }
 }
 
@@ -424,10 +462,9 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
 
 bool ent_fused_ok(const EntArgs& a) {
-  if (a.mimo || a.H != 1 || a.D > 256 * kFusedMaxCPD) return false;
+  if (a.mimo || a.H != 1 || a.D > 16 * 16 * kFusedMaxGPT) return false;
   const int64_t weff = eff_window(a);
-  const int64_t ldq = a.ldq > 0 ? a.ldq : kpad(a.D);
-  return fused_lds(a.R, a.D, weff, ldq, a.dt == kBF16 ? 2 : 4).total <= 64 * 1024;
+  return fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4).total <= 64 * 1024;
 }
 
 int64_t ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W) {
@@ -454,7 +491,7 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
     TESM_REQUIRE(a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c && a.ldq >= a.D && a.ldq % 16 == 0 &&
                      aligned(a.q_te, 16) && aligned(a.q_c, 16),
                  kErrInvalidArg, "local_ent: bad quantized outputs");
-    const FusedLds f = fused_lds(a.R, a.D, weff, a.ldq, a.dt == kBF16 ? 2 : 4);
+    const FusedLds f = fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4);
     dim3 grid(static_cast<unsigned>((a.L + kFusedTP - 1) / kFusedTP), static_cast<unsigned>(a.B));
     if (a.dt == kBF16)
       ent_fused_kernel<kBF16><<<grid, 256, f.total, st>>>(a, weff, f);

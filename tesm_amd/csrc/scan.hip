@@ -36,7 +36,7 @@ struct ScanIn {
       d = ld<DT>(a.decay, tok * a.ld_decay + ch);
       u = ld<DT>(a.update, tok * a.ld_update + ch);
     } else {
-      const float sv = rnd<DT>(tanhf(ld<DT>(a.sv, tok * a.ld_sv + ch)));
+      const float sv = rnd<DT>(tanhf_(ld<DT>(a.sv, tok * a.ld_sv + ch)));
       d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(a.decay, tok * a.ld_decay + ch) + ld<DT>(a.decay_bias, ch))));
       const float w = rnd<DT>(sigmoidf_(ld<DT>(a.update, tok * a.ld_update + ch)));
       u = a.round_update ? rnd<DT>(w * sv) : w * sv;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
         Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2);
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
-          const float sv = rnd<DT>(tanhf(x2[j]));
+          const float sv = rnd<DT>(tanhf_(x2[j]));
           d[i][j] = rnd<DT>(sigmoidf_(rnd<DT>(x0[j] + bias[j])));
           const float w = rnd<DT>(sigmoidf_(x1[j]));
           u[i][j] = a.round_update ? rnd<DT>(w * sv) : w * sv;
