@@ -44,28 +44,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
   if (n0 >= a.N) return;
   const int64_t nch = a.Kp / 64;
 
+  // unconditional loads from clamped rows / chunks (masked afterwards): all in flight at once
   uint4 W[RPG][NCH];
 #pragma unroll
   for (int r = 0; r < RPG; ++r) {
     const int64_t n = n0 + r;
+    const int64_t nc = n < a.N ? n : a.N - 1;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int64_t c = g + LPR * i;
-      W[r][i] = (n < a.N && c < nch) ? *reinterpret_cast<const uint4*>(o.w + n * o.ldw + 16 * c)
-                                     : make_uint4(0, 0, 0, 0);
+      const int64_t cc = c < nch ? c : nch - 1;
+      // rows past N only feed outputs that are never stored; chunks past the row are masked at use
+      W[r][i] = *reinterpret_cast<const uint4*>(o.w + nc * o.ldw + 16 * cc);
     }
   }
   uint32_t X[MR][NCH][16];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
+    const int64_t mc = m < a.M ? m : a.M - 1;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int64_t c = g + LPR * i;
-      const bool ok = m < a.M && c < nch;
+      const int64_t cc = c < nch ? c : nch - 1;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const uint4 v = ok ? *reinterpret_cast<const uint4*>(o.q + m * o.ldq + 64 * c + 16 * d)
-                           : make_uint4(0, 0, 0, 0);
+        const uint4 v = *reinterpret_cast<const uint4*>(o.q + mc * o.ldq + 64 * cc + 16 * d);
         X[m][i][4 * d + 0] = v.x;
         X[m][i][4 * d + 1] = v.y;
         X[m][i][4 * d + 2] = v.z;
@@ -83,7 +86,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
   for (int r = 0; r < RPG; ++r) {
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-      const uint32_t wd[4] = {W[r][i].x, W[r][i].y, W[r][i].z, W[r][i].w};
+      // a lane's chunk past the end of the row contributes nothing (code 0 everywhere)
+      const bool live = g + LPR * i < nch;
+      const uint32_t wd[4] = {live ? W[r][i].x : 0u, live ? W[r][i].y : 0u, live ? W[r][i].z : 0u,
+                              live ? W[r][i].w : 0u};
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
 #pragma unroll
@@ -155,59 +161,76 @@ __device__ __forceinline__ v4i unpack_frag(uint32_t w) {
              static_cast<int>(unpack_u(w, 3))};
 }
 
+template <class C>
+__device__ __forceinline__ void gemm_gload(const int8_t* const (&pa)[C::A_PT], const uint8_t* const (&pb)[C::B_PT],
+                                           const bool (&vb)[C::B_PT], int64_t k0, v4i (&ra)[C::A_PT],
+                                           v4i (&rb)[C::B_PT]) {
+#pragma unroll
+  for (int p = 0; p < C::A_PT; ++p) ra[p] = *reinterpret_cast<const v4i*>(pa[p] + k0);
+#pragma unroll
+  for (int p = 0; p < C::B_PT; ++p)
+    if (vb[p]) rb[p] = *reinterpret_cast<const v4i*>(pb[p] + k0 / 4);
+}
+
+// dword d of a packed B chunk is code group 4h + d, which sits 16 lanes (64 bytes) further on in
+// the fragment
+template <class C>
+__device__ __forceinline__ void gemm_sstore(const int (&la)[C::A_PT], const int (&lb)[C::B_PT],
+                                            const bool (&vb)[C::B_PT], const v4i (&ra)[C::A_PT],
+                                            const v4i (&rb)[C::B_PT], char* stage) {
+#pragma unroll
+  for (int p = 0; p < C::A_PT; ++p) *reinterpret_cast<v4i*>(stage + la[p]) = ra[p];
+#pragma unroll
+  for (int p = 0; p < C::B_PT; ++p) {
+    if (vb[p]) {
+      *reinterpret_cast<int*>(stage + lb[p]) = rb[p].x;
+      *reinterpret_cast<int*>(stage + lb[p] + 64) = rb[p].y;
+      *reinterpret_cast<int*>(stage + lb[p] + 128) = rb[p].z;
+      *reinterpret_cast<int*>(stage + lb[p] + 192) = rb[p].w;
+    }
+  }
+}
+
 template <class C, int WN, int TM, int TN>
 __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
                                               int64_t Kp, v4i (&acc)[TM][TN], char* smem) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x;
+  __builtin_assume(t < C::NT);
+  const int lane = t & 63, w = t >> 6;
   const int wm = w / WN, wn = w % WN;
-  uint4 ra[C::A_PT], rb[C::B_PT];
+  constexpr bool kAllB = (C::B_CHUNKS % C::NT) == 0;
 
-  auto gload = [&](int64_t k0) {
+  // per-chunk global sources and LDS destinations; rows past M / columns past N read the last
+  // valid one and only feed accumulator entries that are never stored
+  const int8_t* pa[C::A_PT];
+  int la[C::A_PT];
 #pragma unroll
-    for (int p = 0; p < C::A_PT; ++p) {
-      const int c = t + p * C::NT;
-      if (c < C::A_CHUNKS) {
-        const int64_t m = m0 + (c >> 3);
-        ra[p] = m < M ? *reinterpret_cast<const uint4*>(o.q + m * o.ldq + k0 + 16 * (c & 7))
-                      : make_uint4(0, 0, 0, 0);
-      }
-    }
+  for (int p = 0; p < C::A_PT; ++p) {
+    const int c = t + p * C::NT;
+    const int64_t m = m0 + (c >> 3);
+    pa[p] = o.q + (m < M ? m : M - 1) * o.ldq + 16 * (c & 7);
+    la[p] = a_frag_off(c >> 3, c & 7);
+  }
+  const uint8_t* pb[C::B_PT];
+  int lb[C::B_PT];
+  bool vb[C::B_PT];
 #pragma unroll
-    for (int p = 0; p < C::B_PT; ++p) {
-      const int c = t + p * C::NT;
-      if (c < C::B_CHUNKS) {
-        const int64_t n = n0 + (c >> 1);
-        rb[p] = n < N ? *reinterpret_cast<const uint4*>(o.w + n * o.ldw + k0 / 4 + 16 * (c & 1))
-                      : make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-  auto sstore = [&](char* stage) {
-#pragma unroll
-    for (int p = 0; p < C::A_PT; ++p) {
-      const int c = t + p * C::NT;
-      if (c < C::A_CHUNKS) *reinterpret_cast<uint4*>(stage + a_frag_off(c >> 3, c & 7)) = ra[p];
-    }
-    char* sb = stage + C::A_BYTES;
-#pragma unroll
-    for (int p = 0; p < C::B_PT; ++p) {
-      const int c = t + p * C::NT;
-      if (c < C::B_CHUNKS) {
-        const int r = c >> 1, h = c & 1;
-        const uint32_t wd[4] = {rb[p].x, rb[p].y, rb[p].z, rb[p].w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(sb + b_frag_off(r, 4 * h + d)) = wd[d];
-      }
-    }
-  };
-
+  for (int p = 0; p < C::B_PT; ++p) {
+    const int c = t + p * C::NT;
+    vb[p] = kAllB || c < C::B_CHUNKS;
+    const int64_t n = n0 + (c >> 1);
+    pb[p] = o.w + (n < N ? n : N - 1) * o.ldw + 16 * (c & 1);
+    lb[p] = C::A_BYTES + b_frag_off(c >> 1, 4 * (c & 1));
+  }
+  v4i ra[C::A_PT], rb[C::B_PT];
   const int64_t nk = Kp / C::BK;
-  gload(0);
-  sstore(smem);
+  gemm_gload<C>(pa, pb, vb, 0, ra, rb);
+  gemm_sstore<C>(la, lb, vb, ra, rb, smem);
   __syncthreads();
   for (int64_t kt = 0; kt < nk; ++kt) {
     const char* cur = smem + (kt & 1) * C::STAGE;
-    if (kt + 1 < nk) gload((kt + 1) * C::BK);
+    const bool more = kt + 1 < nk;
+    if (more) gemm_gload<C>(pa, pb, vb, (kt + 1) * C::BK, ra, rb);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v4i af[TM];
@@ -227,7 +250,7 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
         for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[i], acc[i][j], 0, 0, 0);
       }
     }
-    if (kt + 1 < nk) sstore(smem + ((kt + 1) & 1) * C::STAGE);
+    if (more) gemm_sstore<C>(la, lb, vb, ra, rb, smem + ((kt + 1) & 1) * C::STAGE);
     __syncthreads();
   }
 }
@@ -407,15 +430,19 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
   }
   v4i xa0, xa1, na0, na1;
   uint32_t bw0[NCT], bw1[NCT], nb0[NCT], nb1[NCT];
+  // unconditional loads keep every load of a k-step in flight: rows past M / columns past N read
+  // the last valid one and only feed accumulator entries that are never used
+  const int64_t mc = mok ? m : a.M - 1;
   auto load = [&](int64_t ks, v4i& r0, v4i& r1, uint32_t (&w0)[NCT], uint32_t (&w1)[NCT]) {
     const int64_t ko = 64 * ks + 16 * (lane >> 4);
-    r0 = mok ? *reinterpret_cast<const v4i*>(o0.q + m * o0.ldq + ko) : v4i{0, 0, 0, 0};
-    r1 = mok ? *reinterpret_cast<const v4i*>(o1.q + m * o1.ldq + ko) : v4i{0, 0, 0, 0};
+    r0 = *reinterpret_cast<const v4i*>(o0.q + mc * o0.ldq + ko);
+    r1 = *reinterpret_cast<const v4i*>(o1.q + mc * o1.ldq + ko);
 #pragma unroll
     for (int j = 0; j < NCT; ++j) {
       const int64_t n = col0 + 16 * j + (lane & 15);
-      w0[j] = n < a.N ? *reinterpret_cast<const uint32_t*>(o0.w + n * o0.ldw + ko / 4) : 0u;
-      w1[j] = n < a.N ? *reinterpret_cast<const uint32_t*>(o1.w + n * o1.ldw + ko / 4) : 0u;
+      const int64_t nc = n < a.N ? n : a.N - 1;
+      w0[j] = *reinterpret_cast<const uint32_t*>(o0.w + nc * o0.ldw + ko / 4);
+      w1[j] = *reinterpret_cast<const uint32_t*>(o1.w + nc * o1.ldw + ko / 4);
     }
   };
   load(0, xa0, xa1, bw0, bw1);

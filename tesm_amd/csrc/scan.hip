@@ -123,35 +123,32 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
   const int64_t t0 = c * T;
   const int n = static_cast<int>((t0 + T < a.L ? t0 + T : a.L) - t0);
 
-  float d[TM][CPT], u[TM][CPT], bias[CPT];
+  // All loads are issued unconditionally (positions past the end re-read the last valid one and
+  // are masked afterwards) so that the whole chunk's loads are in flight at once.
+  float x0[TM][CPT], x1[TM][CPT], x2[TM][CPT], bias[CPT];
   if constexpr (MODE == 1) Vec<DT, CPT>::load(a.decay_bias, ch, bias);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    if (i < n) {
-      const int64_t tok = b * a.L + t0 + i;
-      float x0[CPT], x1[CPT];
-      Vec<DT, CPT>::load(a.decay, tok * a.ld_decay + ch, x0);
-      Vec<DT, CPT>::load(a.update, tok * a.ld_update + ch, x1);
+    const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
+    Vec<DT, CPT>::load(a.decay, tok * a.ld_decay + ch, x0[i]);
+    Vec<DT, CPT>::load(a.update, tok * a.ld_update + ch, x1[i]);
+    if constexpr (MODE == 1) Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2[i]);
+  }
+  float d[TM][CPT], u[TM][CPT];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
       if constexpr (MODE == 0) {
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-          d[i][j] = x0[j];
-          u[i][j] = x1[j];
-        }
+        d[i][j] = x0[i][j];
+        u[i][j] = x1[i][j];
       } else {
-        float x2[CPT];
-        Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2);
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-          const float sv = rnd<DT>(tanhf_(x2[j]));
-          d[i][j] = rnd<DT>(sigmoidf_(rnd<DT>(x0[j] + bias[j])));
-          const float w = rnd<DT>(sigmoidf_(x1[j]));
-          u[i][j] = a.round_update ? rnd<DT>(w * sv) : w * sv;
-        }
+        const float sv = rnd<DT>(tanhf_(x2[i][j]));
+        d[i][j] = rnd<DT>(sigmoidf_(rnd<DT>(x0[i][j] + bias[j])));
+        const float w = rnd<DT>(sigmoidf_(x1[i][j]));
+        u[i][j] = a.round_update ? rnd<DT>(w * sv) : w * sv;
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPT; ++j) {
+      if (i >= n) {
         d[i][j] = 1.0f;
         u[i][j] = 0.0f;
       }
