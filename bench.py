@@ -43,6 +43,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel measurements")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
+    p.add_argument("--copy-calib", action="store_true",
+                   help="run one 256 MiB device-to-device copy first (a known-size reference for "
+                        "FETCH_SIZE / WRITE_SIZE counter runs)")
     return p.parse_args()
 
 
@@ -187,6 +190,12 @@ def main():
     m = TESM_SISO(**LAYER).to(dev).to(torch.bfloat16).eval()
     u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
 
+    if args.copy_calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     with torch.no_grad():
         for _ in range(args.warmup):
             m(u)

@@ -274,8 +274,8 @@ template <int OUT_DT>
 __device__ __forceinline__ void store4(void* out, int64_t idx, const float (&v)[4], bool vec) {
   if (vec) {
     if constexpr (OUT_DT == kBF16) {
-      const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-      const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      const uint32_t lo = pack_bf16x2(v[0], v[1]);
+      const uint32_t hi = pack_bf16x2(v[2], v[3]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + idx) = make_uint2(lo, hi);
     } else {
       *reinterpret_cast<float4*>(static_cast<float*>(out) + idx) = make_float4(v[0], v[1], v[2], v[3]);
@@ -399,28 +399,153 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Output gate over whole rows: a workgroup owns 16 rows and all N = d_model columns (4 waves side by
-// side, NCT 16-column tiles each), so after y = local + sigmoid(gate)*state_proj + ent_proj it can
-// quantize y per token for out_proj without writing y.  Operands stream from global/L2 into
-// registers (A: 16 code rows; B: one packed dword per lane per tile), double buffered per k-step.
+// Output gate over whole rows: a workgroup owns 16 rows and all N = d_model columns (NW waves side
+// by side, NCT 16-column tiles each), so after y = local + sigmoid(gate)*state_proj + ent_proj it
+// can quantize y per token for out_proj without writing y.  Every global operand of the epilogue
+// (local, gate, s_x, rowsum) is requested before the K loop and kept as raw bits, so the whole
+// workgroup's memory traffic is in flight at once; the K loop runs two k-steps per iteration on
+// ping-pong registers so each MFMA group waits only for its own operands.
 // ---------------------------------------------------------------------------
-template <int NCT, int DT>
-__global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o) {
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+// Raw 32-bit words holding four consecutive epilogue values of one row: two bf16 pairs when the
+// row can be read with one 8-byte load, else one word per value.
+template <int DT, bool VEC>
+struct EpRaw {
+  static constexpr int W = (DT == kBF16 && VEC) ? 2 : 4;
+};
+
+// Columns past N read the last valid ones (their results are never stored).
+template <int DT, bool VEC>
+__device__ __forceinline__ void ep_load(const void* base, int64_t ld, int64_t m, int64_t nb, int64_t N,
+                                        uint32_t (&raw)[EpRaw<DT, VEC>::W]) {
+  if constexpr (VEC) {
+    const int64_t c = nb < N ? nb : N - 4;  // N % 4 == 0
+    if constexpr (DT == kBF16) {
+      const v2u x = *reinterpret_cast<const v2u*>(static_cast<const uint16_t*>(base) + m * ld + c);
+      raw[0] = x.x;
+      raw[1] = x.y;
+    } else {
+      const v4i x = *reinterpret_cast<const v4i*>(static_cast<const float*>(base) + m * ld + c);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) raw[r] = static_cast<uint32_t>(x[r]);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t c = nb + r < N ? nb + r : N - 1;
+      if constexpr (DT == kBF16)
+        raw[r] = static_cast<const uint16_t*>(base)[m * ld + c];
+      else
+        raw[r] = static_cast<const uint32_t*>(base)[m * ld + c];
+    }
+  }
+}
+
+template <int DT, bool VEC>
+__device__ __forceinline__ float ep_get(const uint32_t (&raw)[EpRaw<DT, VEC>::W], int r) {
+  if constexpr (DT == kF32) {
+    return __uint_as_float(raw[r]);
+  } else if constexpr (VEC) {
+    return __uint_as_float((r & 1) ? (raw[r >> 1] & 0xffff0000u) : (raw[r >> 1] << 16));
+  } else {
+    return __uint_as_float(raw[r] << 16);
+  }
+}
+
+// One k-step of both operands for the lanes' row (A: 16 code bytes) and tiles (B: a packed dword).
+template <int NCT>
+__device__ __forceinline__ void rowq_load(const LinearArgs& a, int64_t mc, int64_t col0, int lane, int64_t ks,
+                                          v4i& x0, v4i& x1, uint32_t (&w0)[NCT], uint32_t (&w1)[NCT]) {
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+  const int64_t ko = 64 * ks + 16 * (lane >> 4);
+  x0 = *reinterpret_cast<const v4i*>(o0.q + mc * o0.ldq + ko);
+  x1 = *reinterpret_cast<const v4i*>(o1.q + mc * o1.ldq + ko);
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int64_t n = col0 + 16 * j + (lane & 15);
+    const int64_t nc = n < a.N ? n : a.N - 1;
+    w0[j] = *reinterpret_cast<const uint32_t*>(o0.w + nc * o0.ldw + ko / 4);
+    w1[j] = *reinterpret_cast<const uint32_t*>(o1.w + nc * o1.ldw + ko / 4);
+  }
+}
+
+template <int NCT>
+__device__ __forceinline__ void rowq_mma(v4i (&acc0)[NCT], v4i (&acc1)[NCT], const v4i& x0, const v4i& x1,
+                                         const uint32_t (&w0)[NCT], const uint32_t (&w1)[NCT]) {
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    acc0[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(w0[j]), x0, acc0[j], 0, 0, 0);
+    acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(w1[j]), x1, acc1[j], 0, 0, 0);
+  }
+}
+
+// y = local + sigmoid(gate) * state_proj + ent_proj in the reference's op order (tesm.py:1256-1260),
+// every op rounded to the layer dtype; entries outside the matrix are 0.  PER_ROW: c_w0 / c_w1
+// index per output column, else they point at one scalar each.
+template <int NCT, int DT, bool VEC, bool PER_ROW>
+__device__ __forceinline__ void rowq_gate(const LinearArgs& a, const uint32_t (&lraw)[NCT][EpRaw<DT, VEC>::W],
+                                          const uint32_t (&graw)[NCT][EpRaw<DT, VEC>::W], const v4i (&acc0)[NCT],
+                                          const v4i (&acc1)[NCT], int32_t rs0, int32_t rs1, float inv0, float inv1,
+                                          const float* c_w0, const float* c_w1, bool mok, int64_t col0, int lane,
+                                          float (&y)[NCT][4]) {
+  const float cws0 = c_w0[0], cws1 = c_w1[0];
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = col0 + 16 * j + 4 * (lane >> 4) + r;
+      const int64_t nc = n < a.N ? n : a.N - 1;
+      const float cw0 = PER_ROW ? c_w0[nc] : cws0;
+      const float cw1 = PER_ROW ? c_w1[nc] : cws1;
+      const float sp = rnd<DT>((static_cast<float>(acc0[j][r] - rs0) * inv0) * cw0);
+      const float ep = rnd<DT>((static_cast<float>(acc1[j][r] - rs1) * inv1) * cw1);
+      const float g = rnd<DT>(sigmoidf_(ep_get<DT, VEC>(graw[j], r)));
+      const float v = rnd<DT>(rnd<DT>(ep_get<DT, VEC>(lraw[j], r) + rnd<DT>(g * sp)) + ep);
+      y[j][r] = (mok && n < a.N) ? v : 0.0f;
+    }
+  }
+}
+
+template <int NW, int NCT, int DT, bool VEC, int NKS>
+__global__ __launch_bounds__(NW * 64) void gate_rowq_kernel(LinearArgs a, RowQuant o) {
+  constexpr int RW = EpRaw<DT, VEC>::W;
   extern __shared__ __attribute__((aligned(16))) char lds_rowq[];
-  int8_t* codes = reinterpret_cast<int8_t*>(lds_rowq);                              // [16][ldq]
-  float* red = reinterpret_cast<float*>(lds_rowq + 16 * o.ldq);                     // [16 rows][4 waves]
-  int32_t* redi = reinterpret_cast<int32_t*>(lds_rowq + 16 * o.ldq + 16 * 4 * 4);   // [16 rows][4 waves]
+  int8_t* codes = reinterpret_cast<int8_t*>(lds_rowq);                          // [16][ldq]
+  float* red = reinterpret_cast<float*>(lds_rowq + 16 * o.ldq);                 // [16 rows][NW waves]
+  int32_t* redi = reinterpret_cast<int32_t*>(red + 16 * NW);                   // [16 rows][NW waves]
+  float* cwl = reinterpret_cast<float*>(redi + 16 * NW);                       // [2][N] per-row scales
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 16;
   const int64_t col0 = static_cast<int64_t>(w) * NCT * 16;
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
-  const int row = lane & 15;            // the activation row this lane feeds and the output row it holds
+  const int row = lane & 15;  // the activation row this lane feeds and the output row it holds
   const int64_t m = m0 + row;
   const bool mok = m < a.M;
-  const int64_t nks = a.Kp / 64;
+  const int64_t mc = mok ? m : a.M - 1;
+  const int64_t nks = a.Kp / 64;  // even: Kp is a multiple of 128
+  const bool per_row = o0.c_w_per_row || o1.c_w_per_row;
 
-  for (int64_t i = tid; i < 16 * o.ldq / 16; i += 256) reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
+  if (per_row) {
+    for (int64_t i = tid; i < a.N; i += NW * 64) {
+      cwl[i] = o0.c_w_per_row ? o0.c_w[i] : o0.c_w[0];
+      cwl[a.N + i] = o1.c_w_per_row ? o1.c_w[i] : o1.c_w[0];
+    }
+  }
+  // epilogue operands first, as raw bits: nothing waits on them before the K loop is done
+  uint32_t lraw[NCT][RW], graw[NCT][RW];
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int64_t nb = col0 + 16 * j + 4 * (lane >> 4);
+    ep_load<DT, VEC>(a.local, a.ld_local, mc, nb, a.N, lraw[j]);
+    ep_load<DT, VEC>(a.gate, a.ld_gate, mc, nb, a.N, graw[j]);
+  }
+  const float sx0 = o0.s_x[mc], sx1 = o1.s_x[mc];
+  const int32_t rs0 = o0.rowsum[mc], rs1 = o1.rowsum[mc];
+  const float cws0 = o0.c_w[0], cws1 = o1.c_w[0];
+  for (int64_t i = tid; i < 16 * o.ldq / 16; i += NW * 64) reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
 
   v4i acc0[NCT], acc1[NCT];
 #pragma unroll
@@ -428,94 +553,63 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
     acc0[j] = v4i{0, 0, 0, 0};
     acc1[j] = v4i{0, 0, 0, 0};
   }
-  v4i xa0, xa1, na0, na1;
-  uint32_t bw0[NCT], bw1[NCT], nb0[NCT], nb1[NCT];
-  // unconditional loads keep every load of a k-step in flight: rows past M / columns past N read
-  // the last valid one and only feed accumulator entries that are never used
-  const int64_t mc = mok ? m : a.M - 1;
-  auto load = [&](int64_t ks, v4i& r0, v4i& r1, uint32_t (&w0)[NCT], uint32_t (&w1)[NCT]) {
-    const int64_t ko = 64 * ks + 16 * (lane >> 4);
-    r0 = *reinterpret_cast<const v4i*>(o0.q + mc * o0.ldq + ko);
-    r1 = *reinterpret_cast<const v4i*>(o1.q + mc * o1.ldq + ko);
+  if constexpr (NKS > 0) {
+    // the whole K extent at once (NKS == Kp / 64): one round trip for all of the wave's operands
+    v4i x0[NKS], x1[NKS];
+    uint32_t w0[NKS][NCT], w1[NKS][NCT];
 #pragma unroll
-    for (int j = 0; j < NCT; ++j) {
-      const int64_t n = col0 + 16 * j + (lane & 15);
-      const int64_t nc = n < a.N ? n : a.N - 1;
-      w0[j] = *reinterpret_cast<const uint32_t*>(o0.w + nc * o0.ldw + ko / 4);
-      w1[j] = *reinterpret_cast<const uint32_t*>(o1.w + nc * o1.ldw + ko / 4);
-    }
-  };
-  load(0, xa0, xa1, bw0, bw1);
-  for (int64_t ks = 0; ks < nks; ++ks) {
-    if (ks + 1 < nks) load(ks + 1, na0, na1, nb0, nb1);
+    for (int ks = 0; ks < NKS; ++ks) rowq_load<NCT>(a, mc, col0, lane, ks, x0[ks], x1[ks], w0[ks], w1[ks]);
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first MFMA
 #pragma unroll
-    for (int j = 0; j < NCT; ++j) {
-      acc0[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(bw0[j]), xa0, acc0[j], 0, 0, 0);
-      acc1[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(bw1[j]), xa1, acc1[j], 0, 0, 0);
-    }
-    if (ks + 1 < nks) {
-      xa0 = na0;
-      xa1 = na1;
-#pragma unroll
-      for (int j = 0; j < NCT; ++j) {
-        bw0[j] = nb0[j];
-        bw1[j] = nb1[j];
-      }
+    for (int ks = 0; ks < NKS; ++ks) rowq_mma<NCT>(acc0, acc1, x0[ks], x1[ks], w0[ks], w1[ks]);
+  } else {
+    v4i xa0, xa1, xb0, xb1;
+    uint32_t wa0[NCT], wa1[NCT], wb0[NCT], wb1[NCT];
+    rowq_load<NCT>(a, mc, col0, lane, 0, xa0, xa1, wa0, wa1);
+    for (int64_t ks = 0; ks < nks; ks += 2) {
+      rowq_load<NCT>(a, mc, col0, lane, ks + 1, xb0, xb1, wb0, wb1);
+      rowq_mma<NCT>(acc0, acc1, xa0, xa1, wa0, wa1);
+      // the last iteration re-reads k-step ks + 1 instead of branching (the values are unused)
+      rowq_load<NCT>(a, mc, col0, lane, ks + 2 < nks ? ks + 2 : ks + 1, xa0, xa1, wa0, wa1);
+      rowq_mma<NCT>(acc0, acc1, xb0, xb1, wb0, wb1);
     }
   }
+  if (per_row) __syncthreads();
 
   // epilogue: lane holds row m, columns col0 + 16j + 4*(lane/16) + r
-  const float inv0 = mok ? 1.0f / o0.s_x[m] : 0.0f, inv1 = mok ? 1.0f / o1.s_x[m] : 0.0f;
-  const int32_t rs0 = mok ? o0.rowsum[m] : 0, rs1 = mok ? o1.rowsum[m] : 0;
-  const float cws0 = o0.c_w[0], cws1 = o1.c_w[0];
-  const bool vin = vec4_ok<DT>(a.local, a.ld_local) && vec4_ok<DT>(a.gate, a.ld_gate);
+  const float inv0 = 1.0f / sx0, inv1 = 1.0f / sx1;
   float y[NCT][4];
+  if (per_row)
+    rowq_gate<NCT, DT, VEC, true>(a, lraw, graw, acc0, acc1, rs0, rs1, inv0, inv1, cwl, cwl + a.N, mok, col0, lane, y);
+  else
+    rowq_gate<NCT, DT, VEC, false>(a, lraw, graw, acc0, acc1, rs0, rs1, inv0, inv1, &cws0, &cws1, mok, col0, lane, y);
   float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < NCT; ++j) {
-    const int64_t nb = col0 + 16 * j + 4 * (lane >> 4);
-    float lo[4], gt[4];
-    const bool full = nb + 3 < a.N;
-    if (mok && full) {
-      load4<DT>(a.local, m * a.ld_local + nb, vin, lo);
-      load4<DT>(a.gate, m * a.ld_gate + nb, vin, gt);
-    } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = mok && nb + r < a.N;
-        lo[r] = ok ? ld<DT>(a.local, m * a.ld_local + nb + r) : 0.0f;
-        gt[r] = ok ? ld<DT>(a.gate, m * a.ld_gate + nb + r) : 0.0f;
-      }
-    }
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fabsf(y[j][r]));
+  }
+  if (o.y && mok) {
+    const bool vout = vec4_ok<DT>(o.y, o.ldy);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t n = nb + r;
-      y[j][r] = 0.0f;
-      if (!mok || n >= a.N) continue;
-      const float cw0 = o0.c_w_per_row ? o0.c_w[n] : cws0;
-      const float cw1 = o1.c_w_per_row ? o1.c_w[n] : cws1;
-      const float sp = rnd<DT>((static_cast<float>(acc0[j][r] - rs0) * inv0) * cw0);
-      const float ep = rnd<DT>((static_cast<float>(acc1[j][r] - rs1) * inv1) * cw1);
-      const float g = rnd<DT>(sigmoidf_(gt[r]));
-      const float v = rnd<DT>(rnd<DT>(lo[r] + rnd<DT>(g * sp)) + ep);
-      y[j][r] = v;
-      mx = fmaxf(mx, fabsf(v));
-    }
-    if (o.y && mok) {
-      if (full) {
-        store4<DT>(o.y, m * o.ldy + nb, y[j], vec4_ok<DT>(o.y, o.ldy));
+    for (int j = 0; j < NCT; ++j) {
+      const int64_t nb = col0 + 16 * j + 4 * (lane >> 4);
+      if (vout && nb + 3 < a.N) {
+        store4<DT>(o.y, m * o.ldy + nb, y[j], true);
       } else {
         for (int r = 0; r < 4 && nb + r < a.N; ++r) st<DT>(o.y, m * o.ldy + nb + r, y[j][r]);
       }
     }
   }
-  // row max over the 4 lanes sharing the row, then over the 4 waves
+  // row max over the 4 lanes sharing the row, then over the NW waves
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  if (lane < 16) red[row * 4 + w] = mx;
+  if (lane < 16) red[row * NW + w] = mx;
   __syncthreads();
-  const float* rr = red + row * 4;
-  const float sc = act_scale<DT>(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])), o.eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) amax = fmaxf(amax, red[row * NW + i]);
+  const float sc = act_scale<DT>(amax, o.eps);
   int sum = 0;
 #pragma unroll
   for (int j = 0; j < NCT; ++j) {
@@ -531,19 +625,311 @@ __global__ __launch_bounds__(256) void gate_rowq_kernel(LinearArgs a, RowQuant o
   }
   sum += __shfl_xor(sum, 16, 64);
   sum += __shfl_xor(sum, 32, 64);
-  if (lane < 16) redi[row * 4 + w] = sum;
+  if (lane < 16) redi[row * NW + w] = sum;
   __syncthreads();
   if (tid < 16 && m0 + tid < a.M) {
-    const int32_t* ri = redi + tid * 4;
-    const float* rm = red + tid * 4;
-    o.s[m0 + tid] = act_scale<DT>(fmaxf(fmaxf(rm[0], rm[1]), fmaxf(rm[2], rm[3])), o.eps);
-    o.rs[m0 + tid] = (ri[0] + ri[1]) + (ri[2] + ri[3]);
+    float am = 0.0f;
+    int32_t rsum = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      am = fmaxf(am, red[tid * NW + i]);
+      rsum += redi[tid * NW + i];
+    }
+    o.s[m0 + tid] = act_scale<DT>(am, o.eps);
+    o.rs[m0 + tid] = rsum;
   }
   const int64_t chunks = o.ldq / 16;
-  for (int r = w; r < 16; r += 4) {
+  for (int r = w; r < 16; r += NW) {
     if (m0 + r >= a.M) continue;
     for (int64_t ck = lane; ck < chunks; ck += 64)
       reinterpret_cast<uint4*>(o.q + (m0 + r) * o.ldq)[ck] = reinterpret_cast<const uint4*>(codes + r * o.ldq)[ck];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent output gate with both packed weight matrices resident in LDS (gfx950: 160 KB per
+// workgroup).  Each workgroup stages state_proj and ent_proj once with coalesced 16-byte loads and
+// then walks 16-row tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the next tile's activation codes
+// (one 16-byte piece per thread, staged through LDS) and local/gate operands are requested before
+// the current tile is computed.
+//
+// Staged weight row n of operand p sits at (p * N + n) * RS bytes, RS = 16 * NKS + 16; dword
+// q * NKS + ks of a row holds codes 64 ks + 16 q .. + 15, so one lane reads all its k-steps with
+// wide LDS loads and a 16-lane row group covers all 64 banks once.  Activation rows are staged at
+// a pitch of Kp + 16 bytes for the same reason.
+// ---------------------------------------------------------------------------
+template <int NKS>
+struct RowqLds {
+  static constexpr int RS = 16 * NKS + 16;           // staged weight row pitch
+  static constexpr int ARS = 64 * NKS + 16;          // staged activation row pitch
+  static constexpr int ABUF = 2 * 16 * ARS;          // one tile of both operands
+};
+
+inline int64_t rowq_lds_bytes(int64_t N, int64_t nks, int64_t ldq, int nw) {
+  return 2 * N * (16 * nks + 16) + 2 * 2 * 16 * (64 * nks + 16) + 16 * (ldq + 16) + 2 * 2 * 16 * nw * 4 + 2 * N * 4;
+}
+
+template <int NCT, int AC, int RW>
+struct RowqIn {
+  v4i ac[AC];                          // this thread's share of the tile's activation codes
+  uint32_t lr[NCT][RW], gr[NCT][RW];   // raw local / gate values of the lane's row
+  float sx0, sx1;
+  int32_t rs0, rs1;
+};
+
+// Requests for tile t; rows past M read the last row (never stored).
+template <int NW, int NCT, int NKS, int DT, int AC>
+__device__ __forceinline__ void rowq_in_load(const LinearArgs& a, int64_t t, int64_t col0, int tid,
+                                             RowqIn<NCT, AC, EpRaw<DT, true>::W>& in) {
+  const int lane = tid & 63;
+  const int64_t m0 = t * 16;
+  const int64_t m = m0 + (lane & 15);
+  const int64_t mc = m < a.M ? m : a.M - 1;
+#pragma unroll
+  for (int i = 0; i < AC; ++i) {
+    int g = tid + i * NW * 64;
+    g = g < 128 * NKS ? g : 128 * NKS - 1;
+    const int p = g / (64 * NKS), rem = g - p * 64 * NKS;
+    const int r = rem / (4 * NKS), c = rem - r * 4 * NKS;
+    const int64_t mr = m0 + r < a.M ? m0 + r : a.M - 1;
+    const LinearOperand& op = a.op[0];
+    const int8_t* src = p == 0 ? op.q + mr * op.ldq : a.op[1].q + mr * a.op[1].ldq;
+    in.ac[i] = *reinterpret_cast<const v4i*>(src + 16 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int64_t nb = col0 + 16 * j + 4 * (lane >> 4);
+    ep_load<DT, true>(a.local, a.ld_local, mc, nb, a.N, in.lr[j]);
+    ep_load<DT, true>(a.gate, a.ld_gate, mc, nb, a.N, in.gr[j]);
+  }
+  in.sx0 = a.op[0].s_x[mc];
+  in.sx1 = a.op[1].s_x[mc];
+  in.rs0 = a.op[0].rowsum[mc];
+  in.rs1 = a.op[1].rowsum[mc];
+}
+
+// NKS consecutive dwords of staged LDS (16-byte aligned when NKS % 4 == 0, else 8-byte aligned).
+template <int NKS>
+__device__ __forceinline__ void lds_frag(const char* p, uint32_t (&f)[NKS]) {
+  if constexpr (NKS % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NKS / 4; ++i) {
+      const v4i v = reinterpret_cast<const v4i*>(p)[i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) f[4 * i + r] = static_cast<uint32_t>(v[r]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NKS / 2; ++i) {
+      const v2u v = reinterpret_cast<const v2u*>(p)[i];
+      f[2 * i] = v.x;
+      f[2 * i + 1] = v.y;
+    }
+  }
+}
+
+struct RowqShared {
+  const char* wl;     // staged weights
+  char* abuf;         // staged activation tile (this tile's buffer)
+  int8_t* codes;      // [16][ldq]
+  float* red;         // [16][NW] (this tile's buffer)
+  int32_t* redi;      // [16][NW] (this tile's buffer)
+  const float* cwl;   // [2][N] output scale of every column (c_w, or its one scalar repeated)
+};
+
+template <int NW, int NCT, int DT, int NKS, int AC>
+__device__ __forceinline__ void rowq_tile(const LinearArgs& a, const RowQuant& o, int64_t t,
+                                          const RowqIn<NCT, AC, EpRaw<DT, true>::W>& in, const RowqShared& sh,
+                                          int tid) {
+  using L = RowqLds<NKS>;
+  // all in-tile indices fit 32 bits: N <= 1024 and the LDS is 160 KB
+  const int N = static_cast<int>(a.N);
+  const int cp = static_cast<int>(o.ldq) + 16;  // staged code row pitch (16 rows spread over all banks)
+  const int lane = tid & 63, w = tid >> 6, q = lane >> 4;
+  const int col0 = w * NCT * 16;
+  const int row = lane & 15;
+  const int64_t m0 = t * 16;
+
+  // activation tile into LDS, then each lane's row fragments for every k-step
+#pragma unroll
+  for (int i = 0; i < AC; ++i) {
+    const int g = tid + i * NW * 64;
+    if (g >= 128 * NKS) continue;
+    const int p = g / (64 * NKS), rem = g - p * 64 * NKS;
+    const int r = rem / (4 * NKS), c = rem - r * 4 * NKS;
+    *reinterpret_cast<v4i*>(sh.abuf + (p * 16 + r) * L::ARS + 16 * c) = in.ac[i];
+  }
+  __syncthreads();
+  v4i x0[NKS], x1[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    x0[ks] = *reinterpret_cast<const v4i*>(sh.abuf + row * L::ARS + 64 * ks + 16 * q);
+    x1[ks] = *reinterpret_cast<const v4i*>(sh.abuf + (16 + row) * L::ARS + 64 * ks + 16 * q);
+  }
+
+  // per 16-column tile: both products, then y = local + sigmoid(gate) * state_proj + ent_proj in the
+  // reference's op order (tesm.py:1256-1260), every op rounded to the layer dtype.  Rows past M
+  // compute finite values from clamped operands and are never stored.
+  const float inv0 = 1.0f / in.sx0, inv1 = 1.0f / in.sx1;
+  float y[NCT][4];
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    const int n = col0 + 16 * j + row;
+    const int nc = n < N ? n : N - 1;
+    uint32_t f0[NKS], f1[NKS];
+    lds_frag<NKS>(sh.wl + nc * L::RS + q * NKS * 4, f0);
+    lds_frag<NKS>(sh.wl + (N + nc) * L::RS + q * NKS * 4, f1);
+    v4i acc0 = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(f0[ks]), x0[ks], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack_frag(f1[ks]), x1[ks], acc1, 0, 0, 0);
+    }
+    const int nb = col0 + 16 * j + 4 * q;
+    const int nbc = nb < N ? nb : N - 4;  // N % 4 == 0
+    const float4 cw0 = *reinterpret_cast<const float4*>(sh.cwl + nbc);
+    const float4 cw1 = *reinterpret_cast<const float4*>(sh.cwl + N + nbc);
+    const float c0[4] = {cw0.x, cw0.y, cw0.z, cw0.w}, c1[4] = {cw1.x, cw1.y, cw1.z, cw1.w};
+    const bool nok = nb < N;  // N % 4 == 0: the lane's 4 columns are all in range or all out
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float sp = rnd<DT>((static_cast<float>(acc0[r] - in.rs0) * inv0) * c0[r]);
+      const float ep = rnd<DT>((static_cast<float>(acc1[r] - in.rs1) * inv1) * c1[r]);
+      const float g = rnd<DT>(sigmoidf_(ep_get<DT, true>(in.gr[j], r)));
+      const float v = rnd<DT>(rnd<DT>(ep_get<DT, true>(in.lr[j], r) + rnd<DT>(g * sp)) + ep);
+      y[j][r] = nok ? v : 0.0f;
+      mx = fmaxf(mx, fabsf(y[j][r]));
+    }
+  }
+  const int64_t m = m0 + row;
+  if (o.y && m < a.M) {
+    const bool vout = vec4_ok<DT>(o.y, o.ldy);
+#pragma unroll
+    for (int j = 0; j < NCT; ++j) {
+      const int nb = col0 + 16 * j + 4 * q;
+      if (vout && nb < N) {
+        store4<DT>(o.y, m * o.ldy + nb, y[j], true);
+      } else {
+        for (int r = 0; r < 4 && nb + r < N; ++r) st<DT>(o.y, m * o.ldy + nb + r, y[j][r]);
+      }
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (lane < 16) sh.red[row * NW + w] = mx;
+  __syncthreads();
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) amax = fmaxf(amax, sh.red[row * NW + i]);
+  const float sc = act_scale<DT>(amax, o.eps);
+  // layout 1: column n = 16 g + 4 q + r sits at byte 16 g + 4 r + q of its row
+  int sum = 0;
+  int8_t* crow = sh.codes + row * cp + col0 + q;
+#pragma unroll
+  for (int j = 0; j < NCT; ++j) {
+    if (col0 + 16 * j + 4 * q >= N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qv = act_code<DT>(y[j][r], sc);
+      crow[16 * j + 4 * r] = static_cast<int8_t>(qv);
+      sum += qv;
+    }
+  }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+  if (lane < 16) sh.redi[row * NW + w] = sum;
+  __syncthreads();
+  if (tid < 16 && m0 + tid < a.M) {
+    float am = 0.0f;
+    int32_t rsum = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      am = fmaxf(am, sh.red[tid * NW + i]);
+      rsum += sh.redi[tid * NW + i];
+    }
+    o.s[m0 + tid] = act_scale<DT>(am, o.eps);
+    o.rs[m0 + tid] = rsum;
+  }
+  const int chunks = static_cast<int>(o.ldq / 16);
+  for (int r = w; r < 16; r += NW) {
+    if (m0 + r >= a.M) continue;
+    uint4* dst = reinterpret_cast<uint4*>(o.q + (m0 + r) * o.ldq);
+    const uint4* src = reinterpret_cast<const uint4*>(sh.codes + r * cp);
+    for (int ck = lane; ck < chunks; ck += 64) dst[ck] = src[ck];
+  }
+}
+
+template <int NW, int NCT, int DT, int NKS>
+__global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, RowQuant o, int64_t ntiles) {
+  using L = RowqLds<NKS>;
+  constexpr int NT = NW * 64;
+  constexpr int SB = (2 * NW * NCT * 16 * NKS + NT - 1) / NT;  // staged weight chunks per thread
+  constexpr int AC = (128 * NKS + NT - 1) / NT;                // activation chunks per thread per tile
+  using In = RowqIn<NCT, AC, EpRaw<DT, true>::W>;
+  extern __shared__ __attribute__((aligned(16))) char lds_rowq[];
+  char* wl = lds_rowq;                                                    // [2][N][RS]
+  char* abuf = wl + 2 * a.N * L::RS;                                      // [2 tiles][2][16][ARS]
+  int8_t* codes = reinterpret_cast<int8_t*>(abuf + 2 * L::ABUF);          // [16][ldq + 16]
+  float* red = reinterpret_cast<float*>(codes + 16 * (o.ldq + 16));       // [2 tiles][16][NW]
+  int32_t* redi = reinterpret_cast<int32_t*>(red + 2 * 16 * NW);         // [2 tiles][16][NW]
+  float* cwl = reinterpret_cast<float*>(redi + 2 * 16 * NW);             // [2][N]
+  const int tid = threadIdx.x;
+  const int64_t col0 = static_cast<int64_t>(tid >> 6) * NCT * 16;
+
+  // weights: every load of the stage first, then this workgroup's first tile, then the LDS writes
+  const int64_t total = 2 * a.N * NKS;
+  v4i sb[SB];
+#pragma unroll
+  for (int b = 0; b < SB; ++b) {
+    const int64_t g = tid + static_cast<int64_t>(b) * NT;
+    const int64_t gc = g < total ? g : total - 1;
+    const int64_t pn = gc / NKS, c = gc - pn * NKS;  // pn = p * N + n
+    const uint8_t* wp = pn < a.N ? a.op[0].w + pn * a.op[0].ldw : a.op[1].w + (pn - a.N) * a.op[1].ldw;
+    sb[b] = *reinterpret_cast<const v4i*>(wp + 16 * c);
+  }
+  RowqShared sh0, sh1;
+  sh0.wl = sh1.wl = wl;
+  sh0.abuf = abuf;
+  sh1.abuf = abuf + L::ABUF;
+  sh0.codes = sh1.codes = codes;
+  sh0.red = red;
+  sh1.red = red + 16 * NW;
+  sh0.redi = redi;
+  sh1.redi = redi + 16 * NW;
+  sh0.cwl = sh1.cwl = cwl;
+  In ta, tb;
+  int64_t t = blockIdx.x;
+  rowq_in_load<NW, NCT, NKS, DT, AC>(a, t, col0, tid, ta);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int b = 0; b < SB; ++b) {
+    const int64_t g = tid + static_cast<int64_t>(b) * NT;
+    if (g >= total) continue;
+    const int64_t pn = g / NKS, c = g - pn * NKS;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(wl + pn * L::RS) + c;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) dst[qq * NKS] = static_cast<uint32_t>(sb[b][qq]);
+  }
+  for (int64_t i = tid; i < a.N; i += NT) {
+    cwl[i] = a.op[0].c_w_per_row ? a.op[0].c_w[i] : a.op[0].c_w[0];
+    cwl[a.N + i] = a.op[1].c_w_per_row ? a.op[1].c_w[i] : a.op[1].c_w[0];
+  }
+  for (int64_t i = tid; i < (o.ldq + 16); i += NT) reinterpret_cast<uint4*>(codes)[i] = make_uint4(0, 0, 0, 0);
+  // (the first tile's barrier after its activation staging also orders these LDS writes)
+
+  // two tiles per iteration on ping-pong registers and LDS buffers; a prefetch past the end
+  // re-reads the current tile
+  for (;;) {
+    const int64_t t1 = t + gridDim.x;
+    rowq_in_load<NW, NCT, NKS, DT, AC>(a, t1 < ntiles ? t1 : t, col0, tid, tb);
+    rowq_tile<NW, NCT, DT, NKS, AC>(a, o, t, ta, sh0, tid);
+    if (t1 >= ntiles) break;
+    const int64_t t2 = t1 + gridDim.x;
+    rowq_in_load<NW, NCT, NKS, DT, AC>(a, t2 < ntiles ? t2 : t1, col0, tid, ta);
+    rowq_tile<NW, NCT, DT, NKS, AC>(a, o, t1, tb, sh1, tid);
+    if (t2 >= ntiles) break;
+    t = t2;
   }
 }
 
@@ -560,14 +946,76 @@ int run_mfma(const LinearArgs& a, hipStream_t st) {
   return check_launch("bitlinear mfma");
 }
 
-template <int NCT>
-int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
-  const size_t lds = static_cast<size_t>(16 * o.ldq + 2 * 16 * 4 * 4);
-  const unsigned grid = static_cast<unsigned>((a.M + 15) / 16);
+inline bool host_vec4_ok(const void* p, int64_t ld, int dt) {
+  const int64_t bytes = dt == kBF16 ? 8 : 16;
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (dt == kBF16 ? 2 : 4)) % bytes == 0;
+}
+
+struct DeviceLimits {
+  int cus = 0;
+  int64_t lds = 0;
+};
+
+// Compute units and LDS bytes per workgroup of the current device (queried once per device).
+inline DeviceLimits device_limits() {
+  static DeviceLimits cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceLimits{};
+  DeviceLimits& d = cache[dev];
+  if (d.cus == 0) {
+    int cus = 0, lds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return DeviceLimits{};
+    d.lds = lds;
+    d.cus = cus;
+  }
+  return d;
+}
+
+template <int NW, int NCT, int NKS>
+void launch_rowq_lds(const LinearArgs& a, const RowQuant& o, int64_t ntiles, int64_t lds, int cus, hipStream_t st) {
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / lds));
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ntiles, cus * per_cu));
   if (a.out_dt == kBF16)
-    gate_rowq_kernel<NCT, kBF16><<<grid, 256, lds, st>>>(a, o);
+    gate_rowq_lds_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, st>>>(a, o, ntiles);
   else
-    gate_rowq_kernel<NCT, kF32><<<grid, 256, lds, st>>>(a, o);
+    gate_rowq_lds_kernel<NW, NCT, kF32, NKS><<<grid, NW * 64, lds, st>>>(a, o, ntiles);
+}
+
+template <int NW, int NCT>
+int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
+  const bool per_row = a.op[0].c_w_per_row || a.op[1].c_w_per_row;
+  const int64_t ntiles = (a.M + 15) / 16;
+  const bool vec = a.N % 4 == 0 && host_vec4_ok(a.local, a.ld_local, a.out_dt) &&
+                   host_vec4_ok(a.gate, a.ld_gate, a.out_dt);
+  const int64_t nks = a.Kp / 64;
+  if (vec && (nks == 2 || nks == 4 || nks == 8)) {
+    const DeviceLimits dl = device_limits();
+    const int64_t lds = rowq_lds_bytes(a.N, nks, o.ldq, NW);
+    if (dl.cus > 0 && lds <= dl.lds) {
+      if (nks == 2)
+        launch_rowq_lds<NW, NCT, 2>(a, o, ntiles, lds, dl.cus, st);
+      else if (nks == 4)
+        launch_rowq_lds<NW, NCT, 4>(a, o, ntiles, lds, dl.cus, st);
+      else
+        launch_rowq_lds<NW, NCT, 8>(a, o, ntiles, lds, dl.cus, st);
+      return check_launch("output gate rowq (LDS weights)");
+    }
+  }
+  const size_t lds = static_cast<size_t>(16 * o.ldq + 2 * 16 * NW * 4 + (per_row ? 2 * a.N * 4 : 0));
+  const unsigned grid = static_cast<unsigned>(ntiles);
+  if (a.out_dt == kBF16) {
+    if (vec)
+      gate_rowq_kernel<NW, NCT, kBF16, true, 0><<<grid, NW * 64, lds, st>>>(a, o);
+    else
+      gate_rowq_kernel<NW, NCT, kBF16, false, 0><<<grid, NW * 64, lds, st>>>(a, o);
+  } else {
+    if (vec)
+      gate_rowq_kernel<NW, NCT, kF32, true, 0><<<grid, NW * 64, lds, st>>>(a, o);
+    else
+      gate_rowq_kernel<NW, NCT, kF32, false, 0><<<grid, NW * 64, lds, st>>>(a, o);
+  }
   return check_launch("output gate rowq");
 }
 
@@ -649,15 +1097,15 @@ int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
   TESM_REQUIRE(o.q && o.s && o.rs && o.ldq >= a.N && o.ldq % 16 == 0 && aligned(o.q, 16), kErrInvalidArg,
                "gate_rowq: bad code outputs");
   TESM_REQUIRE(!o.y || o.ldy >= a.N, kErrInvalidArg, "gate_rowq: bad y output");
-  const int64_t nct = (a.N + 63) / 64;
-  if (nct <= 1) return run_rowq<1>(a, o, st);
-  if (nct <= 2) return run_rowq<2>(a, o, st);
-  if (nct <= 3) return run_rowq<3>(a, o, st);
-  if (nct <= 4) return run_rowq<4>(a, o, st);
-  if (nct <= 6) return run_rowq<6>(a, o, st);
-  if (nct <= 8) return run_rowq<8>(a, o, st);
-  if (nct <= 12) return run_rowq<12>(a, o, st);
-  return run_rowq<16>(a, o, st);
+  const int64_t tiles = (a.N + 15) / 16;
+  if (tiles <= 4) return run_rowq<4, 1>(a, o, st);
+  if (tiles <= 8) return run_rowq<4, 2>(a, o, st);
+  if (tiles <= 12) return run_rowq<4, 3>(a, o, st);
+  if (tiles <= 16) return run_rowq<4, 4>(a, o, st);
+  if (tiles <= 24) return run_rowq<8, 3>(a, o, st);
+  if (tiles <= 32) return run_rowq<8, 4>(a, o, st);
+  if (tiles <= 48) return run_rowq<8, 6>(a, o, st);
+  return run_rowq<8, 8>(a, o, st);
 }
 
 }  // namespace tesm

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
       if (PHASE == 3) {
         const int64_t o = (b * a.L + t0 + i) * a.ld_states + ch;
         if constexpr (OUT_DT == kBF16 && CPT == 2) {
-          const uint32_t w = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
+          const uint32_t w = pack_bf16x2(out[0], out[1]);
           *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.states) + o) = w;
         } else {
 #pragma unroll
