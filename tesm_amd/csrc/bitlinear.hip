@@ -331,13 +331,51 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
       acc0[i][j] = v4i{0, 0, 0, 0};
       acc1[i][j] = v4i{0, 0, 0, 0};
     }
-  mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
-
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w / WN, wn = w % WN;
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
+  // plain products (one scalar c_w, no bias, no accumulator dump) take the short epilogue, whose
+  // per-row operands are requested before the main loop
+  const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
+  float sx[TM];
+  int32_t rsum[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
+    const int64_t mc = m < a.M ? m : a.M - 1;
+    sx[i] = o0.s_x[mc];
+    rsum[i] = o0.rowsum[mc];
+  }
+  const float cws = o0.c_w[0];
+  mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+
+  if (plain) {
+    const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));  // columns of this tile
+    const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
+      if (m >= a.M) continue;
+      const float inv = 1.0f / sx[i];
+      char* orow = static_cast<char*>(a.out) + (m * a.ldo + n0) * (OUT_DT == kBF16 ? 2 : 4);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nb = (wn * TN + j) * 16 + 4 * (lane >> 4);  // within the tile
+        if (nb >= nrem) continue;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc0[i][j][r] - rsum[i]) * inv) * cws;
+        if (vout && nb + 4 <= nrem) {
+          store4<OUT_DT>(orow, nb, v, true);
+        } else {
+          for (int r = 0; r < 4 && nb + r < nrem; ++r) st<OUT_DT>(orow, nb + r, v[r]);
+        }
+      }
+    }
+    return;
+  }
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
   bool vin = false;
   if constexpr (EPI == kEpiOutputGate) vin = vec4_ok<OUT_DT>(a.local, a.ld_local) && vec4_ok<OUT_DT>(a.gate, a.ld_gate);
@@ -345,8 +383,8 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   for (int i = 0; i < TM; ++i) {
     const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
     if (m >= a.M) continue;
-    const float inv0 = 1.0f / o0.s_x[m];
-    const int32_t rs0 = o0.rowsum[m];
+    const float inv0 = 1.0f / sx[i];
+    const int32_t rs0 = rsum[i];
     float inv1 = 0.0f;
     int32_t rs1 = 0;
     if constexpr (EPI == kEpiOutputGate) {
