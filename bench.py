@@ -153,6 +153,17 @@ def measure_kernels(torch, only):
     return res
 
 
+def gemm_traffic():
+    """HBM bytes per in_proj GEMM launch from the committed FETCH_SIZE / WRITE_SIZE counter runs, scaled by
+    the same counters' reading for a 256 MiB copy (profiles/in_proj_gemm_traffic.json); None if absent."""
+    path = os.path.join(ROOT, "profiles", "in_proj_gemm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(torch, seconds: float):
     """The oracle's torch path (restating the reference's kernel_backend='torch') on host cores."""
     from oracle import tesm_torch as ot
@@ -244,8 +255,10 @@ def main():
                    "weights": "INT2 ternary", "activations": "bf16"},
         "roofline": {"kernel": "in_proj INT2xINT8 MFMA GEMM (M=8192, K=768, N=2432)", "bound": "mfma",
                      "achieved": ops / t_gemm / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": ops / t_gemm / 1e12 / INT8_PEAK_TOPS, "traffic": None, "us": t_gemm * 1e6,
-                     "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak"},
+                     "frac": ops / t_gemm / 1e12 / INT8_PEAK_TOPS, "traffic": gemm_traffic(), "us": t_gemm * 1e6,
+                     "algorithmic_bytes": M * K + N * (K // 4) + 8 * M + 2 * M * N,
+                     "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes per "
+                             "launch from profiles/in_proj_gemm_traffic.json"},
         "kernels": kernels,
     }
     if not args.no_cpu:
