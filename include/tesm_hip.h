@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 1
+#define TESM_HIP_ABI_VERSION 2
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -188,9 +188,12 @@ typedef struct tesm_hip_output_gate {
 int tesm_hip_output_gate_i2(const tesm_hip_output_gate* p, void* stream);
 
 /* Whole TESM_SISO prefill forward (eval, no grad).  Replaces TESM_SISO.forward
- * (tesm.py:1175-1272) for L > 1 without an inference cache: in_proj, gates, RoPE, cross-layer
- * query bias, state scan, local entanglement, mix, state_proj/ent_proj with the output gate
- * y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(E - S), out_proj. */
+ * (tesm.py:1175-1272): in_proj, gates, RoPE, cross-layer query bias, state scan, local
+ * entanglement, mix, state_proj/ent_proj with the output gate
+ * y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(E - S), out_proj.  With k_cache and
+ * v_cache set it also fills the decode ring buffers as the reference's prefill does
+ * (tesm.py:1235-1253): the last n = min(L, window) RoPE'd keys and states go to slots
+ * window - n .. window - 1 (the caller sets cache_idx = 0, seq_pos = L, state = h_final). */
 typedef struct tesm_hip_siso_layer {
   int dt;                     /* activations / module dtype */
   int64_t B, L, d_model, d_state, ent_rank, window, chunk_size;
@@ -206,10 +209,44 @@ typedef struct tesm_hip_siso_layer {
   void* states;               /* (B, L, d_state) in dt */
   double* h_final;            /* optional (B, d_state) */
   void* proj_out;             /* optional (B, L, N_in) copy target; NULL = workspace only */
+  void* k_cache;              /* optional (B, window, ent_rank) ring of keys, cache_dt */
+  void* v_cache;              /* optional (B, window, d_state) ring of states, cache_dt */
+  int cache_dt;               /* 0 f32, 1 bf16 */
 } tesm_hip_siso_layer;
 
 int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p);
 int tesm_hip_siso_prefill(const tesm_hip_siso_layer* p, void* ws, int64_t ws_bytes, void* stream);
+
+/* One TESM_SISO decode step for B sequences (one token each).  Replaces
+ * TESM_SISO._forward_incremental (tesm.py:1274-1400) on the cache of allocate_inference_cache
+ * (tesm.py:620-670): in_proj, gates, RoPE at position seq_pos, cross-layer query, the float64
+ * state update new = decay * state + write * tanh(sv), ring write of (key, new) at slot cache_idx,
+ * window scores over the ring in the reference's read order, strict ternary, count
+ * normalisation, mix, the output gate and out_proj.  The caller then advances the host
+ * bookkeeping: cache_idx = (cache_idx + 1) % window, seq_pos += 1. */
+typedef struct tesm_hip_siso_step {
+  int dt;                     /* module dtype */
+  int cache_dt;               /* ring buffer dtype: 0 f32, 1 bf16 */
+  int64_t B, d_model, d_state, ent_rank, window;
+  int64_t seq_pos;            /* tokens seen before this one (its RoPE position) */
+  int64_t cache_idx;          /* ring slot this step writes */
+  float bit_eps, thr, ent_scale;
+  const void* u;              /* (B, d_model) in dt */
+  tesm_hip_linear in_proj, state_proj, ent_proj, out_proj, cross_q_proj;
+  const void* decay_bias;     /* (d_state) in dt */
+  const float* local_bias;    /* (window) float32 holding dt values */
+  const void* rope;           /* tesm_hip_rope_table with at least seq_pos + 1 rows from position 0 */
+  const void* cross_state;    /* optional (B, d_state) in dt */
+  const double* state;        /* (B, d_state) float64 state before the step */
+  double* state_out;          /* (B, d_state) float64 state after the step (may equal state) */
+  void* k_cache;              /* (B, window, ent_rank) cache_dt, updated in place */
+  void* v_cache;              /* (B, window, d_state) cache_dt, updated in place */
+  void* y;                    /* (B, d_model) in dt */
+  void* new_state;            /* optional (B, d_state) in dt: this step's state */
+} tesm_hip_siso_step;
+
+int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);
+int tesm_hip_siso_decode(const tesm_hip_siso_step* p, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -71,6 +71,22 @@ class SisoLayer(ctypes.Structure):
         ("cross_q_proj", Linear),
         ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P), ("h0", P),
         ("y", P), ("states", P), ("h_final", P), ("proj_out", P),
+        ("k_cache", P), ("v_cache", P), ("cache_dt", I32),
+    ]
+
+
+class SisoStep(ctypes.Structure):
+    """``tesm_hip_siso_step``."""
+    _fields_ = [
+        ("dt", I32), ("cache_dt", I32),
+        ("B", I64), ("d_model", I64), ("d_state", I64), ("ent_rank", I64), ("window", I64),
+        ("seq_pos", I64), ("cache_idx", I64),
+        ("bit_eps", F32), ("thr", F32), ("ent_scale", F32),
+        ("u", P),
+        ("in_proj", Linear), ("state_proj", Linear), ("ent_proj", Linear), ("out_proj", Linear),
+        ("cross_q_proj", Linear),
+        ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P),
+        ("state", P), ("state_out", P), ("k_cache", P), ("v_cache", P), ("y", P), ("new_state", P),
     ]
 
 
@@ -94,6 +110,8 @@ _SIGNATURES = {
     "tesm_hip_output_gate_i2": ([ctypes.POINTER(OutputGate), P], I32),
     "tesm_hip_siso_prefill_ws_bytes": ([ctypes.POINTER(SisoLayer)], I64),
     "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
+    "tesm_hip_siso_decode_ws_bytes": ([ctypes.POINTER(SisoStep)], I64),
+    "tesm_hip_siso_decode": ([ctypes.POINTER(SisoStep), P, I64, P], I32),
 }
 
 _lock = threading.Lock()

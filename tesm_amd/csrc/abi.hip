@@ -4,6 +4,7 @@
 #include <cstring>
 #include <string>
 
+#include "decode.h"
 #include "entangle.h"
 #include "scan.h"
 #include "tesm_hip_internal.h"
@@ -156,6 +157,85 @@ int run_linear(const CodeBuf& x, const tesm_hip_linear& w, int64_t M, int64_t N,
   a.out_dt = dt;
   a.ldo = ldo;
   return launch_linear(a, st);
+}
+
+// state_proj(tanh E), ent_proj(C) and the output gate y = local + sigmoid(gate) * sp + ep
+// (tesm.py:1256-1260), quantized per token for out_proj, then out_proj (tesm.py:1261; dropout is
+// identity in eval).  Rows: M; local / gate are column slices of the in_proj output.
+struct OutputPath {
+  CodeBuf xe, xc, xy;
+  void* yg;  // (M, d_model) scratch for the tiled gate when the row-complete kernel cannot run
+  const tesm_hip_linear *state_proj, *ent_proj, *out_proj;
+  int64_t M, dm, D;
+  int dt;
+  float eps;
+  const void* local;
+  const void* gate;
+  int64_t ld;
+  void* y;
+};
+
+int run_output_path(const OutputPath& o, hipStream_t st) {
+  LinearArgs ga;
+  ga.op[0] = operand(o.xe, *o.state_proj);
+  ga.op[1] = operand(o.xc, *o.ent_proj);
+  ga.M = o.M;
+  ga.N = o.dm;
+  ga.Kp = kpad(o.D);
+  ga.out_dt = o.dt;
+  ga.epilogue = kEpiOutputGate;
+  ga.local = o.local;
+  ga.ld_local = o.ld;
+  ga.gate = o.gate;
+  ga.ld_gate = o.ld;
+  int rc;
+  if (!o.yg) {
+    RowQuant rq;
+    rq.q = o.xy.q;
+    rq.ldq = o.xy.ldq;
+    rq.s = o.xy.s;
+    rq.rs = o.xy.rs;
+    rq.eps = o.eps;
+    if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
+  } else {
+    ga.out = o.yg;
+    ga.ldo = o.dm;
+    if ((rc = launch_linear(ga, st))) return rc;
+    if ((rc = launch_quant_act(o.yg, o.dt, o.M, o.dm, o.dm, o.eps, 1, o.xy.q, o.xy.ldq, o.xy.s, o.xy.rs, st)))
+      return rc;
+  }
+  return run_linear(o.xy, *o.out_proj, o.M, o.dm, o.dm, o.y, o.dt, o.dm, st);
+}
+
+// Workspace layout of the SISO decode step; with base == nullptr it only measures.
+struct DecodePlan {
+  CodeBuf xu, xs, xe, xc, xy;
+  void* proj;
+  void* cq;
+  void* yg;
+  int64_t total;
+};
+
+DecodePlan plan_decode(const tesm_hip_siso_step& p, void* base) {
+  Carve c(base);
+  DecodePlan s;
+  const int64_t n_in = 2 * p.d_model + 3 * p.d_state + 2 * p.ent_rank;
+  const int es = esize(p.dt);
+  s.xu = take_codes(c, p.B, p.d_model);
+  s.proj = c.take<void>(p.B * n_in * es);
+  if (p.cross_state) {
+    s.xs = take_codes(c, p.B, p.d_state);
+    s.cq = c.take<void>(p.B * p.ent_rank * es);
+  } else {
+    s.xs = CodeBuf{nullptr, nullptr, nullptr, 0};
+    s.cq = nullptr;
+  }
+  s.xe = take_codes(c, p.B, p.d_state);
+  s.xc = take_codes(c, p.B, p.d_state);
+  s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(p.B * p.d_model * es);
+  s.xy = take_codes(c, p.B, p.d_model);
+  s.total = c.off;
+  return s;
 }
 
 }  // namespace
@@ -466,35 +546,147 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
       return rc;
   }
-  // 5. state_proj(tanh E), ent_proj(C) and the output gate (tesm.py:1256-1260), quantized for out_proj
-  LinearArgs ga;
-  ga.op[0] = operand(s.xe, p.state_proj);
-  ga.op[1] = operand(s.xc, p.ent_proj);
-  ga.M = M;
-  ga.N = dm;
-  ga.Kp = kpad(D);
-  ga.out_dt = dt;
-  ga.epilogue = kEpiOutputGate;
-  ga.local = proj + o_local * es;
-  ga.ld_local = n_in;
-  ga.gate = proj + o_gate * es;
-  ga.ld_gate = n_in;
-  if (s.rowq) {
-    RowQuant rq;
-    rq.q = s.xy.q;
-    rq.ldq = s.xy.ldq;
-    rq.s = s.xy.s;
-    rq.rs = s.xy.rs;
-    rq.eps = p.bit_eps;
-    if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
-  } else {
-    ga.out = s.yg;
-    ga.ldo = dm;
-    if ((rc = launch_linear(ga, st))) return rc;
-    if ((rc = launch_quant_act(s.yg, dt, M, dm, dm, p.bit_eps, 1, s.xy.q, s.xy.ldq, s.xy.s, s.xy.rs, st))) return rc;
+  // 5. decode caches (tesm.py:1235-1253)
+  if (p.k_cache || p.v_cache) {
+    CacheFillArgs cf;
+    cf.dt = dt;
+    cf.cdt = p.cache_dt;
+    cf.B = p.B;
+    cf.L = p.L;
+    cf.R = R;
+    cf.D = D;
+    cf.W = p.window;
+    cf.k = proj + o_k * es;
+    cf.ld_k = n_in;
+    cf.rope = static_cast<const float2*>(p.rope);
+    cf.states = p.states;
+    cf.ld_states = D;
+    cf.k_cache = p.k_cache;
+    cf.v_cache = p.v_cache;
+    if ((rc = launch_cache_fill(cf, st))) return rc;
   }
-  // 6. out_proj (tesm.py:1261; dropout is identity in eval)
-  return run_linear(s.xy, p.out_proj, M, dm, dm, p.y, dt, dm, st);
+  // 6. output gate and out_proj
+  OutputPath op;
+  op.xe = s.xe;
+  op.xc = s.xc;
+  op.xy = s.xy;
+  op.yg = s.rowq ? nullptr : s.yg;
+  op.state_proj = &p.state_proj;
+  op.ent_proj = &p.ent_proj;
+  op.out_proj = &p.out_proj;
+  op.M = M;
+  op.dm = dm;
+  op.D = D;
+  op.dt = dt;
+  op.eps = p.bit_eps;
+  op.local = proj + o_local * es;
+  op.gate = proj + o_gate * es;
+  op.ld = n_in;
+  op.y = p.y;
+  return run_output_path(op, st);
+}
+
+int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p) {
+  if (!p) return -1;
+  return plan_decode(*p, nullptr).total;
+}
+
+int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso decode: null descriptor");
+  const tesm_hip_siso_step& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso decode: dtype must be 0 or 1");
+  TESM_REQUIRE(p.B >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.ent_rank >= 2 && p.ent_rank % 2 == 0 &&
+                   p.window >= 1 && p.window <= 64 && p.seq_pos >= 0 && p.cache_idx >= 0 && p.cache_idx < p.window,
+               kErrInvalidArg, "siso decode: bad sizes or ring position (need even ent_rank, 1 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.state && p.state_out && p.k_cache && p.v_cache &&
+                   p.y,
+               kErrInvalidArg, "siso decode: null pointer");
+  if (int rc = check_linear(p.in_proj, p.d_model, "in_proj")) return rc;
+  if (int rc = check_linear(p.state_proj, p.d_state, "state_proj")) return rc;
+  if (int rc = check_linear(p.ent_proj, p.d_state, "ent_proj")) return rc;
+  if (int rc = check_linear(p.out_proj, p.d_model, "out_proj")) return rc;
+  if (p.cross_state)
+    if (int rc = check_linear(p.cross_q_proj, p.d_state, "cross_q_proj")) return rc;
+  const DecodePlan s = plan_decode(p, ws);
+  TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "siso decode: workspace too small");
+
+  const int dt = p.dt;
+  const int es = esize(dt);
+  const int64_t Bn = p.B, dm = p.d_model, D = p.d_state, R = p.ent_rank;
+  const int64_t n_in = 2 * dm + 3 * D + 2 * R;
+  char* proj = static_cast<char*>(s.proj);
+  const int64_t o_local = 0, o_sv = dm, o_decay = dm + D, o_write = dm + 2 * D, o_gate = dm + 3 * D,
+                o_q = 2 * dm + 3 * D, o_k = 2 * dm + 3 * D + R;
+  int rc;
+  // 1. in_proj on the B new tokens
+  if ((rc = launch_quant_act(p.u, dt, Bn, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  if ((rc = run_linear(s.xu, p.in_proj, Bn, n_in, dm, proj, dt, n_in, st))) return rc;
+  // 2. cross-layer query (tesm.py:1302-1305)
+  if (p.cross_state) {
+    if ((rc = launch_quant_act(p.cross_state, dt, Bn, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs, st)))
+      return rc;
+    if ((rc = run_linear(s.xs, p.cross_q_proj, Bn, R, D, s.cq, dt, R, st))) return rc;
+  }
+  // 3. state update, ring write, window entanglement, codes of tanh(E) and C
+  DecodeArgs da;
+  da.dt = dt;
+  da.cdt = p.cache_dt;
+  da.B = Bn;
+  da.R = R;
+  da.D = D;
+  da.W = p.window;
+  da.pos = p.seq_pos;
+  da.slot = p.cache_idx;
+  da.valid = std::min<int64_t>(p.seq_pos + 1, p.window);
+  da.full = da.valid >= p.window;
+  da.proj = proj;
+  da.ld_proj = n_in;
+  da.o_sv = o_sv;
+  da.o_decay = o_decay;
+  da.o_write = o_write;
+  da.o_q = o_q;
+  da.o_k = o_k;
+  da.rope = static_cast<const float2*>(p.rope);
+  da.decay_bias = p.decay_bias;
+  da.bias = p.local_bias;
+  da.q_add = s.cq;
+  da.ld_qadd = R;
+  da.thr = p.thr;
+  da.ent_scale = p.ent_scale;
+  da.eps = p.bit_eps;
+  da.state = p.state;
+  da.state_out = p.state_out;
+  da.k_cache = p.k_cache;
+  da.v_cache = p.v_cache;
+  da.new_state = p.new_state;
+  da.q_te = s.xe.q;
+  da.s_te = s.xe.s;
+  da.rs_te = s.xe.rs;
+  da.q_c = s.xc.q;
+  da.s_c = s.xc.s;
+  da.rs_c = s.xc.rs;
+  da.ldq = s.xe.ldq;
+  if ((rc = launch_decode_ent(da, st))) return rc;
+  // 4. output gate and out_proj
+  OutputPath op;
+  op.xe = s.xe;
+  op.xc = s.xc;
+  op.xy = s.xy;
+  op.yg = s.yg;
+  op.state_proj = &p.state_proj;
+  op.ent_proj = &p.ent_proj;
+  op.out_proj = &p.out_proj;
+  op.M = Bn;
+  op.dm = dm;
+  op.D = D;
+  op.dt = dt;
+  op.eps = p.bit_eps;
+  op.local = proj + o_local * es;
+  op.gate = proj + o_gate * es;
+  op.ld = n_in;
+  op.y = p.y;
+  return run_output_path(op, st);
 }
 
 }  // extern "C"

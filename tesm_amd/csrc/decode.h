@@ -1,0 +1,59 @@
+// TESM_SISO decode step and prefill cache fill: arguments shared by the kernels and the drivers.
+#pragma once
+
+#include "entangle.h"
+
+namespace tesm {
+
+// One decode step of the entanglement block for B rows (one token each).
+struct DecodeArgs {
+  int dt = 0;                  // layer dtype
+  int cdt = 0;                 // ring buffer dtype
+  int64_t B = 0, R = 0, D = 0, W = 0;
+  int64_t pos = 0;             // RoPE position of this token (seq_pos before the step)
+  int64_t slot = 0;            // ring slot written by this step (cache_idx)
+  int64_t valid = 0;           // min(seq_pos + 1, W)
+  int full = 0;                // valid >= W
+  // in_proj output (B, ld_proj) in dt; column offsets of the sv, decay, write, q and k slices
+  const void* proj = nullptr;
+  int64_t ld_proj = 0, o_sv = 0, o_decay = 0, o_write = 0, o_q = 0, o_k = 0;
+  const float2* rope = nullptr;     // table whose row `pos` holds this token's (cos, sin)
+  const void* decay_bias = nullptr; // (D) dt
+  const float* bias = nullptr;      // (W) window bias, dt values as floats
+  const void* q_add = nullptr;      // optional (B, ld_qadd) cross-layer query in dt
+  int64_t ld_qadd = 0;
+  float thr = 0.0f, ent_scale = 0.0f, eps = 1e-5f;
+  const double* state = nullptr;    // (B, D) float64 before the step
+  double* state_out = nullptr;      // (B, D) float64 after the step (may equal state)
+  void* k_cache = nullptr;          // (B, W, R) cdt
+  void* v_cache = nullptr;          // (B, W, D) cdt
+  void* new_state = nullptr;        // optional (B, D) dt: the step's state (next layer's cross state)
+  // int8 codes (layout 1), scales and row sums of tanh(E) and C = E - S
+  int8_t* q_te = nullptr;
+  float* s_te = nullptr;
+  int32_t* rs_te = nullptr;
+  int8_t* q_c = nullptr;
+  float* s_c = nullptr;
+  int32_t* rs_c = nullptr;
+  int64_t ldq = 0;
+};
+
+int64_t decode_lds_bytes(int64_t R, int64_t D);
+int launch_decode_ent(const DecodeArgs& a, hipStream_t st);
+
+// Ring buffers after a prefill of L tokens: the last min(L, W) RoPE'd keys and states.
+struct CacheFillArgs {
+  int dt = 0, cdt = 0;
+  int64_t B = 0, L = 0, R = 0, D = 0, W = 0;
+  const void* k = nullptr;          // raw (pre-RoPE) keys, element (b, t, r) at k[(b*L + t)*ld_k + r]
+  int64_t ld_k = 0;
+  const float2* rope = nullptr;     // (L, R/2) table, positions 0..L-1
+  const void* states = nullptr;     // (b, t, d) at states[(b*L + t)*ld_states + d]
+  int64_t ld_states = 0;
+  void* k_cache = nullptr;          // (B, W, R) cdt
+  void* v_cache = nullptr;          // (B, W, D) cdt
+};
+
+int launch_cache_fill(const CacheFillArgs& a, hipStream_t st);
+
+}  // namespace tesm

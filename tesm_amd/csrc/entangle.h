@@ -4,7 +4,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.h"
+
 namespace tesm {
+
+// One RoPE'd pair (x[i], x[i + R/2]) rotated by (c, s), rounded like the reference (tesm.py:789-793).
+template <int DT>
+__device__ __forceinline__ void rope_pair(float xa, float xb, float2 cs, float& o1, float& o2) {
+  o1 = rnd<DT>(rnd<DT>(xa * cs.x) - rnd<DT>(xb * cs.y));
+  o2 = rnd<DT>(rnd<DT>(xa * cs.y) + rnd<DT>(xb * cs.x));
+}
 
 // RoPE table: tab[(t * (R/2) + i)] = (cos, sin) of (pos_offset + t) * inv_freq[i], rounded to dt.
 int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, double base, int dt, hipStream_t st);

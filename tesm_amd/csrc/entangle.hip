@@ -40,13 +40,6 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2* __restrict__ ta
   tab[idx] = make_float2(rnd<DT>(static_cast<float>(cos(thd))), rnd<DT>(static_cast<float>(sin(thd))));
 }
 
-// One RoPE'd pair (x[i], x[i + R/2]) rotated by (c, s), rounded like the reference.
-template <int DT>
-__device__ __forceinline__ void rope_pair(float xa, float xb, float2 cs, float& o1, float& o2) {
-  o1 = rnd<DT>(rnd<DT>(xa * cs.x) - rnd<DT>(xb * cs.y));
-  o2 = rnd<DT>(rnd<DT>(xa * cs.y) + rnd<DT>(xb * cs.x));
-}
-
 template <int DT, int MIMO, int WP>
 __global__ __launch_bounds__(256) void ent_scores_kernel(EntArgs a, int64_t weff, float inv_unused) {
   const int lane = threadIdx.x & 63;

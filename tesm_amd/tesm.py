@@ -148,18 +148,19 @@ class TESM_SISO(nn.Module):
         if self.entanglement_window <= 0:
             raise backend_error(self.kernel_backend, "global entanglement",
                                 "entanglement_window=0 is not implemented by the hip backend yet")
-        y, states, h_final = self._prefill(u, cross_layer_state, prev_state)
+        cache = None
         if inference_params is not None:  # tesm.py:1235-1253
             cache = inference_params.get("state_cache")
-            if cache is not None and "state" in cache:
-                self._write_prefill_cache(cache, u, states, h_final)
+            if cache is None or "state" not in cache:
+                cache = None
+        y, states, h_final = self._prefill(u, cross_layer_state, prev_state, cache)
         self._last_cross_layer_state = states
         self._last_scan_state_f64 = h_final
         self.last_entanglement_map = None
         self.last_entanglement_stats = None
         return y, h_final
 
-    def _prefill(self, u, cross_layer_state, prev_state):
+    def _prefill(self, u, cross_layer_state, prev_state, cache=None):
         lib = _lib.load()
         dt = u.dtype
         B, L, dm = u.shape
@@ -205,12 +206,43 @@ class TESM_SISO(nn.Module):
         desc.y = y.data_ptr()
         desc.states = states.data_ptr()
         desc.h_final = h_final.data_ptr()
+        k_cache = v_cache = None
+        if cache is not None:
+            k_cache, v_cache = self._prefill_cache_buffers(cache, B, L, dev)
+            desc.k_cache, desc.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+            desc.cache_dt = hip_ops.dt_code(k_cache.dtype)
         nbytes = int(lib.tesm_hip_siso_prefill_ws_bytes(ctypes.byref(desc)))
         with torch.cuda.device(dev):
             ws = workspace(dev, nbytes)
             _lib.check(lib.tesm_hip_siso_prefill(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                                  ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        if cache is not None:  # tesm.py:1240-1252
+            cache["state"] = h_final.clone()
+            cache["seq_pos"] = L
+            cache["ent_k_cache"], cache["ent_v_cache"] = k_cache, v_cache
+            cache["cache_idx"] = 0
         return y, states, h_final
+
+    def _prefill_cache_buffers(self, cache, B, L, dev):
+        """Ring buffers the prefill writes: with L >= W the reference replaces them by new float32
+        tensors (tesm.py:1244-1247), otherwise it writes the last L slots of the existing ones."""
+        kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
+        W = kc.shape[1]
+        if L >= W:
+            return (torch.empty(B, W, self.ent_rank, dtype=torch.float32, device=dev),
+                    torch.empty(B, W, self.d_state, dtype=torch.float32, device=dev))
+        self._check_cache(kc, vc, B, dev)
+        return kc, vc
+
+    def _check_cache(self, kc, vc, B, dev):
+        W = kc.shape[1] if kc.dim() == 3 else -1
+        ok = (kc.dim() == 3 and vc.dim() == 3 and tuple(kc.shape) == (B, W, self.ent_rank)
+              and tuple(vc.shape) == (B, W, self.d_state) and kc.dtype == vc.dtype
+              and kc.dtype in (torch.float32, torch.bfloat16) and kc.is_contiguous() and vc.is_contiguous()
+              and kc.device == dev and vc.device == dev and 1 <= W <= 64)
+        if not ok:
+            raise RuntimeError("TESM hip decode: the inference cache must hold contiguous (B, W, ent_rank) and "
+                               "(B, W, d_state) float32 or bfloat16 ring buffers on the layer's device, W <= 64")
 
     # -- inference cache (tesm.py:620-670, 1235-1253) -----------------------------------
     def allocate_inference_cache(self, batch_size, max_seqlen, dtype=None, **kwargs):
@@ -229,11 +261,76 @@ class TESM_SISO(nn.Module):
             "cache_filled": False,
         }
 
-    def _write_prefill_cache(self, cache, u, states, h_final):
-        raise backend_error(self.kernel_backend, "TESM prefill-with-cache", "decode caches are not wired yet")
-
     def _forward_incremental(self, u, inference_params, cross_layer_state=None):
-        raise backend_error(self.kernel_backend, "TESM decode", "the incremental decode step is not wired yet")
+        """One decode step per sequence (tesm.py:1274-1400); returns ``(y (B, 1, d_model), state f64)``."""
+        lib = _lib.load()
+        cache = inference_params["state_cache"]
+        dt = u.dtype
+        B, _, dm = u.shape
+        D, R = self.d_state, self.ent_rank
+        dev = u.device
+        if self.entanglement_window <= 0:
+            raise backend_error(self.kernel_backend, "global entanglement decode",
+                                "entanglement_window=0 is not implemented by the hip backend yet")
+        for p in (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj):
+            if p.weight.dtype != dt:
+                raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
+        kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
+        self._check_cache(kc, vc, B, dev)
+        W = kc.shape[1]
+        state = cache["state"]
+        if state.dtype != torch.float64 or tuple(state.shape) != (B, D) or state.device != dev:
+            raise RuntimeError("TESM hip decode: cache['state'] must be a (B, d_state) float64 tensor on the layer's "
+                               "device")
+        state = state.contiguous()
+        pos = int(cache["seq_pos"])
+        slot = int(cache.get("cache_idx", 0))
+        u = u.reshape(B, dm).contiguous()
+        cs = None
+        if cross_layer_state is not None:
+            cs = cross_layer_state.reshape(B, D).to(dt).contiguous()
+        y = torch.empty((B, 1, dm), dtype=dt, device=dev)
+        state_out = torch.empty_like(state)
+        new = torch.empty((B, D), dtype=dt, device=dev)
+        decay_bias = self._decay_bias_dt(dt)
+        local_bias = self._local_bias_f32(dt)
+        rope = self.rope_table(pos + 1, dt, dev)
+        hip_ops.require_device(u, cs, state, kc, vc, decay_bias, local_bias, rope, y, state_out, new)
+        desc = _lib.SisoStep()
+        desc.dt = hip_ops.dt_code(dt)
+        desc.cache_dt = hip_ops.dt_code(kc.dtype)
+        desc.B, desc.d_model, desc.d_state, desc.ent_rank, desc.window = B, dm, D, R, W
+        desc.seq_pos, desc.cache_idx = pos, slot
+        desc.bit_eps = self.in_proj.bit_eps
+        desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
+        desc.ent_scale = float(self.entanglement_scale)
+        desc.u = u.data_ptr()
+        desc.in_proj = self.in_proj.linear_desc()
+        desc.state_proj = self.state_proj.linear_desc()
+        desc.ent_proj = self.ent_proj.linear_desc()
+        desc.out_proj = self.out_proj.linear_desc()
+        if cs is not None:
+            desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
+            desc.cross_state = cs.data_ptr()
+        desc.decay_bias = decay_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr()
+        desc.rope = rope.data_ptr()
+        desc.state, desc.state_out = state.data_ptr(), state_out.data_ptr()
+        desc.k_cache, desc.v_cache = kc.data_ptr(), vc.data_ptr()
+        desc.y = y.data_ptr()
+        desc.new_state = new.data_ptr()
+        nbytes = int(lib.tesm_hip_siso_decode_ws_bytes(ctypes.byref(desc)))
+        with torch.cuda.device(dev):
+            ws = workspace(dev, nbytes)
+            _lib.check(lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                                ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        cache["cache_idx"] = (slot + 1) % W
+        cache["state"] = state_out
+        cache["seq_pos"] = pos + 1
+        self._last_cross_layer_state = new
+        self._last_scan_state_f64 = state_out
+        self.last_entanglement_map = None
+        return y, state_out
 
 
 TESM = TESM_SISO
