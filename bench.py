@@ -153,6 +153,30 @@ def measure_kernels(torch, only):
     return res
 
 
+def measure_decode(torch, m, steps: int = 50):
+    """configs[3] decode: B = 32 sequences, caches filled by a 64-token prefill (>= W), then one-token
+    steps; returns the per-step time (device events around `steps` consecutive steps)."""
+    Bd, P = 32, 64
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(1)
+    u = torch.randn(Bd, P + steps + 3, LAYER["d_model"], generator=g).to(torch.bfloat16).to(dev)
+    cache = m.allocate_inference_cache(Bd, P + steps + 3)
+    ip = {"state_cache": cache}
+    m(u[:, :P], inference_params=ip)
+    for t in range(P, P + 3):
+        m(u[:, t:t + 1], inference_params=ip)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(P + 3, P + 3 + steps):
+        m(u[:, t:t + 1], inference_params=ip)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"batch": Bd, "prefill": P, "ms_per_step": ms, "tokens_per_s": Bd / (ms * 1e-3),
+            "note": "one decode step per sequence, host dispatch included (no graph capture)"}
+
+
 def gemm_traffic():
     """HBM bytes per in_proj GEMM launch from the committed FETCH_SIZE / WRITE_SIZE counter runs, scaled by
     the same counters' reading for a 256 MiB copy (profiles/in_proj_gemm_traffic.json); None if absent."""
@@ -230,6 +254,7 @@ def main():
         t_gemm = time_launches(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K, torch.bfloat16,
                                                                   out=out), 50)
         ops = 2 * M * N * K
+        decode = measure_decode(torch, m)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
         if args.only:
             print(json.dumps({"kernels": kernels}))
@@ -259,6 +284,7 @@ def main():
                      "algorithmic_bytes": M * K + N * (K // 4) + 8 * M + 2 * M * N,
                      "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes per "
                              "launch from profiles/in_proj_gemm_traffic.json"},
+        "decode": decode,
         "kernels": kernels,
     }
     if not args.no_cpu:

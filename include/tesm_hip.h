@@ -248,6 +248,44 @@ typedef struct tesm_hip_siso_step {
 int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);
 int tesm_hip_siso_decode(const tesm_hip_siso_step* p, void* ws, int64_t ws_bytes, void* stream);
 
+/* MIMO rank merge factors.  TESMMIMO_Optimized expands each head's update into mimo_rank copies
+ * scaled by mimo_x and merges the entangled copies with mimo_o (tesm_mimo.py:963-1017); the scan
+ * and the window mix are linear in the update and the window weights do not depend on the rank,
+ * so the merge is the per-channel factor coef[h,d] = sum_r mimo_x[h,r,d]^2 * mimo_o[h,r,d] and the
+ * rank-0 states are x0sq[h,d] = mimo_x[h,0,d]^2 times the rank-free ones.  mimo_x, mimo_o:
+ * (n_heads, mimo_rank, d_state) in dt; coef, x0sq: (n_heads, d_state) float32. */
+int tesm_hip_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t n_heads, int64_t mimo_rank,
+                       int64_t d_state, float* coef, float* x0sq, void* stream);
+
+/* Whole TESMMIMO_Optimized prefill forward (eval, no grad).  Replaces TESMMIMO_Optimized.forward
+ * (tesm_mimo.py:914-1062) with the ranks collapsed (tesm_hip_mimo_coef): in_proj, per-head gates,
+ * one float32 state scan over n_heads * d_state channels (tesm_mimo.py:375-392), RoPE, the
+ * per-head window entanglement with the reference's early-window truncation (tesm_mimo.py:525-588),
+ * the rank merge, state_proj(tanh) / ent_proj with the output gate, out_proj.  With k_cache and
+ * v_cache set it fills the decode ring buffers with the last min(L, window) RoPE'd keys and rank-0
+ * states (tesm_mimo.py:1022-1037). */
+typedef struct tesm_hip_mimo_layer {
+  int dt;                     /* activations / module dtype */
+  int64_t B, L, d_model, d_state, n_heads, ent_rank, window;
+  float bit_eps, thr, ent_scale;
+  const void* u;              /* (B, L, d_model), contiguous */
+  tesm_hip_linear in_proj, state_proj, ent_proj, out_proj;
+  const void* decay_bias;     /* (n_heads, d_state) in dt */
+  const float* local_bias;    /* (n_heads, window) float32 holding dt values */
+  const void* rope;           /* tesm_hip_rope_table(L, ent_rank, 0) */
+  const float* mimo_coef;     /* (n_heads, d_state) from tesm_hip_mimo_coef */
+  const float* mimo_x0sq;     /* (n_heads, d_state) from tesm_hip_mimo_coef */
+  void* y;                    /* (B, L, d_model) */
+  double* h_final;            /* optional (B, n_heads, d_state): rank-0 state after the last token */
+  float* last_state;          /* optional (B, n_heads, d_state): the same in float32 */
+  void* k_cache;              /* optional (B, window, n_heads, ent_rank), cache_dt */
+  void* v_cache;              /* optional (B, window, n_heads, d_state), cache_dt */
+  int cache_dt;               /* 0 f32, 1 bf16 */
+} tesm_hip_mimo_layer;
+
+int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p);
+int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* p, void* ws, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -90,6 +90,20 @@ class SisoStep(ctypes.Structure):
     ]
 
 
+class MimoLayer(ctypes.Structure):
+    """``tesm_hip_mimo_layer``."""
+    _fields_ = [
+        ("dt", I32),
+        ("B", I64), ("L", I64), ("d_model", I64), ("d_state", I64), ("n_heads", I64), ("ent_rank", I64),
+        ("window", I64),
+        ("bit_eps", F32), ("thr", F32), ("ent_scale", F32),
+        ("u", P),
+        ("in_proj", Linear), ("state_proj", Linear), ("ent_proj", Linear), ("out_proj", Linear),
+        ("decay_bias", P), ("local_bias", P), ("rope", P), ("mimo_coef", P), ("mimo_x0sq", P),
+        ("y", P), ("h_final", P), ("last_state", P), ("k_cache", P), ("v_cache", P), ("cache_dt", I32),
+    ]
+
+
 _SIGNATURES = {
     "tesm_hip_abi_version": ([], I32),
     "tesm_hip_last_error": ([], ctypes.c_char_p),
@@ -112,6 +126,9 @@ _SIGNATURES = {
     "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
     "tesm_hip_siso_decode_ws_bytes": ([ctypes.POINTER(SisoStep)], I64),
     "tesm_hip_siso_decode": ([ctypes.POINTER(SisoStep), P, I64, P], I32),
+    "tesm_hip_mimo_coef": ([P, P, I32, I64, I64, I64, P, P, P], I32),
+    "tesm_hip_mimo_prefill_ws_bytes": ([ctypes.POINTER(MimoLayer)], I64),
+    "tesm_hip_mimo_prefill": ([ctypes.POINTER(MimoLayer), P, I64, P], I32),
 }
 
 _lock = threading.Lock()

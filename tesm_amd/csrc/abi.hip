@@ -6,6 +6,7 @@
 
 #include "decode.h"
 #include "entangle.h"
+#include "mimo.h"
 #include "scan.h"
 #include "tesm_hip_internal.h"
 #include "../../include/tesm_hip.h"
@@ -234,6 +235,42 @@ DecodePlan plan_decode(const tesm_hip_siso_step& p, void* base) {
   s.xc = take_codes(c, p.B, p.d_state);
   s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(p.B * p.d_model * es);
   s.xy = take_codes(c, p.B, p.d_model);
+  s.total = c.off;
+  return s;
+}
+
+// Workspace layout of the MIMO prefill; with base == nullptr it only measures.
+struct MimoPlan {
+  CodeBuf xu, xe, xc, xy;
+  void* proj;
+  void* scan_ws;
+  int64_t scan_bytes;
+  float* S;
+  float* wts;
+  void* te;
+  void* cc;
+  void* yg;
+  int64_t total;
+};
+
+MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
+  Carve c(base);
+  MimoPlan s;
+  const int64_t M = p.B * p.L, HD = p.n_heads * p.d_state;
+  const int64_t n_in = 2 * p.d_model + 3 * HD + 2 * p.n_heads * p.ent_rank;
+  const int es = esize(p.dt);
+  s.xu = take_codes(c, M, p.d_model);
+  s.proj = c.take<void>(M * n_in * es);
+  s.scan_bytes = scan_ws_bytes(p.B, p.L, HD, 16);
+  s.scan_ws = c.take<void>(s.scan_bytes);
+  s.S = c.take<float>(M * HD * 4);
+  s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, p.n_heads, p.window));
+  s.te = c.take<void>(M * HD * es);
+  s.cc = c.take<void>(M * HD * es);
+  s.xe = take_codes(c, M, HD);
+  s.xc = take_codes(c, M, HD);
+  s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(M * p.d_model * es);
+  s.xy = take_codes(c, M, p.d_model);
   s.total = c.off;
   return s;
 }
@@ -680,6 +717,151 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   op.M = Bn;
   op.dm = dm;
   op.D = D;
+  op.dt = dt;
+  op.eps = p.bit_eps;
+  op.local = proj + o_local * es;
+  op.gate = proj + o_gate * es;
+  op.ld = n_in;
+  op.y = p.y;
+  return run_output_path(op, st);
+}
+
+int tesm_hip_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t n_heads, int64_t mimo_rank,
+                       int64_t d_state, float* coef, float* x0sq, void* stream) {
+  return launch_mimo_coef(mimo_x, mimo_o, dt, n_heads, mimo_rank, d_state, coef, x0sq,
+                          static_cast<hipStream_t>(stream));
+}
+
+int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p) {
+  if (!p) return -1;
+  return plan_mimo(*p, nullptr).total;
+}
+
+int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "mimo layer: null descriptor");
+  const tesm_hip_mimo_layer& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "mimo layer: dtype must be 0 or 1");
+  TESM_REQUIRE(p.B >= 1 && p.L >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.n_heads >= 1 && p.ent_rank >= 2 &&
+                   p.ent_rank % 2 == 0 && p.window >= 1 && p.window <= 64,
+               kErrInvalidArg, "mimo layer: bad sizes (need even ent_rank, 1 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.mimo_coef && p.mimo_x0sq && p.y, kErrInvalidArg,
+               "mimo layer: null pointer");
+  const int64_t H = p.n_heads, D = p.d_state, R = p.ent_rank, dm = p.d_model, HD = H * D, HR = H * R;
+  if (int rc = check_linear(p.in_proj, dm, "in_proj")) return rc;
+  if (int rc = check_linear(p.state_proj, HD, "state_proj")) return rc;
+  if (int rc = check_linear(p.ent_proj, HD, "ent_proj")) return rc;
+  if (int rc = check_linear(p.out_proj, dm, "out_proj")) return rc;
+  const MimoPlan s = plan_mimo(p, ws);
+  TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "mimo layer: workspace too small");
+
+  const int dt = p.dt;
+  const int es = esize(dt);
+  const int64_t M = p.B * p.L;
+  const int64_t n_in = 2 * dm + 3 * HD + 2 * HR;
+  char* proj = static_cast<char*>(s.proj);
+  // slice offsets of the in_proj output (tesm_mimo.py:940-949)
+  const int64_t o_local = 0, o_sv = dm, o_decay = dm + HD, o_write = dm + 2 * HD, o_gate = dm + 3 * HD,
+                o_q = 2 * dm + 3 * HD, o_k = 2 * dm + 3 * HD + HR;
+  int rc;
+  // 1. in_proj
+  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
+  // 2. gates + rank-free state scan: sequential float32 recurrence h = d h + w tanh(sv) per channel
+  ScanArgs sa;
+  sa.mode = 1;
+  sa.dt = dt;
+  sa.out_dt = kF32;
+  sa.clamp = 0;
+  sa.round_update = 0;
+  sa.B = p.B;
+  sa.L = p.L;
+  sa.C = HD;
+  sa.cs = 16;
+  sa.decay = proj + o_decay * es;
+  sa.ld_decay = n_in;
+  sa.update = proj + o_write * es;
+  sa.ld_update = n_in;
+  sa.sv = proj + o_sv * es;
+  sa.ld_sv = n_in;
+  sa.decay_bias = p.decay_bias;
+  sa.states = s.S;
+  sa.ld_states = HD;
+  if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
+  if ((rc = launch_mimo_final(s.S, p.mimo_x0sq, p.B, p.L, HD, p.h_final, p.last_state, st))) return rc;
+  // 3. per-head window scores, strict ternary, count normalisation (tesm_mimo.py:536-586)
+  EntArgs ea;
+  ea.dt = dt;
+  ea.mimo = 1;
+  ea.B = p.B;
+  ea.L = p.L;
+  ea.H = H;
+  ea.R = R;
+  ea.D = D;
+  ea.W = p.window;
+  ea.q = proj + o_q * es;
+  ea.ld_q = n_in;
+  ea.k = proj + o_k * es;
+  ea.ld_k = n_in;
+  ea.rope = static_cast<const float2*>(p.rope);
+  ea.bias = p.local_bias;
+  ea.thr = p.thr;
+  ea.ent_scale = p.ent_scale;
+  ea.S = s.S;
+  ea.ld_s = HD;
+  ea.wts = s.wts;
+  if ((rc = launch_local_ent(ea, st))) return rc;
+  // 4. window mix, entangled state, rank merge; tanh(E c) and C c in dt for the projections
+  MimoMixArgs ma;
+  ma.dt = dt;
+  ma.B = p.B;
+  ma.L = p.L;
+  ma.H = H;
+  ma.D = D;
+  ma.W = p.window;
+  ma.S = s.S;
+  ma.wts = s.wts;
+  ma.coef = p.mimo_coef;
+  ma.ent_scale = p.ent_scale;
+  ma.te = s.te;
+  ma.cc = s.cc;
+  if ((rc = launch_mimo_mix(ma, st))) return rc;
+  if ((rc = launch_quant_act(s.te, dt, M, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
+  if ((rc = launch_quant_act(s.cc, dt, M, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  // 5. decode caches
+  if (p.k_cache || p.v_cache) {
+    CacheFillArgs cf;
+    cf.dt = dt;
+    cf.cdt = p.cache_dt;
+    cf.sdt = kF32;
+    cf.B = p.B;
+    cf.L = p.L;
+    cf.H = H;
+    cf.R = R;
+    cf.D = D;
+    cf.W = p.window;
+    cf.k = proj + o_k * es;
+    cf.ld_k = n_in;
+    cf.rope = static_cast<const float2*>(p.rope);
+    cf.states = s.S;
+    cf.ld_states = HD;
+    cf.vscale = p.mimo_x0sq;
+    cf.k_cache = p.k_cache;
+    cf.v_cache = p.v_cache;
+    if ((rc = launch_cache_fill(cf, st))) return rc;
+  }
+  // 6. output gate and out_proj
+  OutputPath op;
+  op.xe = s.xe;
+  op.xc = s.xc;
+  op.xy = s.xy;
+  op.yg = s.yg;
+  op.state_proj = &p.state_proj;
+  op.ent_proj = &p.ent_proj;
+  op.out_proj = &p.out_proj;
+  op.M = M;
+  op.dm = dm;
+  op.D = HD;
   op.dt = dt;
   op.eps = p.bit_eps;
   op.local = proj + o_local * es;

@@ -44,14 +44,16 @@ int launch_decode_ent(const DecodeArgs& a, hipStream_t st);
 // Ring buffers after a prefill of L tokens: the last min(L, W) RoPE'd keys and states.
 struct CacheFillArgs {
   int dt = 0, cdt = 0;
-  int64_t B = 0, L = 0, R = 0, D = 0, W = 0;
-  const void* k = nullptr;          // raw (pre-RoPE) keys, element (b, t, r) at k[(b*L + t)*ld_k + r]
+  int sdt = -1;                     // states dtype (-1: dt)
+  int64_t B = 0, L = 0, H = 1, R = 0, D = 0, W = 0;
+  const void* k = nullptr;          // raw (pre-RoPE) keys, element (b, t, h, r) at k[(b*L + t)*ld_k + h*R + r]
   int64_t ld_k = 0;
   const float2* rope = nullptr;     // (L, R/2) table, positions 0..L-1
-  const void* states = nullptr;     // (b, t, d) at states[(b*L + t)*ld_states + d]
+  const void* states = nullptr;     // (b, t, h, d) at states[(b*L + t)*ld_states + h*D + d]
   int64_t ld_states = 0;
-  void* k_cache = nullptr;          // (B, W, R) cdt
-  void* v_cache = nullptr;          // (B, W, D) cdt
+  const float* vscale = nullptr;    // optional per-channel factor (H*D) applied to the states
+  void* k_cache = nullptr;          // (B, W, H, R) cdt
+  void* v_cache = nullptr;          // (B, W, H, D) cdt
 };
 
 int launch_cache_fill(const CacheFillArgs& a, hipStream_t st);

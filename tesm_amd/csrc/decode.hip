@@ -170,24 +170,31 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   }
 }
 
-// Prefill cache fill (tesm.py:1244-1251): rows t in [L - n, L), n = min(L, W), go to slot
-// t - L + W, keys RoPE'd at position t, states as computed.
-template <int DT, int CDT>
+// Prefill cache fill (tesm.py:1244-1251; MIMO tesm_mimo.py:1022-1037): rows t in [L - n, L),
+// n = min(L, W), go to slot t - L + W, keys RoPE'd at position t (per head), states as computed
+// (MIMO: the rank-0 states, S * vscale).
+template <int DT, int CDT, int SDT>
 __global__ __launch_bounds__(256) void cache_fill_kernel(CacheFillArgs a) {
   const int64_t n = a.L < a.W ? a.L : a.W;
   const int64_t r = blockIdx.x, b = blockIdx.y;  // r < n
   const int64_t t = a.L - n + r, slot = t - a.L + a.W;
   const int half = static_cast<int>(a.R / 2);
   const int64_t row = b * a.L + t;
-  for (int i = threadIdx.x; i < half; i += 256) {
+  const int64_t HR = a.H * a.R, HD = a.H * a.D;
+  for (int i = threadIdx.x; i < a.H * half; i += 256) {
+    const int h = i / half, p = i - h * half;
+    const int64_t ki = row * a.ld_k + h * a.R + p;
     float k1, k2;
-    rope_pair<DT>(ld<DT>(a.k, row * a.ld_k + i), ld<DT>(a.k, row * a.ld_k + half + i), a.rope[t * half + i], k1, k2);
-    const int64_t ko = (b * a.W + slot) * a.R;
-    st<CDT>(a.k_cache, ko + i, k1);
-    st<CDT>(a.k_cache, ko + half + i, k2);
+    rope_pair<DT>(ld<DT>(a.k, ki), ld<DT>(a.k, ki + half), a.rope[t * half + p], k1, k2);
+    const int64_t ko = (b * a.W + slot) * HR + h * a.R + p;
+    st<CDT>(a.k_cache, ko, k1);
+    st<CDT>(a.k_cache, ko + half, k2);
   }
-  for (int64_t c = threadIdx.x; c < a.D; c += 256)
-    st<CDT>(a.v_cache, (b * a.W + slot) * a.D + c, ld<DT>(a.states, row * a.ld_states + c));
+  for (int64_t c = threadIdx.x; c < HD; c += 256) {
+    float v = ld<SDT>(a.states, row * a.ld_states + c);
+    if (a.vscale) v *= a.vscale[c];
+    st<CDT>(a.v_cache, (b * a.W + slot) * HD + c, v);
+  }
 }
 
 }  // namespace
@@ -226,20 +233,29 @@ int launch_cache_fill(const CacheFillArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "cache fill: dtype must be 0 or 1");
   TESM_REQUIRE(a.cdt == kF32 || a.cdt == kBF16, kErrInvalidArg, "cache fill: cache dtype must be 0 or 1");
   TESM_REQUIRE(a.k && a.states && a.rope && a.k_cache && a.v_cache, kErrInvalidArg, "cache fill: null pointer");
-  TESM_REQUIRE(a.W >= 1 && a.R % 2 == 0, kErrInvalidArg, "cache fill: bad sizes");
+  TESM_REQUIRE(a.W >= 1 && a.R % 2 == 0 && a.H >= 1, kErrInvalidArg, "cache fill: bad sizes");
   if (a.B == 0 || a.L == 0) return kOk;
   const int64_t n = a.L < a.W ? a.L : a.W;
   const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>(a.B));
+  const int sdt = a.sdt < 0 ? a.dt : a.sdt;
+  TESM_REQUIRE(sdt == a.dt || sdt == kF32, kErrUnsupported, "cache fill: states must be in dt or f32");
   if (a.dt == kBF16) {
-    if (a.cdt == kBF16)
-      cache_fill_kernel<kBF16, kBF16><<<grid, 256, 0, st>>>(a);
-    else
-      cache_fill_kernel<kBF16, kF32><<<grid, 256, 0, st>>>(a);
+    if (sdt == kF32) {
+      if (a.cdt == kBF16)
+        cache_fill_kernel<kBF16, kBF16, kF32><<<grid, 256, 0, st>>>(a);
+      else
+        cache_fill_kernel<kBF16, kF32, kF32><<<grid, 256, 0, st>>>(a);
+    } else {
+      if (a.cdt == kBF16)
+        cache_fill_kernel<kBF16, kBF16, kBF16><<<grid, 256, 0, st>>>(a);
+      else
+        cache_fill_kernel<kBF16, kF32, kBF16><<<grid, 256, 0, st>>>(a);
+    }
   } else {
     if (a.cdt == kBF16)
-      cache_fill_kernel<kF32, kBF16><<<grid, 256, 0, st>>>(a);
+      cache_fill_kernel<kF32, kBF16, kF32><<<grid, 256, 0, st>>>(a);
     else
-      cache_fill_kernel<kF32, kF32><<<grid, 256, 0, st>>>(a);
+      cache_fill_kernel<kF32, kF32, kF32><<<grid, 256, 0, st>>>(a);
   }
   return check_launch("cache fill");
 }

@@ -1,0 +1,31 @@
+// TESMMIMO_Optimized pieces around the shared scan / window-score kernels.
+#pragma once
+
+#include "entangle.h"
+
+namespace tesm {
+
+// c[h, d] = sum_r mimo_x[h,r,d]^2 * mimo_o[h,r,d] and x0sq[h, d] = mimo_x[h,0,d]^2 in float32.
+int launch_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t H, int64_t Rm, int64_t D, float* coef,
+                     float* x0sq, hipStream_t st);
+
+// Window mix of the rank-free states S (float32, (B, L, H*D)) with the window weights of
+// ent_scores_kernel (MIMO form, (B, L, H, W)), entangled state E = S + scale (A - S) and
+// C = E - S in float32, then tanh(E * c) and C * c rounded to dt, (B*L, H*D) each.
+struct MimoMixArgs {
+  int dt = 0;
+  int64_t B = 0, L = 0, H = 0, D = 0, W = 0;
+  const float* S = nullptr;
+  const float* wts = nullptr;
+  const float* coef = nullptr;
+  float ent_scale = 0.0f;
+  void* te = nullptr;
+  void* cc = nullptr;
+};
+int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st);
+
+// Rank-0 final state h[b, c] = float64(S[b, L-1, c] * x0sq[c]) and, optionally, its float32 copy.
+int launch_mimo_final(const float* S, const float* x0sq, int64_t B, int64_t L, int64_t C, double* h_final,
+                      float* last, hipStream_t st);
+
+}  // namespace tesm

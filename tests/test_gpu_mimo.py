@@ -1,0 +1,103 @@
+"""GPU parity of the TESMMIMO_Optimized prefill (hip backend, ranks collapsed) against the
+reference fixtures and the oracle (tesm_mimo.py:914-1062)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_meta, load_golden
+from hip_helpers import DEV, TOL, flip_aware, need_gpu, normwise, rel_l2, to_np
+from oracle import tesm_torch as ot
+from tesm_amd import TESMMIMO_Optimized
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    need_gpu()
+
+
+def build(cls, meta, **kw):
+    """The fixtures' construction: seeded module, then random mimo_x / mimo_o / window bias so that the
+    rank merge is not trivial."""
+    torch.manual_seed(meta["seed"])
+    m = cls(d_model=meta["dm"], d_state=meta["D"], n_heads=meta["H"], mimo_rank=meta["Rm"], ent_rank=meta["R"],
+            entanglement_window=meta["W"], entanglement_threshold=meta["thr"], entanglement_scale=0.2,
+            max_seq_len=meta.get("max_seq_len", 64), decay_init_bias=meta["decay_bias"], **kw).eval()
+    with torch.no_grad():
+        gg = torch.Generator().manual_seed(meta["seed"] + 7)
+        H, Rm, D, W = meta["H"], meta["Rm"], meta["D"], meta["W"]
+        m.mimo_x.copy_(torch.rand(H, Rm, D, generator=gg) + 0.25)
+        m.mimo_o.copy_(torch.rand(H, Rm, D, generator=gg) + 0.25)
+        m.local_entanglement_bias.copy_(torch.randn(H, W, generator=gg) * 0.3)
+    return m
+
+
+@pytest.mark.parametrize("name", ["mimo_f32", "mimo_f32_w3"])
+def test_mimo_prefill_vs_reference_fixture(name):
+    g, meta = load_golden(name), golden_meta(name)
+    m = build(TESMMIMO_Optimized, meta)
+    sd = m.state_dict()
+    for k, v in g.items():  # seeded construction reproduces the reference's parameters
+        if k.startswith("param/") and k not in ("param/mimo_x", "param/mimo_o", "param/local_entanglement_bias"):
+            assert np.array_equal(sd[k[6:]].float().numpy(), v), k
+    m = m.to(DEV)
+    with torch.no_grad():
+        y, fin = m(torch.from_numpy(g["u"]).to(DEV))
+    assert y.shape == g["y"].shape and fin.dtype == torch.float64 and fin.shape == g["final_state"].shape
+    flip_aware(to_np(y).reshape(-1, meta["dm"]), g["y"].reshape(-1, meta["dm"]), row_tol=1e-4, max_flip_frac=0.05,
+               bound=2e-2)
+    assert normwise(to_np(y), g["y"]) <= TOL[torch.float32]
+    np.testing.assert_allclose(fin.cpu().numpy(), g["final_state"], rtol=1e-5, atol=1e-6)
+    # the reference's rank-0 scan output at the last position is the next layer's cross state
+    s0 = g["_parallel_state_scan_mimo/out#0"][:, -1]
+    np.testing.assert_allclose(to_np(m._last_cross_layer_state), s0, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,L,H,Rm,D,R,W", [(2, 100, 4, 3, 32, 16, 16), (1, 37, 2, 4, 24, 8, 8),
+                                            (3, 5, 3, 2, 16, 8, 8)])
+def test_mimo_prefill_random_vs_oracle(dtype, B, L, H, Rm, D, R, W):
+    meta = dict(seed=L + H, dm=128, D=D, H=H, Rm=Rm, R=R, W=W, thr=0.05, decay_bias=2.0, max_seq_len=128)
+    ref = build(ot.TESMMIMO_Optimized, meta).to(dtype)
+    m = build(TESMMIMO_Optimized, meta).to(DEV).to(dtype)
+    u = torch.randn(B, L, 128, generator=torch.Generator().manual_seed(3)).to(dtype)
+    with torch.no_grad():
+        yr, fr = ref(u)
+        y, f = m(u.to(DEV))
+    if dtype == torch.float32:
+        flip_aware(to_np(y).reshape(-1, 128), to_np(yr).reshape(-1, 128), row_tol=1e-4, max_flip_frac=0.02,
+                   bound=2e-2)
+        np.testing.assert_allclose(f.cpu().numpy(), fr.numpy(), rtol=1e-4, atol=1e-5)
+    else:
+        assert rel_l2(to_np(y), to_np(yr)) <= TOL[dtype]
+        flip_aware(to_np(y).reshape(-1, 128), to_np(yr).reshape(-1, 128), row_tol=TOL[dtype], max_flip_frac=0.05,
+                   bound=0.1)
+        assert normwise(f.cpu().numpy(), fr.numpy()) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("L", [20, 5])
+def test_mimo_prefill_fills_caches_like_reference(L):
+    meta = dict(seed=9, dm=64, D=16, H=2, Rm=3, R=8, W=8, thr=0.05, decay_bias=2.0)
+    ref = build(ot.TESMMIMO_Optimized, meta)
+    m = build(TESMMIMO_Optimized, meta).to(DEV)
+    u = torch.randn(2, L, 64, generator=torch.Generator().manual_seed(4))
+    cr, cm = ref.allocate_inference_cache(2, 64), m.allocate_inference_cache(2, 64)
+    with torch.no_grad():
+        ref(u, inference_params={"state_cache": cr})
+        m(u.to(DEV), inference_params={"state_cache": cm})
+    assert cm["seq_pos"] == cr["seq_pos"] == L and cm["cache_idx"] == cr["cache_idx"] == 0
+    np.testing.assert_allclose(cm["state"].cpu().numpy(), cr["state"].numpy(), rtol=1e-5, atol=1e-6)
+    for key in ("ent_k_cache", "ent_v_cache"):
+        assert cm[key].dtype == cr[key].dtype and cm[key].shape == cr[key].shape, key
+        np.testing.assert_allclose(to_np(cm[key]), to_np(cr[key]), rtol=1e-4, atol=1e-5, err_msg=key)
+
+
+def test_mimo_decode_step_is_refused():
+    meta = dict(seed=9, dm=64, D=16, H=2, Rm=2, R=8, W=8, thr=0.05, decay_bias=2.0)
+    m = build(TESMMIMO_Optimized, meta).to(DEV)
+    cache = m.allocate_inference_cache(2, 64)
+    with torch.no_grad():
+        m(torch.randn(2, 9, 64, device=DEV), inference_params={"state_cache": cache})
+        with pytest.raises(RuntimeError, match="kernel_backend"):
+            m(torch.randn(2, 1, 64, device=DEV), inference_params={"state_cache": cache})
