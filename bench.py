@@ -42,6 +42,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel measurements")
+    p.add_argument("--no-mimo", action="store_true", help="skip the configs[4] MIMO layer measurement")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
     p.add_argument("--copy-calib", action="store_true",
                    help="run one 256 MiB device-to-device copy first (a known-size reference for "
@@ -177,6 +178,35 @@ def measure_decode(torch, m, steps: int = 50):
             "note": "one decode step per sequence, host dispatch included (no graph capture)"}
 
 
+MIMO = dict(d_model=4096, d_state=2048, n_heads=4, mimo_rank=4, ent_rank=256, entanglement_window=64,
+            entanglement_threshold=0.05, entanglement_scale=0.2, max_seq_len=32768)
+
+
+def measure_mimo(torch, reps: int = 3):
+    """one TESMMIMO_Optimized layer at large_40b() dims (d_model 4096, d_state 2048, 4 heads,
+    mimo_rank 4, ent_rank 256, window 64), batch 1 x 32768-token prefill, bf16, INT2 weights."""
+    from tesm_amd import TESMMIMO_Optimized
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    m = TESMMIMO_Optimized(**MIMO).to(dev).to(torch.bfloat16).eval()
+    L = MIMO["max_seq_len"]
+    u = torch.randn(1, L, MIMO["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    m(u)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        m(u)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del m, u
+    torch.cuda.empty_cache()
+    return {"workload": "TESMMIMO_Optimized prefill, large_40b dims (configs[4]), B1 x L32768, bf16",
+            "ms_per_forward": ms, "tokens_per_s": L / (ms * 1e-3), "reps": reps}
+
+
 def gemm_traffic():
     """HBM bytes per in_proj GEMM launch from the committed FETCH_SIZE / WRITE_SIZE counter runs, scaled by
     the same counters' reading for a 256 MiB copy (profiles/in_proj_gemm_traffic.json); None if absent."""
@@ -255,6 +285,7 @@ def main():
                                                                   out=out), 50)
         ops = 2 * M * N * K
         decode = measure_decode(torch, m)
+        mimo = None if args.no_mimo else measure_mimo(torch)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
         if args.only:
             print(json.dumps({"kernels": kernels}))
@@ -285,6 +316,7 @@ def main():
                      "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes per "
                              "launch from profiles/in_proj_gemm_traffic.json"},
         "decode": decode,
+        "mimo_layer": mimo,
         "kernels": kernels,
     }
     if not args.no_cpu:
