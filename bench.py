@@ -192,14 +192,15 @@ def measure_mimo(torch, reps: int = 3):
     m = TESMMIMO_Optimized(**MIMO).to(dev).to(torch.bfloat16).eval()
     L = MIMO["max_seq_len"]
     u = torch.randn(1, L, MIMO["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
-    m(u)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    with torch.no_grad():
         m(u)
-    e1.record()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            m(u)
+        e1.record()
+        torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     del m, u
     torch.cuda.empty_cache()

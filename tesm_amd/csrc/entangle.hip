@@ -103,6 +103,123 @@ __global__ __launch_bounds__(256) void ent_scores_kernel(EntArgs a, int64_t weff
   }
 }
 
+// ---------------------------------------------------------------------------
+// MIMO window scores, tiled (tesm_mimo.py:536-586): a workgroup per (batch row, head, kScTP
+// positions).  RoPE'd q rows and the key rows the window reaches (kScTP + W - 1 of them) are
+// staged in LDS 32 RoPE pairs at a time, so each q / k element is rotated once per workgroup;
+// each thread accumulates a 4-position x 4-window-slot tile of dot products (products rounded to
+// dt before the sum, as the reference's (q * k).sum(-1) in dt).  Same arithmetic as
+// ent_scores_kernel<DT, 1, .>.
+// ---------------------------------------------------------------------------
+constexpr int kScTP = 64;        // positions per workgroup
+constexpr int kScPairs = 32;     // RoPE pairs per LDS slice (64 values per row)
+constexpr int kScPitch = 2 * kScPairs + 1;
+
+template <int DT>
+__global__ __launch_bounds__(256) void ent_scores_mimo_kernel(EntArgs a) {
+  extern __shared__ float lds_sc[];
+  const int W = static_cast<int>(a.W);
+  const int krows = kScTP + W - 1;
+  float* qs = lds_sc;                    // [kScTP][kScPitch]
+  float* ks = qs + kScTP * kScPitch;     // [krows][kScPitch]
+  float* tt = lds_sc;                    // after the dots: [kScTP][W] ternary values
+  float* nrm = ks;                       // after the dots: [kScTP] norms
+  const int tid = threadIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kScTP;
+  const int64_t tk0 = t0 - (W - 1);      // position of staged key row 0
+  const int half = static_cast<int>(a.R / 2);
+  const int nwt = (W + 3) / 4;           // 4-slot tiles along the window
+  const int tile = tid;                  // tile = pg * nwt + wg
+  const int pg = tile / nwt, wg = tile - pg * nwt;
+  const bool active = pg < kScTP / 4;
+  const int p0 = 4 * pg, w0 = 4 * wg;
+  float dot[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dot[i][j] = 0.0f;
+
+  for (int i0 = 0; i0 < half; i0 += kScPairs) {
+    const int np = half - i0 < kScPairs ? half - i0 : kScPairs;
+    // stage RoPE'd pairs (interleaved q1, q2 per pair) of the slice
+    for (int idx = tid; idx < (kScTP + krows) * kScPairs; idx += 256) {
+      const int r = idx / kScPairs, i = idx - r * kScPairs;
+      const bool isq = r < kScTP;
+      const int rr = isq ? r : r - kScTP;
+      int64_t tt_ = isq ? t0 + rr : tk0 + rr;
+      const bool ok = i < np && tt_ >= 0 && tt_ < a.L;
+      tt_ = tt_ < 0 ? 0 : (tt_ >= a.L ? a.L - 1 : tt_);
+      float o1 = 0.0f, o2 = 0.0f;
+      if (ok) {
+        const void* src = isq ? a.q : a.k;
+        const int64_t off = (b * a.L + tt_) * (isq ? a.ld_q : a.ld_k) + h * a.R + i0 + i;
+        rope_pair<DT>(ld<DT>(src, off), ld<DT>(src, off + half), a.rope[tt_ * half + i0 + i], o1, o2);
+      }
+      float* dst = (isq ? qs : ks) + rr * kScPitch + 2 * i;
+      dst[0] = o1;
+      dst[1] = o2;
+    }
+    __syncthreads();
+    if (active) {
+      for (int c = 0; c < 2 * np; ++c) {
+        float qv[4], kv[7];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = qs[(p0 + i) * kScPitch + c];
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+          const int r = p0 + w0 + i;
+          kv[i] = r < krows ? ks[r * kScPitch + c] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dot[i][j] += rnd<DT>(qv[i] * kv[i + j]);
+      }
+    }
+    __syncthreads();
+  }
+  // scores, strict ternary and validity (tesm_mimo.py:540-560)
+  const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t t = t0 + p0 + i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int w = w0 + j;
+        if (w >= W) continue;
+        const int64_t jk = t - W + 1 + w;
+        const bool valid = t < a.L && w < t + 1 && jk >= 0;
+        float tern = 0.0f;
+        if (valid) {
+          float sc = rnd<DT>(rnd<DT>(dot[i][j]) / sq);
+          sc = rnd<DT>(sc + a.bias[h * a.W + w]);
+          tern = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
+        }
+        tt[(p0 + i) * W + w] = tern;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < kScTP) {
+    float n = 0.0f;
+    for (int w = 0; w < W; ++w) n += fabsf(tt[tid * W + w]);
+    nrm[tid] = fmaxf(n, 1.0f);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kScTP * W; idx += 256) {
+    const int p = idx / W, w = idx - p * W;
+    const int64_t t = t0 + p;
+    if (t >= a.L) continue;
+    const int64_t o = ((b * a.L + t) * a.H + h) * W + w;
+    const float tv = tt[idx];
+    a.wts[o] = rnd<DT>(tv / nrm[p]);
+    if (a.tern) a.tern[o] = static_cast<int8_t>(tv);
+  }
+}
+
 constexpr int kMixTP = 64;  // positions per workgroup
 constexpr int kMixDS = 64;  // channels per workgroup
 
@@ -466,6 +583,12 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
 
 template <int DT, int MIMO>
 int run_scores(const EntArgs& a, int64_t weff, hipStream_t st) {
+  if (MIMO && a.q_add == nullptr) {
+    const size_t lds = static_cast<size_t>((kScTP + kScTP + a.W - 1) * kScPitch) * sizeof(float);
+    dim3 grid(static_cast<unsigned>((a.L + kScTP - 1) / kScTP), static_cast<unsigned>(a.B * a.H));
+    ent_scores_mimo_kernel<DT><<<grid, 256, lds, st>>>(a);
+    return check_launch("entanglement scores (MIMO, tiled)");
+  }
   const int64_t groups = a.B * a.L * a.H;
   auto blocks = [&](int wp) { return static_cast<unsigned>((groups * wp + 255) / 256); };
   if (weff <= 8) ent_scores_kernel<DT, MIMO, 8><<<blocks(8), 256, 0, st>>>(a, weff, 0.f);
