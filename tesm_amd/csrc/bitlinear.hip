@@ -149,8 +149,14 @@ struct Cfg {
 // the 16 code bytes of row 16t + L%16, code group 4ks + L/16.  B: fragment (tile t of 16 columns,
 // ks) is 256 bytes; lane L holds the packed dword (16 codes) of column 16t + L%16, group 4ks + L/16.
 // Lane L's A and B operands therefore cover the same 16 codes, in the order the unpack produces.
+// Inside an A fragment lane L's 16 bytes sit at slot a_slot(L, ks): the low 4 bits are XORed with
+// the code group so that the staging stores (8 lanes per row, one row's 8 code groups) hit
+// distinct banks; the 64 lanes of a fragment read still form a permutation of its 64 slots.
+__device__ __forceinline__ int a_slot(int lane, int ks) {
+  return ((lane & 15) ^ (4 * (lane >> 4)) ^ (2 * ks)) + 16 * (lane >> 4);
+}
 __device__ __forceinline__ int a_frag_off(int r, int kg) {
-  return (((r >> 4) * 2 + (kg >> 2)) << 10) + (((r & 15) + 16 * (kg & 3)) << 4);
+  return (((r >> 4) * 2 + (kg >> 2)) << 10) + (a_slot((r & 15) + 16 * (kg & 3), kg >> 2) << 4);
 }
 __device__ __forceinline__ int b_frag_off(int r, int kg) {
   return (((r >> 4) * 2 + (kg >> 2)) << 8) + (((r & 15) + 16 * (kg & 3)) << 2);
@@ -173,20 +179,25 @@ __device__ __forceinline__ void gemm_gload(const int8_t* const (&pa)[C::A_PT], c
 }
 
 // dword d of a packed B chunk is code group 4h + d, which sits 16 lanes (64 bytes) further on in
-// the fragment
+// the fragment.  The four lanes whose chunks start on the same bank write their dwords in rotated
+// order (rot = 0..3), so each store instruction covers all 64 banks once.
 template <class C>
 __device__ __forceinline__ void gemm_sstore(const int (&la)[C::A_PT], const int (&lb)[C::B_PT],
                                             const bool (&vb)[C::B_PT], const v4i (&ra)[C::A_PT],
                                             const v4i (&rb)[C::B_PT], char* stage) {
 #pragma unroll
   for (int p = 0; p < C::A_PT; ++p) *reinterpret_cast<v4i*>(stage + la[p]) = ra[p];
+  const int t = threadIdx.x;
+  const int rot = 2 * ((t >> 5) & 1) + (t & 1);
 #pragma unroll
   for (int p = 0; p < C::B_PT; ++p) {
     if (vb[p]) {
-      *reinterpret_cast<int*>(stage + lb[p]) = rb[p].x;
-      *reinterpret_cast<int*>(stage + lb[p] + 64) = rb[p].y;
-      *reinterpret_cast<int*>(stage + lb[p] + 128) = rb[p].z;
-      *reinterpret_cast<int*>(stage + lb[p] + 192) = rb[p].w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = (i + rot) & 3;
+        const int v = d == 0 ? rb[p].x : (d == 1 ? rb[p].y : (d == 2 ? rb[p].z : rb[p].w));
+        *reinterpret_cast<int*>(stage + lb[p] + 64 * d) = v;
+      }
     }
   }
 }
@@ -235,9 +246,10 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
     for (int ks = 0; ks < 2; ++ks) {
       v4i af[TM];
       uint32_t bw[TN];
+      const int aoff = a_slot(lane, ks) * 16;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(cur + (((wm * TM + i) * 2 + ks) << 10) + lane * 16);
+        af[i] = *reinterpret_cast<const v4i*>(cur + (((wm * TM + i) * 2 + ks) << 10) + aoff);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
         bw[j] = *reinterpret_cast<const uint32_t*>(cur + C::A_BYTES + (((wn * TN + j) * 2 + ks) << 8) + lane * 4);
@@ -1092,6 +1104,8 @@ int check_operand(const LinearOperand& o, int64_t Kp, const char* which) {
 
 }  // namespace
 
+inline int64_t tiles128(const LinearArgs& a) { return ((a.M + 127) / 128) * ((a.N + 127) / 128); }
+
 int launch_linear(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.M >= 0 && a.N >= 0, kErrInvalidArg, "bitlinear: negative size");
   TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "bitlinear: Kp must be a positive multiple of 128");
@@ -1114,11 +1128,13 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
   }
   if (a.epilogue == kEpiStore) {
     if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
-    // 64x128 tiles with the four waves along N: measured fastest for M >= 64 at the layer's
-    // shapes (more resident workgroups per CU hide the load latency better than 128x128)
+    // 128x128 tiles (4 waves of 64x64) when they still give two workgroups per CU, else 64x128
+    // (waves along N); measured at the layer shapes (in_proj / out_proj / configs[1] / configs[4])
+    if (tiles128(a) >= 512) return run_mfma<2, 2, 4, 4, kEpiStore>(a, st);
     return run_mfma<1, 4, 4, 2, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
+  if (tiles128(a) >= 512) return run_mfma<2, 2, 4, 4, kEpiOutputGate>(a, st);
   return run_mfma<1, 4, 4, 2, kEpiOutputGate>(a, st);
 }
 
