@@ -84,6 +84,7 @@ struct SisoPlan {
   void* proj;
   void* scan_ws;
   int64_t scan_bytes;
+  void* gated;  // gated decay / update handed from the scan's summary pass to its apply pass
   float* wts;
   void* e_tanh;
   void* c_mix;
@@ -118,6 +119,7 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   s.proj = c.take<void>(M * n_in * es);
   s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
   s.scan_ws = c.take<void>(s.scan_bytes);
+  s.gated = c.take<void>(2 * M * p.d_state * es);
   s.wts = nullptr;
   s.e_tanh = s.c_mix = nullptr;
   if (!s.fuse_ent) {
@@ -547,6 +549,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   sa.states = p.states;
   sa.ld_states = D;
   sa.h_final = p.h_final;
+  sa.gated = s.gated;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   // 4. local entanglement + mix (tesm.py:853-952, 1231-1232), quantized for state_proj / ent_proj
   EntArgs ea = siso_ent_shape(p);

@@ -26,6 +26,9 @@ struct ScanArgs {
   void* states = nullptr;        // (b, t, c) at states[(b*L + t)*ld_states + c], out_dt
   int64_t ld_states = 0;
   double* h_final = nullptr;     // (B, C) final state or null
+  // mode 1 with round_update: optional (2, B*L, C) dt buffer; the summary pass stores the gated
+  // decay and update there and the apply pass reads them instead of recomputing the gates
+  void* gated = nullptr;
 };
 
 int64_t scan_chunk_len(int64_t L, int64_t cs);

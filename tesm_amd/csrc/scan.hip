@@ -26,6 +26,7 @@ namespace tesm {
 namespace {
 
 constexpr float kScanEps = 1e-12f;
+constexpr float kScanInvEps = 1e12f;  // the clamp factor A / 1e-12 as a product
 
 template <int DT, int MODE>
 struct ScanIn {
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(64) void scan_chunk_kernel(ScanArgs a, int64_t T, i
     if (a.clamp) {
       d = fmaxf(d, kScanEps);
       A = ((t % a.cs) == 0) ? d : A * d;
-      if (A < kScanEps) g = A / kScanEps;
+      if (A < kScanEps) g = A * kScanInvEps;
     }
     h = d * h + g * u;
     if (PHASE == 1) {
@@ -154,6 +155,26 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
       }
     }
   }
+  if constexpr (MODE == 1 && PHASE == 1) {
+    if (a.gated) {  // the gated decay and update, for the apply pass (dt values, (B*L, C) each)
+      const int64_t plane = a.B * a.L * a.C;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        if (i >= n) continue;
+        const int64_t o = (b * a.L + t0 + i) * a.C + ch;
+        if constexpr (DT == kBF16 && CPT == 2) {
+          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.gated) + o) = pack_bf16x2(d[i][0], d[i][1]);
+          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.gated) + plane + o) = pack_bf16x2(u[i][0], u[i][1]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < CPT; ++j) {
+            st<DT>(a.gated, o + j, d[i][j]);
+            st<DT>(a.gated, plane + o + j, u[i][j]);
+          }
+        }
+      }
+    }
+  }
   const int64_t sidx = (b * nc + c) * a.C + ch;
   const int cs = static_cast<int>(a.cs);  // the thread-chunk start is a multiple of cs
   float h[CPT], P[CPT], A[CPT];
@@ -174,7 +195,7 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
         if (a.clamp) {
           dd = fmaxf(dd, kScanEps);
           A[j] = reset ? dd : A[j] * dd;
-          if (A[j] < kScanEps) g = A[j] / kScanEps;
+          if (A[j] < kScanEps) g = A[j] * kScanInvEps;
         }
         h[j] = dd * h[j] + g * u[i][j];
         P[j] *= dd;
@@ -247,8 +268,31 @@ int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* 
     scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, st>>>(a, nc, summ, carry);
   else
     scan_carry_seg_kernel<4><<<g2, 4 * 64, 0, st>>>(a, nc, summ, carry);
-  scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+  if (MODE == 1 && a.gated) {
+    // apply pass on the stored gates: a plain decay / update scan
+    ScanArgs g = a;
+    g.mode = 0;
+    g.decay = a.gated;
+    g.ld_decay = a.C;
+    g.update = static_cast<const char*>(a.gated) + a.B * a.L * a.C * (DT == kBF16 ? 2 : 4);
+    g.ld_update = a.C;
+    scan_fast_kernel<DT, OUT_DT, 0, 3, TM, CPT><<<nb, 256, 0, st>>>(g, T, nc, summ, carry);
+  } else {
+    scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+  }
   return check_launch("scan");
+}
+
+template <int DT, int OUT_DT, int MODE>
+int scan_fast_dispatch(const ScanArgs& e, int64_t T, int64_t nc, float* summ, float* carry, bool pairs,
+                       hipStream_t st) {
+  if constexpr (DT == kBF16) {
+    if (pairs)
+      return T <= 16 ? run_scan_fast<DT, OUT_DT, MODE, 16, 2>(e, T, nc, summ, carry, st)
+                     : run_scan_fast<DT, OUT_DT, MODE, 32, 2>(e, T, nc, summ, carry, st);
+  }
+  return T <= 16 ? run_scan_fast<DT, OUT_DT, MODE, 16, 1>(e, T, nc, summ, carry, st)
+                 : run_scan_fast<DT, OUT_DT, MODE, 32, 1>(e, T, nc, summ, carry, st);
 }
 
 template <int DT, int OUT_DT, int MODE>
@@ -287,6 +331,8 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   TESM_REQUIRE(a.ld_decay >= a.C && a.ld_update >= a.C && a.ld_states >= a.C, kErrInvalidArg, "scan: ld < C");
   if (a.mode == 1)
     TESM_REQUIRE(a.sv && a.decay_bias && a.ld_sv >= a.C, kErrInvalidArg, "scan mode 1: need sv and decay_bias");
+  TESM_REQUIRE(!a.gated || (a.mode == 1 && a.round_update && a.out_dt == a.dt), kErrInvalidArg,
+               "scan: a gate buffer needs mode 1 with rounded updates");
   const int64_t need = scan_ws_bytes(a.B, a.L, a.C, a.cs);
   TESM_REQUIRE(ws && ws_bytes >= need, kErrWorkspace, "scan: workspace too small");
   const int64_t T = scan_chunk_len(a.L, a.cs);
@@ -300,28 +346,19 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   const bool pairs = a.dt == kBF16 && a.C % 2 == 0 && a.ld_decay % 2 == 0 && a.ld_update % 2 == 0 &&
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
                      aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
-                     aligned(a.states, 4);
+                     aligned(a.states, 4) && (!a.gated || aligned(a.gated, 4));
   if (T <= 32) {
-    const int key = a.dt * 1000 + a.out_dt * 100 + a.mode * 10 + (T <= 16 ? 1 : 2);
-    switch (key) {
-      case 1: return run_scan_fast<kF32, kF32, 0, 16, 1>(e, T, nc, summ, carry, st);
-      case 2: return run_scan_fast<kF32, kF32, 0, 32, 1>(e, T, nc, summ, carry, st);
-      case 11: return run_scan_fast<kF32, kF32, 1, 16, 1>(e, T, nc, summ, carry, st);
-      case 12: return run_scan_fast<kF32, kF32, 1, 32, 1>(e, T, nc, summ, carry, st);
-      case 1101:
-        return pairs ? run_scan_fast<kBF16, kBF16, 0, 16, 2>(e, T, nc, summ, carry, st)
-                     : run_scan_fast<kBF16, kBF16, 0, 16, 1>(e, T, nc, summ, carry, st);
-      case 1102:
-        return pairs ? run_scan_fast<kBF16, kBF16, 0, 32, 2>(e, T, nc, summ, carry, st)
-                     : run_scan_fast<kBF16, kBF16, 0, 32, 1>(e, T, nc, summ, carry, st);
-      case 1111:
-        return pairs ? run_scan_fast<kBF16, kBF16, 1, 16, 2>(e, T, nc, summ, carry, st)
-                     : run_scan_fast<kBF16, kBF16, 1, 16, 1>(e, T, nc, summ, carry, st);
-      case 1112:
-        return pairs ? run_scan_fast<kBF16, kBF16, 1, 32, 2>(e, T, nc, summ, carry, st)
-                     : run_scan_fast<kBF16, kBF16, 1, 32, 1>(e, T, nc, summ, carry, st);
-      default:
-        break;  // mixed dtypes: generic kernels below
+    if (a.dt == kBF16) {
+      if (a.out_dt == kBF16) {
+        if (a.mode == 0) return scan_fast_dispatch<kBF16, kBF16, 0>(e, T, nc, summ, carry, pairs, st);
+        return scan_fast_dispatch<kBF16, kBF16, 1>(e, T, nc, summ, carry, pairs, st);
+      }
+      if (a.mode == 0) return scan_fast_dispatch<kBF16, kF32, 0>(e, T, nc, summ, carry, pairs, st);
+      return scan_fast_dispatch<kBF16, kF32, 1>(e, T, nc, summ, carry, pairs, st);
+    }
+    if (a.out_dt == kF32) {
+      if (a.mode == 0) return scan_fast_dispatch<kF32, kF32, 0>(e, T, nc, summ, carry, false, st);
+      return scan_fast_dispatch<kF32, kF32, 1>(e, T, nc, summ, carry, false, st);
     }
   }
   const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
