@@ -262,7 +262,10 @@ template <int DT, int OUT_DT, int MODE, int TM, int CPT>
 int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
   const int64_t threads = a.B * nc * (a.C / CPT);
   const unsigned nb = static_cast<unsigned>((threads + 255) / 256);
-  scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+  // the gate pass is VALU-heavy: one channel per thread for twice the waves
+  constexpr int CPT1 = MODE == 1 ? 1 : CPT;
+  const unsigned nb1 = static_cast<unsigned>((a.B * nc * (a.C / CPT1) + 255) / 256);
+  scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT1><<<nb1, 256, 0, st>>>(a, T, nc, summ, carry);
   dim3 g2(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.B));
   if (nc >= 64)
     scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, st>>>(a, nc, summ, carry);
