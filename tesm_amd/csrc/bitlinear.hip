@@ -158,9 +158,10 @@ __device__ __forceinline__ int a_slot(int lane, int ks) {
 __device__ __forceinline__ int a_frag_off(int r, int kg) {
   return (((r >> 4) * 2 + (kg >> 2)) << 10) + (a_slot((r & 15) + 16 * (kg & 3), kg >> 2) << 4);
 }
-__device__ __forceinline__ int b_frag_off(int r, int kg) {
-  return (((r >> 4) * 2 + (kg >> 2)) << 8) + (((r & 15) + 16 * (kg & 3)) << 2);
-}
+// B stays in its global order in LDS: column n of the tile owns 32 bytes (the 128 codes of the K
+// tile), its two 16-byte halves swapped on every other group of 8 columns so that a fragment read
+// (16 columns x 4 dwords) covers 64 distinct banks.
+__device__ __forceinline__ int b_col_off(int n, int half) { return n * 32 + 16 * (half ^ ((n >> 3) & 1)); }
 
 __device__ __forceinline__ v4i unpack_frag(uint32_t w) {
   return v4i{static_cast<int>(unpack_u(w, 0)), static_cast<int>(unpack_u(w, 1)), static_cast<int>(unpack_u(w, 2)),
@@ -178,28 +179,15 @@ __device__ __forceinline__ void gemm_gload(const int8_t* const (&pa)[C::A_PT], c
     if (vb[p]) rb[p] = *reinterpret_cast<const v4i*>(pb[p] + k0 / 4);
 }
 
-// dword d of a packed B chunk is code group 4h + d, which sits 16 lanes (64 bytes) further on in
-// the fragment.  The four lanes whose chunks start on the same bank write their dwords in rotated
-// order (rot = 0..3), so each store instruction covers all 64 banks once.
 template <class C>
 __device__ __forceinline__ void gemm_sstore(const int (&la)[C::A_PT], const int (&lb)[C::B_PT],
                                             const bool (&vb)[C::B_PT], const v4i (&ra)[C::A_PT],
                                             const v4i (&rb)[C::B_PT], char* stage) {
 #pragma unroll
   for (int p = 0; p < C::A_PT; ++p) *reinterpret_cast<v4i*>(stage + la[p]) = ra[p];
-  const int t = threadIdx.x;
-  const int rot = 2 * ((t >> 5) & 1) + (t & 1);
 #pragma unroll
-  for (int p = 0; p < C::B_PT; ++p) {
-    if (vb[p]) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = (i + rot) & 3;
-        const int v = d == 0 ? rb[p].x : (d == 1 ? rb[p].y : (d == 2 ? rb[p].z : rb[p].w));
-        *reinterpret_cast<int*>(stage + lb[p] + 64 * d) = v;
-      }
-    }
-  }
+  for (int p = 0; p < C::B_PT; ++p)
+    if (vb[p]) *reinterpret_cast<v4i*>(stage + lb[p]) = rb[p];
 }
 
 template <class C, int WN, int TM, int TN>
@@ -231,28 +219,23 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
     vb[p] = kAllB || c < C::B_CHUNKS;
     const int64_t n = n0 + (c >> 1);
     pb[p] = o.w + (n < N ? n : N - 1) * o.ldw + 16 * (c & 1);
-    lb[p] = C::A_BYTES + b_frag_off(c >> 1, 4 * (c & 1));
+    lb[p] = C::A_BYTES + b_col_off(c >> 1, c & 1);
   }
-  v4i ra[C::A_PT], rb[C::B_PT];
   const int64_t nk = Kp / C::BK;
-  gemm_gload<C>(pa, pb, vb, 0, ra, rb);
-  gemm_sstore<C>(la, lb, vb, ra, rb, smem);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const char* cur = smem + (kt & 1) * C::STAGE;
-    const bool more = kt + 1 < nk;
-    if (more) gemm_gload<C>(pa, pb, vb, (kt + 1) * C::BK, ra, rb);
+  const int aoff0 = a_slot(lane, 0) * 16, aoff1 = a_slot(lane, 1) * 16;
+  // one 128-deep K tile from an LDS stage
+  auto compute = [&](const char* cur) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v4i af[TM];
       uint32_t bw[TN];
-      const int aoff = a_slot(lane, ks) * 16;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const v4i*>(cur + (((wm * TM + i) * 2 + ks) << 10) + aoff);
+        af[i] = *reinterpret_cast<const v4i*>(cur + (((wm * TM + i) * 2 + ks) << 10) + (ks ? aoff1 : aoff0));
 #pragma unroll
       for (int j = 0; j < TN; ++j)
-        bw[j] = *reinterpret_cast<const uint32_t*>(cur + C::A_BYTES + (((wn * TN + j) * 2 + ks) << 8) + lane * 4);
+        bw[j] = *reinterpret_cast<const uint32_t*>(cur + C::A_BYTES + b_col_off((wn * TN + j) * 16 + (lane & 15), ks) +
+                                                   4 * (lane >> 4));
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const v4i bf = unpack_frag(bw[j]);
@@ -262,9 +245,31 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
         for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af[i], acc[i][j], 0, 0, 0);
       }
     }
-    if (more) gemm_sstore<C>(la, lb, vb, ra, rb, smem + ((kt + 1) & 1) * C::STAGE);
+  };
+  // Two register sets keep two K tiles of global loads in flight beyond the one in LDS: set 0
+  // holds even tiles, set 1 odd tiles; loads past the last tile re-read it (never computed).
+  v4i ra0[C::A_PT], rb0[C::B_PT], ra1[C::A_PT], rb1[C::B_PT];
+  auto kofs = [&](int64_t kt) { return (kt < nk ? kt : nk - 1) * C::BK; };
+  char* const s0 = smem;
+  char* const s1 = smem + C::STAGE;
+  gemm_gload<C>(pa, pb, vb, kofs(0), ra0, rb0);
+  gemm_gload<C>(pa, pb, vb, kofs(1), ra1, rb1);
+  gemm_sstore<C>(la, lb, vb, ra0, rb0, s0);
+  __syncthreads();
+  gemm_gload<C>(pa, pb, vb, kofs(2), ra0, rb0);
+  int64_t kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    compute(s0);                                     // tile kt
+    gemm_sstore<C>(la, lb, vb, ra1, rb1, s1);        // tile kt + 1
     __syncthreads();
+    gemm_gload<C>(pa, pb, vb, kofs(kt + 3), ra1, rb1);
+    compute(s1);                                     // tile kt + 1
+    gemm_sstore<C>(la, lb, vb, ra0, rb0, s0);        // tile kt + 2 (past the end: never computed)
+    __syncthreads();
+    gemm_gload<C>(pa, pb, vb, kofs(kt + 4), ra0, rb0);
   }
+  if (kt < nk) compute(s0);                          // odd number of K tiles
+  __syncthreads();  // the stages may be refilled by a following main loop (output-gate products)
 }
 
 // Tile order for a 1-D grid: workgroups are handed to the 8 XCDs round-robin by id, so id is
@@ -449,6 +454,290 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// GEMM on v_mfma_i32_32x32x32_i8, which on gfx950 delivers about twice the int8 rate of the
+// 16x16x64 form.  Block tile BM x BN (waves WM x WN, each TM x TN tiles of 32 x 32), K tiles of
+// 128 codes in 4 k-steps of 32.  Weights are the MFMA's A operand: lane L feeds weight column
+// L%32 with codes 16*(L/32) .. +15 of the k-step (one packed dword, unpacked in registers) and
+// activation row L%32 with the same 16 codes (16 bytes).  Accumulator element r of lane L is
+// weight column 8*(r/4) + 4*(L/32) + r%4 and activation row L%32, so every lane stores runs of 4
+// consecutive outputs.
+//
+// LDS, per stage: activations in k-step planes [s][row][32 bytes]; a row's slot inside its plane
+// is row ^ 2s and its two 16-byte halves are swapped on odd groups of 8 slots, so both the staging
+// stores (8 lanes per row) and the fragment reads (32 rows x 2 halves) hit distinct banks.  Packed
+// weights keep their global order, 32 bytes per column and K tile, dword d (k-step d/2, half d%2)
+// at position d ^ 2*((col/8)%4), which makes a fragment read (32 columns x 2 dwords) bank-free.
+// ---------------------------------------------------------------------------
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+template <int WM, int WN, int TM, int TN>
+struct Cfg32 {
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int BM = WM * TM * 32, BN = WN * TN * 32, BK = 128;
+  static constexpr int A_BYTES = BM * BK;
+  static constexpr int B_BYTES = BN * BK / 4;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_CHUNKS = BM * BK / 16;
+  static constexpr int B_CHUNKS = BN * BK / 64;
+  static constexpr int A_PT = (A_CHUNKS + NT - 1) / NT;
+  static constexpr int B_PT = (B_CHUNKS + NT - 1) / NT;
+};
+
+template <int BM>
+__device__ __forceinline__ int a32_off(int row, int q) {
+  const int s = q >> 1, h = q & 1;
+  const int rr = row ^ (2 * s);
+  return s * BM * 32 + rr * 32 + 16 * (h ^ ((rr >> 3) & 1));
+}
+__device__ __forceinline__ int b32_off(int col, int d) { return col * 32 + 4 * (d ^ (2 * ((col >> 3) & 3))); }
+
+template <class C, int WN, int TM, int TN>
+__device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
+                                                int64_t Kp, v16i (&acc)[TM][TN], char* smem) {
+  const int t = threadIdx.x;
+  __builtin_assume(t < C::NT);
+  const int lane = t & 63, w = t >> 6;
+  const int wm = w / WN, wn = w % WN;
+  constexpr bool kAllA = (C::A_CHUNKS % C::NT) == 0;
+  constexpr bool kAllB = (C::B_CHUNKS % C::NT) == 0;
+  static_assert(kAllA, "A chunks must divide evenly over the workgroup");
+
+  // rows past M / columns past N read the last valid one and only feed outputs never stored
+  const int8_t* pa[C::A_PT];
+  int la[C::A_PT];
+#pragma unroll
+  for (int p = 0; p < C::A_PT; ++p) {
+    const int c = t + p * C::NT;
+    const int64_t m = m0 + (c >> 3);
+    pa[p] = o.q + (m < M ? m : M - 1) * o.ldq + 16 * (c & 7);
+    la[p] = a32_off<C::BM>(c >> 3, c & 7);
+  }
+  const uint8_t* pb[C::B_PT];
+  int lb[C::B_PT], lb2[C::B_PT];
+  bool vb[C::B_PT];
+#pragma unroll
+  for (int p = 0; p < C::B_PT; ++p) {
+    const int c = t + p * C::NT;
+    vb[p] = kAllB || c < C::B_CHUNKS;
+    const int64_t n = n0 + (c >> 1);
+    pb[p] = o.w + (n < N ? n : N - 1) * o.ldw + 16 * (c & 1);
+    lb[p] = C::A_BYTES + b32_off(c >> 1, 4 * (c & 1));       // dwords 4q, 4q+1
+    lb2[p] = C::A_BYTES + b32_off(c >> 1, 4 * (c & 1) + 2);  // dwords 4q+2, 4q+3
+  }
+  const int64_t nk = Kp / C::BK;
+  auto gload = [&](int64_t kt, v4i (&ra)[C::A_PT], v4i (&rb)[C::B_PT]) {
+    const int64_t k0 = (kt < nk ? kt : nk - 1) * C::BK;
+#pragma unroll
+    for (int p = 0; p < C::A_PT; ++p) ra[p] = *reinterpret_cast<const v4i*>(pa[p] + k0);
+#pragma unroll
+    for (int p = 0; p < C::B_PT; ++p)
+      if (vb[p]) rb[p] = *reinterpret_cast<const v4i*>(pb[p] + k0 / 4);
+  };
+  auto sstore = [&](const v4i (&ra)[C::A_PT], const v4i (&rb)[C::B_PT], char* stage) {
+#pragma unroll
+    for (int p = 0; p < C::A_PT; ++p) *reinterpret_cast<v4i*>(stage + la[p]) = ra[p];
+#pragma unroll
+    for (int p = 0; p < C::B_PT; ++p) {
+      if (vb[p]) {  // dword pairs (4q, 4q+1) and (4q+2, 4q+3) stay adjacent under the swizzle
+        *reinterpret_cast<v2u*>(stage + lb[p]) = v2u{static_cast<uint32_t>(rb[p][0]), static_cast<uint32_t>(rb[p][1])};
+        *reinterpret_cast<v2u*>(stage + lb2[p]) = v2u{static_cast<uint32_t>(rb[p][2]), static_cast<uint32_t>(rb[p][3])};
+      }
+    }
+  };
+  // per-lane fragment offsets
+  int ar[4][TM];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ar[s][i] = a32_off<C::BM>((wm * TM + i) * 32 + (lane & 31), 2 * s + (lane >> 5));
+  int br[4][TN];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) br[s][j] = C::A_BYTES + b32_off((wn * TN + j) * 32 + (lane & 31), 2 * s + (lane >> 5));
+  auto compute = [&](const char* cur) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      v4i af[TM];
+      uint32_t bw[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i*>(cur + ar[s][i]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const uint32_t*>(cur + br[s][j]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const v4i bf = unpack_frag(bw[j]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  // two register sets keep two K tiles of loads in flight beyond the one in LDS
+  v4i ra0[C::A_PT], rb0[C::B_PT], ra1[C::A_PT], rb1[C::B_PT];
+  char* const s0 = smem;
+  char* const s1 = smem + C::STAGE;
+  gload(0, ra0, rb0);
+  gload(1, ra1, rb1);
+  sstore(ra0, rb0, s0);
+  __syncthreads();
+  gload(2, ra0, rb0);
+  int64_t kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    compute(s0);
+    sstore(ra1, rb1, s1);
+    __syncthreads();
+    gload(kt + 3, ra1, rb1);
+    compute(s1);
+    sstore(ra0, rb0, s0);
+    __syncthreads();
+    gload(kt + 4, ra0, rb0);
+  }
+  if (kt < nk) compute(s0);
+  __syncthreads();
+}
+
+// Outputs (m, nb .. nb+3) from exact accumulators q0 (op0) and q1 (op1, output gate): per-tensor or
+// per-row scales, optional bias and accumulator dump, the output gate; columns past N skipped.
+template <int EPI, int OUT_DT>
+__device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64_t nb, const int32_t (&q0)[4],
+                                           const int32_t (&q1)[4], float inv0, int32_t rs0, float inv1, int32_t rs1,
+                                           bool vout, bool vin) {
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+  const bool full = nb + 3 < a.N;
+  float v[4], lo[4], gt[4];
+  if constexpr (EPI == kEpiOutputGate) {
+    if (full) {
+      load4<OUT_DT>(a.local, m * a.ld_local + nb, vin, lo);
+      load4<OUT_DT>(a.gate, m * a.ld_gate + nb, vin, gt);
+    } else {
+      for (int r = 0; r < 4; ++r) {
+        lo[r] = nb + r < a.N ? ld<OUT_DT>(a.local, m * a.ld_local + nb + r) : 0.0f;
+        gt[r] = nb + r < a.N ? ld<OUT_DT>(a.gate, m * a.ld_gate + nb + r) : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t n = nb + r;
+    v[r] = 0.0f;
+    if (n >= a.N) continue;
+    const float cw0 = o0.c_w_per_row ? o0.c_w[n] : o0.c_w[0];
+    const int32_t a0 = q0[r] - rs0;
+    if (a.acc_dump) a.acc_dump[m * a.N + n] = a0;
+    const float v0 = (static_cast<float>(a0) * inv0) * cw0;
+    if constexpr (EPI == kEpiStore) {
+      v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n) : v0;
+    } else {
+      const float cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
+      const float sp = rnd<OUT_DT>(v0);
+      const float ep = rnd<OUT_DT>((static_cast<float>(q1[r] - rs1) * inv1) * cw1);
+      const float g = rnd<OUT_DT>(sigmoidf_(gt[r]));
+      v[r] = rnd<OUT_DT>(rnd<OUT_DT>(lo[r] + rnd<OUT_DT>(g * sp)) + ep);
+    }
+  }
+  if (full) {
+    store4<OUT_DT>(a.out, m * a.ldo + nb, v, vout);
+  } else {
+    for (int r = 0; r < 4 && nb + r < a.N; ++r) st<OUT_DT>(a.out, m * a.ldo + nb + r, v[r]);
+  }
+}
+
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
+__global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
+  using C = Cfg32<WM, WN, TM, TN>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+  int64_t tm, tn;
+  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
+  const int64_t m0 = tm * C::BM;
+  const int64_t n0 = tn * C::BN;
+  v16i acc0[TM][TN], acc1[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc0[i][j] = v16i{};
+      acc1[i][j] = v16i{};
+    }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w / WN, wn = w % WN;
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+  const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
+  float sx[TM];
+  int32_t rsum[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31);
+    const int64_t mc = m < a.M ? m : a.M - 1;
+    sx[i] = o0.s_x[mc];
+    rsum[i] = o0.rowsum[mc];
+  }
+  const float cws = o0.c_w[0];
+  mfma32_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+  if constexpr (EPI == kEpiOutputGate) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+
+  const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+  if (plain) {
+    const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31);
+      if (m >= a.M) continue;
+      const float inv = 1.0f / sx[i];
+      char* orow = static_cast<char*>(a.out) + (m * a.ldo + n0) * (OUT_DT == kBF16 ? 2 : 4);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int nb = (wn * TN + j) * 32 + 8 * g + 4 * (lane >> 5);
+          if (nb >= nrem) continue;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc0[i][j][4 * g + r] - rsum[i]) * inv) * cws;
+          if (vout && nb + 4 <= nrem) {
+            store4<OUT_DT>(orow, nb, v, true);
+          } else {
+            for (int r = 0; r < 4 && nb + r < nrem; ++r) st<OUT_DT>(orow, nb + r, v[r]);
+          }
+        }
+      }
+    }
+    return;
+  }
+  bool vin = false;
+  if constexpr (EPI == kEpiOutputGate) vin = vec4_ok<OUT_DT>(a.local, a.ld_local) && vec4_ok<OUT_DT>(a.gate, a.ld_gate);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31);
+    if (m >= a.M) continue;
+    const float inv0 = 1.0f / sx[i];
+    float inv1 = 0.0f;
+    int32_t rs1 = 0;
+    if constexpr (EPI == kEpiOutputGate) {
+      inv1 = 1.0f / o1.s_x[m];
+      rs1 = o1.rowsum[m];
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t nb = n0 + (wn * TN + j) * 32 + 8 * g + 4 * (lane >> 5);
+        if (nb >= a.N) continue;
+        int32_t q0[4], q1[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          q0[r] = acc0[i][j][4 * g + r];
+          q1[r] = acc1[i][j][4 * g + r];
+        }
+        epi_store4<EPI, OUT_DT>(a, m, nb, q0, q1, inv0, rsum[i], inv1, rs1, vout, vin);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Output gate over whole rows: a workgroup owns 16 rows and all N = d_model columns (NW waves side
 // by side, NCT 16-column tiles each), so after y = local + sigmoid(gate)*state_proj + ent_proj it
 // can quantize y per token for out_proj without writing y.  Every global operand of the epilogue
@@ -456,7 +745,6 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
 // workgroup's memory traffic is in flight at once; the K loop runs two k-steps per iteration on
 // ping-pong registers so each MFMA group waits only for its own operands.
 // ---------------------------------------------------------------------------
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 // Raw 32-bit words holding four consecutive epilogue values of one row: two bf16 pairs when the
 // row can be read with one 8-byte load, else one word per value.
@@ -981,6 +1269,19 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
     if (t2 >= ntiles) break;
     t = t2;
   }
+}
+
+template <int WM, int WN, int TM, int TN, int EPI>
+int run_mfma32(const LinearArgs& a, hipStream_t st) {
+  using C = Cfg32<WM, WN, TM, TN>;
+  const int64_t tiles = ((a.N + C::BN - 1) / C::BN) * ((a.M + C::BM - 1) / C::BM);
+  TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
+  const unsigned grid = static_cast<unsigned>(tiles);
+  if (a.out_dt == kBF16)
+    mfma32_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
+  else
+    mfma32_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
+  return check_launch("bitlinear mfma32");
 }
 
 template <int WM, int WN, int TM, int TN, int EPI>
