@@ -281,8 +281,15 @@ __device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, 
   const int64_t x = pid % kXcd, i = pid / kXcd;
   const int64_t q = total / kXcd, r = total % kXcd;
   const int64_t tile = x * q + (x < r ? x : r) + i;
-  tm = tile / ntn;
-  tn = tile - tm * ntn;
+  // groups of kGroupM M-tile rows with M fastest: the tiles an XCD runs at once cover a few M rows
+  // and N columns, so both operands' K slabs are shared through its L2
+  constexpr int64_t kGroupM = 8;
+  const int64_t g = tile / (kGroupM * ntn);
+  const int64_t first_m = g * kGroupM;
+  const int64_t gsz = ntm - first_m < kGroupM ? ntm - first_m : kGroupM;
+  const int64_t local = tile - g * kGroupM * ntn;
+  tm = first_m + local % gsz;
+  tn = local / gsz;
 }
 
 // With the weights as the A operand, element r of lane L's accumulator is output row L%16 and
@@ -644,6 +651,72 @@ __device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64
   }
 }
 
+// Plain epilogue staged through LDS.  The accumulator layout gives each lane 4 consecutive outputs
+// of one row, so direct stores cover 32 rows x 16 bytes per instruction; instead each wave writes
+// one 32-row slab of its (already scaled and rounded) outputs into a private LDS buffer and reads
+// it back as 16-byte row-contiguous chunks, so a store instruction covers whole row segments.
+// Output values are the same as the direct path's.  Needs a 16-byte aligned output and row pitch.
+template <class C, int NWV, int TM, int TN, int OUT_DT>
+__device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v16i (&acc)[TM][TN], const float (&sx)[TM],
+                                                   const int32_t (&rsum)[TM], float cws, int64_t m0, int64_t n0,
+                                                   int wm, int wn, char* smem) {
+  constexpr int ES = OUT_DT == kBF16 ? 2 : 4;
+  constexpr int JU = (NWV * 32 * (TN * 32 * ES + 16) <= 2 * C::STAGE) ? TN : 1;  // 32-col tiles per slab
+  constexpr int RB = JU * 32 * ES;   // bytes of one staged row
+  constexpr int PITCH = RB + 16;     // padded so the column-wise staging stores spread over the banks
+  constexpr int CPR = RB / 16;       // 16-byte chunks per row
+  constexpr int VPC = 16 / ES;       // outputs per chunk
+  static_assert(NWV * 32 * PITCH <= 2 * C::STAGE, "staging buffers exceed the stage LDS");
+  static_assert((32 * CPR) % 64 == 0, "chunks must divide over the wave");
+  const int lane = threadIdx.x & 63;
+  char* wb = smem + (threadIdx.x >> 6) * 32 * PITCH;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const float inv = 1.0f / sx[i];
+    const int64_t mb = m0 + (wm * TM + i) * 32;
+#pragma unroll
+    for (int jb = 0; jb < TN; jb += JU) {
+      __syncthreads();  // the buffer's previous contents (or the last K tile) are consumed
+#pragma unroll
+      for (int jj = 0; jj < JU; ++jj) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc[i][jb + jj][4 * g + r] - rsum[i]) * inv) * cws;
+          char* p = wb + (lane & 31) * PITCH + (jj * 32 + 8 * g + 4 * (lane >> 5)) * ES;
+          if constexpr (OUT_DT == kBF16)
+            *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+          else
+            *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+      __syncthreads();
+      const int64_t nb = n0 + (wn * TN + jb) * 32;
+#pragma unroll
+      for (int it = 0; it < 32 * CPR / 64; ++it) {
+        const int idx = it * 64 + lane;
+        const int row = idx / CPR, ch = idx % CPR;
+        const int64_t m = mb + row, n = nb + ch * VPC;
+        if (m >= a.M || n >= a.N) continue;
+        const uint4 d = *reinterpret_cast<const uint4*>(wb + row * PITCH + ch * 16);
+        char* dst = static_cast<char*>(a.out) + (m * a.ldo + n) * ES;
+        if (n + VPC <= a.N) {
+          *reinterpret_cast<uint4*>(dst) = d;
+        } else {
+          const uint32_t wd[4] = {d.x, d.y, d.z, d.w};
+          for (int e = 0; e < a.N - n; ++e) {
+            if constexpr (OUT_DT == kBF16)
+              reinterpret_cast<uint16_t*>(dst)[e] = static_cast<uint16_t>(wd[e >> 1] >> (16 * (e & 1)));
+            else
+              reinterpret_cast<uint32_t*>(dst)[e] = wd[e];
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
 __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   using C = Cfg32<WM, WN, TM, TN>;
@@ -679,6 +752,10 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   if constexpr (EPI == kEpiOutputGate) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
 
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+  if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
+    epi32_plain_staged<C, WM * WN, TM, TN, OUT_DT>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
+    return;
+  }
   if (plain) {
     const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));
 #pragma unroll
@@ -1429,10 +1506,12 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
   }
   if (a.epilogue == kEpiStore) {
     if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
-    // 128x128 tiles (4 waves of 64x64) when they still give two workgroups per CU, else 64x128
-    // (waves along N); measured at the layer shapes (in_proj / out_proj / configs[1] / configs[4])
-    if (tiles128(a) >= 512) return run_mfma<2, 2, 4, 4, kEpiStore>(a, st);
-    return run_mfma<1, 4, 4, 2, kEpiStore>(a, st);
+    // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
+    // enough of them, else 64x128 (4 waves side by side along N); measured at the layer shapes
+    // (in_proj / out_proj / configs[1] / configs[4])
+    const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+    if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
+    return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
   if (tiles128(a) >= 512) return run_mfma<2, 2, 4, 4, kEpiOutputGate>(a, st);
