@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 2
+#define TESM_HIP_ABI_VERSION 3
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -281,6 +281,11 @@ typedef struct tesm_hip_mimo_layer {
   void* k_cache;              /* optional (B, window, n_heads, ent_rank), cache_dt */
   void* v_cache;              /* optional (B, window, n_heads, d_state), cache_dt */
   int cache_dt;               /* 0 f32, 1 bf16 */
+  /* optional entanglement statistics (tesm_mimo.py:458-523, window branch): hard ternary of
+   * q.k/sqrt(ent_rank) over the first S = min(L, 64) positions' complete windows of W = min(window, L)
+   * slots, (B, S-W+1, n_heads, W) in dt, and per batch row (#positive, #negative, #zero) */
+  void* stats_ternary;
+  int32_t* stats_counts;      /* (B, 3) */
 } tesm_hip_mimo_layer;
 
 int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p);

@@ -168,6 +168,8 @@ class TESM_SISO(nn.Module):
         self.last_entanglement_stats = None
         self._last_cross_layer_state = None
         self._last_scan_state_f64 = None
+        self.register_buffer("_stats_ternary_buffer", None, persistent=False)  # tesm.py:582-584
+        self.register_buffer("_stats_total_buffer", torch.tensor(1.0), persistent=False)
 
     # -- temperature and ternary decision (tesm.py:587-618, 672-714) -----------
     def get_temperature(self):
@@ -518,6 +520,40 @@ class TESMMIMO_Optimized(TESM_SISO):
         self._record_map(tern)
         return ent, ent - states
 
+    def _update_entanglement_stats_mimo(self, q, k):
+        """tesm_mimo.py:458-523: hard-threshold ternary statistics of the first positions (q, k RoPE'd)."""
+        with torch.no_grad():
+            B, L, H, R = q.shape
+            W = min(self.entanglement_window, L) if self.entanglement_window > 0 else L
+            thr = self.entanglement_threshold
+            if self.entanglement_window == 0:  # :469-482, sampled global scores
+                n = min(L, 32)
+                scores = torch.einsum("bshr,bthr->bst", q[:, :n], k[:, :n]) / math.sqrt(R)
+            else:  # :483-503
+                n = min(L, 64)
+                qs, ks = q[:, :n], k[:, :n]
+                kw = ks.unfold(1, W, 1)  # (B, n-W+1, H, R, W)
+                V = kw.size(1)
+                qv = qs[:, W - 1:W - 1 + V]
+                scores = (qv.unsqueeze(-1) * kw).sum(dim=-2) / math.sqrt(R)
+            tern = torch.where(scores > thr, torch.ones_like(scores),
+                               torch.where(scores < -thr, -torch.ones_like(scores), torch.zeros_like(scores)))
+            total = float(tern.numel())
+            if total > 0:  # :506-519
+                flat = tern.detach().flatten()
+                self._ternary_stats_for_logging = (flat, total)
+                self._stats_ternary_buffer = flat
+                self._stats_total_buffer = torch.tensor(total, device=tern.device)
+                self.last_entanglement_stats = {
+                    "positive": float((tern > 0).sum().item()) / total,
+                    "negative": float((tern < 0).sum().item()) / total,
+                    "zero": float((tern == 0).sum().item()) / total,
+                }
+            else:
+                self._ternary_stats_for_logging = None
+                self._stats_ternary_buffer = None
+                self.last_entanglement_stats = None
+
     def _split_heads(self, proj, B, L):
         H, D, R = self.n_heads, self.d_state, self.ent_rank
         local, sv, decay, write, gate, q, k = torch.split(
@@ -562,6 +598,7 @@ class TESMMIMO_Optimized(TESM_SISO):
             changes.append(c.unsqueeze(2))
         ent = torch.einsum("blrhd,hrd->blhd", torch.cat(ents, dim=2).float(), self.mimo_o.float())
         chg = torch.einsum("blrhd,hrd->blhd", torch.cat(changes, dim=2).float(), self.mimo_o.float())
+        self._update_entanglement_stats_mimo(q, k)  # tesm_mimo.py:1019-1020
         if inference_params is not None:  # tesm_mimo.py:1022-1037
             cache = inference_params.get("state_cache")
             if cache is not None and "state" in cache:

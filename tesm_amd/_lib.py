@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -101,6 +101,7 @@ class MimoLayer(ctypes.Structure):
         ("in_proj", Linear), ("state_proj", Linear), ("ent_proj", Linear), ("out_proj", Linear),
         ("decay_bias", P), ("local_bias", P), ("rope", P), ("mimo_coef", P), ("mimo_x0sq", P),
         ("y", P), ("h_final", P), ("last_state", P), ("k_cache", P), ("v_cache", P), ("cache_dt", I32),
+        ("stats_ternary", P), ("stats_counts", P),
     ]
 
 

@@ -814,6 +814,26 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   ea.ld_s = HD;
   ea.wts = s.wts;
   if ((rc = launch_local_ent(ea, st))) return rc;
+  if (p.stats_ternary || p.stats_counts) {  // tesm_mimo.py:1019-1020 -> 458-523
+    MimoStatsArgs sa2;
+    sa2.dt = dt;
+    sa2.B = p.B;
+    sa2.L = p.L;
+    sa2.H = H;
+    sa2.R = R;
+    sa2.W = std::min<int64_t>(p.window, p.L);
+    sa2.S = std::min<int64_t>(p.L, 64);
+    sa2.q = ea.q;
+    sa2.ld_q = n_in;
+    sa2.k = ea.k;
+    sa2.ld_k = n_in;
+    sa2.rope = ea.rope;
+    sa2.sqrt_r = static_cast<float>(std::sqrt(static_cast<double>(R)));
+    sa2.thr = p.thr;
+    sa2.ternary = p.stats_ternary;
+    sa2.counts = p.stats_counts;
+    if ((rc = launch_mimo_stats(sa2, st))) return rc;
+  }
   // 4. window mix, entangled state, rank merge; tanh(E c) and C c in dt for the projections
   MimoMixArgs ma;
   ma.dt = dt;

@@ -24,6 +24,27 @@ struct MimoMixArgs {
 };
 int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st);
 
+// Entanglement statistics of tesm_mimo.py:458-523 (window > 0 branch), taken on the RoPE'd q and k
+// of the first S = min(L, 64) positions: for every complete window v in [0, S - W + 1), head h and
+// slot w, score = fl(fl(sum_r fl(q[W-1+v, h, r] * k[v+w, h, r])) / sqrt(R)) (no local bias) and its hard
+// ternary against +-thr, written in dt as (B, V, H, W); counts[b] = (#positive, #negative, #zero).
+struct MimoStatsArgs {
+  int dt = 0;
+  int64_t B = 0, L = 0, H = 0, R = 0;
+  int64_t W = 0;                 // window actually used: min(entanglement_window, L)
+  int64_t S = 0;                 // sampled positions: min(L, 64); V = S - W + 1 >= 1
+  const void* q = nullptr;       // (b, t, h, r) at q[(b*L + t)*ld_q + h*R + r], raw (pre-RoPE)
+  int64_t ld_q = 0;
+  const void* k = nullptr;
+  int64_t ld_k = 0;
+  const float2* rope = nullptr;  // (L, R/2) cos/sin rounded to dt
+  float sqrt_r = 0.0f;           // float(sqrt(R)), the divisor
+  float thr = 0.0f;              // threshold rounded to dt
+  void* ternary = nullptr;       // (B, V, H, W) in dt
+  int32_t* counts = nullptr;     // (B, 3)
+};
+int launch_mimo_stats(const MimoStatsArgs& a, hipStream_t st);
+
 // Rank-0 final state h[b, c] = float64(S[b, L-1, c] * x0sq[c]) and, optionally, its float32 copy.
 int launch_mimo_final(const float* S, const float* x0sq, int64_t B, int64_t L, int64_t C, double* h_final,
                       float* last, hipStream_t st);

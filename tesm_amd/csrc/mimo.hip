@@ -85,7 +85,68 @@ __global__ __launch_bounds__(256) void mimo_final_kernel(const float* S, const f
   if (last) last[i] = v;
 }
 
+// One workgroup per batch row; one thread per (v, h, w) score, products summed in natural r order.
+template <int DT>
+__global__ __launch_bounds__(256) void mimo_stats_kernel(MimoStatsArgs a) {
+  __shared__ int32_t cnt[3][4];
+  const int64_t b = blockIdx.x;
+  const int64_t V = a.S - a.W + 1, half = a.R / 2;
+  const int64_t n = V * a.H * a.W;
+  int32_t pos = 0, neg = 0;
+  for (int64_t e = threadIdx.x; e < n; e += 256) {
+    const int64_t v = e / (a.H * a.W), h = (e / a.W) % a.H, w = e % a.W;
+    const int64_t tq = a.W - 1 + v, tk = v + w;
+    const int64_t qo = (b * a.L + tq) * a.ld_q + h * a.R, ko = (b * a.L + tk) * a.ld_k + h * a.R;
+    float acc = 0.0f;
+    for (int part = 0; part < 2; ++part) {
+      for (int64_t i = 0; i < half; ++i) {
+        float q1, q2, k1, k2;
+        rope_pair<DT>(ld<DT>(a.q, qo + i), ld<DT>(a.q, qo + i + half), a.rope[tq * half + i], q1, q2);
+        rope_pair<DT>(ld<DT>(a.k, ko + i), ld<DT>(a.k, ko + i + half), a.rope[tk * half + i], k1, k2);
+        acc += part == 0 ? rnd<DT>(q1 * k1) : rnd<DT>(q2 * k2);
+      }
+    }
+    const float sc = rnd<DT>(rnd<DT>(acc) / a.sqrt_r);
+    const float t = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
+    pos += t > 0.0f;
+    neg += t < 0.0f;
+    st<DT>(a.ternary, b * n + e, t);
+  }
+  // wave sums, then the workgroup's
+  for (int o = 32; o > 0; o >>= 1) {
+    pos += __shfl_xor(pos, o);
+    neg += __shfl_xor(neg, o);
+  }
+  const int wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    cnt[0][wv] = pos;
+    cnt[1][wv] = neg;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int32_t p = cnt[0][0] + cnt[0][1] + cnt[0][2] + cnt[0][3];
+    const int32_t q = cnt[1][0] + cnt[1][1] + cnt[1][2] + cnt[1][3];
+    a.counts[b * 3 + 0] = p;
+    a.counts[b * 3 + 1] = q;
+    a.counts[b * 3 + 2] = static_cast<int32_t>(n) - p - q;
+  }
+}
+
 }  // namespace
+
+int launch_mimo_stats(const MimoStatsArgs& a, hipStream_t st) {
+  TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "mimo stats: dtype must be 0 or 1");
+  if (a.B == 0) return kOk;
+  TESM_REQUIRE(a.q && a.k && a.rope && a.ternary && a.counts, kErrInvalidArg, "mimo stats: null pointer");
+  TESM_REQUIRE(a.W >= 1 && a.S >= a.W && a.S <= a.L && a.R >= 2 && a.R % 2 == 0 && a.H >= 1, kErrInvalidArg,
+               "mimo stats: need 1 <= W <= S <= L and an even R");
+  TESM_REQUIRE((a.S - a.W + 1) * a.H * a.W <= 0x7fffffff, kErrUnsupported, "mimo stats: too many scores");
+  if (a.dt == kBF16)
+    mimo_stats_kernel<kBF16><<<static_cast<unsigned>(a.B), 256, 0, st>>>(a);
+  else
+    mimo_stats_kernel<kF32><<<static_cast<unsigned>(a.B), 256, 0, st>>>(a);
+  return check_launch("mimo stats");
+}
 
 int launch_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t H, int64_t Rm, int64_t D, float* coef,
                      float* x0sq, hipStream_t st) {

@@ -101,6 +101,8 @@ class TESM_SISO(nn.Module):
         self.last_entanglement_stats = None
         self._last_cross_layer_state = None
         self._last_scan_state_f64 = None
+        self.register_buffer("_stats_ternary_buffer", None, persistent=False)  # tesm.py:582-584
+        self.register_buffer("_stats_total_buffer", torch.tensor(1.0), persistent=False)
         self._rope = {}
         self._bias_cache = None
 

@@ -64,6 +64,36 @@ class TESMMIMO_Optimized(TESM_SISO):
         self.state_proj = BitLinear(self.d_state_total, d_model, **bl)
         self.ent_proj = BitLinear(self.d_state_total, d_model, **bl)
         self._coef_cache = None
+        self._stats_totals = {}
+
+    # -- entanglement statistics (tesm_mimo.py:458-523) --------------------------------
+    # The forward leaves the per-row counts on the device; the dict the reference fills with three
+    # .item() calls is formed when the attribute is first read, so a forward never waits on the host.
+    @property
+    def last_entanglement_stats(self):
+        pending = self.__dict__.get("_stats_pending")
+        if pending is not None:
+            counts, total = pending
+            pos, neg, zero = (int(v) for v in counts.cpu().sum(dim=0).tolist())
+            self.__dict__["_stats_value"] = {"positive": pos / total, "negative": neg / total, "zero": zero / total}
+            self.__dict__["_stats_pending"] = None
+        return self.__dict__.get("_stats_value")
+
+    @last_entanglement_stats.setter
+    def last_entanglement_stats(self, value):
+        self.__dict__["_stats_value"] = value
+        self.__dict__["_stats_pending"] = None
+
+    def _stats_buffers(self, B, L, dt, dev):
+        """Ternary (B, V, n_heads, W) and per-row counts for the statistics of the first min(L, 64)
+        positions; V = min(L, 64) - min(window, L) + 1 complete windows (tesm_mimo.py:465, 485-490)."""
+        W = min(self.entanglement_window, L)
+        S = min(L, 64)
+        if W > S:  # the reference's unfold (tesm_mimo.py:487) raises here
+            raise RuntimeError(f"maximum size for tensor at dimension 1 is {S} but size is {W}")
+        tern = torch.empty((B, S - W + 1, self.n_heads, W), dtype=dt, device=dev)
+        counts = torch.empty((B, 3), dtype=torch.int32, device=dev)
+        return tern, counts
 
     # -- cached device constants ---------------------------------------------------
     def _mimo_coef(self, dtype):
@@ -142,6 +172,8 @@ class TESMMIMO_Optimized(TESM_SISO):
         desc.y = y.data_ptr()
         desc.h_final = h_final.data_ptr()
         desc.last_state = last.data_ptr()
+        stern, scount = self._stats_buffers(B, L, dt, dev)
+        desc.stats_ternary, desc.stats_counts = stern.data_ptr(), scount.data_ptr()
         k_cache = v_cache = None
         if cache is not None:
             k_cache, v_cache = self._mimo_cache_buffers(cache, B, L, dev)
@@ -160,7 +192,15 @@ class TESMMIMO_Optimized(TESM_SISO):
         self._last_cross_layer_state = last
         self._last_scan_state_f64 = h_final
         self.last_entanglement_map = None
-        self.last_entanglement_stats = None
+        flat = stern.reshape(-1)  # tesm_mimo.py:506-519
+        total = float(flat.numel())
+        key = (total, dev)
+        if key not in self._stats_totals:
+            self._stats_totals[key] = torch.tensor(total, device=dev)
+        self._stats_ternary_buffer = flat
+        self._stats_total_buffer = self._stats_totals[key]
+        self._ternary_stats_for_logging = (flat, total)
+        self.__dict__["_stats_pending"] = (scount, total)
         return y, h_final
 
     # -- inference cache (tesm_mimo.py:689-731) ----------------------------------------

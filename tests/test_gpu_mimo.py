@@ -101,3 +101,33 @@ def test_mimo_decode_step_is_refused():
         m(torch.randn(2, 9, 64, device=DEV), inference_params={"state_cache": cache})
         with pytest.raises(RuntimeError, match="kernel_backend"):
             m(torch.randn(2, 1, 64, device=DEV), inference_params={"state_cache": cache})
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,L,H,R,W", [(2, 100, 4, 16, 16), (1, 37, 2, 8, 8), (3, 5, 3, 8, 8), (1, 64, 2, 16, 64)])
+def test_mimo_entanglement_stats_vs_oracle(dtype, B, L, H, R, W):
+    """tesm_mimo.py:458-523: ternary of the first min(L, 64) positions' complete windows and the
+    positive / negative / zero fractions, set on every prefill forward."""
+    meta = dict(seed=5 + L, dm=64, D=16, H=H, Rm=2, R=R, W=W, thr=0.05, decay_bias=2.0, max_seq_len=128)
+    ref = build(ot.TESMMIMO_Optimized, meta).to(dtype)
+    m = build(TESMMIMO_Optimized, meta).to(DEV).to(dtype)
+    u = torch.randn(B, L, 64, generator=torch.Generator().manual_seed(9)).to(dtype)
+    with torch.no_grad():
+        ref(u)
+        m(u.to(DEV))
+    want, got = ref._stats_ternary_buffer, m._stats_ternary_buffer
+    assert got.dtype == dtype and got.shape == want.shape
+    # a one-ulp difference of a score (summation order) may flip a decision at the threshold
+    diff = (got.cpu() != want).float().mean().item()
+    assert diff <= (0.002 if dtype == torch.float32 else 0.01), diff
+    a, b = m.last_entanglement_stats, ref.last_entanglement_stats
+    assert set(a) == {"positive", "negative", "zero"}
+    assert abs(sum(a.values()) - 1.0) < 1e-9
+    for k in a:
+        assert abs(a[k] - b[k]) <= diff + 1e-12, (k, a[k], b[k])
+    assert m._ternary_stats_for_logging[1] == float(want.numel())
+    assert float(m._stats_total_buffer) == float(want.numel())
+    # the dict is formed once; assigning None clears it as in the reference
+    assert m.last_entanglement_stats is a
+    m.last_entanglement_stats = None
+    assert m.last_entanglement_stats is None
