@@ -275,9 +275,9 @@ __device__ __forceinline__ void mfma_mainloop(const LinearOperand& o, int64_t M,
 // Tile order for a 1-D grid: workgroups are handed to the 8 XCDs round-robin by id, so id is
 // mapped to a tile such that each XCD gets a contiguous run of tiles (row-major over
 // (M tile, N tile)); consecutive tiles of one XCD share A rows in that XCD's L2.
-__device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
+__device__ __forceinline__ void xcd_tile_of(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
   constexpr int64_t kXcd = 8;
-  const int64_t total = ntm * ntn, pid = blockIdx.x;
+  const int64_t total = ntm * ntn;
   const int64_t x = pid % kXcd, i = pid / kXcd;
   const int64_t q = total / kXcd, r = total % kXcd;
   const int64_t tile = x * q + (x < r ? x : r) + i;
@@ -290,6 +290,9 @@ __device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, 
   const int64_t local = tile - g * kGroupM * ntn;
   tm = first_m + local % gsz;
   tn = local / gsz;
+}
+__device__ __forceinline__ void xcd_tile(int64_t ntm, int64_t ntn, int64_t& tm, int64_t& tn) {
+  xcd_tile_of(blockIdx.x, ntm, ntn, tm, tn);
 }
 
 // With the weights as the A operand, element r of lane L's accumulator is output row L%16 and
@@ -656,17 +659,23 @@ __device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64
 // one 32-row slab of its (already scaled and rounded) outputs into a private LDS buffer and reads
 // it back as 16-byte row-contiguous chunks, so a store instruction covers whole row segments.
 // Output values are the same as the direct path's.  Needs a 16-byte aligned output and row pitch.
-template <class C, int NWV, int TM, int TN, int OUT_DT>
+// LDS bytes the staged epilogue of NWV waves needs with JU 32-column tiles per slab.
+template <int NWV, int JU, int OUT_DT>
+constexpr int epi32_bytes() {
+  return NWV * 32 * (JU * 32 * (OUT_DT == kBF16 ? 2 : 4) + 16);
+}
+
+template <int NWV, int TM, int TN, int OUT_DT, int AVAIL>
 __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v16i (&acc)[TM][TN], const float (&sx)[TM],
                                                    const int32_t (&rsum)[TM], float cws, int64_t m0, int64_t n0,
                                                    int wm, int wn, char* smem) {
   constexpr int ES = OUT_DT == kBF16 ? 2 : 4;
-  constexpr int JU = (NWV * 32 * (TN * 32 * ES + 16) <= 2 * C::STAGE) ? TN : 1;  // 32-col tiles per slab
+  constexpr int JU = epi32_bytes<NWV, TN, OUT_DT>() <= AVAIL ? TN : 1;  // 32-col tiles per slab
   constexpr int RB = JU * 32 * ES;   // bytes of one staged row
   constexpr int PITCH = RB + 16;     // padded so the column-wise staging stores spread over the banks
   constexpr int CPR = RB / 16;       // 16-byte chunks per row
   constexpr int VPC = 16 / ES;       // outputs per chunk
-  static_assert(NWV * 32 * PITCH <= 2 * C::STAGE, "staging buffers exceed the stage LDS");
+  static_assert(NWV * 32 * PITCH <= AVAIL, "staging buffers exceed the LDS given");
   static_assert((32 * CPR) % 64 == 0, "chunks must divide over the wave");
   const int lane = threadIdx.x & 63;
   char* wb = smem + (threadIdx.x >> 6) * 32 * PITCH;
@@ -676,7 +685,7 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
     const int64_t mb = m0 + (wm * TM + i) * 32;
 #pragma unroll
     for (int jb = 0; jb < TN; jb += JU) {
-      __syncthreads();  // the buffer's previous contents (or the last K tile) are consumed
+      lds_barrier();  // the buffer's previous contents (or the last K tile) are consumed
 #pragma unroll
       for (int jj = 0; jj < JU; ++jj) {
 #pragma unroll
@@ -691,7 +700,7 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
             *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
         }
       }
-      __syncthreads();
+      lds_barrier();
       const int64_t nb = n0 + (wn * TN + jb) * 32;
 #pragma unroll
       for (int it = 0; it < 32 * CPR / 64; ++it) {
@@ -753,7 +762,7 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
 
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
   if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
-    epi32_plain_staged<C, WM * WN, TM, TN, OUT_DT>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
+    epi32_plain_staged<WM * WN, TM, TN, OUT_DT, 2 * C::STAGE>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
     return;
   }
   if (plain) {
@@ -1361,24 +1370,6 @@ int run_mfma32(const LinearArgs& a, hipStream_t st) {
   return check_launch("bitlinear mfma32");
 }
 
-template <int WM, int WN, int TM, int TN, int EPI>
-int run_mfma(const LinearArgs& a, hipStream_t st) {
-  using C = Cfg<WM, WN, TM, TN>;
-  const int64_t tiles = ((a.N + C::BN - 1) / C::BN) * ((a.M + C::BM - 1) / C::BM);
-  TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
-  const unsigned grid = static_cast<unsigned>(tiles);
-  if (a.out_dt == kBF16)
-    mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
-  else
-    mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
-  return check_launch("bitlinear mfma");
-}
-
-inline bool host_vec4_ok(const void* p, int64_t ld, int dt) {
-  const int64_t bytes = dt == kBF16 ? 8 : 16;
-  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (dt == kBF16 ? 2 : 4)) % bytes == 0;
-}
-
 struct DeviceLimits {
   int cus = 0;
   int64_t lds = 0;
@@ -1399,6 +1390,24 @@ inline DeviceLimits device_limits() {
     d.cus = cus;
   }
   return d;
+}
+
+template <int WM, int WN, int TM, int TN, int EPI>
+int run_mfma(const LinearArgs& a, hipStream_t st) {
+  using C = Cfg<WM, WN, TM, TN>;
+  const int64_t tiles = ((a.N + C::BN - 1) / C::BN) * ((a.M + C::BM - 1) / C::BM);
+  TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
+  const unsigned grid = static_cast<unsigned>(tiles);
+  if (a.out_dt == kBF16)
+    mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
+  else
+    mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
+  return check_launch("bitlinear mfma");
+}
+
+inline bool host_vec4_ok(const void* p, int64_t ld, int dt) {
+  const int64_t bytes = dt == kBF16 ? 8 : 16;
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (dt == kBF16 ? 2 : 4)) % bytes == 0;
 }
 
 template <int NW, int NCT, int NKS>
@@ -1482,8 +1491,6 @@ int check_operand(const LinearOperand& o, int64_t Kp, const char* which) {
 
 }  // namespace
 
-inline int64_t tiles128(const LinearArgs& a) { return ((a.M + 127) / 128) * ((a.N + 127) / 128); }
-
 int launch_linear(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.M >= 0 && a.N >= 0, kErrInvalidArg, "bitlinear: negative size");
   TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "bitlinear: Kp must be a positive multiple of 128");
@@ -1514,8 +1521,9 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
-  if (tiles128(a) >= 512) return run_mfma<2, 2, 4, 4, kEpiOutputGate>(a, st);
-  return run_mfma<1, 4, 4, 2, kEpiOutputGate>(a, st);
+  const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+  if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiOutputGate>(a, st);
+  return run_mfma32<1, 4, 2, 1, kEpiOutputGate>(a, st);
 }
 
 int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {

@@ -34,6 +34,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Two floats rounded to bf16 and packed low / high into one dword (a single conversion).
+// Workgroup barrier that orders LDS only: each wave waits for its own LDS operations, not for its
+// outstanding global loads and stores (which __syncthreads' workgroup fence would drain).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
@@ -74,6 +82,18 @@ __device__ __forceinline__ void st(void* p, int64_t i, float v) {
     static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
   } else {
     static_cast<float*>(p)[i] = v;
+  }
+}
+
+// Four consecutive elements at p[i .. i+3] in one store; needs i*size 8-byte (bf16) / 16-byte (f32) aligned.
+template <int DT>
+__device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {
+  if constexpr (DT == kBF16) {
+    const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+    const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = make_uint2(lo, hi);
+  } else {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 

@@ -29,49 +29,138 @@ __global__ __launch_bounds__(256) void mimo_coef_kernel(const void* x, const voi
   x0sq[i] = x0 * x0;
 }
 
-constexpr int kMimoTP = 64;  // positions per workgroup
-constexpr int kMimoDS = 64;  // channels per workgroup
+constexpr int kMixTP = 64;           // positions per workgroup
+constexpr int kMixDS = 32;           // channels per block
+constexpr int kMixSP = kMixDS + 8;   // state row pitch (floats): rows r and r + 4 fall in opposite bank halves
+constexpr int kMixWP = kMixTP + 4;   // weight row pitch (floats)
+constexpr int kMixCB = 16;           // channel blocks per workgroup
+constexpr int kMixLD = 4;            // float4 state loads per thread per block: (kMixTP + 63) * 8 <= 4 * 256
 
-// Window mix for one (batch row, head) pair, kMimoTP positions x kMimoDS channels: key position of
-// window slot w is t - W + 1 + w (tesm_mimo.py:536-586); slots the reference drops carry weight 0.
-template <int DT>
+// Window mix for one (batch row, head) pair, kMixTP positions x kMixCB blocks of kMixDS channels.
+// Key position of window slot w is t - W + 1 + w (tesm_mimo.py:536-586); slots the reference drops
+// carry weight 0.  The weights (transposed, [w][position]) are staged in LDS once; the states of one
+// channel block plus its W - 1 row halo are staged per block, and the next block's states are loaded
+// into registers while the current one is mixed and stored.  Each thread owns 2 positions x 4 channels
+// and walks the window keeping the 2 state rows it needs in registers, so every 8 multiply-adds cost
+// one state and one weight read.  Sums run over w in increasing order.  WT is W when it is a
+// compile-time case (index math by shifts), else 0.
+template <int DT, bool VEC, int WT>
 __global__ __launch_bounds__(256) void mimo_mix_kernel(MimoMixArgs a) {
-  extern __shared__ float lds_mimo[];
-  const int64_t W = a.W;
-  const int64_t rows = kMimoTP + W - 1;
-  float* srow = lds_mimo;                 // [rows][kMimoDS]
-  float* wt = lds_mimo + rows * kMimoDS;  // [kMimoTP][W]
+  extern __shared__ __attribute__((aligned(16))) float lds_mimo[];
+  const int W = WT > 0 ? WT : static_cast<int>(a.W);
+  const int rows = kMixTP + W - 1;
+  float* srow = lds_mimo;                  // [rows][kMixSP]
+  float* wtT = lds_mimo + rows * kMixSP;   // [W][kMixWP]
   const int64_t bh = blockIdx.z;
   const int64_t b = bh / a.H, h = bh - b * a.H;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kMimoTP;
-  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kMimoDS;
-  const int c = threadIdx.x & 63, pq = threadIdx.x >> 6;
-  const int64_t d = d0 + c;
-  const bool dok = d < a.D;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kMixTP;
+  const int64_t nblk = (a.D + kMixDS - 1) / kMixDS;
+  const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kMixCB;
+  const int64_t cb1 = cb0 + kMixCB < nblk ? cb0 + kMixCB : nblk;
+  const int tid = threadIdx.x;
   const int64_t C = a.H * a.D;
-  for (int64_t r = pq; r < rows; r += 4) {
-    const int64_t t = t0 - (W - 1) + r;
-    srow[r * kMimoDS + c] = (dok && t >= 0 && t < a.L) ? a.S[(b * a.L + t) * C + h * a.D + d] : 0.0f;
+  const int64_t tlo = t0 - (W - 1);  // position of LDS row 0
+  const int nvalid = static_cast<int>(a.L - t0 < kMixTP ? a.L - t0 : kMixTP);
+  const float* Sh = a.S + (b * a.L) * C + h * a.D;
+
+  // state prefetch of channel block cb into registers (rows outside [0, L) and channels past D are 0)
+  float4 pre[kMixLD];
+  auto prefetch = [&](int64_t cb) {
+#pragma unroll
+    for (int k = 0; k < kMixLD; ++k) {
+      const int i = tid + k * 256;
+      const int r = i >> 3, c4 = 4 * (i & 7);
+      const int64_t t = tlo + r;
+      const int64_t dc = cb * kMixDS + c4;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (r < rows && t >= 0 && t < a.L) {
+        const float* src = Sh + t * C + dc;
+        if (VEC && dc + 3 < a.D) {
+          v = *reinterpret_cast<const float4*>(src);
+        } else {
+          if (dc + 0 < a.D) v.x = src[0];
+          if (dc + 1 < a.D) v.y = src[1];
+          if (dc + 2 < a.D) v.z = src[2];
+          if (dc + 3 < a.D) v.w = src[3];
+        }
+      }
+      pre[k] = v;
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int k = 0; k < kMixLD; ++k) {
+      const int i = tid + k * 256;
+      const int r = i >> 3, c4 = 4 * (i & 7);
+      if (r < rows) *reinterpret_cast<float4*>(srow + r * kMixSP + c4) = pre[k];
+    }
+  };
+  prefetch(cb0);
+  const float* wb = a.wts + ((b * a.L + t0) * a.H + h) * W;
+  const int64_t wrow = a.H * W;  // floats between the weights of consecutive positions
+  for (int i = tid; i < kMixTP * W; i += 256) {
+    const int p = i / W, w = i - p * W;
+    wtT[w * kMixWP + p] = p < nvalid ? wb[p * wrow + w] : 0.0f;
   }
-  for (int64_t i = threadIdx.x; i < kMimoTP * W; i += 256) {
-    const int64_t p = i / W, w = i - p * W;
-    const int64_t t = t0 + p;
-    wt[i] = t < a.L ? a.wts[((b * a.L + t) * a.H + h) * W + w] : 0.0f;
-  }
+  stage();
   __syncthreads();
-  if (!dok) return;
-  const float cf = a.coef[h * a.D + d];
-  for (int p = pq; p < kMimoTP; p += 4) {
-    const int64_t t = t0 + p;
-    if (t >= a.L) break;
-    float acc = 0.0f;
-    for (int64_t w = 0; w < W; ++w) acc += wt[p * W + w] * srow[(p + w) * kMimoDS + c];
-    const float s = srow[(p + W - 1) * kMimoDS + c];
-    const float e = s + a.ent_scale * (acc - s);
-    const float ch = e - s;
-    const int64_t o = (b * a.L + t) * C + h * a.D + d;
-    st<DT>(a.te, o, tanhf_(e * cf));
-    st<DT>(a.cc, o, ch * cf);
+  const int p0 = 2 * (tid >> 3), c0 = 4 * (tid & 7);
+  const float* sp = srow + p0 * kMixSP + c0;
+  for (int64_t cb = cb0; cb < cb1; ++cb) {
+    prefetch(cb + 1 < cb1 ? cb + 1 : cb);  // the last block re-reads itself (never staged)
+    float acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    float4 s0 = *reinterpret_cast<const float4*>(sp);
+#pragma unroll 4
+    for (int w = 0; w < W; ++w) {
+      const float4 s1 = *reinterpret_cast<const float4*>(sp + (w + 1) * kMixSP);
+      const float2 wv = *reinterpret_cast<const float2*>(wtT + w * kMixWP + p0);
+      acc[0][0] = __builtin_fmaf(wv.x, s0.x, acc[0][0]);
+      acc[0][1] = __builtin_fmaf(wv.x, s0.y, acc[0][1]);
+      acc[0][2] = __builtin_fmaf(wv.x, s0.z, acc[0][2]);
+      acc[0][3] = __builtin_fmaf(wv.x, s0.w, acc[0][3]);
+      acc[1][0] = __builtin_fmaf(wv.y, s1.x, acc[1][0]);
+      acc[1][1] = __builtin_fmaf(wv.y, s1.y, acc[1][1]);
+      acc[1][2] = __builtin_fmaf(wv.y, s1.z, acc[1][2]);
+      acc[1][3] = __builtin_fmaf(wv.y, s1.w, acc[1][3]);
+      s0 = s1;
+    }
+    const int64_t d = cb * kMixDS + c0;
+    float cf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cf[j] = d + j < a.D ? a.coef[h * a.D + d + j] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (p0 + i >= nvalid) break;
+      const int64_t t = t0 + p0 + i;
+      const float* srq = srow + (p0 + i + W - 1) * kMixSP + c0;  // the query position's own state
+      float te[4], cc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sv = srq[j];
+        const float e = sv + a.ent_scale * (acc[i][j] - sv);
+        te[j] = tanhf_(e * cf[j]);
+        cc[j] = (e - sv) * cf[j];
+      }
+      const int64_t o = (b * a.L + t) * C + h * a.D + d;
+      if (VEC && d + 3 < a.D) {
+        st4<DT>(a.te, o, te);
+        st4<DT>(a.cc, o, cc);
+      } else {
+        for (int j = 0; j < 4 && d + j < a.D; ++j) {
+          st<DT>(a.te, o + j, te[j]);
+          st<DT>(a.cc, o + j, cc[j]);
+        }
+      }
+    }
+    __syncthreads();  // every thread is done with this block's states
+    if (cb + 1 < cb1) {
+      stage();
+      __syncthreads();
+    }
   }
 }
 
@@ -166,14 +255,25 @@ int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.W >= 1 && a.W <= 64 && a.H >= 1 && a.D >= 1, kErrInvalidArg, "mimo mix: bad sizes");
   TESM_REQUIRE(a.S && a.wts && a.coef && a.te && a.cc, kErrInvalidArg, "mimo mix: null pointer");
   if (a.B == 0 || a.L == 0) return kOk;
-  TESM_REQUIRE(a.B * a.H <= 65535 && (a.L + kMimoTP - 1) / kMimoTP <= 65535, kErrUnsupported, "mimo mix: grid too large");
-  const dim3 grid(static_cast<unsigned>((a.D + kMimoDS - 1) / kMimoDS), static_cast<unsigned>((a.L + kMimoTP - 1) / kMimoTP),
+  TESM_REQUIRE(a.B * a.H <= 65535 && (a.L + kMixTP - 1) / kMixTP <= 65535, kErrUnsupported, "mimo mix: grid too large");
+  static_assert((kMixTP + 63) * (kMixDS / 4) <= kMixLD * 256, "state prefetch must cover the block and its halo");
+  const int64_t nblk = (a.D + kMixDS - 1) / kMixDS;
+  const dim3 grid(static_cast<unsigned>((nblk + kMixCB - 1) / kMixCB), static_cast<unsigned>((a.L + kMixTP - 1) / kMixTP),
                   static_cast<unsigned>(a.B * a.H));
-  const size_t lds = static_cast<size_t>(((kMimoTP + a.W - 1) * kMimoDS + kMimoTP * a.W) * sizeof(float));
-  if (a.dt == kBF16)
-    mimo_mix_kernel<kBF16><<<grid, 256, lds, st>>>(a);
-  else
-    mimo_mix_kernel<kF32><<<grid, 256, lds, st>>>(a);
+  const size_t lds = static_cast<size_t>(((kMixTP + a.W - 1) * kMixSP + a.W * kMixWP) * sizeof(float));
+  // float4 state loads and 4-wide stores need every channel group 4-aligned in memory
+  const bool vec = a.D % 4 == 0 && (a.H * a.D) % 4 == 0 && reinterpret_cast<uintptr_t>(a.S) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(a.te) % (a.dt == kBF16 ? 8 : 16) == 0 &&
+                   reinterpret_cast<uintptr_t>(a.cc) % (a.dt == kBF16 ? 8 : 16) == 0;
+  if (a.dt == kBF16) {
+    if (vec && a.W == 64) mimo_mix_kernel<kBF16, true, 64><<<grid, 256, lds, st>>>(a);
+    else if (vec) mimo_mix_kernel<kBF16, true, 0><<<grid, 256, lds, st>>>(a);
+    else mimo_mix_kernel<kBF16, false, 0><<<grid, 256, lds, st>>>(a);
+  } else {
+    if (vec && a.W == 64) mimo_mix_kernel<kF32, true, 64><<<grid, 256, lds, st>>>(a);
+    else if (vec) mimo_mix_kernel<kF32, true, 0><<<grid, 256, lds, st>>>(a);
+    else mimo_mix_kernel<kF32, false, 0><<<grid, 256, lds, st>>>(a);
+  }
   return check_launch("mimo mix");
 }
 

@@ -99,7 +99,8 @@ def _codes(x):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,dm,D", [(37, 64, 32), (300, 768, 256), (16, 96, 64), (129, 1024, 384), (5, 200, 130)])
+@pytest.mark.parametrize("M,dm,D", [(37, 64, 32), (300, 768, 256), (16, 96, 64), (129, 1024, 384), (5, 200, 130),
+                                    (4096, 1024, 256)])
 def test_output_gate_vs_integer_reference(dtype, M, dm, D):
     g = torch.Generator().manual_seed(M + dm + D)
     te_x = torch.tanh(torch.randn(M, D, generator=g)).to(dtype)
