@@ -466,18 +466,20 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
 // ---------------------------------------------------------------------------
 // GEMM on v_mfma_i32_32x32x32_i8, which on gfx950 delivers about twice the int8 rate of the
 // 16x16x64 form.  Block tile BM x BN (waves WM x WN, each TM x TN tiles of 32 x 32), K tiles of
-// 128 codes in 4 k-steps of 32.  Weights are the MFMA's A operand: lane L feeds weight column
-// L%32 with codes 16*(L/32) .. +15 of the k-step (one packed dword, unpacked in registers) and
-// activation row L%32 with the same 16 codes (16 bytes).  Accumulator element r of lane L is
-// weight column 8*(r/4) + 4*(L/32) + r%4 and activation row L%32, so every lane stores runs of 4
-// consecutive outputs.
+// 128 codes = 8 chunks of 16 codes in 4 k-steps.  Weights are the MFMA's A operand: in k-step s,
+// lane L feeds weight column L%32 with chunk 4*(L/32) + s (one packed dword, unpacked in registers)
+// and activation row L%32 with the same chunk (16 bytes); any pairing of chunks to k-steps gives the
+// same sums as long as both operands use it, and this one makes a lane's four weight dwords of a K
+// tile one contiguous 16-byte read.  Accumulator element r of lane L is weight column
+// 8*(r/4) + 4*(L/32) + r%4 and activation row L%32, so every lane stores runs of 4 consecutive
+// outputs.
 //
-// LDS, per stage: activations in k-step planes [s][row][32 bytes]; a row's slot inside its plane
-// is row ^ 2s and its two 16-byte halves are swapped on odd groups of 8 slots, so both the staging
-// stores (8 lanes per row) and the fragment reads (32 rows x 2 halves) hit distinct banks.  Packed
-// weights keep their global order, 32 bytes per column and K tile, dword d (k-step d/2, half d%2)
-// at position d ^ 2*((col/8)%4), which makes a fragment read (32 columns x 2 dwords) bank-free.
-// ---------------------------------------------------------------------------
+// LDS, per stage (bank model measured on the device: 16-byte reads are served 16 lanes per pass over
+// 256 bytes, 16-byte writes 8 lanes per pass over 128 bytes): activations in chunk planes
+// [q][row][16 bytes] with row slot row ^ q, so a fragment read (16 consecutive rows, one chunk) and
+// a staging store (8 chunks of one row) both hit distinct banks; packed weights [col][half][16 bytes]
+// with the halves swapped on odd groups of 8 columns, so a fragment read (16 columns, one half)
+// covers all banks and a staging store (4 columns x 2 halves) 128 contiguous bytes.
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
@@ -495,12 +497,8 @@ struct Cfg32 {
 };
 
 template <int BM>
-__device__ __forceinline__ int a32_off(int row, int q) {
-  const int s = q >> 1, h = q & 1;
-  const int rr = row ^ (2 * s);
-  return s * BM * 32 + rr * 32 + 16 * (h ^ ((rr >> 3) & 1));
-}
-__device__ __forceinline__ int b32_off(int col, int d) { return col * 32 + 4 * (d ^ (2 * ((col >> 3) & 3))); }
+__device__ __forceinline__ int a32_off(int row, int q) { return q * BM * 16 + (row ^ q) * 16; }
+__device__ __forceinline__ int b32_off(int col, int h) { return col * 32 + 16 * (h ^ ((col >> 3) & 1)); }
 
 template <class C, int WN, int TM, int TN>
 __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
@@ -524,7 +522,7 @@ __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t 
     la[p] = a32_off<C::BM>(c >> 3, c & 7);
   }
   const uint8_t* pb[C::B_PT];
-  int lb[C::B_PT], lb2[C::B_PT];
+  int lb[C::B_PT];
   bool vb[C::B_PT];
 #pragma unroll
   for (int p = 0; p < C::B_PT; ++p) {
@@ -532,8 +530,7 @@ __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t 
     vb[p] = kAllB || c < C::B_CHUNKS;
     const int64_t n = n0 + (c >> 1);
     pb[p] = o.w + (n < N ? n : N - 1) * o.ldw + 16 * (c & 1);
-    lb[p] = C::A_BYTES + b32_off(c >> 1, 4 * (c & 1));       // dwords 4q, 4q+1
-    lb2[p] = C::A_BYTES + b32_off(c >> 1, 4 * (c & 1) + 2);  // dwords 4q+2, 4q+3
+    lb[p] = C::A_BYTES + b32_off(c >> 1, c & 1);
   }
   const int64_t nk = Kp / C::BK;
   auto gload = [&](int64_t kt, v4i (&ra)[C::A_PT], v4i (&rb)[C::B_PT]) {
@@ -548,36 +545,31 @@ __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t 
 #pragma unroll
     for (int p = 0; p < C::A_PT; ++p) *reinterpret_cast<v4i*>(stage + la[p]) = ra[p];
 #pragma unroll
-    for (int p = 0; p < C::B_PT; ++p) {
-      if (vb[p]) {  // dword pairs (4q, 4q+1) and (4q+2, 4q+3) stay adjacent under the swizzle
-        *reinterpret_cast<v2u*>(stage + lb[p]) = v2u{static_cast<uint32_t>(rb[p][0]), static_cast<uint32_t>(rb[p][1])};
-        *reinterpret_cast<v2u*>(stage + lb2[p]) = v2u{static_cast<uint32_t>(rb[p][2]), static_cast<uint32_t>(rb[p][3])};
-      }
-    }
+    for (int p = 0; p < C::B_PT; ++p)
+      if (vb[p]) *reinterpret_cast<v4i*>(stage + lb[p]) = rb[p];
   };
-  // per-lane fragment offsets
+  // per-lane fragment offsets: chunk 4*(lane/32) + s of the lane's row / column
+  const int hq = 4 * (lane >> 5);
   int ar[4][TM];
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int i = 0; i < TM; ++i) ar[s][i] = a32_off<C::BM>((wm * TM + i) * 32 + (lane & 31), 2 * s + (lane >> 5));
-  int br[4][TN];
+    for (int i = 0; i < TM; ++i) ar[s][i] = a32_off<C::BM>((wm * TM + i) * 32 + (lane & 31), hq + s);
+  int br[TN];
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) br[s][j] = C::A_BYTES + b32_off((wn * TN + j) * 32 + (lane & 31), 2 * s + (lane >> 5));
+  for (int j = 0; j < TN; ++j) br[j] = C::A_BYTES + b32_off((wn * TN + j) * 32 + (lane & 31), lane >> 5);
   auto compute = [&](const char* cur) {
+    v4i bw[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const v4i*>(cur + br[j]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       v4i af[TM];
-      uint32_t bw[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const v4i*>(cur + ar[s][i]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const uint32_t*>(cur + br[s][j]);
-#pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const v4i bf = unpack_frag(bw[j]);
+        const v4i bf = unpack_frag(static_cast<uint32_t>(bw[j][s]));
 #pragma unroll
         for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i], acc[i][j], 0, 0, 0);
       }
@@ -1514,10 +1506,13 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
   if (a.epilogue == kEpiStore) {
     if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
     // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
-    // enough of them, else 64x128 (4 waves side by side along N); measured at the layer shapes
-    // (in_proj / out_proj / configs[1] / configs[4])
+    // enough of them, 128x128 (4 waves of 64x64) when those still give two workgroups per CU,
+    // else 64x128 (4 waves side by side along N); measured at the layer shapes (in_proj /
+    // out_proj / configs[1] / configs[4])
     const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+    const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
     if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
+    if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
