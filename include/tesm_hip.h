@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 3
+#define TESM_HIP_ABI_VERSION 4
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -243,6 +243,7 @@ typedef struct tesm_hip_siso_step {
   void* v_cache;              /* (B, window, d_state) cache_dt, updated in place */
   void* y;                    /* (B, d_model) in dt */
   void* new_state;            /* optional (B, d_state) in dt: this step's state */
+  int64_t ld_u;               /* row pitch of u in elements (0: d_model) */
 } tesm_hip_siso_step;
 
 int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);

@@ -235,7 +235,9 @@ DecodePlan plan_decode(const tesm_hip_siso_step& p, void* base) {
   }
   s.xe = take_codes(c, p.B, p.d_state);
   s.xc = take_codes(c, p.B, p.d_state);
-  s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(p.B * p.d_model * es);
+  // the row-complete gate stages both weight matrices in LDS per workgroup, which only pays with
+  // many 16-row tiles; a decode batch takes the tiled gate and a separate quantization (same values)
+  s.yg = p.d_model <= 1024 && p.B >= 256 ? nullptr : c.take<void>(p.B * p.d_model * es);
   s.xy = take_codes(c, p.B, p.d_model);
   s.total = c.off;
   return s;
@@ -660,7 +662,9 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
                 o_q = 2 * dm + 3 * D, o_k = 2 * dm + 3 * D + R;
   int rc;
   // 1. in_proj on the B new tokens
-  if ((rc = launch_quant_act(p.u, dt, Bn, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  const int64_t ld_u = p.ld_u > 0 ? p.ld_u : dm;
+  TESM_REQUIRE(ld_u >= dm, kErrInvalidArg, "decode step: ld_u must be >= d_model");
+  if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
   if ((rc = run_linear(s.xu, p.in_proj, Bn, n_in, dm, proj, dt, n_in, st))) return rc;
   // 2. cross-layer query (tesm.py:1302-1305)
   if (p.cross_state) {

@@ -11,6 +11,7 @@ projection output are passed without copies.
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Optional
 
 import torch
@@ -63,6 +64,7 @@ def kpad(K: int) -> int:
     return int(_lib.load().tesm_hip_kpad(K))
 
 
+@functools.lru_cache(maxsize=1024)
 def round_dtype(v: float, dtype: torch.dtype) -> float:
     """The float value that torch uses for a Python scalar compared against a ``dtype`` tensor."""
     return float(torch.tensor(v, dtype=torch.float32).to(dtype).float())

@@ -25,9 +25,10 @@ from .bitlinear import BitLinear, backend_error, check_hip_call
 _WORKSPACES = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
     """A per-(device, stream) scratch buffer, grown on demand; reused across calls on that stream."""
-    stream = torch.cuda.current_stream(device)
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
@@ -263,20 +264,57 @@ class TESM_SISO(nn.Module):
             "cache_filled": False,
         }
 
+    def _step_plan(self, B, dt, dev, cdt, W, cross):
+        """The decode descriptor's fields that stay fixed from step to step, rebuilt when a shape, a
+        dtype, a weight or a bias changes (the packed weights follow tesm.py:226-236's cache rule)."""
+        lins = (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj)
+        db, lb = self.decay_bias, self.local_entanglement_bias
+        key = (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
+               db.data_ptr(), db.dtype, lb._version, lb.data_ptr(),
+               tuple((p.weight._version, p.weight.data_ptr(), p.weight.dtype) for p in lins))
+        plan = self.__dict__.get("_decode_plan")
+        if plan is not None and plan[0] == key:
+            return plan[1]
+        for p in lins:
+            if p.weight.dtype != dt:
+                raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
+        decay_bias = self._decay_bias_dt(dt)
+        local_bias = self._local_bias_f32(dt)
+        D, R, dm = self.d_state, self.ent_rank, self.d_model
+        desc = _lib.SisoStep()
+        desc.dt = hip_ops.dt_code(dt)
+        desc.cache_dt = hip_ops.dt_code(cdt)
+        desc.B, desc.d_model, desc.d_state, desc.ent_rank, desc.window = B, dm, D, R, W
+        desc.bit_eps = self.in_proj.bit_eps
+        desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
+        desc.ent_scale = float(self.entanglement_scale)
+        desc.in_proj = self.in_proj.linear_desc()
+        desc.state_proj = self.state_proj.linear_desc()
+        desc.ent_proj = self.ent_proj.linear_desc()
+        desc.out_proj = self.out_proj.linear_desc()
+        if cross:
+            desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
+        hip_ops.require_device(decay_bias, local_bias)
+        if decay_bias.device != dev:
+            raise RuntimeError(f"hip backend ops need all tensors on one device, got {decay_bias.device} and {dev}")
+        desc.decay_bias = decay_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr()
+        keep = (decay_bias, local_bias) + tuple(p.packed_weight() for p in lins[:4 + int(cross)])
+        nbytes = int(_lib.load().tesm_hip_siso_decode_ws_bytes(ctypes.byref(desc)))
+        self.__dict__["_decode_plan"] = (key, (desc, nbytes, keep))
+        return desc, nbytes, keep
+
     def _forward_incremental(self, u, inference_params, cross_layer_state=None):
         """One decode step per sequence (tesm.py:1274-1400); returns ``(y (B, 1, d_model), state f64)``."""
         lib = _lib.load()
         cache = inference_params["state_cache"]
         dt = u.dtype
         B, _, dm = u.shape
-        D, R = self.d_state, self.ent_rank
+        D = self.d_state
         dev = u.device
         if self.entanglement_window <= 0:
             raise backend_error(self.kernel_backend, "global entanglement decode",
                                 "entanglement_window=0 is not implemented by the hip backend yet")
-        for p in (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj):
-            if p.weight.dtype != dt:
-                raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
         kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
         self._check_cache(kc, vc, B, dev)
         W = kc.shape[1]
@@ -287,45 +325,38 @@ class TESM_SISO(nn.Module):
         state = state.contiguous()
         pos = int(cache["seq_pos"])
         slot = int(cache.get("cache_idx", 0))
-        u = u.reshape(B, dm).contiguous()
+        u2 = u.reshape(B, dm)  # a view for a one-token slice of a longer sequence
+        if u2.stride(1) != 1:
+            u2 = u2.contiguous()
         cs = None
         if cross_layer_state is not None:
             cs = cross_layer_state.reshape(B, D).to(dt).contiguous()
+            if cs.device != dev:
+                raise RuntimeError(f"hip backend ops need all tensors on one device, got {cs.device} and {dev}")
+        desc, nbytes, _ = self._step_plan(B, dt, dev, kc.dtype, W, cs is not None)
         y = torch.empty((B, 1, dm), dtype=dt, device=dev)
         state_out = torch.empty_like(state)
         new = torch.empty((B, D), dtype=dt, device=dev)
-        decay_bias = self._decay_bias_dt(dt)
-        local_bias = self._local_bias_f32(dt)
         rope = self.rope_table(pos + 1, dt, dev)
-        hip_ops.require_device(u, cs, state, kc, vc, decay_bias, local_bias, rope, y, state_out, new)
-        desc = _lib.SisoStep()
-        desc.dt = hip_ops.dt_code(dt)
-        desc.cache_dt = hip_ops.dt_code(kc.dtype)
-        desc.B, desc.d_model, desc.d_state, desc.ent_rank, desc.window = B, dm, D, R, W
         desc.seq_pos, desc.cache_idx = pos, slot
-        desc.bit_eps = self.in_proj.bit_eps
-        desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
-        desc.ent_scale = float(self.entanglement_scale)
-        desc.u = u.data_ptr()
-        desc.in_proj = self.in_proj.linear_desc()
-        desc.state_proj = self.state_proj.linear_desc()
-        desc.ent_proj = self.ent_proj.linear_desc()
-        desc.out_proj = self.out_proj.linear_desc()
-        if cs is not None:
-            desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
-            desc.cross_state = cs.data_ptr()
-        desc.decay_bias = decay_bias.data_ptr()
-        desc.local_bias = local_bias.data_ptr()
+        desc.u, desc.ld_u = u2.data_ptr(), u2.stride(0)
+        desc.cross_state = cs.data_ptr() if cs is not None else None
         desc.rope = rope.data_ptr()
         desc.state, desc.state_out = state.data_ptr(), state_out.data_ptr()
         desc.k_cache, desc.v_cache = kc.data_ptr(), vc.data_ptr()
         desc.y = y.data_ptr()
         desc.new_state = new.data_ptr()
-        nbytes = int(lib.tesm_hip_siso_decode_ws_bytes(ctypes.byref(desc)))
-        with torch.cuda.device(dev):
-            ws = workspace(dev, nbytes)
-            _lib.check(lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                                                ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+        stream = torch.cuda.current_stream(dev)
+        if torch.cuda.current_device() == dev.index:
+            ws = workspace(dev, nbytes, stream)
+            rc = lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                          ctypes.c_void_p(stream.cuda_stream))
+        else:
+            with torch.cuda.device(dev):
+                ws = workspace(dev, nbytes, stream)
+                rc = lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                              ctypes.c_void_p(stream.cuda_stream))
+        _lib.check(rc)
         cache["cache_idx"] = (slot + 1) % W
         cache["state"] = state_out
         cache["seq_pos"] = pos + 1
