@@ -19,7 +19,10 @@ namespace {
 
 constexpr int kDecMaxCPT = 8;  // channels per thread: d_state <= 2048
 
-template <int DT, int CDT>
+// STG: the window's ring rows are copied to LDS at the start (keys at pitch R + 1 so the per-window
+// dot products of one wave hit distinct banks), so their latency overlaps the RoPE and the state
+// update instead of following them.
+template <int DT, int CDT, bool STG>
 __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_dec[];
   const int R = static_cast<int>(a.R), D = static_cast<int>(a.D), W = static_cast<int>(a.W);
@@ -30,11 +33,20 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   float* wn = nv + D;        // 64  ternary / norm per padded window position
   float* red = wn + 64;      // 16  block reductions
   int* redi = reinterpret_cast<int*>(red + 8);
+  float* kw = red + 16;      // STG: W x (R + 1) ring keys in the layer dtype
+  float* vw = kw + (STG ? W * (R + 1) : 0);  // STG: W x D ring states in the layer dtype
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
   const int es = DT == kBF16 ? 2 : 4;
   const char* prow = static_cast<const char*>(a.proj) + b * a.ld_proj * es;
   const int64_t slot = a.slot;
+  if constexpr (STG) {  // this step's slot is read too but never used: its fresh key / state come from kv / nv
+    for (int i = tid; i < W * R; i += 256) {
+      const int s = i / R, r = i - s * R;
+      kw[s * (R + 1) + r] = rnd<DT>(ld<CDT>(a.k_cache, (b * a.W + s) * a.R + r));
+    }
+    for (int i = tid; i < W * D; i += 256) vw[i] = rnd<DT>(ld<CDT>(a.v_cache, b * a.W * a.D + i));
+  }
 
   // 1. RoPE at position pos (tesm.py:1311-1313), cross query (1302-1305), key into the ring
   for (int i = tid; i < half; i += 256) {
@@ -82,6 +94,9 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
         if (s == slot) {
           k1 = kv[i];
           k2 = kv[half + i];
+        } else if constexpr (STG) {
+          k1 = kw[s * (R + 1) + i];
+          k2 = kw[s * (R + 1) + half + i];
         } else {
           const int64_t ko = (b * a.W + s) * a.R;
           k1 = rnd<DT>(ld<CDT>(a.k_cache, ko + i));
@@ -113,7 +128,13 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
     for (int w = static_cast<int>(W - valid); w < W; ++w) {
       const int64_t e = w - (W - valid);
       const int64_t s = a.full ? (slot + w) % a.W : e;
-      const float x = (s == slot) ? nv[c] : rnd<DT>(ld<CDT>(a.v_cache, (b * a.W + s) * a.D + c));
+      float x;
+      if (s == slot)
+        x = nv[c];
+      else if constexpr (STG)
+        x = vw[s * D + c];
+      else
+        x = rnd<DT>(ld<CDT>(a.v_cache, (b * a.W + s) * a.D + c));
       acc += wn[w] * x;
     }
     const float avg = rnd<DT>(acc);
@@ -201,6 +222,13 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(CacheFillArgs a) {
 
 int64_t decode_lds_bytes(int64_t R, int64_t D) { return (2 * R + D + 64 + 16) * static_cast<int64_t>(sizeof(float)); }
 
+namespace {
+constexpr int64_t kDecStageMax = 64 * 1024;  // LDS bytes up to which the ring rows are staged
+int64_t decode_stage_bytes(int64_t R, int64_t D, int64_t W) {
+  return decode_lds_bytes(R, D) + (W * (R + 1) + W * D) * static_cast<int64_t>(sizeof(float));
+}
+}  // namespace
+
 int launch_decode_ent(const DecodeArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "decode: dtype must be 0 or 1");
   TESM_REQUIRE(a.cdt == kF32 || a.cdt == kBF16, kErrInvalidArg, "decode: cache dtype must be 0 or 1");
@@ -213,19 +241,28 @@ int launch_decode_ent(const DecodeArgs& a, hipStream_t st) {
                    a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c,
                kErrInvalidArg, "decode: null pointer");
   TESM_REQUIRE(a.ldq >= a.D, kErrInvalidArg, "decode: ldq < d_state");
-  const size_t lds = static_cast<size_t>(decode_lds_bytes(a.R, a.D));
+  const bool stg = decode_stage_bytes(a.R, a.D, a.W) <= kDecStageMax;
+  const size_t lds = static_cast<size_t>(stg ? decode_stage_bytes(a.R, a.D, a.W) : decode_lds_bytes(a.R, a.D));
   const dim3 grid(static_cast<unsigned>(a.B));
+#define TESM_DEC_LAUNCH(DT_, CDT_)                                                     \
+  do {                                                                                 \
+    if (stg)                                                                           \
+      decode_ent_kernel<DT_, CDT_, true><<<grid, 256, lds, st>>>(a);                   \
+    else                                                                               \
+      decode_ent_kernel<DT_, CDT_, false><<<grid, 256, lds, st>>>(a);                  \
+  } while (0)
   if (a.dt == kBF16) {
     if (a.cdt == kBF16)
-      decode_ent_kernel<kBF16, kBF16><<<grid, 256, lds, st>>>(a);
+      TESM_DEC_LAUNCH(kBF16, kBF16);
     else
-      decode_ent_kernel<kBF16, kF32><<<grid, 256, lds, st>>>(a);
+      TESM_DEC_LAUNCH(kBF16, kF32);
   } else {
     if (a.cdt == kBF16)
-      decode_ent_kernel<kF32, kBF16><<<grid, 256, lds, st>>>(a);
+      TESM_DEC_LAUNCH(kF32, kBF16);
     else
-      decode_ent_kernel<kF32, kF32><<<grid, 256, lds, st>>>(a);
+      TESM_DEC_LAUNCH(kF32, kF32);
   }
+#undef TESM_DEC_LAUNCH
   return check_launch("decode step");
 }
 
