@@ -599,6 +599,121 @@ __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t 
   __syncthreads();
 }
 
+// Main loop with direct-to-LDS loads (global_load_lds_dwordx4): NS stages in LDS, no staging
+// registers.  One such instruction moves 64 lanes x 16 bytes into 1 KB of LDS in lane order, so the
+// layouts are chosen through the lanes' global addresses: activation rows in blocks of 8 rows x 8
+// chunks (a row's 8 lanes read one 128-byte line, chunk q of row r lands in slot
+// r*8 + (q ^ ((r/2) % 8))), weights in blocks of 32 columns x 2 halves (half h of column n in slot
+// 2n + (h ^ ((n/8) % 2))); both make the fragment reads (16 lanes: consecutive rows or columns, one
+// chunk) hit 16 distinct 16-byte slots of 256 bytes.  Every wave issues the same number D of these
+// per K tile; the wait for tile kt is "at most (NS - 2) * D outstanding" (loads past the last K tile
+// re-read it, so the count never shrinks), then one barrier, then the refill of the stage the
+// previous tile used.
+template <int BM>
+__device__ __forceinline__ int a32d_off(int row, int q) { return 16 * (row * 8 + (q ^ ((row >> 1) & 7))); }
+__device__ __forceinline__ int b32d_off(int col, int h) { return 16 * (col * 2 + (h ^ ((col >> 3) & 1))); }
+
+__device__ __forceinline__ void lds_dma16(const void* src, char* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(dst), 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt bits [3:0] and
+// [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt out of range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <class C, int WN, int TM, int TN, int NS>
+__device__ __forceinline__ void mfma32d_mainloop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
+                                                 int64_t Kp, v16i (&acc)[TM][TN], char* smem) {
+  constexpr int NW = C::NT / 64;
+  constexpr int NA = C::BM / 8, NB = C::BN / 32;  // 1 KB blocks per K tile
+  static_assert((NA + NB) % NW == 0, "DMA blocks must divide evenly over the waves");
+  constexpr int D = (NA + NB) / NW;
+  static_assert((NS - 2) * D < 64, "too many loads in flight for vmcnt");
+  const int t = threadIdx.x;
+  __builtin_assume(t < C::NT);
+  const int lane = t & 63, w = t >> 6;
+  const int wm = w / WN, wn = w % WN;
+  // this lane's source of each of the wave's D blocks (rows / columns past M / N read the last one)
+  const char* src[D];
+  int dst[D], adv[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int blk = w + i * NW;
+    if (blk < NA) {
+      const int row = blk * 8 + (lane >> 3);
+      const int q = (lane & 7) ^ ((row >> 1) & 7);
+      const int64_t m = m0 + row;
+      src[i] = reinterpret_cast<const char*>(o.q) + (m < M ? m : M - 1) * o.ldq + 16 * q;
+      dst[i] = blk * 1024;
+      adv[i] = C::BK;
+    } else {
+      const int col = (blk - NA) * 32 + (lane >> 1);
+      const int h = (lane & 1) ^ ((col >> 3) & 1);
+      const int64_t n = n0 + col;
+      src[i] = reinterpret_cast<const char*>(o.w) + (n < N ? n : N - 1) * o.ldw + 16 * h;
+      dst[i] = C::A_BYTES + (blk - NA) * 1024;
+      adv[i] = C::BK / 4;
+    }
+  }
+  const int64_t nk = Kp / C::BK;
+  auto issue = [&](int64_t kt) {
+    const int64_t k = kt < nk ? kt : nk - 1;
+    char* stage = smem + static_cast<int>(kt % NS) * C::STAGE;
+#pragma unroll
+    for (int i = 0; i < D; ++i) lds_dma16(src[i] + k * adv[i], stage + dst[i]);
+  };
+  const int hq = 4 * (lane >> 5);
+  int ar[4][TM], br[TN];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) ar[s][i] = a32d_off<C::BM>((wm * TM + i) * 32 + (lane & 31), hq + s);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) br[j] = C::A_BYTES + b32d_off((wn * TN + j) * 32 + (lane & 31), lane >> 5);
+  // fragments double-buffered by one k-step: the reads for step s + 1 are issued before the MFMAs
+  // of step s (scheduling barriers keep the compiler from sinking them), so their latency hides
+  // behind TM x TN MFMAs instead of one
+  auto compute = [&](const char* cur) {
+    v4i bw[TN], af[2][TM];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const v4i*>(cur + br[j]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) af[0][i] = *reinterpret_cast<const v4i*>(cur + ar[0][i]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < 3) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[(s + 1) & 1][i] = *reinterpret_cast<const v4i*>(cur + ar[s + 1][i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const v4i bf = unpack_frag(static_cast<uint32_t>(bw[j][s]));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[s & 1][i], acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  __syncthreads();  // the stages may still be read by a previous main loop or epilogue
+#pragma unroll
+  for (int g = 0; g < NS - 1; ++g) issue(g);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    wait_vmcnt<(NS - 2) * D>();  // this wave's loads of tile kt have landed
+    __builtin_amdgcn_s_barrier();  // ... every wave's, and every wave is done with tile kt - 1
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    issue(kt + NS - 1);           // into the stage tile kt - 1 used
+    compute(smem + static_cast<int>(kt % NS) * C::STAGE);
+  }
+  wait_vmcnt<0>();  // the re-reads past the last tile
+  __syncthreads();
+}
+
 // Outputs (m, nb .. nb+3) from exact accumulators q0 (op0) and q1 (op1, output gate): per-tensor or
 // per-row scales, optional bias and accumulator dump, the output gate; columns past N skipped.
 template <int EPI, int OUT_DT>
@@ -718,10 +833,12 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
   }
 }
 
-template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
+// NS == 0: register-staged main loop (two LDS stages); NS >= 3: direct-to-LDS loads into NS stages.
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT, int NS = 0>
 __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   using C = Cfg32<WM, WN, TM, TN>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+  constexpr int SMEM = (NS == 0 ? 2 : NS) * C::STAGE;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
   int64_t tm, tn;
   xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
   const int64_t m0 = tm * C::BM;
@@ -749,12 +866,18 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
     rsum[i] = o0.rowsum[mc];
   }
   const float cws = o0.c_w[0];
-  mfma32_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-  if constexpr (EPI == kEpiOutputGate) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+  if constexpr (NS == 0) {
+    mfma32_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+    if constexpr (EPI == kEpiOutputGate) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+  } else {
+    mfma32d_mainloop<C, WN, TM, TN, NS>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+    if constexpr (EPI == kEpiOutputGate)
+      mfma32d_mainloop<C, WN, TM, TN, NS>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+  }
 
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
   if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
-    epi32_plain_staged<WM * WN, TM, TN, OUT_DT, 2 * C::STAGE>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
+    epi32_plain_staged<WM * WN, TM, TN, OUT_DT, SMEM>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
     return;
   }
   if (plain) {
@@ -1349,16 +1472,16 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
   }
 }
 
-template <int WM, int WN, int TM, int TN, int EPI>
+template <int WM, int WN, int TM, int TN, int EPI, int NS = 0>
 int run_mfma32(const LinearArgs& a, hipStream_t st) {
   using C = Cfg32<WM, WN, TM, TN>;
   const int64_t tiles = ((a.N + C::BN - 1) / C::BN) * ((a.M + C::BM - 1) / C::BM);
   TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
   const unsigned grid = static_cast<unsigned>(tiles);
   if (a.out_dt == kBF16)
-    mfma32_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
+    mfma32_kernel<WM, WN, TM, TN, EPI, kBF16, NS><<<grid, C::NT, 0, st>>>(a);
   else
-    mfma32_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
+    mfma32_kernel<WM, WN, TM, TN, EPI, kF32, NS><<<grid, C::NT, 0, st>>>(a);
   return check_launch("bitlinear mfma32");
 }
 
@@ -1511,12 +1634,15 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // out_proj / configs[1] / configs[4])
     const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
     const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+    // long K loops: direct-to-LDS loads into three stages (no staging registers)
+    if (a.N % 256 == 0 && tiles256 >= 128 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
     if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
     if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
   const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+  if (a.N % 256 == 0 && tiles256 >= 128 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiOutputGate, 3>(a, st);
   if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiOutputGate>(a, st);
   return run_mfma32<1, 4, 2, 1, kEpiOutputGate>(a, st);
 }

@@ -189,3 +189,29 @@ def test_bitlinear_strict_errors():
         bl.eval()(x)  # grad enabled
     with torch.no_grad(), pytest.raises(RuntimeError, match="kernel_backend"):
         BitLinear(64, 8, kernel_backend="torch").to(DEV).eval()(x)
+
+
+@pytest.mark.parametrize("M,K,N,ragged", [(4096, 2048, 1024, False), (4100, 2100, 1024, True), (2048, 768, 2432, False),
+                                          (4096, 4096, 256, False)])
+def test_accumulators_bit_exact_large(M, K, N, ragged):
+    """int32 accumulators of the large-tile GEMMs (direct-to-LDS main loop for K >= 2048 when N fills
+    256-wide tiles; register-staged otherwise) vs the exact product: integer-valued float32 matrices
+    multiply exactly on the device while |sums| < 2^24 (here <= 127 * K)."""
+    g = torch.Generator().manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).to(DEV)
+    w = torch.randn(N, K, generator=g).to(DEV)
+    s_w = (1.0 / w.abs().mean()).reshape(1)
+    q, s, rs = hip_ops.quant_act(x)
+    packed = hip_ops.pack_weight(w, s_w)
+    c_w = 1.0 / s_w
+    out, acc = hip_ops.bitlinear(q, s, rs, packed, c_w, N, K, torch.float32, acc_dump=True)
+    codes = hip_ops.unpack_weight(packed, K).to(torch.float32)                    # (N, K) in {-1, 0, 1}
+    from hip_helpers import unpermute_layout1
+    xq = torch.from_numpy(unpermute_layout1(q.cpu().numpy()[:, : hip_ops.kpad(K)], K)).to(DEV).to(torch.float32)
+    acc_ref = (xq @ codes.t().contiguous()).to(torch.int64)
+    assert torch.equal(acc.to(torch.int64), acc_ref)
+    y_ref = (acc_ref.to(torch.float64) / s.to(torch.float64)[:, None]) * float(c_w.cpu()[0])
+    assert normwise(out.cpu().numpy(), y_ref.cpu().numpy()) < 1e-6
+    # the plain (no dump) epilogue path writes the same values
+    out2 = hip_ops.bitlinear(q, s, rs, packed, c_w, N, K, torch.float32)
+    assert torch.equal(out, out2)

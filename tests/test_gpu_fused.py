@@ -135,3 +135,34 @@ def test_output_gate_vs_integer_reference(dtype, M, dm, D):
     assert err <= (1e-6 if dtype == torch.float32 else 2 ** -7), err
     qr, sr, rr = hip_ops.quant_act(y)
     assert torch.equal(qy[0], qr) and torch.equal(qy[1], sr) and torch.equal(qy[2], rr)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_output_gate_large_tiles(dtype):
+    """The tiled output gate at a shape that takes the 128x256-tile, direct-to-LDS GEMM (d_state 2048
+    as in the MIMO layer): both accumulators exact (integer-valued float32 products on the device),
+    then the gate in the reference's op order."""
+    M, dm, D = 4096, 1024, 2048
+    g = torch.Generator().manual_seed(7)
+    te_x = torch.tanh(torch.randn(M, D, generator=g)).to(dtype).to(DEV)
+    c_x = (torch.randn(M, D, generator=g) * 0.1).to(dtype).to(DEV)
+    local = torch.randn(M, dm, generator=g).to(dtype).to(DEV)
+    gate = torch.randn(M, dm, generator=g).to(dtype).to(DEV)
+    w_sp = (torch.randn(dm, D, generator=g) * 0.02).to(DEV)
+    w_ep = (torch.randn(dm, D, generator=g) * 0.02).to(DEV)
+    te, cc = _codes(te_x), _codes(c_x)
+    s_sp, c_sp = hip_ops.absmean_scale(w_sp)
+    s_ep, c_ep = hip_ops.absmean_scale(w_ep)
+    p_sp, p_ep = hip_ops.pack_weight(w_sp, s_sp), hip_ops.pack_weight(w_ep, s_ep)
+    y, _ = hip_ops.output_gate(te, cc, p_sp, c_sp, p_ep, c_ep, local, gate, D, quantize=False)
+    from hip_helpers import unpermute_layout1
+
+    def lin(codes, packed, c_w):
+        wq = hip_ops.unpack_weight(packed, D).to(torch.float32)
+        xq = torch.from_numpy(unpermute_layout1(codes[0].cpu().numpy()[:, : hip_ops.kpad(D)], D)).to(DEV).float()
+        acc = xq @ wq.t().contiguous()                 # exact: |sums| <= 127 * D < 2^24
+        return ((acc * (1.0 / codes[1])[:, None]) * c_w[0]).to(dtype)
+
+    y_ref = local + torch.sigmoid(gate) * lin(te, p_sp, c_sp) + lin(cc, p_ep, c_ep)
+    err = normwise(to_np(y), to_np(y_ref))
+    assert err <= (1e-6 if dtype == torch.float32 else 2 ** -7), err
