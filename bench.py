@@ -72,6 +72,23 @@ def time_launches(torch, fn, n: int, warm: int = 3):
     return sum(a.elapsed_time(b) for a, b in evs) / n * 1e-3  # seconds
 
 
+def time_back_to_back(torch, fn, n: int, warm: int = 3):
+    """Average device time per launch of n back-to-back fn() launches between one event pair on the
+    current stream (the launches are queued behind a device-side wait first, so host launch latency
+    does not leave gaps)."""
+    for _ in range(warm):
+        fn(0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    busy(torch)
+    e0.record()
+    for i in range(n):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e-3  # seconds
+
+
 def packed_codes(torch, N, ldw, device, gen):
     c = [torch.randint(0, 3, (N, ldw), dtype=torch.uint8, device=device, generator=gen) for _ in range(4)]
     return c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6)
@@ -282,8 +299,8 @@ def main():
         pw = m.in_proj.packed_weight()
         q, s, rs = hip_ops.quant_act(u.reshape(M, K))
         out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        t_gemm = time_launches(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K, torch.bfloat16,
-                                                                  out=out), 50)
+        t_gemm = time_back_to_back(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K,
+                                                                      torch.bfloat16, out=out), 50)
         ops = 2 * M * N * K
         decode = measure_decode(torch, m)
         mimo = None if args.no_mimo else measure_mimo(torch)

@@ -1634,15 +1634,15 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // out_proj / configs[1] / configs[4])
     const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
     const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-    // long K loops: direct-to-LDS loads into three stages (no staging registers)
-    if (a.N % 256 == 0 && tiles256 >= 128 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
+    // long K loops over many tiles: direct-to-LDS loads into three stages (no staging registers)
+    if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
     if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
     if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
   if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
   const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-  if (a.N % 256 == 0 && tiles256 >= 128 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiOutputGate, 3>(a, st);
+  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiOutputGate, 3>(a, st);
   if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiOutputGate>(a, st);
   return run_mfma32<1, 4, 2, 1, kEpiOutputGate>(a, st);
 }

@@ -186,8 +186,11 @@ __global__ __launch_bounds__(256) void mimo_stats_kernel(MimoStatsArgs a) {
     const int64_t v = e / (a.H * a.W), h = (e / a.W) % a.H, w = e % a.W;
     const int64_t tq = a.W - 1 + v, tk = v + w;
     const int64_t qo = (b * a.L + tq) * a.ld_q + h * a.R, ko = (b * a.L + tk) * a.ld_k + h * a.R;
+    // products in natural r order: the first halves (r < R/2) then the second halves; the loop is
+    // unrolled so a batch of loads is in flight before the running sum needs it
     float acc = 0.0f;
     for (int part = 0; part < 2; ++part) {
+#pragma unroll 8
       for (int64_t i = 0; i < half; ++i) {
         float q1, q2, k1, k2;
         rope_pair<DT>(ld<DT>(a.q, qo + i), ld<DT>(a.q, qo + i + half), a.rope[tq * half + i], q1, q2);

@@ -191,8 +191,8 @@ def test_bitlinear_strict_errors():
         BitLinear(64, 8, kernel_backend="torch").to(DEV).eval()(x)
 
 
-@pytest.mark.parametrize("M,K,N,ragged", [(4096, 2048, 1024, False), (4100, 2100, 1024, True), (2048, 768, 2432, False),
-                                          (4096, 4096, 256, False)])
+@pytest.mark.parametrize("M,K,N,ragged", [(16384, 2048, 4096, False), (16388, 2100, 4096, True), (2048, 768, 2432, False),
+                                          (4096, 4096, 256, False), (4096, 2048, 1024, False)])
 def test_accumulators_bit_exact_large(M, K, N, ragged):
     """int32 accumulators of the large-tile GEMMs (direct-to-LDS main loop for K >= 2048 when N fills
     256-wide tiles; register-staged otherwise) vs the exact product: integer-valued float32 matrices

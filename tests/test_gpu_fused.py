@@ -142,7 +142,7 @@ def test_output_gate_large_tiles(dtype):
     """The tiled output gate at a shape that takes the 128x256-tile, direct-to-LDS GEMM (d_state 2048
     as in the MIMO layer): both accumulators exact (integer-valued float32 products on the device),
     then the gate in the reference's op order."""
-    M, dm, D = 4096, 1024, 2048
+    M, dm, D = 16384, 4096, 2048
     g = torch.Generator().manual_seed(7)
     te_x = torch.tanh(torch.randn(M, D, generator=g)).to(dtype).to(DEV)
     c_x = (torch.randn(M, D, generator=g) * 0.1).to(dtype).to(DEV)
