@@ -199,6 +199,33 @@ MIMO = dict(d_model=4096, d_state=2048, n_heads=4, mimo_rank=4, ent_rank=256, en
             entanglement_threshold=0.05, entanglement_scale=0.2, max_seq_len=32768)
 
 
+def measure_global(torch, steps: int = 10):
+    """TESM_SISO with global causal entanglement (entanglement_window = 0, the next row after the
+    local-window layer) at configs[3]'s dims, B4 x L2048 prefill, bf16: per-forward time."""
+    from tesm_amd import TESM_SISO
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = dict(LAYER)
+    cfg["entanglement_window"] = 0
+    m = TESM_SISO(**cfg, kernel_backend="hip").to(dev).to(torch.bfloat16).eval()
+    B, L = 4, LAYER["max_seq_len"]
+    u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        for _ in range(2):
+            m(u)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            m(u)
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": "TESM_SISO prefill with entanglement_window=0 (global causal ternary entanglement), "
+                        "configs[3] dims, B4 x L2048, bf16", "ms_per_forward": ms, "tokens_per_s": B * L / (ms * 1e-3)}
+
+
 def measure_mimo(torch, reps: int = 3):
     """one TESMMIMO_Optimized layer at large_40b() dims (d_model 4096, d_state 2048, 4 heads,
     mimo_rank 4, ent_rank 256, window 64), batch 1 x 32768-token prefill, bf16, INT2 weights."""
@@ -304,6 +331,7 @@ def main():
         ops = 2 * M * N * K
         decode = measure_decode(torch, m)
         mimo = None if args.no_mimo else measure_mimo(torch)
+        glob = measure_global(torch)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
         if args.only:
             print(json.dumps({"kernels": kernels}))
@@ -335,6 +363,7 @@ def main():
                              "launch from profiles/in_proj_gemm_traffic.json"},
         "decode": decode,
         "mimo_layer": mimo,
+        "global_layer": glob,
         "kernels": kernels,
     }
     if not args.no_cpu:

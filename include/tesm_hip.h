@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 4
+#define TESM_HIP_ABI_VERSION 5
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -188,8 +188,8 @@ typedef struct tesm_hip_output_gate {
 int tesm_hip_output_gate_i2(const tesm_hip_output_gate* p, void* stream);
 
 /* Whole TESM_SISO prefill forward (eval, no grad).  Replaces TESM_SISO.forward
- * (tesm.py:1175-1272): in_proj, gates, RoPE, cross-layer query bias, state scan, local
- * entanglement, mix, state_proj/ent_proj with the output gate
+ * (tesm.py:1175-1272): in_proj, gates, RoPE, cross-layer query bias, state scan, local (window > 0)
+ * or global (window == 0) entanglement, mix, state_proj/ent_proj with the output gate
  * y = local + sigmoid(gate) * state_proj(tanh E) + ent_proj(E - S), out_proj.  With k_cache and
  * v_cache set it also fills the decode ring buffers as the reference's prefill does
  * (tesm.py:1235-1253): the last n = min(L, window) RoPE'd keys and states go to slots
@@ -209,9 +209,16 @@ typedef struct tesm_hip_siso_layer {
   void* states;               /* (B, L, d_state) in dt */
   double* h_final;            /* optional (B, d_state) */
   void* proj_out;             /* optional (B, L, N_in) copy target; NULL = workspace only */
-  void* k_cache;              /* optional (B, window, ent_rank) ring of keys, cache_dt */
-  void* v_cache;              /* optional (B, window, d_state) ring of states, cache_dt */
+  void* k_cache;              /* optional (B, cache_window, ent_rank) ring of keys, cache_dt */
+  void* v_cache;              /* optional (B, cache_window, d_state) ring of states, cache_dt */
   int cache_dt;               /* 0 f32, 1 bf16 */
+  /* window == 0: global causal entanglement (tesm.py:963-1063) with the relative-position bias
+   * parameters global_rel_pos_embed (global_dim), _scale (1), _bias (1), float32 holding dt values */
+  const float* global_embed;
+  int64_t global_dim;
+  const float* global_scale;
+  const float* global_bias;
+  int64_t cache_window;       /* ring size of k_cache / v_cache (0: window) */
 } tesm_hip_siso_layer;
 
 int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p);
@@ -287,6 +294,12 @@ typedef struct tesm_hip_mimo_layer {
    * slots, (B, S-W+1, n_heads, W) in dt, and per batch row (#positive, #negative, #zero) */
   void* stats_ternary;
   int32_t* stats_counts;      /* (B, 3) */
+  /* window == 0: global causal entanglement over the flattened heads (tesm_mimo.py:590-687) */
+  const float* global_embed;
+  int64_t global_dim;
+  const float* global_scale;
+  const float* global_bias;
+  int64_t cache_window;       /* ring size of k_cache / v_cache (0: window) */
 } tesm_hip_mimo_layer;
 
 int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p);

@@ -15,7 +15,9 @@ Reference = WANGLILIN360/tesm; paths are relative to its root.
 Deviations, each only where the reference itself raises:
 * ``amend_bf16`` (default True).  In bf16 the reference's MIMO forward feeds a
   float32 tensor into a bf16 BitLinear (tesm_mimo.py:1016-1045 -> F.linear dtype
-  error), and the SISO/MIMO decode step mixes bf16 queries with float32 ring
+  error), its global branch multiplies bf16 weights with the float32 rank states
+  (tesm_mimo.py:678 -> matmul dtype error; amended: weights cast to float32), and
+  the SISO/MIMO decode step mixes bf16 queries with float32 ring
   buffers in ``einsum`` (tesm.py:1352, tesm_mimo.py:865).  With the amendment the
   oracle casts those tensors to the module dtype (lossless for the ring
   buffers, whose entries are all module-dtype values) so the path runs.  In
@@ -516,7 +518,10 @@ class TESMMIMO_Optimized(TESM_SISO):
         causal = torch.tril(torch.ones(L, L, dtype=torch.bool, device=q.device))
         tern = self.ternary_entanglement(scores) * causal.unsqueeze(0).to(scores.dtype)
         norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)
-        ent = torch.matmul(tern / norm, states.reshape(B, L, H * D)).reshape(B, L, H, D)
+        w = tern / norm
+        if self.amend_bf16 and w.dtype != states.dtype:  # bf16 weights against float32 rank states
+            w = w.to(states.dtype)
+        ent = torch.matmul(w, states.reshape(B, L, H * D)).reshape(B, L, H, D)
         self._record_map(tern)
         return ent, ent - states
 

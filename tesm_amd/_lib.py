@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -72,6 +72,7 @@ class SisoLayer(ctypes.Structure):
         ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P), ("h0", P),
         ("y", P), ("states", P), ("h_final", P), ("proj_out", P),
         ("k_cache", P), ("v_cache", P), ("cache_dt", I32),
+        ("global_embed", P), ("global_dim", I64), ("global_scale", P), ("global_bias", P), ("cache_window", I64),
     ]
 
 
@@ -103,6 +104,7 @@ class MimoLayer(ctypes.Structure):
         ("decay_bias", P), ("local_bias", P), ("rope", P), ("mimo_coef", P), ("mimo_x0sq", P),
         ("y", P), ("h_final", P), ("last_state", P), ("k_cache", P), ("v_cache", P), ("cache_dt", I32),
         ("stats_ternary", P), ("stats_counts", P),
+        ("global_embed", P), ("global_dim", I64), ("global_scale", P), ("global_bias", P), ("cache_window", I64),
     ]
 
 

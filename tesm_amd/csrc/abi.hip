@@ -6,6 +6,7 @@
 
 #include "decode.h"
 #include "entangle.h"
+#include "global.h"
 #include "mimo.h"
 #include "scan.h"
 #include "tesm_hip_internal.h"
@@ -90,6 +91,10 @@ struct SisoPlan {
   void* c_mix;
   void* yg;
   void* cq;
+  int8_t* g_tern;   // global entanglement (window == 0): decisions, counts, bias table, RoPE'd q / k
+  int32_t* g_count;
+  float* g_table;
+  float *g_qr, *g_kr;
   int64_t total;
 };
 
@@ -113,7 +118,8 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   const int64_t M = p.B * p.L;
   const int64_t n_in = 2 * p.d_model + 3 * p.d_state + 2 * p.ent_rank;
   const int es = esize(p.dt);
-  s.fuse_ent = ent_fused_ok(siso_ent_shape(p));
+  const bool global = p.window == 0;
+  s.fuse_ent = !global && ent_fused_ok(siso_ent_shape(p));
   s.rowq = p.d_model <= 1024;
   s.xu = take_codes(c, M, p.d_model);
   s.proj = c.take<void>(M * n_in * es);
@@ -122,8 +128,20 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   s.gated = c.take<void>(2 * M * p.d_state * es);
   s.wts = nullptr;
   s.e_tanh = s.c_mix = nullptr;
+  s.g_tern = nullptr;
+  s.g_count = nullptr;
+  s.g_table = nullptr;
+  s.g_qr = s.g_kr = nullptr;
   if (!s.fuse_ent) {
-    s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
+    if (global) {
+      s.g_tern = c.take<int8_t>(p.B * p.L * global_tern_pitch(p.L));
+      s.g_count = c.take<int32_t>(p.B * p.L * ((p.L + 63) / 64) * 4);
+      s.g_table = c.take<float>(2 * p.L * 4);
+      s.g_qr = c.take<float>(p.B * p.L * p.ent_rank * 4);
+      s.g_kr = c.take<float>(p.B * p.L * p.ent_rank * 4);
+    } else {
+      s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
+    }
     s.e_tanh = c.take<void>(M * p.d_state * es);
     s.c_mix = c.take<void>(M * p.d_state * es);
   }
@@ -254,6 +272,10 @@ struct MimoPlan {
   void* te;
   void* cc;
   void* yg;
+  int8_t* g_tern;  // global entanglement (window == 0)
+  int32_t* g_count;
+  float* g_table;
+  float *g_qr, *g_kr;
   int64_t total;
 };
 
@@ -268,7 +290,20 @@ MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
   s.scan_bytes = scan_ws_bytes(p.B, p.L, HD, 16);
   s.scan_ws = c.take<void>(s.scan_bytes);
   s.S = c.take<float>(M * HD * 4);
-  s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, p.n_heads, p.window));
+  s.wts = nullptr;
+  s.g_tern = nullptr;
+  s.g_count = nullptr;
+  s.g_table = nullptr;
+  s.g_qr = s.g_kr = nullptr;
+  if (p.window > 0) {
+    s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, p.n_heads, p.window));
+  } else {
+    s.g_tern = c.take<int8_t>(p.B * p.L * global_tern_pitch(p.L));
+    s.g_count = c.take<int32_t>(p.B * p.L * ((p.L + 63) / 64) * 4);
+    s.g_table = c.take<float>(2 * p.L * 4);
+    s.g_qr = c.take<float>(p.B * p.L * p.n_heads * p.ent_rank * 4);
+    s.g_kr = c.take<float>(p.B * p.L * p.n_heads * p.ent_rank * 4);
+  }
   s.te = c.take<void>(M * HD * es);
   s.cc = c.take<void>(M * HD * es);
   s.xe = take_codes(c, M, HD);
@@ -494,10 +529,14 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso layer: dtype must be 0 or 1");
   TESM_REQUIRE(p.B >= 1 && p.L >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.ent_rank >= 2 && p.ent_rank % 2 == 0 &&
-                   p.window >= 1 && p.window <= 64 && p.chunk_size >= 1,
-               kErrInvalidArg, "siso layer: bad sizes (need even ent_rank, 1 <= window <= 64)");
-  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.y && p.states, kErrInvalidArg,
+                   p.window >= 0 && p.window <= 64 && p.chunk_size >= 1,
+               kErrInvalidArg, "siso layer: bad sizes (need even ent_rank, 0 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && (p.local_bias || p.window == 0) && p.rope && p.y && p.states, kErrInvalidArg,
                "siso layer: null pointer");
+  TESM_REQUIRE(p.window > 0 || (p.global_embed && p.global_dim >= 1 && p.global_scale && p.global_bias),
+               kErrInvalidArg, "siso layer: global entanglement (window 0) needs the relative-position parameters");
+  TESM_REQUIRE(p.cache_window >= 0 && (p.window > 0 || p.cache_window > 0 || !(p.k_cache || p.v_cache)),
+               kErrInvalidArg, "siso layer: a cache with window 0 needs cache_window");
   if (int rc = check_linear(p.in_proj, p.d_model, "in_proj")) return rc;
   if (int rc = check_linear(p.state_proj, p.d_state, "state_proj")) return rc;
   if (int rc = check_linear(p.ent_proj, p.d_state, "ent_proj")) return rc;
@@ -568,7 +607,44 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   ea.S = p.states;
   ea.ld_s = D;
   ea.eps = p.bit_eps;
-  if (s.fuse_ent) {
+  if (p.window == 0) {  // global causal entanglement (tesm.py:963-1063), then the same quantizations
+    if ((rc = launch_global_bias_table(dt, 2 * p.L, p.global_embed, p.global_dim, p.global_scale, p.global_bias,
+                                       s.g_table, st)))
+      return rc;
+    GlobalArgs ga;
+    ga.dt = dt;
+    ga.mimo = 0;
+    ga.B = p.B;
+    ga.L = p.L;
+    ga.H = 1;
+    ga.R = R;
+    ga.D = D;
+    ga.q = ea.q;
+    ga.ld_q = n_in;
+    ga.k = ea.k;
+    ga.ld_k = n_in;
+    ga.rope = ea.rope;
+    ga.q_add = s.cq;
+    ga.ld_qadd = R;
+    ga.table = s.g_table;
+    ga.thr = p.thr;
+    ga.sqrt_div = static_cast<float>(std::sqrt(static_cast<double>(R)));
+    ga.ent_scale = p.ent_scale;
+    ga.S = p.states;
+    ga.ld_s = D;
+    ga.e_tanh = s.e_tanh;
+    ga.c_out = s.c_mix;
+    ga.ld_out = D;
+    ga.tern = s.g_tern;
+    ga.count = s.g_count;
+    ga.qr = s.g_qr;
+    ga.kr = s.g_kr;
+    if ((rc = launch_global_ent(ga, st))) return rc;
+    if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
+      return rc;
+    if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
+      return rc;
+  } else if (s.fuse_ent) {
     ea.q_te = s.xe.q;
     ea.s_te = s.xe.s;
     ea.rs_te = s.xe.rs;
@@ -597,7 +673,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     cf.L = p.L;
     cf.R = R;
     cf.D = D;
-    cf.W = p.window;
+    cf.W = p.cache_window > 0 ? p.cache_window : p.window;  // the ring's size (tesm.py:1243)
     cf.k = proj + o_k * es;
     cf.ld_k = n_in;
     cf.rope = static_cast<const float2*>(p.rope);
@@ -750,10 +826,14 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "mimo layer: dtype must be 0 or 1");
   TESM_REQUIRE(p.B >= 1 && p.L >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.n_heads >= 1 && p.ent_rank >= 2 &&
-                   p.ent_rank % 2 == 0 && p.window >= 1 && p.window <= 64,
-               kErrInvalidArg, "mimo layer: bad sizes (need even ent_rank, 1 <= window <= 64)");
-  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.mimo_coef && p.mimo_x0sq && p.y, kErrInvalidArg,
-               "mimo layer: null pointer");
+                   p.ent_rank % 2 == 0 && p.window >= 0 && p.window <= 64,
+               kErrInvalidArg, "mimo layer: bad sizes (need even ent_rank, 0 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && (p.local_bias || p.window == 0) && p.rope && p.mimo_coef && p.mimo_x0sq && p.y,
+               kErrInvalidArg, "mimo layer: null pointer");
+  TESM_REQUIRE(p.window > 0 || (p.global_embed && p.global_dim >= 1 && p.global_scale && p.global_bias),
+               kErrInvalidArg, "mimo layer: global entanglement (window 0) needs the relative-position parameters");
+  TESM_REQUIRE(p.cache_window >= 0 && (p.window > 0 || p.cache_window > 0 || !(p.k_cache || p.v_cache)),
+               kErrInvalidArg, "mimo layer: a cache with window 0 needs cache_window");
   const int64_t H = p.n_heads, D = p.d_state, R = p.ent_rank, dm = p.d_model, HD = H * D, HR = H * R;
   if (int rc = check_linear(p.in_proj, dm, "in_proj")) return rc;
   if (int rc = check_linear(p.state_proj, HD, "state_proj")) return rc;
@@ -796,63 +876,100 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   sa.ld_states = HD;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   if ((rc = launch_mimo_final(s.S, p.mimo_x0sq, p.B, p.L, HD, p.h_final, p.last_state, st))) return rc;
-  // 3. per-head window scores, strict ternary, count normalisation (tesm_mimo.py:536-586)
-  EntArgs ea;
-  ea.dt = dt;
-  ea.mimo = 1;
-  ea.B = p.B;
-  ea.L = p.L;
-  ea.H = H;
-  ea.R = R;
-  ea.D = D;
-  ea.W = p.window;
-  ea.q = proj + o_q * es;
-  ea.ld_q = n_in;
-  ea.k = proj + o_k * es;
-  ea.ld_k = n_in;
-  ea.rope = static_cast<const float2*>(p.rope);
-  ea.bias = p.local_bias;
-  ea.thr = p.thr;
-  ea.ent_scale = p.ent_scale;
-  ea.S = s.S;
-  ea.ld_s = HD;
-  ea.wts = s.wts;
-  if ((rc = launch_local_ent(ea, st))) return rc;
+  const void* q_raw = proj + o_q * es;
+  const void* k_raw = proj + o_k * es;
+  if (p.window > 0) {
+    // 3. per-head window scores, strict ternary, count normalisation (tesm_mimo.py:536-586)
+    EntArgs ea;
+    ea.dt = dt;
+    ea.mimo = 1;
+    ea.B = p.B;
+    ea.L = p.L;
+    ea.H = H;
+    ea.R = R;
+    ea.D = D;
+    ea.W = p.window;
+    ea.q = q_raw;
+    ea.ld_q = n_in;
+    ea.k = k_raw;
+    ea.ld_k = n_in;
+    ea.rope = static_cast<const float2*>(p.rope);
+    ea.bias = p.local_bias;
+    ea.thr = p.thr;
+    ea.ent_scale = p.ent_scale;
+    ea.S = s.S;
+    ea.ld_s = HD;
+    ea.wts = s.wts;
+    if ((rc = launch_local_ent(ea, st))) return rc;
+    // 4. window mix, entangled state, rank merge; tanh(E c) and C c in dt for the projections
+    MimoMixArgs ma;
+    ma.dt = dt;
+    ma.B = p.B;
+    ma.L = p.L;
+    ma.H = H;
+    ma.D = D;
+    ma.W = p.window;
+    ma.S = s.S;
+    ma.wts = s.wts;
+    ma.coef = p.mimo_coef;
+    ma.ent_scale = p.ent_scale;
+    ma.te = s.te;
+    ma.cc = s.cc;
+    if ((rc = launch_mimo_mix(ma, st))) return rc;
+  } else {
+    // 3-4. global causal entanglement over the flattened heads (tesm_mimo.py:655-687), E = A, merged
+    if ((rc = launch_global_bias_table(dt, 2 * p.L, p.global_embed, p.global_dim, p.global_scale, p.global_bias,
+                                       s.g_table, st)))
+      return rc;
+    GlobalArgs ga;
+    ga.dt = dt;
+    ga.mimo = 1;
+    ga.B = p.B;
+    ga.L = p.L;
+    ga.H = H;
+    ga.R = R;
+    ga.D = D;
+    ga.q = q_raw;
+    ga.ld_q = n_in;
+    ga.k = k_raw;
+    ga.ld_k = n_in;
+    ga.rope = static_cast<const float2*>(p.rope);
+    ga.table = s.g_table;
+    ga.thr = p.thr;
+    ga.sqrt_div = static_cast<float>(std::sqrt(static_cast<double>(HR)));
+    ga.S = s.S;
+    ga.ld_s = HD;
+    ga.coef = p.mimo_coef;
+    ga.e_tanh = s.te;
+    ga.c_out = s.cc;
+    ga.ld_out = HD;
+    ga.tern = s.g_tern;
+    ga.count = s.g_count;
+    ga.qr = s.g_qr;
+    ga.kr = s.g_kr;
+    if ((rc = launch_global_ent(ga, st))) return rc;
+  }
   if (p.stats_ternary || p.stats_counts) {  // tesm_mimo.py:1019-1020 -> 458-523
     MimoStatsArgs sa2;
     sa2.dt = dt;
+    sa2.global = p.window == 0;
     sa2.B = p.B;
     sa2.L = p.L;
     sa2.H = H;
     sa2.R = R;
-    sa2.W = std::min<int64_t>(p.window, p.L);
-    sa2.S = std::min<int64_t>(p.L, 64);
-    sa2.q = ea.q;
+    sa2.W = p.window > 0 ? std::min<int64_t>(p.window, p.L) : 0;
+    sa2.S = std::min<int64_t>(p.L, p.window > 0 ? 64 : 32);
+    sa2.q = q_raw;
     sa2.ld_q = n_in;
-    sa2.k = ea.k;
+    sa2.k = k_raw;
     sa2.ld_k = n_in;
-    sa2.rope = ea.rope;
+    sa2.rope = static_cast<const float2*>(p.rope);
     sa2.sqrt_r = static_cast<float>(std::sqrt(static_cast<double>(R)));
     sa2.thr = p.thr;
     sa2.ternary = p.stats_ternary;
     sa2.counts = p.stats_counts;
     if ((rc = launch_mimo_stats(sa2, st))) return rc;
   }
-  // 4. window mix, entangled state, rank merge; tanh(E c) and C c in dt for the projections
-  MimoMixArgs ma;
-  ma.dt = dt;
-  ma.B = p.B;
-  ma.L = p.L;
-  ma.H = H;
-  ma.D = D;
-  ma.W = p.window;
-  ma.S = s.S;
-  ma.wts = s.wts;
-  ma.coef = p.mimo_coef;
-  ma.ent_scale = p.ent_scale;
-  ma.te = s.te;
-  ma.cc = s.cc;
-  if ((rc = launch_mimo_mix(ma, st))) return rc;
   if ((rc = launch_quant_act(s.te, dt, M, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
   if ((rc = launch_quant_act(s.cc, dt, M, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
   // 5. decode caches
@@ -866,7 +983,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
     cf.H = H;
     cf.R = R;
     cf.D = D;
-    cf.W = p.window;
+    cf.W = p.cache_window > 0 ? p.cache_window : p.window;  // the ring's size (tesm_mimo.py:1028)
     cf.k = proj + o_k * es;
     cf.ld_k = n_in;
     cf.rope = static_cast<const float2*>(p.rope);

@@ -30,6 +30,8 @@ int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st);
 // ternary against +-thr, written in dt as (B, V, H, W); counts[b] = (#positive, #negative, #zero).
 struct MimoStatsArgs {
   int dt = 0;
+  int global = 0;                // 1: global branch (:469-482): S = min(L, 32) positions, all pairs,
+                                 //    one score per pair summed over heads, output (B, S, S)
   int64_t B = 0, L = 0, H = 0, R = 0;
   int64_t W = 0;                 // window actually used: min(entanglement_window, L)
   int64_t S = 0;                 // sampled positions: min(L, 64); V = S - W + 1 >= 1

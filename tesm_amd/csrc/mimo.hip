@@ -179,23 +179,38 @@ template <int DT>
 __global__ __launch_bounds__(256) void mimo_stats_kernel(MimoStatsArgs a) {
   __shared__ int32_t cnt[3][4];
   const int64_t b = blockIdx.x;
-  const int64_t V = a.S - a.W + 1, half = a.R / 2;
-  const int64_t n = V * a.H * a.W;
+  const int64_t half = a.R / 2;
+  // window branch: (v, h, w) over V = S - W + 1 complete windows; global branch: (s, t) over S x S
+  const int64_t V = a.global ? a.S : a.S - a.W + 1;
+  const int64_t n = a.global ? a.S * a.S : V * a.H * a.W;
   int32_t pos = 0, neg = 0;
   for (int64_t e = threadIdx.x; e < n; e += 256) {
-    const int64_t v = e / (a.H * a.W), h = (e / a.W) % a.H, w = e % a.W;
-    const int64_t tq = a.W - 1 + v, tk = v + w;
-    const int64_t qo = (b * a.L + tq) * a.ld_q + h * a.R, ko = (b * a.L + tk) * a.ld_k + h * a.R;
-    // products in natural r order: the first halves (r < R/2) then the second halves; the loop is
-    // unrolled so a batch of loads is in flight before the running sum needs it
+    int64_t tq, tk, h0, h1;
+    if (a.global) {
+      tq = e / a.S;
+      tk = e % a.S;
+      h0 = 0;
+      h1 = a.H;
+    } else {
+      const int64_t v = e / (a.H * a.W), w = e % a.W;
+      h0 = (e / a.W) % a.H;
+      h1 = h0 + 1;
+      tq = a.W - 1 + v;
+      tk = v + w;
+    }
+    // products in natural (h, r) order: per head the first halves (r < R/2) then the second halves;
+    // the loop is unrolled so a batch of loads is in flight before the running sum needs it
     float acc = 0.0f;
-    for (int part = 0; part < 2; ++part) {
+    for (int64_t h = h0; h < h1; ++h) {
+      const int64_t qo = (b * a.L + tq) * a.ld_q + h * a.R, ko = (b * a.L + tk) * a.ld_k + h * a.R;
+      for (int part = 0; part < 2; ++part) {
 #pragma unroll 8
-      for (int64_t i = 0; i < half; ++i) {
-        float q1, q2, k1, k2;
-        rope_pair<DT>(ld<DT>(a.q, qo + i), ld<DT>(a.q, qo + i + half), a.rope[tq * half + i], q1, q2);
-        rope_pair<DT>(ld<DT>(a.k, ko + i), ld<DT>(a.k, ko + i + half), a.rope[tk * half + i], k1, k2);
-        acc += part == 0 ? rnd<DT>(q1 * k1) : rnd<DT>(q2 * k2);
+        for (int64_t i = 0; i < half; ++i) {
+          float q1, q2, k1, k2;
+          rope_pair<DT>(ld<DT>(a.q, qo + i), ld<DT>(a.q, qo + i + half), a.rope[tq * half + i], q1, q2);
+          rope_pair<DT>(ld<DT>(a.k, ko + i), ld<DT>(a.k, ko + i + half), a.rope[tk * half + i], k1, k2);
+          acc += part == 0 ? rnd<DT>(q1 * k1) : rnd<DT>(q2 * k2);
+        }
       }
     }
     const float sc = rnd<DT>(rnd<DT>(acc) / a.sqrt_r);
@@ -230,8 +245,9 @@ int launch_mimo_stats(const MimoStatsArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "mimo stats: dtype must be 0 or 1");
   if (a.B == 0) return kOk;
   TESM_REQUIRE(a.q && a.k && a.rope && a.ternary && a.counts, kErrInvalidArg, "mimo stats: null pointer");
-  TESM_REQUIRE(a.W >= 1 && a.S >= a.W && a.S <= a.L && a.R >= 2 && a.R % 2 == 0 && a.H >= 1, kErrInvalidArg,
-               "mimo stats: need 1 <= W <= S <= L and an even R");
+  TESM_REQUIRE(a.global ? (a.S >= 1 && a.S <= a.L) : (a.W >= 1 && a.S >= a.W && a.S <= a.L), kErrInvalidArg,
+               "mimo stats: need 1 <= W <= S <= L");
+  TESM_REQUIRE(a.R >= 2 && a.R % 2 == 0 && a.H >= 1, kErrInvalidArg, "mimo stats: need an even R");
   TESM_REQUIRE((a.S - a.W + 1) * a.H * a.W <= 0x7fffffff, kErrUnsupported, "mimo stats: too many scores");
   if (a.dt == kBF16)
     mimo_stats_kernel<kBF16><<<static_cast<unsigned>(a.B), 256, 0, st>>>(a);

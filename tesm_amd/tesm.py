@@ -129,6 +129,17 @@ class TESM_SISO(nn.Module):
             self._bias_cache = (key, v)
         return self._bias_cache[1]
 
+    def _global_params_f32(self, dtype):
+        """global_rel_pos_embed / _scale / _bias rounded to the layer dtype (tesm.py:980-982), as float32."""
+        ps = (self.global_rel_pos_embed, self.global_rel_pos_scale, self.global_rel_pos_bias)
+        key = tuple((p._version, p.data_ptr()) for p in ps) + (dtype,)
+        cached = self.__dict__.get("_global_cache")
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                vals = tuple(p.detach().to(dtype).to(torch.float32).contiguous() for p in ps)
+            self.__dict__["_global_cache"] = (key, vals)
+        return self.__dict__["_global_cache"][1]
+
     def _decay_bias_dt(self, dtype):
         if self.decay_bias.dtype != dtype:
             raise RuntimeError(
@@ -148,9 +159,6 @@ class TESM_SISO(nn.Module):
             cache = inference_params.get("state_cache")
             if cache is not None and "state" in cache:
                 return self._forward_incremental(u, inference_params, cross_layer_state)
-        if self.entanglement_window <= 0:
-            raise backend_error(self.kernel_backend, "global entanglement",
-                                "entanglement_window=0 is not implemented by the hip backend yet")
         cache = None
         if inference_params is not None:  # tesm.py:1235-1253
             cache = inference_params.get("state_cache")
@@ -184,13 +192,16 @@ class TESM_SISO(nn.Module):
             cs = cs.to(dt).contiguous()
         h0 = prev_state.to(device=dev, dtype=torch.float64).contiguous() if prev_state is not None else None
         decay_bias = self._decay_bias_dt(dt)
-        local_bias = self._local_bias_f32(dt)
+        glob = self.entanglement_window <= 0
+        local_bias = None if glob else self._local_bias_f32(dt)
+        gparams = self._global_params_f32(dt) if glob else None
         rope = self.rope_table(L, dt, dev)
-        hip_ops.require_device(u, cs, h0, decay_bias, local_bias, rope, y, states, h_final)
+        hip_ops.require_device(u, cs, h0, decay_bias, local_bias, rope, y, states, h_final,
+                               *(gparams if gparams is not None else ()))
         desc = _lib.SisoLayer()
         desc.dt = hip_ops.dt_code(dt)
         desc.B, desc.L, desc.d_model, desc.d_state, desc.ent_rank = B, L, dm, D, R
-        desc.window, desc.chunk_size = self.entanglement_window, self.state_scan_chunk_size
+        desc.window, desc.chunk_size = max(self.entanglement_window, 0), self.state_scan_chunk_size
         desc.bit_eps = self.in_proj.bit_eps
         desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
         desc.ent_scale = float(self.entanglement_scale)
@@ -203,7 +214,11 @@ class TESM_SISO(nn.Module):
             desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
             desc.cross_state = cs.data_ptr()
         desc.decay_bias = decay_bias.data_ptr()
-        desc.local_bias = local_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr() if local_bias is not None else None
+        if gparams is not None:
+            emb, scale, bias = gparams
+            desc.global_embed, desc.global_dim = emb.data_ptr(), emb.numel()
+            desc.global_scale, desc.global_bias = scale.data_ptr(), bias.data_ptr()
         desc.rope = rope.data_ptr()
         desc.h0 = h0.data_ptr() if h0 is not None else None
         desc.y = y.data_ptr()
@@ -214,6 +229,7 @@ class TESM_SISO(nn.Module):
             k_cache, v_cache = self._prefill_cache_buffers(cache, B, L, dev)
             desc.k_cache, desc.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
             desc.cache_dt = hip_ops.dt_code(k_cache.dtype)
+            desc.cache_window = k_cache.shape[1]
         nbytes = int(lib.tesm_hip_siso_prefill_ws_bytes(ctypes.byref(desc)))
         with torch.cuda.device(dev):
             ws = workspace(dev, nbytes)

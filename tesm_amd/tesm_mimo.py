@@ -85,14 +85,18 @@ class TESMMIMO_Optimized(TESM_SISO):
         self.__dict__["_stats_pending"] = None
 
     def _stats_buffers(self, B, L, dt, dev):
-        """Ternary (B, V, n_heads, W) and per-row counts for the statistics of the first min(L, 64)
-        positions; V = min(L, 64) - min(window, L) + 1 complete windows (tesm_mimo.py:465, 485-490)."""
+        """Ternary and per-row counts for the statistics: window branch (B, V, n_heads, W) over the first
+        min(L, 64) positions, V = min(L, 64) - min(window, L) + 1 complete windows (tesm_mimo.py:465,
+        485-490); global branch (B, S, S) over the first S = min(L, 32) positions (:469-482)."""
+        counts = torch.empty((B, 3), dtype=torch.int32, device=dev)
+        if self.entanglement_window <= 0:
+            S = min(L, 32)
+            return torch.empty((B, S, S), dtype=dt, device=dev), counts
         W = min(self.entanglement_window, L)
         S = min(L, 64)
         if W > S:  # the reference's unfold (tesm_mimo.py:487) raises here
             raise RuntimeError(f"maximum size for tensor at dimension 1 is {S} but size is {W}")
         tern = torch.empty((B, S - W + 1, self.n_heads, W), dtype=dt, device=dev)
-        counts = torch.empty((B, 3), dtype=torch.int32, device=dev)
         return tern, counts
 
     # -- cached device constants ---------------------------------------------------
@@ -129,9 +133,6 @@ class TESMMIMO_Optimized(TESM_SISO):
             if cache is not None and "state" in cache:
                 raise backend_error(self.kernel_backend, "TESMMIMO decode",
                                     "the MIMO decode step is not implemented by the hip backend yet")
-        if self.entanglement_window <= 0:
-            raise backend_error(self.kernel_backend, "global MIMO entanglement",
-                                "entanglement_window=0 is not implemented by the hip backend yet")
         cache = None
         if inference_params is not None:
             cache = inference_params.get("state_cache")
@@ -148,15 +149,18 @@ class TESMMIMO_Optimized(TESM_SISO):
         h_final = torch.empty((B, H, D), dtype=torch.float64, device=dev)
         last = torch.empty((B, H, D), dtype=torch.float32, device=dev)
         decay_bias = self._decay_bias_dt(dt).contiguous()
-        local_bias = self._local_bias_f32(dt)
+        glob = self.entanglement_window <= 0
+        local_bias = None if glob else self._local_bias_f32(dt)
+        gparams = self._global_params_f32(dt) if glob else None
         rope = self.rope_table(L, dt, dev)
         coef, x0sq = self._mimo_coef(dt)
-        hip_ops.require_device(u, decay_bias, local_bias, rope, coef, x0sq, y, h_final, last)
+        hip_ops.require_device(u, decay_bias, local_bias, rope, coef, x0sq, y, h_final, last,
+                               *(gparams if gparams is not None else ()))
         lib = _lib.load()
         desc = _lib.MimoLayer()
         desc.dt = hip_ops.dt_code(dt)
         desc.B, desc.L, desc.d_model, desc.d_state, desc.n_heads = B, L, dm, D, H
-        desc.ent_rank, desc.window = R, self.entanglement_window
+        desc.ent_rank, desc.window = R, max(self.entanglement_window, 0)
         desc.bit_eps = self.in_proj.bit_eps
         desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
         desc.ent_scale = float(self.entanglement_scale)
@@ -166,7 +170,11 @@ class TESMMIMO_Optimized(TESM_SISO):
         desc.ent_proj = self.ent_proj.linear_desc()
         desc.out_proj = self.out_proj.linear_desc()
         desc.decay_bias = decay_bias.data_ptr()
-        desc.local_bias = local_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr() if local_bias is not None else None
+        if gparams is not None:
+            emb, scale, bias = gparams
+            desc.global_embed, desc.global_dim = emb.data_ptr(), emb.numel()
+            desc.global_scale, desc.global_bias = scale.data_ptr(), bias.data_ptr()
         desc.rope = rope.data_ptr()
         desc.mimo_coef, desc.mimo_x0sq = coef.data_ptr(), x0sq.data_ptr()
         desc.y = y.data_ptr()
@@ -179,6 +187,7 @@ class TESMMIMO_Optimized(TESM_SISO):
             k_cache, v_cache = self._mimo_cache_buffers(cache, B, L, dev)
             desc.k_cache, desc.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
             desc.cache_dt = hip_ops.dt_code(k_cache.dtype)
+            desc.cache_window = k_cache.shape[1]
         nbytes = int(lib.tesm_hip_mimo_prefill_ws_bytes(ctypes.byref(desc)))
         with torch.cuda.device(dev):
             ws = workspace(dev, nbytes)
