@@ -19,6 +19,9 @@ Contents
   packing, and the exact int32 BitLinear accumulators.  Built by
   ``oracle/Makefile`` into ``oracle/_build/liboracle_int.so`` and loaded by
   ``oracle.int_ref``.
+* ``int2_export`` -- the reference's INT2 export format (``pack_int2_to_uint8``,
+  ``unpack_uint8_to_int2``, ``export_model_to_int2``), the checker of the hip
+  export and loader.
 * ``brute``       -- tiny pure-Python/numpy brute-force versions of the scan and
   of the local-window ternary entanglement, used to pin ``tesm_torch``.
 

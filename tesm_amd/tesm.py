@@ -285,9 +285,10 @@ class TESM_SISO(nn.Module):
         dtype, a weight or a bias changes (the packed weights follow tesm.py:226-236's cache rule)."""
         lins = (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj)
         db, lb = self.decay_bias, self.local_entanglement_bias
+        lb_key = (lb._version, lb.data_ptr()) if lb is not None else None
         key = (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
-               db.data_ptr(), db.dtype, lb._version, lb.data_ptr(),
-               tuple((p.weight._version, p.weight.data_ptr(), p.weight.dtype) for p in lins))
+               db.data_ptr(), db.dtype, lb_key,
+               tuple(p.cache_key() for p in lins))
         plan = self.__dict__.get("_decode_plan")
         if plan is not None and plan[0] == key:
             return plan[1]
@@ -295,7 +296,12 @@ class TESM_SISO(nn.Module):
             if p.weight.dtype != dt:
                 raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
         decay_bias = self._decay_bias_dt(dt)
-        local_bias = self._local_bias_f32(dt)
+        if lb is not None:
+            local_bias = self._local_bias_f32(dt)
+        else:
+            # global layers decode over their one-slot ring with no bias (tesm.py:633, 1355-1357);
+            # adding 0 to a score leaves it unchanged
+            local_bias = torch.zeros(W, dtype=torch.float32, device=dev)
         D, R, dm = self.d_state, self.ent_rank, self.d_model
         desc = _lib.SisoStep()
         desc.dt = hip_ops.dt_code(dt)
@@ -328,9 +334,6 @@ class TESM_SISO(nn.Module):
         B, _, dm = u.shape
         D = self.d_state
         dev = u.device
-        if self.entanglement_window <= 0:
-            raise backend_error(self.kernel_backend, "global entanglement decode",
-                                "entanglement_window=0 is not implemented by the hip backend yet")
         kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
         self._check_cache(kc, vc, B, dev)
         W = kc.shape[1]

@@ -76,8 +76,10 @@ def test_decode_vs_reference_fixture(name):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("P,steps,W,cross", [(12, 6, 8, False), (3, 9, 8, True), (0, 11, 4, False),
-                                             (40, 5, 16, True)])
+                                             (40, 5, 16, True), (12, 6, 0, False), (0, 7, 0, True)])
 def test_decode_random_vs_oracle(dtype, P, steps, W, cross):
+    """W = 0 is a global layer: its cache rings hold one slot and its steps add no bias (tesm.py:633,
+    1324-1357)."""
     B, dm, D, R = 5, 96, 48, 16
     meta = dict(seed=11 + P + W, dm=dm, D=D, R=R, W=W)
     ref = _module(ot.TESM_SISO, meta).to(dtype)
