@@ -171,13 +171,14 @@ def measure_kernels(torch, only):
     return res
 
 
-def measure_decode(torch, m, steps: int = 50):
-    """configs[3] decode: B = 32 sequences, caches filled by a 64-token prefill (>= W), then one-token
-    steps; returns the per-step time (device events around `steps` consecutive steps)."""
+def measure_decode(torch, m, steps: int = 50, d_model: int = LAYER["d_model"]):
+    """Decode of layer `m` (configs[3]'s SISO layer, or the configs[4] MIMO layer): B = 32 sequences,
+    caches filled by a 64-token prefill (>= W), then one-token steps; returns the per-step time (device
+    events around `steps` consecutive steps)."""
     Bd, P = 32, 64
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(1)
-    u = torch.randn(Bd, P + steps + 3, LAYER["d_model"], generator=g).to(torch.bfloat16).to(dev)
+    u = torch.randn(Bd, P + steps + 3, d_model, generator=g).to(torch.bfloat16).to(dev)
     cache = m.allocate_inference_cache(Bd, P + steps + 3)
     ip = {"state_cache": cache}
     m(u[:, :P], inference_params=ip)
@@ -246,10 +247,13 @@ def measure_mimo(torch, reps: int = 3):
         e1.record()
         torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    del m, u
+    del u
+    with torch.no_grad():
+        dec = measure_decode(torch, m, steps=30, d_model=MIMO["d_model"])
+    del m
     torch.cuda.empty_cache()
     return {"workload": "TESMMIMO_Optimized prefill, large_40b dims (configs[4]), B1 x L32768, bf16",
-            "ms_per_forward": ms, "tokens_per_s": L / (ms * 1e-3), "reps": reps}
+            "ms_per_forward": ms, "tokens_per_s": L / (ms * 1e-3), "reps": reps, "decode": dec}
 
 
 def gemm_traffic():

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 5
+#define TESM_HIP_ABI_VERSION 6
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -304,6 +304,41 @@ typedef struct tesm_hip_mimo_layer {
 
 int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p);
 int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* p, void* ws, int64_t ws_bytes, void* stream);
+
+/* One TESMMIMO_Optimized decode step for B sequences (one token each).  Replaces
+ * TESMMIMO_Optimized._forward_incremental (tesm_mimo.py:753-912) on the cache of
+ * allocate_inference_cache (tesm_mimo.py:689-731): in_proj, per-head gates, RoPE at position
+ * seq_pos, the optional cross-layer query cross_q_proj(cross_state) per head (a (B, n_heads, d_state)
+ * state, tesm_mimo.py:818-826), the float64 per-head state update (no rank expansion, as the
+ * reference's step), ring write of (key, state) at slot cache_idx, per-head window scores with the
+ * head's bias row, strict ternary, count normalisation, mix, then state_proj(tanh(E)) and ent_proj(C)
+ * over the flattened heads, the output gate and out_proj.  The caller then advances
+ * cache_idx = (cache_idx + 1) % window and seq_pos += 1.  window 1 with a zero bias is the
+ * global-entanglement layer's step (its rings hold one slot). */
+typedef struct tesm_hip_mimo_step {
+  int dt;                     /* module dtype */
+  int cache_dt;               /* ring buffer dtype: 0 f32, 1 bf16 */
+  int64_t B, d_model, d_state, n_heads, ent_rank, window;
+  int64_t seq_pos;            /* tokens seen before this one (its RoPE position) */
+  int64_t cache_idx;          /* ring slot this step writes */
+  float bit_eps, thr, ent_scale;
+  const void* u;              /* (B, d_model) in dt, row pitch ld_u */
+  int64_t ld_u;               /* row pitch of u in elements (0: d_model) */
+  tesm_hip_linear in_proj, state_proj, ent_proj, out_proj, cross_q_proj;
+  const void* decay_bias;     /* (n_heads, d_state) in dt */
+  const float* local_bias;    /* (n_heads, window) float32 holding dt values */
+  const void* rope;           /* tesm_hip_rope_table with at least seq_pos + 1 rows from position 0 */
+  const void* cross_state;    /* optional (B, n_heads, d_state) in dt */
+  const double* state;        /* (B, n_heads, d_state) float64 state before the step */
+  double* state_out;          /* (B, n_heads, d_state) float64 state after the step (may equal state) */
+  void* k_cache;              /* (B, window, n_heads, ent_rank) cache_dt, updated in place */
+  void* v_cache;              /* (B, window, n_heads, d_state) cache_dt, updated in place */
+  void* y;                    /* (B, d_model) in dt */
+  void* new_state;            /* optional (B, n_heads, d_state) in dt: this step's state */
+} tesm_hip_mimo_step;
+
+int64_t tesm_hip_mimo_decode_ws_bytes(const tesm_hip_mimo_step* p);
+int tesm_hip_mimo_decode(const tesm_hip_mimo_step* p, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

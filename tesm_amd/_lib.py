@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -108,6 +108,21 @@ class MimoLayer(ctypes.Structure):
     ]
 
 
+class MimoStep(ctypes.Structure):
+    """``tesm_hip_mimo_step``."""
+    _fields_ = [
+        ("dt", I32), ("cache_dt", I32),
+        ("B", I64), ("d_model", I64), ("d_state", I64), ("n_heads", I64), ("ent_rank", I64), ("window", I64),
+        ("seq_pos", I64), ("cache_idx", I64),
+        ("bit_eps", F32), ("thr", F32), ("ent_scale", F32),
+        ("u", P), ("ld_u", I64),
+        ("in_proj", Linear), ("state_proj", Linear), ("ent_proj", Linear), ("out_proj", Linear),
+        ("cross_q_proj", Linear),
+        ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P),
+        ("state", P), ("state_out", P), ("k_cache", P), ("v_cache", P), ("y", P), ("new_state", P),
+    ]
+
+
 _SIGNATURES = {
     "tesm_hip_abi_version": ([], I32),
     "tesm_hip_last_error": ([], ctypes.c_char_p),
@@ -130,6 +145,8 @@ _SIGNATURES = {
     "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
     "tesm_hip_siso_decode_ws_bytes": ([ctypes.POINTER(SisoStep)], I64),
     "tesm_hip_siso_decode": ([ctypes.POINTER(SisoStep), P, I64, P], I32),
+    "tesm_hip_mimo_decode_ws_bytes": ([ctypes.POINTER(MimoStep)], I64),
+    "tesm_hip_mimo_decode": ([ctypes.POINTER(MimoStep), P, I64, P], I32),
     "tesm_hip_mimo_coef": ([P, P, I32, I64, I64, I64, P, P, P], I32),
     "tesm_hip_mimo_prefill_ws_bytes": ([ctypes.POINTER(MimoLayer)], I64),
     "tesm_hip_mimo_prefill": ([ctypes.POINTER(MimoLayer), P, I64, P], I32),

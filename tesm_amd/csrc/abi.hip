@@ -809,6 +809,151 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   return run_output_path(op, st);
 }
 
+// Workspace layout of the MIMO decode step; with base == nullptr it only measures.
+struct MimoDecodePlan {
+  CodeBuf xu, xs, xe, xc, xy;
+  void* proj;
+  void* cq;
+  void* te;  // (B, H*D) tanh(E) in dt
+  void* cc;  // (B, H*D) C = E - S in dt
+  void* yg;
+  int64_t total;
+};
+
+MimoDecodePlan plan_mimo_decode(const tesm_hip_mimo_step& p, void* base) {
+  Carve c(base);
+  MimoDecodePlan s;
+  const int64_t HD = p.n_heads * p.d_state;
+  const int64_t n_in = 2 * p.d_model + 3 * HD + 2 * p.n_heads * p.ent_rank;
+  const int es = esize(p.dt);
+  s.xu = take_codes(c, p.B, p.d_model);
+  s.proj = c.take<void>(p.B * n_in * es);
+  if (p.cross_state) {
+    s.xs = take_codes(c, p.B * p.n_heads, p.d_state);
+    s.cq = c.take<void>(p.B * p.n_heads * p.ent_rank * es);
+  } else {
+    s.xs = CodeBuf{nullptr, nullptr, nullptr, 0};
+    s.cq = nullptr;
+  }
+  s.te = c.take<void>(p.B * HD * es);
+  s.cc = c.take<void>(p.B * HD * es);
+  s.xe = take_codes(c, p.B, HD);
+  s.xc = take_codes(c, p.B, HD);
+  s.yg = p.d_model <= 1024 && p.B >= 256 ? nullptr : c.take<void>(p.B * p.d_model * es);
+  s.xy = take_codes(c, p.B, p.d_model);
+  s.total = c.off;
+  return s;
+}
+
+int64_t tesm_hip_mimo_decode_ws_bytes(const tesm_hip_mimo_step* p) {
+  if (!p) return -1;
+  return plan_mimo_decode(*p, nullptr).total;
+}
+
+int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "mimo decode: null descriptor");
+  const tesm_hip_mimo_step& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "mimo decode: dtype must be 0 or 1");
+  TESM_REQUIRE(p.B >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.n_heads >= 1 && p.ent_rank >= 2 &&
+                   p.ent_rank % 2 == 0 && p.window >= 1 && p.window <= 64 && p.seq_pos >= 0 && p.cache_idx >= 0 &&
+                   p.cache_idx < p.window,
+               kErrInvalidArg,
+               "mimo decode: bad sizes or ring position (need even ent_rank, 1 <= window <= 64)");
+  TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.state && p.state_out && p.k_cache && p.v_cache &&
+                   p.y,
+               kErrInvalidArg, "mimo decode: null pointer");
+  const int64_t Bn = p.B, dm = p.d_model, D = p.d_state, H = p.n_heads, R = p.ent_rank;
+  const int64_t HD = H * D, HR = H * R;
+  if (int rc = check_linear(p.in_proj, dm, "in_proj")) return rc;
+  if (int rc = check_linear(p.state_proj, HD, "state_proj")) return rc;
+  if (int rc = check_linear(p.ent_proj, HD, "ent_proj")) return rc;
+  if (int rc = check_linear(p.out_proj, dm, "out_proj")) return rc;
+  if (p.cross_state)
+    if (int rc = check_linear(p.cross_q_proj, D, "cross_q_proj")) return rc;
+  const MimoDecodePlan s = plan_mimo_decode(p, ws);
+  TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "mimo decode: workspace too small");
+
+  const int dt = p.dt;
+  const int es = esize(dt);
+  const int64_t n_in = 2 * dm + 3 * HD + 2 * HR;
+  char* proj = static_cast<char*>(s.proj);
+  const int64_t o_local = 0, o_sv = dm, o_decay = dm + HD, o_write = dm + 2 * HD, o_gate = dm + 3 * HD,
+                o_q = 2 * dm + 3 * HD, o_k = 2 * dm + 3 * HD + HR;
+  int rc;
+  // 1. in_proj on the B new tokens (tesm_mimo.py:765-781)
+  const int64_t ld_u = p.ld_u > 0 ? p.ld_u : dm;
+  TESM_REQUIRE(ld_u >= dm, kErrInvalidArg, "mimo decode: ld_u must be >= d_model");
+  if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  if ((rc = run_linear(s.xu, p.in_proj, Bn, n_in, dm, proj, dt, n_in, st))) return rc;
+  // 2. cross-layer query per head: cross_q_proj over the B * n_heads state rows (tesm_mimo.py:818-826)
+  if (p.cross_state) {
+    if ((rc = launch_quant_act(p.cross_state, dt, Bn * H, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs,
+                               st)))
+      return rc;
+    if ((rc = run_linear(s.xs, p.cross_q_proj, Bn * H, R, D, s.cq, dt, R, st))) return rc;
+  }
+  // 3. per-head state update, ring write, window entanglement (tesm_mimo.py:838-887)
+  DecodeArgs da;
+  da.dt = dt;
+  da.cdt = p.cache_dt;
+  da.B = Bn;
+  da.H = H;
+  da.R = R;
+  da.D = D;
+  da.W = p.window;
+  da.pos = p.seq_pos;
+  da.slot = p.cache_idx;
+  da.valid = std::min<int64_t>(p.seq_pos + 1, p.window);
+  da.full = da.valid >= p.window;
+  da.proj = proj;
+  da.ld_proj = n_in;
+  da.o_sv = o_sv;
+  da.o_decay = o_decay;
+  da.o_write = o_write;
+  da.o_q = o_q;
+  da.o_k = o_k;
+  da.rope = static_cast<const float2*>(p.rope);
+  da.decay_bias = p.decay_bias;
+  da.bias = p.local_bias;
+  da.q_add = s.cq;
+  da.ld_qadd = R;
+  da.thr = p.thr;
+  da.ent_scale = p.ent_scale;
+  da.eps = p.bit_eps;
+  da.state = p.state;
+  da.state_out = p.state_out;
+  da.k_cache = p.k_cache;
+  da.v_cache = p.v_cache;
+  da.new_state = p.new_state;
+  da.te_out = s.te;
+  da.c_out = s.cc;
+  da.ld_out = HD;
+  if ((rc = launch_decode_ent(da, st))) return rc;
+  // 4. per-token codes of tanh(E) and C over the flattened heads (tesm_mimo.py:895-900)
+  if ((rc = launch_quant_act(s.te, dt, Bn, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
+  if ((rc = launch_quant_act(s.cc, dt, Bn, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  // 5. output gate and out_proj (tesm_mimo.py:902-906)
+  OutputPath op;
+  op.xe = s.xe;
+  op.xc = s.xc;
+  op.xy = s.xy;
+  op.yg = s.yg;
+  op.state_proj = &p.state_proj;
+  op.ent_proj = &p.ent_proj;
+  op.out_proj = &p.out_proj;
+  op.M = Bn;
+  op.dm = dm;
+  op.D = HD;
+  op.dt = dt;
+  op.eps = p.bit_eps;
+  op.local = proj + o_local * es;
+  op.gate = proj + o_gate * es;
+  op.ld = n_in;
+  op.y = p.y;
+  return run_output_path(op, st);
+}
+
 int tesm_hip_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t n_heads, int64_t mimo_rank,
                        int64_t d_state, float* coef, float* x0sq, void* stream) {
   return launch_mimo_coef(mimo_x, mimo_o, dt, n_heads, mimo_rank, d_state, coef, x0sq,

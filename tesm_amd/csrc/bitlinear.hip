@@ -342,67 +342,14 @@ __device__ __forceinline__ bool vec4_ok(const void* p, int64_t ld) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (DT == kBF16 ? 2 : 4)) % bytes == 0;
 }
 
-template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
-__global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
-  using C = Cfg<WM, WN, TM, TN>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
-  int64_t tm, tn;
-  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
-  const int64_t m0 = tm * C::BM;
-  const int64_t n0 = tn * C::BN;
-  v4i acc0[TM][TN], acc1[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      acc0[i][j] = v4i{0, 0, 0, 0};
-      acc1[i][j] = v4i{0, 0, 0, 0};
-    }
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w / WN, wn = w % WN;
+// General epilogue of the 16 x 16 tiles of one wave (tile rows wm*TM.., columns wn*TN..): scale the
+// exact accumulators, optional bias / accumulator dump, or the output gate
+// y = local + sigmoid(gate) * state_proj + ent_proj in the module dtype's op order.
+template <int TM, int TN, int EPI, int OUT_DT>
+__device__ __forceinline__ void epilogue16(const LinearArgs& a, const v4i (&acc0)[TM][TN], const v4i (&acc1)[TM][TN],
+                                           int64_t m0, int64_t n0, int wm, int wn, int lane) {
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
-  // plain products (one scalar c_w, no bias, no accumulator dump) take the short epilogue, whose
-  // per-row operands are requested before the main loop
-  const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
-  float sx[TM];
-  int32_t rsum[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
-    const int64_t mc = m < a.M ? m : a.M - 1;
-    sx[i] = o0.s_x[mc];
-    rsum[i] = o0.rowsum[mc];
-  }
-  const float cws = o0.c_w[0];
-  mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
-
-  if (plain) {
-    const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));  // columns of this tile
-    const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
-      if (m >= a.M) continue;
-      const float inv = 1.0f / sx[i];
-      char* orow = static_cast<char*>(a.out) + (m * a.ldo + n0) * (OUT_DT == kBF16 ? 2 : 4);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int nb = (wn * TN + j) * 16 + 4 * (lane >> 4);  // within the tile
-        if (nb >= nrem) continue;
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc0[i][j][r] - rsum[i]) * inv) * cws;
-        if (vout && nb + 4 <= nrem) {
-          store4<OUT_DT>(orow, nb, v, true);
-        } else {
-          for (int r = 0; r < 4 && nb + r < nrem; ++r) st<OUT_DT>(orow, nb + r, v[r]);
-        }
-      }
-    }
-    return;
-  }
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
   bool vin = false;
   if constexpr (EPI == kEpiOutputGate) vin = vec4_ok<OUT_DT>(a.local, a.ld_local) && vec4_ok<OUT_DT>(a.gate, a.ld_gate);
@@ -410,8 +357,8 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   for (int i = 0; i < TM; ++i) {
     const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
     if (m >= a.M) continue;
-    const float inv0 = 1.0f / sx[i];
-    const int32_t rs0 = rsum[i];
+    const float inv0 = 1.0f / o0.s_x[m];
+    const int32_t rs0 = o0.rowsum[m];
     float inv1 = 0.0f;
     int32_t rs1 = 0;
     if constexpr (EPI == kEpiOutputGate) {
@@ -461,6 +408,191 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
       }
     }
   }
+}
+
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT>
+__global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
+  using C = Cfg<WM, WN, TM, TN>;
+  __shared__ __attribute__((aligned(16))) char smem[2 * C::STAGE];
+  int64_t tm, tn;
+  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
+  const int64_t m0 = tm * C::BM;
+  const int64_t n0 = tn * C::BN;
+  v4i acc0[TM][TN], acc1[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc0[i][j] = v4i{0, 0, 0, 0};
+      acc1[i][j] = v4i{0, 0, 0, 0};
+    }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w / WN, wn = w % WN;
+  const LinearOperand& o0 = a.op[0];
+  // plain products (one scalar c_w, no bias, no accumulator dump) take the short epilogue, whose
+  // per-row operands are requested before the main loop
+  const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
+  float sx[TM];
+  int32_t rsum[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
+    const int64_t mc = m < a.M ? m : a.M - 1;
+    sx[i] = o0.s_x[mc];
+    rsum[i] = o0.rowsum[mc];
+  }
+  const float cws = o0.c_w[0];
+  mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
+  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+
+  if (plain) {
+    const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));  // columns of this tile
+    const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = m0 + (wm * TM + i) * 16 + (lane & 15);
+      if (m >= a.M) continue;
+      const float inv = 1.0f / sx[i];
+      char* orow = static_cast<char*>(a.out) + (m * a.ldo + n0) * (OUT_DT == kBF16 ? 2 : 4);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nb = (wn * TN + j) * 16 + 4 * (lane >> 4);  // within the tile
+        if (nb >= nrem) continue;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc0[i][j][r] - rsum[i]) * inv) * cws;
+        if (vout && nb + 4 <= nrem) {
+          store4<OUT_DT>(orow, nb, v, true);
+        } else {
+          for (int r = 0; r < 4 && nb + r < nrem; ++r) st<OUT_DT>(orow, nb + r, v[r]);
+        }
+      }
+    }
+    return;
+  }
+  epilogue16<TM, TN, EPI, OUT_DT>(a, acc0, acc1, m0, n0, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Small-M products (decode batches, M <= 16*TM): one workgroup per 16*TM x 16*TN output tile, the K
+// loop split over its NW waves.  Wave w takes the 256-code blocks w, w + NW, ...; per block, lane L
+// (weight column / activation row L%16, group g = L/16) reads one b128 of packed weights per column
+// tile (codes 64g .. 64g+63 of the block) and four b128 of activation codes per row tile (the same
+// 64 codes of its row).  In k-step s the lane feeds codes 64g + 16s .. +15 to both MFMA operands, so
+// every code of the block meets its weight exactly once.  Operands come straight from global
+// memory with the next block's loads issued before the current block's MFMAs; the waves' int32
+// partial sums are added through LDS (exact, order-free) and wave 0 runs the epilogue.  This gives
+// N/(16*TN) workgroups of NW waves instead of the LDS-staged kernel's N/64 single-stream tiles.
+template <int TM, int TN>
+struct SkinnyRegs {
+  uint4 w[TN];      // packed weights of the block: dword s feeds k-step s
+  v4i x[TM][4];     // activation codes: x[i][s] feeds k-step s of row tile i
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void skinny_load(SkinnyRegs<TM, TN>& r, const uint8_t* const (&pw)[TN],
+                                            const int8_t* const (&pa)[TM], int64_t kb, bool live) {
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) r.w[j] = *reinterpret_cast<const uint4*>(pw[j] + 64 * kb);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) r.x[i][s] = *reinterpret_cast<const v4i*>(pa[i] + 256 * kb + 16 * s);
+  } else {  // codes past Kp: zero activations contribute nothing whatever the weights
+#pragma unroll
+    for (int j = 0; j < TN; ++j) r.w[j] = make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) r.x[i][s] = v4i{0, 0, 0, 0};
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void skinny_mma(const SkinnyRegs<TM, TN>& r, v4i (&acc)[TM][TN]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint32_t wd = s == 0 ? r.w[j].x : s == 1 ? r.w[j].y : s == 2 ? r.w[j].z : r.w[j].w;
+      const v4i bf = unpack_frag(wd);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, r.x[i][s], acc[i][j], 0, 0, 0);
+    }
+}
+
+// K loop of one wave over the blocks w, w + NW, ... of Kp (a trailing 128-code half block is read by
+// groups 0 and 1 only).
+template <int NW, int TM, int TN>
+__device__ __forceinline__ void skinny_loop(const LinearOperand& o, int64_t M, int64_t N, int64_t m0, int64_t n0,
+                                            int64_t Kp, int w, int lane, v4i (&acc)[TM][TN]) {
+  const int g = lane >> 4, l16 = lane & 15;
+  const uint8_t* pw[TN];
+  const int8_t* pa[TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t n = n0 + 16 * j + l16;
+    pw[j] = o.w + (n < N ? n : N - 1) * o.ldw + 16 * g;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + 16 * i + l16;
+    pa[i] = o.q + (m < M ? m : M - 1) * o.ldq + 64 * g;
+  }
+  const int64_t nblk = (Kp + 255) / 256;
+  const bool half_tail = (Kp & 255) != 0;  // last block holds 128 codes: groups 0 and 1
+  auto live = [&](int64_t kb) { return kb < nblk && (!half_tail || kb + 1 < nblk || g < 2); };
+  SkinnyRegs<TM, TN> r0, r1;
+  int64_t kb = w;
+  skinny_load<TM, TN>(r0, pw, pa, kb, live(kb));
+  for (; kb < nblk; kb += 2 * NW) {
+    skinny_load<TM, TN>(r1, pw, pa, kb + NW, live(kb + NW));
+    skinny_mma<TM, TN>(r0, acc);
+    if (kb + NW >= nblk) break;
+    skinny_load<TM, TN>(r0, pw, pa, kb + 2 * NW, live(kb + 2 * NW));
+    skinny_mma<TM, TN>(r1, acc);
+  }
+}
+
+template <int NW, int TM, int TN, int EPI, int OUT_DT>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
+  constexpr int NOP = EPI == kEpiOutputGate ? 2 : 1;
+  __shared__ v4i red[(NW - 1) * NOP * TM * TN * 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t ntn = (a.N + 16 * TN - 1) / (16 * TN);
+  const int64_t tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
+  const int64_t m0 = tm * 16 * TM, n0 = tn * 16 * TN;
+  v4i acc0[TM][TN], acc1[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc0[i][j] = v4i{0, 0, 0, 0};
+      acc1[i][j] = v4i{0, 0, 0, 0};
+    }
+  skinny_loop<NW, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, w, lane, acc0);
+  if constexpr (EPI == kEpiOutputGate) skinny_loop<NW, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, w, lane, acc1);
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        red[((((w - 1) * NOP) * TM + i) * TN + j) * 64 + lane] = acc0[i][j];
+        if constexpr (NOP == 2) red[((((w - 1) * NOP + 1) * TM + i) * TN + j) * 64 + lane] = acc1[i][j];
+      }
+  }
+  __syncthreads();
+  if (w != 0) return;
+  for (int src = 0; src < NW - 1; ++src)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc0[i][j] += red[(((src * NOP) * TM + i) * TN + j) * 64 + lane];
+        if constexpr (NOP == 2) acc1[i][j] += red[(((src * NOP + 1) * TM + i) * TN + j) * 64 + lane];
+      }
+  epilogue16<TM, TN, EPI, OUT_DT>(a, acc0, acc1, m0, n0, 0, 0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1507,6 +1639,17 @@ inline DeviceLimits device_limits() {
   return d;
 }
 
+template <int NW, int TM, int TN, int EPI>
+int run_skinny(const LinearArgs& a, hipStream_t st) {
+  const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 16 * TN - 1) / (16 * TN));
+  TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
+  if (a.out_dt == kBF16)
+    skinny_kernel<NW, TM, TN, EPI, kBF16><<<static_cast<unsigned>(tiles), NW * 64, 0, st>>>(a);
+  else
+    skinny_kernel<NW, TM, TN, EPI, kF32><<<static_cast<unsigned>(tiles), NW * 64, 0, st>>>(a);
+  return check_launch("bitlinear skinny");
+}
+
 template <int WM, int WN, int TM, int TN, int EPI>
 int run_mfma(const LinearArgs& a, hipStream_t st) {
   using C = Cfg<WM, WN, TM, TN>;
@@ -1627,6 +1770,10 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     return dispatch_gemv<4>(a, nch, st);
   }
   if (a.epilogue == kEpiStore) {
+    // decode-size batches: the split-K kernel while the LDS-staged one would have too few 64-column
+    // tiles to fill the chip (measured at M = 32: N = 768 .. 4096 faster split, N = 34816 staged)
+    if (a.M <= 16 && a.N < 16384) return run_skinny<4, 1, 1, kEpiStore>(a, st);
+    if (a.M <= 32 && a.N < 16384) return run_skinny<4, 2, 1, kEpiStore>(a, st);
     if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
     // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
     // enough of them, 128x128 (4 waves of 64x64) when those still give two workgroups per CU,
@@ -1640,7 +1787,8 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
-  if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiOutputGate>(a, st);
+  if (a.M <= 16) return run_skinny<4, 1, 1, kEpiOutputGate>(a, st);
+  if (a.M <= 32) return run_skinny<4, 2, 1, kEpiOutputGate>(a, st);
   const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
   if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiOutputGate, 3>(a, st);
   if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiOutputGate>(a, st);

@@ -1,15 +1,21 @@
-// TESM_SISO decode step and prefill cache fill: arguments shared by the kernels and the drivers.
+// TESM_SISO / TESMMIMO_Optimized decode step and prefill cache fill: arguments shared by the kernels and
+// the drivers.
 #pragma once
 
 #include "entangle.h"
 
 namespace tesm {
 
-// One decode step of the entanglement block for B rows (one token each).
+// One decode step of the entanglement block for B rows (one token each) and H heads (SISO: H = 1).
+// Per-head data: state / new state / cross query rows b*H + h; proj slices at o_* + h*D (h*R for q, k);
+// decay bias (H, D); window bias (H, W); rings (B, W, H, R) and (B, W, H, D).
 struct DecodeArgs {
   int dt = 0;                  // layer dtype
   int cdt = 0;                 // ring buffer dtype
   int64_t B = 0, R = 0, D = 0, W = 0;
+  int64_t H = 1;
+  int64_t chunk = 0;           // channels per workgroup (set by launch_decode_ent)
+  int vec4 = 0;                // ring states may be read four at a time (set by launch_decode_ent)
   int64_t pos = 0;             // RoPE position of this token (seq_pos before the step)
   int64_t slot = 0;            // ring slot written by this step (cache_idx)
   int64_t valid = 0;           // min(seq_pos + 1, W)
@@ -20,15 +26,19 @@ struct DecodeArgs {
   const float2* rope = nullptr;     // table whose row `pos` holds this token's (cos, sin)
   const void* decay_bias = nullptr; // (D) dt
   const float* bias = nullptr;      // (W) window bias, dt values as floats
-  const void* q_add = nullptr;      // optional (B, ld_qadd) cross-layer query in dt
+  const void* q_add = nullptr;      // optional (B*H, ld_qadd) cross-layer query in dt
   int64_t ld_qadd = 0;
   float thr = 0.0f, ent_scale = 0.0f, eps = 1e-5f;
-  const double* state = nullptr;    // (B, D) float64 before the step
-  double* state_out = nullptr;      // (B, D) float64 after the step (may equal state)
-  void* k_cache = nullptr;          // (B, W, R) cdt
-  void* v_cache = nullptr;          // (B, W, D) cdt
-  void* new_state = nullptr;        // optional (B, D) dt: the step's state (next layer's cross state)
-  // int8 codes (layout 1), scales and row sums of tanh(E) and C = E - S
+  const double* state = nullptr;    // (B, H, D) float64 before the step
+  double* state_out = nullptr;      // (B, H, D) float64 after the step (may equal state)
+  void* k_cache = nullptr;          // (B, W, H, R) cdt
+  void* v_cache = nullptr;          // (B, W, H, D) cdt
+  void* new_state = nullptr;        // optional (B, H, D) dt: the step's state (next layer's cross state)
+  // H > 1: tanh(E) and C in dt, element (b, h, d) at te_out[b*ld_out + h*D + d]
+  void* te_out = nullptr;
+  void* c_out = nullptr;
+  int64_t ld_out = 0;
+  // H == 1: int8 codes (layout 1), scales and row sums of tanh(E) and C = E - S
   int8_t* q_te = nullptr;
   float* s_te = nullptr;
   int32_t* rs_te = nullptr;
@@ -38,7 +48,7 @@ struct DecodeArgs {
   int64_t ldq = 0;
 };
 
-int64_t decode_lds_bytes(int64_t R, int64_t D);
+int64_t decode_lds_bytes(int64_t R, int64_t CW);
 int launch_decode_ent(const DecodeArgs& a, hipStream_t st);
 
 // Ring buffers after a prefill of L tokens: the last min(L, W) RoPE'd keys and states.

@@ -1,9 +1,14 @@
-// TESM_SISO one-token decode step and the decode caches written by a prefill.
+// TESM_SISO / TESMMIMO_Optimized one-token decode step and the decode caches written by a prefill.
 //
-// Reference semantics (tesm_ssm/modules/tesm.py):
-//   decode step      _forward_incremental, tesm.py:1274-1400
+// Reference semantics (tesm_ssm/modules/tesm.py, tesm_mimo.py):
+//   decode step      _forward_incremental, tesm.py:1274-1400; MIMO per head, tesm_mimo.py:753-912
 //   prefill caches   TESM_SISO.forward, tesm.py:1235-1253
-//   cache layout     allocate_inference_cache, tesm.py:620-670
+//   cache layout     allocate_inference_cache, tesm.py:620-670; MIMO (B, W, H, .), tesm_mimo.py:689-731
+//
+// One workgroup per (batch row, head); SISO is the one-head case.  The MIMO step has no rank
+// expansion (tesm_mimo.py:827-829): each head is a SISO step with its own decay-bias and window-bias
+// rows, and the per-token quantization of tanh(E) and C spans all heads, so that step writes E's
+// values and a row quantization follows.
 //
 // The ring buffers hold W keys (post-RoPE) and W states per batch row.  A step writes the new key and
 // state into slot `slot` and then reads the window in the reference's order: with a full ring
@@ -17,133 +22,273 @@ namespace tesm {
 
 namespace {
 
-constexpr int kDecMaxCPT = 8;  // channels per thread: d_state <= 2048
+constexpr int kDecMaxCPT = 8;  // channels per thread: at most 2048 channels per workgroup
 
-// STG: the window's ring rows are copied to LDS at the start (keys at pitch R + 1 so the per-window
-// dot products of one wave hit distinct banks), so their latency overlaps the RoPE and the state
-// update instead of following them.
-template <int DT, int CDT, bool STG>
+// Four consecutive ring values at p[i .. i+3] (16-byte aligned for f32, 8-byte for bf16).
+template <int CDT>
+__device__ __forceinline__ void ld4v(const void* p, int64_t i, float (&v)[4]) {
+  if constexpr (CDT == kBF16) {
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xffff0000u);
+  } else {
+    const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  }
+}
+
+// Workgroup (b, h, z) owns channels [z*chunk, z*chunk + chunk) of head h of batch row b.  Every
+// workgroup of a head computes the same query, key, window scores and weights (the key ring is
+// read once per chunk); the state update, ring write of the state, mix and outputs are per channel.
+// The key goes into the ring from chunk 0 only.  Reads of the ring skip this step's slot, whose
+// fresh key / state come from LDS, so the ring writes of other workgroups never race a read.
+// Window keys are loaded four windows at a time; ring slots and offsets are formed in 32-bit
+// arithmetic.  CPT: channels per thread.  With CPT = 1 (chunks of at most 256 channels) lane l of
+// wave v holds channels 4l .. 4l+3 of the chunk at window positions v, v+4, .. (vector loads
+// requested at the start, so they overlap the RoPE, state update and scores), and the four waves'
+// partial mixes are added in a fixed order; with CPT = kDecMaxCPT (up to 2048 channels) each thread
+// sums its channels' positions in order, four positions' loads at a time.  NI: rank elements per
+// lane and half (ent_rank <= 128 * NI).
+// FUSE: one head and one chunk (SISO): the int8 codes of tanh(E) and C are formed here; otherwise
+// tanh(E) and C are written in dt to te_out / c_out (row b, columns h*D + c).
+template <int DT, int CDT, bool FUSE, int CPT, int NI>
 __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_dec[];
-  const int R = static_cast<int>(a.R), D = static_cast<int>(a.D), W = static_cast<int>(a.W);
+  const int R = static_cast<int>(a.R), W = static_cast<int>(a.W), CW = static_cast<int>(a.chunk);
+  const int D = static_cast<int>(a.D);
   const int half = R / 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x, h = blockIdx.y, H = a.H;
+  const int c0 = static_cast<int>(blockIdx.z) * CW;
+  const int cn = min(CW, D - c0);  // channels of this workgroup (>= 1)
   float* qv = lds_dec;       // R   RoPE'd query (+ cross query)
   float* kv = qv + R;        // R   RoPE'd key of this step
-  float* nv = kv + R;        // D   new state in the layer dtype
-  float* wn = nv + D;        // 64  ternary / norm per padded window position
+  float* nv = kv + R;        // CW  new state of this chunk in the layer dtype
+  float* wn = nv + CW;       // 64  ternary / norm per padded window position
   float* red = wn + 64;      // 16  block reductions
   int* redi = reinterpret_cast<int*>(red + 8);
-  float* kw = red + 16;      // STG: W x (R + 1) ring keys in the layer dtype
-  float* vw = kw + (STG ? W * (R + 1) : 0);  // STG: W x D ring states in the layer dtype
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t b = blockIdx.x;
+  float* mixp = red + 16;    // 4 x CW  per-wave partial mixes (CPT = 1)
+  const int64_t bh = b * H + h;  // row of the (B, H, .) state, cross query and new state
   const int es = DT == kBF16 ? 2 : 4;
   const char* prow = static_cast<const char*>(a.proj) + b * a.ld_proj * es;
-  const int64_t slot = a.slot;
-  if constexpr (STG) {  // this step's slot is read too but never used: its fresh key / state come from kv / nv
-    for (int i = tid; i < W * R; i += 256) {
-      const int s = i / R, r = i - s * R;
-      kw[s * (R + 1) + r] = rnd<DT>(ld<CDT>(a.k_cache, (b * a.W + s) * a.R + r));
+  const int64_t o_q = a.o_q + h * a.R, o_k = a.o_k + h * a.R;
+  const int64_t o_sv = a.o_sv + h * a.D, o_decay = a.o_decay + h * a.D, o_write = a.o_write + h * a.D;
+  const float* wbias = a.bias + h * a.W;
+  // ring element (b, s, h, i): keys at kbase + s*kstep + i, states at vbase + s*vstep + i
+  const int64_t kbase = (b * a.W * H + h) * a.R, kstep = H * a.R;
+  const int64_t vbase = (b * a.W * H + h) * a.D + c0, vstep = H * a.D;
+  const int slot = static_cast<int>(a.slot);
+  const int wlo = static_cast<int>(W - a.valid);  // padded positions below wlo hold no entry
+  const bool full = a.full != 0;
+  // ring slot read at padded window position w (w in [wlo, W)), in the reference's order
+  auto slot_of = [&](int w) -> int {
+    if (!full) return w - wlo;
+    const int s = slot + w;
+    return s >= W ? s - W : s;
+  };
+
+  // 0. (CPT = 1) ring states of this thread's four channels at its window positions
+  const int j4 = 4 * lane;
+  float xs[CPT == 1 ? 16 : 1][4];
+  if constexpr (CPT == 1) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {  // W <= 64
+      const int w = wave + 4 * u;
+      const bool on = w < W && w >= wlo;
+      const int s = on ? slot_of(w) : slot;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xs[u][r] = 0.0f;
+      if (on && s != slot) {
+        const int64_t vo = vbase + s * vstep + j4;
+        if (a.vec4 && j4 + 3 < cn) {
+          float v4[4];
+          ld4v<CDT>(a.v_cache, vo, v4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[u][r] = rnd<DT>(v4[r]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (j4 + r < cn) xs[u][r] = rnd<DT>(ld<CDT>(a.v_cache, vo + r));
+        }
+      }
     }
-    for (int i = tid; i < W * D; i += 256) vw[i] = rnd<DT>(ld<CDT>(a.v_cache, b * a.W * a.D + i));
   }
 
   // 1. RoPE at position pos (tesm.py:1311-1313), cross query (1302-1305), key into the ring
   for (int i = tid; i < half; i += 256) {
     const float2 cs = a.rope[a.pos * half + i];
     float q1, q2, k1, k2;
-    rope_pair<DT>(ld<DT>(prow, a.o_q + i), ld<DT>(prow, a.o_q + half + i), cs, q1, q2);
-    rope_pair<DT>(ld<DT>(prow, a.o_k + i), ld<DT>(prow, a.o_k + half + i), cs, k1, k2);
+    rope_pair<DT>(ld<DT>(prow, o_q + i), ld<DT>(prow, o_q + half + i), cs, q1, q2);
+    rope_pair<DT>(ld<DT>(prow, o_k + i), ld<DT>(prow, o_k + half + i), cs, k1, k2);
     if (a.q_add) {
-      q1 = rnd<DT>(q1 + ld<DT>(a.q_add, b * a.ld_qadd + i));
-      q2 = rnd<DT>(q2 + ld<DT>(a.q_add, b * a.ld_qadd + half + i));
+      q1 = rnd<DT>(q1 + ld<DT>(a.q_add, bh * a.ld_qadd + i));
+      q2 = rnd<DT>(q2 + ld<DT>(a.q_add, bh * a.ld_qadd + half + i));
     }
     qv[i] = q1;
     qv[half + i] = q2;
     kv[i] = k1;
     kv[half + i] = k2;
-    const int64_t ko = (b * a.W + slot) * a.R;
-    st<CDT>(a.k_cache, ko + i, k1);
-    st<CDT>(a.k_cache, ko + half + i, k2);
+    if (blockIdx.z == 0) {
+      const int64_t ko = kbase + slot * kstep;
+      st<CDT>(a.k_cache, ko + i, k1);
+      st<CDT>(a.k_cache, ko + half + i, k2);
+    }
   }
   // 2. gates and the float64 state update (tesm.py:1315-1322): new = decay * h + write * tanh(sv)
-  for (int c = tid; c < D; c += 256) {
-    const float d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(prow, a.o_decay + c) + ld<DT>(a.decay_bias, c))));
-    const float wr = rnd<DT>(sigmoidf_(ld<DT>(prow, a.o_write + c)));
-    const float sv = rnd<DT>(tanhf_(ld<DT>(prow, a.o_sv + c)));
-    const double n64 = static_cast<double>(d) * a.state[b * a.D + c] + static_cast<double>(wr) * static_cast<double>(sv);
-    a.state_out[b * a.D + c] = n64;
+  for (int j = tid; j < cn; j += 256) {
+    const int c = c0 + j;
+    const float d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(prow, o_decay + c) + ld<DT>(a.decay_bias, h * a.D + c))));
+    const float wr = rnd<DT>(sigmoidf_(ld<DT>(prow, o_write + c)));
+    const float sv = rnd<DT>(tanhf_(ld<DT>(prow, o_sv + c)));
+    const double n64 = static_cast<double>(d) * a.state[bh * a.D + c] + static_cast<double>(wr) * static_cast<double>(sv);
+    a.state_out[bh * a.D + c] = n64;
     const float nf = rnd<DT>(static_cast<float>(n64));  // torch: float64 -> float -> dtype
-    nv[c] = nf;
-    st<CDT>(a.v_cache, (b * a.W + slot) * a.D + c, nf);
-    if (a.new_state) st<DT>(a.new_state, b * a.D + c, nf);
+    nv[j] = nf;
+    st<CDT>(a.v_cache, vbase + slot * vstep + j, nf);
+    if (a.new_state) st<DT>(a.new_state, bh * a.D + c, nf);
   }
   __syncthreads();
 
-  // 3. window scores, strict ternary, count normalisation (tesm.py:1338-1372); one wave
-  const int64_t valid = a.valid;
-  if (wave == 0) {
-    const int w = lane;
-    float tern = 0.0f;
-    if (w < W && w >= W - valid) {
-      const int64_t e = w - (W - valid);
-      const int64_t s = a.full ? (slot + w) % a.W : e;
-      float dot = 0.0f;
-      for (int i = 0; i < half; ++i) {
-        float k1, k2;
-        if (s == slot) {
-          k1 = kv[i];
-          k2 = kv[half + i];
-        } else if constexpr (STG) {
-          k1 = kw[s * (R + 1) + i];
-          k2 = kw[s * (R + 1) + half + i];
-        } else {
-          const int64_t ko = (b * a.W + s) * a.R;
-          k1 = rnd<DT>(ld<CDT>(a.k_cache, ko + i));
-          k2 = rnd<DT>(ld<CDT>(a.k_cache, ko + half + i));
+  // 3. window scores (tesm.py:1338-1357): wave v scores windows v, v+4, ..; its lanes split the rank
+  const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
+  for (int j0 = 0; j0 < 16; j0 += 4) {  // W <= 64: at most 16 windows per wave
+    if (wave + 4 * j0 >= W) break;       // uniform in the wave
+    float kk[4][2 * NI];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int w = wave + 4 * (j0 + jj);
+      const bool on = w < W && w >= wlo;
+      const int s = on ? slot_of(w) : slot;
+#pragma unroll
+      for (int t = 0; t < NI; ++t) {
+        const int i = lane + 64 * t;
+        float k1 = 0.0f, k2 = 0.0f;
+        if (on && i < half) {
+          if (s == slot) {
+            k1 = kv[i];
+            k2 = kv[half + i];
+          } else {
+            const int64_t ko = kbase + s * kstep;
+            k1 = rnd<DT>(ld<CDT>(a.k_cache, ko + i));
+            k2 = rnd<DT>(ld<CDT>(a.k_cache, ko + half + i));
+          }
         }
-        dot += qv[i] * k1;
-        dot += qv[half + i] * k2;
+        kk[jj][2 * t] = k1;
+        kk[jj][2 * t + 1] = k2;
       }
-      const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
-      float sc = rnd<DT>(rnd<DT>(dot) / sq);
-      sc = rnd<DT>(sc + a.bias[w]);
-      tern = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
     }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int w = wave + 4 * (j0 + jj);
+      float dot = 0.0f;
+#pragma unroll
+      for (int t = 0; t < NI; ++t) {
+        const int i = lane + 64 * t;
+        if (i < half) {
+          dot += qv[i] * kk[jj][2 * t];
+          dot += qv[half + i] * kk[jj][2 * t + 1];
+        }
+      }
+      dot = wave_sum_f<64>(dot);
+      if (lane == 0 && w < W) {
+        if (w < wlo) {
+          wn[w] = 0.0f;
+        } else {
+          float sc = rnd<DT>(rnd<DT>(dot) / sq);
+          sc = rnd<DT>(sc + wbias[w]);
+          wn[w] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);  // strict ternary (1359-1368)
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {  // count normalisation (1370-1372)
+    const float tern = lane < W ? wn[lane] : 0.0f;
     const float n = fmaxf(wave_sum_f<64>(fabsf(tern)), 1.0f);
-    if (w < W) wn[w] = rnd<DT>(tern / n);
+    if (lane < W) wn[lane] = rnd<DT>(tern / n);
   }
   __syncthreads();
 
   // 4. mix, entangled state, tanh(E) and C = E - S (tesm.py:1373-1390)
-  float tv[kDecMaxCPT], cv[kDecMaxCPT];
+  float acc[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) acc[k] = 0.0f;
+  if constexpr (CPT == 1) {
+    float pm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int w = wave + 4 * u;
+      if (w >= W) break;  // uniform in the wave
+      if (w < wlo) continue;
+      const bool fresh = slot_of(w) == slot;
+      const float wv = wn[w];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = fresh ? (j4 + r < cn ? nv[j4 + r] : 0.0f) : xs[u][r];
+        pm[r] += wv * x;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (j4 + r < cn) mixp[wave * CW + j4 + r] = pm[r];
+    __syncthreads();
+    if (tid < cn) acc[0] = ((mixp[tid] + mixp[CW + tid]) + mixp[2 * CW + tid]) + mixp[3 * CW + tid];
+  } else {
+    constexpr int kWB = 4;
+    for (int w0 = wlo; w0 < W; w0 += kWB) {
+      float xb[kWB][CPT];
+#pragma unroll
+      for (int u = 0; u < kWB; ++u) {
+        const int w = w0 + u;
+        const int s = w < W ? slot_of(w) : slot;
+        const int64_t vo = vbase + s * vstep;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+          const int j = tid + 256 * k;
+          float x = 0.0f;
+          if (w < W && j < cn) x = s == slot ? nv[j] : rnd<DT>(ld<CDT>(a.v_cache, vo + j));
+          xb[u][k] = x;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kWB; ++u) {
+        if (w0 + u >= W) break;
+        const float wv = wn[w0 + u];
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) acc[k] += wv * xb[u][k];
+      }
+    }
+  }
+  float tv[CPT], cv[CPT];
   float mx_t = 0.0f, mx_c = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kDecMaxCPT; ++k) {
-    const int c = tid + 256 * k;
+  for (int k = 0; k < CPT; ++k) {
+    const int j = tid + 256 * k;
     tv[k] = 0.0f;
     cv[k] = 0.0f;
-    if (c >= D) continue;
-    float acc = 0.0f;
-    for (int w = static_cast<int>(W - valid); w < W; ++w) {
-      const int64_t e = w - (W - valid);
-      const int64_t s = a.full ? (slot + w) % a.W : e;
-      float x;
-      if (s == slot)
-        x = nv[c];
-      else if constexpr (STG)
-        x = vw[s * D + c];
-      else
-        x = rnd<DT>(ld<CDT>(a.v_cache, (b * a.W + s) * a.D + c));
-      acc += wn[w] * x;
-    }
-    const float avg = rnd<DT>(acc);
-    const float sv = nv[c];
+    if (j >= cn) continue;
+    const float avg = rnd<DT>(acc[k]);
+    const float sv = nv[j];
     const float ev = rnd<DT>(sv + rnd<DT>(a.ent_scale * rnd<DT>(avg - sv)));
     cv[k] = rnd<DT>(ev - sv);
     tv[k] = rnd<DT>(tanhf_(ev));
     mx_t = fmaxf(mx_t, fabsf(tv[k]));
     mx_c = fmaxf(mx_c, fabsf(cv[k]));
+  }
+  if constexpr (!FUSE) {  // MIMO: the row quantization spans the heads
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int j = tid + 256 * k;
+      if (j >= cn) continue;
+      st<DT>(a.te_out, b * a.ld_out + h * a.D + c0 + j, tv[k]);
+      st<DT>(a.c_out, b * a.ld_out + h * a.D + c0 + j, cv[k]);
+    }
+    return;
   }
   // 5. per-token int8 codes of tanh(E) and C for state_proj / ent_proj (tesm.py:206-209), layout 1
   mx_t = wave_max<64>(mx_t);
@@ -161,7 +306,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   int8_t* qt = a.q_te + b * a.ldq;
   int8_t* qc = a.q_c + b * a.ldq;
 #pragma unroll
-  for (int k = 0; k < kDecMaxCPT; ++k) {
+  for (int k = 0; k < CPT; ++k) {
     const int c = tid + 256 * k;
     if (c >= D) continue;
     const int c1 = act_code<DT>(tv[k], sc_t), c2 = act_code<DT>(cv[k], sc_c);
@@ -220,36 +365,68 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(CacheFillArgs a) {
 
 }  // namespace
 
-int64_t decode_lds_bytes(int64_t R, int64_t D) { return (2 * R + D + 64 + 16) * static_cast<int64_t>(sizeof(float)); }
-
-namespace {
-constexpr int64_t kDecStageMax = 64 * 1024;  // LDS bytes up to which the ring rows are staged
-int64_t decode_stage_bytes(int64_t R, int64_t D, int64_t W) {
-  return decode_lds_bytes(R, D) + (W * (R + 1) + W * D) * static_cast<int64_t>(sizeof(float));
-}
-}  // namespace
+int64_t decode_lds_bytes(int64_t R, int64_t CW) { return (2 * R + 5 * CW + 64 + 16) * static_cast<int64_t>(sizeof(float)); }
 
 int launch_decode_ent(const DecodeArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "decode: dtype must be 0 or 1");
   TESM_REQUIRE(a.cdt == kF32 || a.cdt == kBF16, kErrInvalidArg, "decode: cache dtype must be 0 or 1");
   TESM_REQUIRE(a.B >= 1 && a.R >= 2 && a.R % 2 == 0 && a.D >= 1, kErrInvalidArg, "decode: bad sizes");
-  TESM_REQUIRE(a.D <= 256 * kDecMaxCPT, kErrUnsupported, "decode: d_state must be <= 2048");
+  TESM_REQUIRE(a.R <= 512, kErrUnsupported, "decode: ent_rank must be <= 512");
   TESM_REQUIRE(a.W >= 1 && a.W <= 64, kErrUnsupported, "decode: window must be in [1, 64]");
   TESM_REQUIRE(a.valid >= 1 && a.valid <= a.W && a.slot >= 0 && a.slot < a.W, kErrInvalidArg,
                "decode: bad ring position");
-  TESM_REQUIRE(a.proj && a.rope && a.decay_bias && a.bias && a.state && a.state_out && a.k_cache && a.v_cache && a.q_te &&
-                   a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c,
+  TESM_REQUIRE(a.proj && a.rope && a.decay_bias && a.bias && a.state && a.state_out && a.k_cache && a.v_cache,
                kErrInvalidArg, "decode: null pointer");
-  TESM_REQUIRE(a.ldq >= a.D, kErrInvalidArg, "decode: ldq < d_state");
-  const bool stg = decode_stage_bytes(a.R, a.D, a.W) <= kDecStageMax;
-  const size_t lds = static_cast<size_t>(stg ? decode_stage_bytes(a.R, a.D, a.W) : decode_lds_bytes(a.R, a.D));
-  const dim3 grid(static_cast<unsigned>(a.B));
+  TESM_REQUIRE(a.H >= 1 && a.H <= 65535, kErrInvalidArg, "decode: bad head count");
+  const bool fuse = a.q_te != nullptr;
+  if (fuse) {
+    TESM_REQUIRE(a.H == 1, kErrInvalidArg, "decode: fused codes need one head");
+    TESM_REQUIRE(a.D <= 256 * kDecMaxCPT, kErrUnsupported, "decode: d_state must be <= 2048");
+    TESM_REQUIRE(a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c, kErrInvalidArg, "decode: null pointer");
+    TESM_REQUIRE(a.ldq >= a.D, kErrInvalidArg, "decode: ldq < d_state");
+  } else {
+    TESM_REQUIRE(a.te_out && a.c_out && a.ld_out >= a.H * a.D, kErrInvalidArg,
+                 "decode: need te_out / c_out with ld_out >= n_heads * d_state");
+  }
+  // channel chunks: one per workgroup for the fused (one-head) step; otherwise enough chunks of at
+  // least 128 channels for about 1024 workgroups
+  int64_t nz = 1;
+  if (!fuse) {
+    const int64_t want = (1024 + a.B * a.H - 1) / (a.B * a.H);
+    nz = std::max<int64_t>(1, std::min<int64_t>(want, (a.D + 127) / 128));
+  }
+  int64_t cw = (a.D + nz - 1) / nz;
+  nz = (a.D + cw - 1) / cw;  // every chunk non-empty
+  TESM_REQUIRE(cw <= 256 * kDecMaxCPT && nz <= 65535, kErrUnsupported, "decode: d_state too large");
+  DecodeArgs k = a;
+  k.chunk = cw;
+  k.vec4 = a.D % 4 == 0 && cw % 4 == 0 && aligned(a.v_cache, a.cdt == kBF16 ? 8 : 16);
+  const size_t lds = static_cast<size_t>(decode_lds_bytes(a.R, cw));
+  const dim3 grid(static_cast<unsigned>(a.B), static_cast<unsigned>(a.H), static_cast<unsigned>(nz));
+  const bool cpt1 = cw <= 256;
+  const int ni = a.R <= 128 ? 1 : (a.R <= 256 ? 2 : 4);
+#define TESM_DEC_LAUNCH3(DT_, CDT_, FUSE_, CPT_)                                        \
+  do {                                                                                 \
+    if (ni == 1)                                                                       \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 1><<<grid, 256, lds, st>>>(k);         \
+    else if (ni == 2)                                                                  \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 2><<<grid, 256, lds, st>>>(k);         \
+    else                                                                               \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 4><<<grid, 256, lds, st>>>(k);         \
+  } while (0)
+#define TESM_DEC_LAUNCH2(DT_, CDT_, FUSE_)                                             \
+  do {                                                                                 \
+    if (cpt1)                                                                          \
+      TESM_DEC_LAUNCH3(DT_, CDT_, FUSE_, 1);                                           \
+    else                                                                               \
+      TESM_DEC_LAUNCH3(DT_, CDT_, FUSE_, kDecMaxCPT);                                  \
+  } while (0)
 #define TESM_DEC_LAUNCH(DT_, CDT_)                                                     \
   do {                                                                                 \
-    if (stg)                                                                           \
-      decode_ent_kernel<DT_, CDT_, true><<<grid, 256, lds, st>>>(a);                   \
+    if (fuse)                                                                          \
+      TESM_DEC_LAUNCH2(DT_, CDT_, true);                                               \
     else                                                                               \
-      decode_ent_kernel<DT_, CDT_, false><<<grid, 256, lds, st>>>(a);                  \
+      TESM_DEC_LAUNCH2(DT_, CDT_, false);                                              \
   } while (0)
   if (a.dt == kBF16) {
     if (a.cdt == kBF16)
@@ -263,6 +440,8 @@ int launch_decode_ent(const DecodeArgs& a, hipStream_t st) {
       TESM_DEC_LAUNCH(kF32, kF32);
   }
 #undef TESM_DEC_LAUNCH
+#undef TESM_DEC_LAUNCH2
+#undef TESM_DEC_LAUNCH3
   return check_launch("decode step");
 }
 

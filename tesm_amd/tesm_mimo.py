@@ -22,7 +22,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib, hip_ops
-from .bitlinear import BitLinear, backend_error, check_hip_call
+from .bitlinear import BitLinear, check_hip_call
 from .tesm import TESM_SISO, workspace
 
 
@@ -131,8 +131,7 @@ class TESMMIMO_Optimized(TESM_SISO):
         if inference_params is not None and L == 1:
             cache = inference_params.get("state_cache")
             if cache is not None and "state" in cache:
-                raise backend_error(self.kernel_backend, "TESMMIMO decode",
-                                    "the MIMO decode step is not implemented by the hip backend yet")
+                return self._forward_incremental(u, inference_params, cross_layer_state)
         cache = None
         if inference_params is not None:
             cache = inference_params.get("state_cache")
@@ -227,6 +226,124 @@ class TESMMIMO_Optimized(TESM_SISO):
             "cache_idx": 0,
             "cache_filled": False,
         }
+
+    def _check_mimo_cache(self, kc, vc, B, dev):
+        H = self.n_heads
+        W = kc.shape[1] if kc.dim() == 4 else -1
+        ok = (kc.dim() == 4 and vc.dim() == 4 and tuple(kc.shape) == (B, W, H, self.ent_rank)
+              and tuple(vc.shape) == (B, W, H, self.d_state) and kc.dtype == vc.dtype
+              and kc.dtype in (torch.float32, torch.bfloat16) and kc.is_contiguous() and vc.is_contiguous()
+              and kc.device == dev and vc.device == dev and 1 <= W <= 64)
+        if not ok:
+            raise RuntimeError("TESMMIMO hip decode: the inference cache must hold contiguous (B, W, n_heads, ent_rank) "
+                               "and (B, W, n_heads, d_state) float32 or bfloat16 ring buffers on the layer's device, "
+                               "W <= 64")
+
+    def _mimo_step_plan(self, B, dt, dev, cdt, W, cross):
+        """The decode descriptor's fields that stay fixed from step to step, rebuilt when a shape, a
+        dtype, a weight or a bias changes."""
+        lins = (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj)
+        db, lb = self.decay_bias, self.local_entanglement_bias
+        lb_key = (lb._version, lb.data_ptr()) if lb is not None else None
+        key = (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
+               db.data_ptr(), db.dtype, lb_key, tuple(p.cache_key() for p in lins))
+        plan = self.__dict__.get("_mimo_decode_plan")
+        if plan is not None and plan[0] == key:
+            return plan[1]
+        for p in lins[:4 + int(cross)]:
+            if p.weight.dtype != dt:
+                raise RuntimeError(f"expected both operands to have the same dtype, got {dt} and {p.weight.dtype}")
+        decay_bias = self._decay_bias_dt(dt).contiguous()
+        if lb is not None:
+            local_bias = self._local_bias_f32(dt)
+        else:
+            # global layers decode over their one-slot rings with no bias (tesm_mimo.py:698, 862-866)
+            local_bias = torch.zeros(self.n_heads, W, dtype=torch.float32, device=dev)
+        hip_ops.require_device(decay_bias, local_bias)
+        if decay_bias.device != dev or local_bias.shape[-1] != W:
+            raise RuntimeError("TESMMIMO hip decode: the ring size must equal entanglement_window and the biases "
+                               "must live on the input's device")
+        desc = _lib.MimoStep()
+        desc.dt = hip_ops.dt_code(dt)
+        desc.cache_dt = hip_ops.dt_code(cdt)
+        desc.B, desc.d_model, desc.d_state, desc.n_heads = B, self.d_model, self.d_state, self.n_heads
+        desc.ent_rank, desc.window = self.ent_rank, W
+        desc.bit_eps = self.in_proj.bit_eps
+        desc.thr = hip_ops.round_dtype(self.entanglement_threshold, dt)
+        desc.ent_scale = float(self.entanglement_scale)
+        desc.in_proj = self.in_proj.linear_desc()
+        desc.state_proj = self.state_proj.linear_desc()
+        desc.ent_proj = self.ent_proj.linear_desc()
+        desc.out_proj = self.out_proj.linear_desc()
+        if cross:
+            desc.cross_q_proj = self.cross_layer_q_proj.linear_desc()
+        desc.decay_bias = decay_bias.data_ptr()
+        desc.local_bias = local_bias.data_ptr()
+        keep = (decay_bias, local_bias) + tuple(p.packed_weight() for p in lins[:4 + int(cross)])
+        nbytes = int(_lib.load().tesm_hip_mimo_decode_ws_bytes(ctypes.byref(desc)))
+        self.__dict__["_mimo_decode_plan"] = (key, (desc, nbytes, keep))
+        return desc, nbytes, keep
+
+    def _forward_incremental(self, u, inference_params, cross_layer_state=None):
+        """One decode step per sequence (tesm_mimo.py:753-912); returns ``(y (B, 1, d_model), state f64
+        (B, n_heads, d_state))``.  Like the reference's step it runs each head as a single-rank layer (no
+        mimo_x / mimo_o expansion)."""
+        lib = _lib.load()
+        cache = inference_params["state_cache"]
+        dt = u.dtype
+        B, _, dm = u.shape
+        H, D = self.n_heads, self.d_state
+        dev = u.device
+        kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
+        self._check_mimo_cache(kc, vc, B, dev)
+        W = kc.shape[1]
+        if self.entanglement_window > 0 and W != self.entanglement_window:
+            raise RuntimeError(f"TESMMIMO hip decode: ring of {W} slots for entanglement_window "
+                               f"{self.entanglement_window}")
+        state = cache["state"]
+        if state.dtype != torch.float64 or tuple(state.shape) != (B, H, D) or state.device != dev:
+            raise RuntimeError("TESMMIMO hip decode: cache['state'] must be a (B, n_heads, d_state) float64 tensor on "
+                               "the layer's device")
+        state = state.contiguous()
+        pos = int(cache["seq_pos"])
+        slot = int(cache.get("cache_idx", 0))
+        u2 = u.reshape(B, dm)
+        if u2.stride(1) != 1:
+            u2 = u2.contiguous()
+        cs = None
+        if cross_layer_state is not None:
+            if cross_layer_state.dim() != 3:
+                # the reference's step broadcasts a 4-D state into a 5-D query and its einsum raises
+                raise RuntimeError("TESMMIMO decode: cross_layer_state must be (B, n_heads, d_state)")
+            cs = cross_layer_state.reshape(B, H, D).to(dt).contiguous()
+            if cs.device != dev:
+                raise RuntimeError(f"hip backend ops need all tensors on one device, got {cs.device} and {dev}")
+        desc, nbytes, _ = self._mimo_step_plan(B, dt, dev, kc.dtype, W, cs is not None)
+        y = torch.empty((B, 1, dm), dtype=dt, device=dev)
+        state_out = torch.empty_like(state)
+        new = torch.empty((B, H, D), dtype=dt, device=dev)
+        rope = self.rope_table(pos + 1, dt, dev)
+        desc.seq_pos, desc.cache_idx = pos, slot
+        desc.u, desc.ld_u = u2.data_ptr(), u2.stride(0)
+        desc.cross_state = cs.data_ptr() if cs is not None else None
+        desc.rope = rope.data_ptr()
+        desc.state, desc.state_out = state.data_ptr(), state_out.data_ptr()
+        desc.k_cache, desc.v_cache = kc.data_ptr(), vc.data_ptr()
+        desc.y = y.data_ptr()
+        desc.new_state = new.data_ptr()
+        stream = torch.cuda.current_stream(dev)
+        with torch.cuda.device(dev):
+            ws = workspace(dev, nbytes, stream)
+            rc = lib.tesm_hip_mimo_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                          ctypes.c_void_p(stream.cuda_stream))
+        _lib.check(rc)
+        cache["cache_idx"] = (slot + 1) % W
+        cache["state"] = state_out
+        cache["seq_pos"] = pos + 1
+        self._last_cross_layer_state = new
+        self._last_scan_state_f64 = state_out
+        self.last_entanglement_map = None
+        return y, state_out
 
     def _mimo_cache_buffers(self, cache, B, L, dev):
         """With L >= W the reference replaces the rings by new float32 tensors, otherwise it writes the

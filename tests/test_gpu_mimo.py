@@ -93,14 +93,103 @@ def test_mimo_prefill_fills_caches_like_reference(L):
         np.testing.assert_allclose(to_np(cm[key]), to_np(cr[key]), rtol=1e-4, atol=1e-5, err_msg=key)
 
 
-def test_mimo_decode_step_is_refused():
-    meta = dict(seed=9, dm=64, D=16, H=2, Rm=2, R=8, W=8, thr=0.05, decay_bias=2.0)
-    m = build(TESMMIMO_Optimized, meta).to(DEV)
+def _decode_run(m, u, cs, P, steps, B):
+    """Prefill P tokens with a cache, then `steps` single-token steps (tesm_mimo.py:753-912)."""
+    cache = m.allocate_inference_cache(B, 64)
+    ip = {"state_cache": cache}
+    outs = {}
+    with torch.no_grad():
+        if P:
+            outs["prefill_y"] = m(u[:, :P], inference_params=ip)[0]
+        for s in range(steps):
+            t = P + s
+            y, st = m(u[:, t:t + 1], inference_params=ip, cross_layer_state=cs[:, t] if cs is not None else None)
+            outs[f"step{s}_y"] = y.clone()
+            outs[f"step{s}_state"] = st.clone()
+            outs[f"step{s}_kcache"] = cache["ent_k_cache"].clone()
+            outs[f"step{s}_vcache"] = cache["ent_v_cache"].clone()
+            outs[f"step{s}_cache_idx"] = cache["cache_idx"]
+            outs[f"step{s}_seq_pos"] = cache["seq_pos"]
+            outs[f"step{s}_cross"] = m._last_cross_layer_state.clone()
+    return outs
+
+
+def test_mimo_decode_vs_reference_fixture():
+    g, meta = load_golden("mimo_decode_f32"), golden_meta("mimo_decode_f32")
+    torch.manual_seed(meta["seed"])
+    m = TESMMIMO_Optimized(d_model=meta["dm"], d_state=meta["D"], n_heads=meta["H"], mimo_rank=meta["Rm"],
+                           ent_rank=meta["R"], entanglement_window=meta["W"], entanglement_threshold=0.05,
+                           max_seq_len=64).eval()
+    sd = m.state_dict()
+    for k, v in g.items():
+        if k.startswith("param/"):
+            assert np.array_equal(sd[k[6:]].float().numpy(), v), k
+    m = m.to(DEV)
+    B, P = meta["B"], meta["prefill"]
+    outs = _decode_run(m, torch.from_numpy(g["u"]).to(DEV), None, P, meta["steps"], B)
+    assert normwise(to_np(outs["prefill_y"]), g["prefill_y"]) <= TOL[torch.float32]
+    for s in range(meta["steps"]):
+        assert outs[f"step{s}_y"].shape == (B, 1, meta["dm"])
+        flip_aware(to_np(outs[f"step{s}_y"]).reshape(B, -1), g[f"step{s}_y"].reshape(B, -1), row_tol=1e-4,
+                   max_flip_frac=0.5, bound=2e-2)
+        np.testing.assert_allclose(outs[f"step{s}_state"].cpu().numpy(), g[f"step{s}_state"], rtol=1e-5, atol=1e-6)
+
+
+def _mimo_dec(cls, seed, W, dtype):
+    torch.manual_seed(seed)
+    m = cls(d_model=96, d_state=24, n_heads=3, mimo_rank=2, ent_rank=8, entanglement_window=W,
+            entanglement_threshold=0.05, entanglement_scale=0.3, decay_init_bias=1.0, max_seq_len=64).eval()
+    with torch.no_grad():
+        gg = torch.Generator().manual_seed(seed + 7)
+        m.mimo_x.copy_(torch.rand(m.mimo_x.shape, generator=gg) + 0.25)
+        m.mimo_o.copy_(torch.rand(m.mimo_o.shape, generator=gg) + 0.25)
+        if m.local_entanglement_bias is not None:
+            m.local_entanglement_bias.copy_(torch.randn(m.local_entanglement_bias.shape, generator=gg) * 0.3)
+    return m.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("P,steps,W,cross", [(12, 6, 8, False), (3, 9, 8, True), (0, 11, 4, False),
+                                             (40, 5, 16, True), (10, 5, 0, True)])
+def test_mimo_decode_random_vs_oracle(dtype, P, steps, W, cross):
+    """Per-head steps with the heads' own decay / window-bias rows, the (B, W, H, .) rings in the
+    reference's read order, cross-layer queries per head; W = 0 is the global layer's one-slot ring."""
+    B, H, D = 4, 3, 24
+    ref = _mimo_dec(ot.TESMMIMO_Optimized, 31 + P + W, W, dtype)
+    m = _mimo_dec(TESMMIMO_Optimized, 31 + P + W, W, dtype).to(DEV)
+    gen = torch.Generator().manual_seed(5 + P)
+    u = torch.randn(B, P + steps, 96, generator=gen).to(dtype)
+    cs = torch.randn(B, P + steps, H, D, generator=gen).to(dtype) if cross else None
+    want = _decode_run(ref, u, cs, P, steps, B)
+    got = _decode_run(m, u.to(DEV), cs.to(DEV) if cs is not None else None, P, steps, B)
+    tol = TOL[dtype]
+    for s in range(steps):
+        a, b = to_np(got[f"step{s}_y"]).reshape(B, -1), to_np(want[f"step{s}_y"]).reshape(B, -1)
+        if dtype == torch.float32:
+            flip_aware(a, b, row_tol=1e-4, max_flip_frac=0.25, bound=2e-2)
+            np.testing.assert_allclose(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy(),
+                                       rtol=1e-4, atol=1e-5)
+        else:
+            flip_aware(a, b, row_tol=tol, max_flip_frac=0.5, bound=0.1)
+            assert normwise(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy()) <= tol
+        for k in ("kcache", "vcache", "cross"):
+            assert normwise(to_np(got[f"step{s}_{k}"]), to_np(want[f"step{s}_{k}"])) <= (
+                1e-5 if dtype == torch.float32 else tol), k
+        assert got[f"step{s}_state"].shape == (B, H, D) and got[f"step{s}_state"].dtype == torch.float64
+        assert got[f"step{s}_cache_idx"] == want[f"step{s}_cache_idx"]
+        assert got[f"step{s}_seq_pos"] == want[f"step{s}_seq_pos"]
+
+
+def test_mimo_decode_rejects_bad_inputs():
+    m = _mimo_dec(TESMMIMO_Optimized, 3, 8, torch.float32).to(DEV)
     cache = m.allocate_inference_cache(2, 64)
     with torch.no_grad():
-        m(torch.randn(2, 9, 64, device=DEV), inference_params={"state_cache": cache})
-        with pytest.raises(RuntimeError, match="kernel_backend"):
-            m(torch.randn(2, 1, 64, device=DEV), inference_params={"state_cache": cache})
+        with pytest.raises(RuntimeError, match="cross_layer_state"):
+            m(torch.randn(2, 1, 96, device=DEV), inference_params={"state_cache": cache},
+              cross_layer_state=torch.randn(2, 1, 3, 24, device=DEV))
+        cache["ent_k_cache"] = cache["ent_k_cache"][:, :, :, :4]
+        with pytest.raises(RuntimeError, match="inference cache"):
+            m(torch.randn(2, 1, 96, device=DEV), inference_params={"state_cache": cache})
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
