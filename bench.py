@@ -200,6 +200,37 @@ MIMO = dict(d_model=4096, d_state=2048, n_heads=4, mimo_rank=4, ent_rank=256, en
             entanglement_threshold=0.05, entanglement_scale=0.2, max_seq_len=32768)
 
 
+def measure_lm(torch, steps: int = 10):
+    """configs[0]'s model on the GPU: TESMLMHeadModel(TESMConfig.tiny()) from seed 0 (12 layers, d_model 768,
+    vocab 151936), batch 2 x 256 tokens, forward (embeddings, 12 blocks, norm, tied LM head) in float32
+    (configs[0]'s dtype) and bfloat16; random input ids."""
+    from tesm_amd import TESMConfig, TESMLMHeadModel
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = TESMConfig.tiny()
+    model = TESMLMHeadModel(cfg).eval().to(dev)
+    ids = torch.randint(0, cfg.vocab_size, (2, 256), generator=torch.Generator().manual_seed(0)).to(dev)
+    out = {"workload": "TESMLMHeadModel(tiny()) forward, B2 x L256 (configs[0]), random init seed 0"}
+    with torch.no_grad():
+        for name, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+            model = model.to(dt)
+            for _ in range(2):
+                model(ids)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                model(ids)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            out[name] = {"ms_per_forward": ms, "tokens_per_s": 512 / (ms * 1e-3)}
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_global(torch, steps: int = 10):
     """TESM_SISO with global causal entanglement (entanglement_window = 0, the next row after the
     local-window layer) at configs[3]'s dims, B4 x L2048 prefill, bf16: per-forward time."""
@@ -336,6 +367,7 @@ def main():
         decode = measure_decode(torch, m)
         mimo = None if args.no_mimo else measure_mimo(torch)
         glob = measure_global(torch)
+        lm = measure_lm(torch)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
         if args.only:
             print(json.dumps({"kernels": kernels}))
@@ -368,6 +400,7 @@ def main():
         "decode": decode,
         "mimo_layer": mimo,
         "global_layer": glob,
+        "lm_tiny": lm,
         "kernels": kernels,
     }
     if not args.no_cpu:

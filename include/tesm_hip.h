@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 6
+#define TESM_HIP_ABI_VERSION 7
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -339,6 +339,61 @@ typedef struct tesm_hip_mimo_step {
 
 int64_t tesm_hip_mimo_decode_ws_bytes(const tesm_hip_mimo_step* p);
 int tesm_hip_mimo_decode(const tesm_hip_mimo_step* p, void* ws, int64_t ws_bytes, void* stream);
+
+/* Residual add + RMSNorm of the TESM block (block.py:7-17, 27-31 and 38-41): with `residual` set,
+ * s = x + residual in the promoted dtype (float32 when either is float32); `residual_out` (may alias
+ * `residual`) receives s in residual_out_dt (float32 for residual_in_fp32); then
+ * y = RMSNorm(s.to(dt)) = x * rsqrt(mean(x^2) + eps) * weight, every op rounded to dt.  With `q` set
+ * the kernel also writes y's per-token int8 codes (tesm.py:206-209) in the product layout, as
+ * tesm_hip_quant_act_i8(layout 1) would, for a BitLinear that reads y; `y` itself is then optional.
+ * D <= 16384. */
+typedef struct tesm_hip_rmsnorm {
+  int dt;                     /* module dtype: x, weight, y */
+  int64_t M, D;
+  float eps;
+  const void* x;              /* (M, ld_x) */
+  int64_t ld_x;
+  const void* residual;       /* optional (M, ld_res) in residual_dt */
+  int residual_dt;
+  int64_t ld_res;
+  void* residual_out;         /* optional (M, ld_res_out) in residual_out_dt */
+  int residual_out_dt;
+  int64_t ld_res_out;
+  const void* weight;         /* (D) in dt */
+  void* y;                    /* optional (M, ld_y) in dt */
+  int64_t ld_y;
+  int8_t* q;                  /* optional (M, ldq) int8 codes of y, ldq >= tesm_hip_kpad(D) */
+  int64_t ldq;
+  float* s_x;                 /* (M) code scales (with q) */
+  int32_t* rowsum;            /* (M) code sums (with q) */
+  float bit_eps;
+} tesm_hip_rmsnorm;
+
+int tesm_hip_add_rmsnorm(const tesm_hip_rmsnorm* p, void* stream);
+
+/* FeedForward of the TESM block (mixer_seq_simple.py:25-67, eval): gate and up share the per-token
+ * int8 codes of x (the reference's grouped projection, :45-57: one quantized input against the
+ * concatenated gate / up weights, each with its own absmean scale); one pass computes both products
+ * and h = silu(gate) * up in the module dtype's op order; h is quantized per token and down_proj
+ * gives y.  x is either given in dt or as layout-1 codes (x_codes, x_scale, x_rowsum, e.g. from
+ * tesm_hip_add_rmsnorm). */
+typedef struct tesm_hip_ffn {
+  int dt;
+  int64_t M, d_model, d_inter;
+  float bit_eps;
+  const void* x;              /* (M, ld_x) in dt, or NULL with x_codes */
+  int64_t ld_x;
+  const int8_t* x_codes;      /* optional (M, ldq_x) layout-1 codes of x, ldq_x >= tesm_hip_kpad(d_model) */
+  int64_t ldq_x;
+  const float* x_scale;       /* (M) */
+  const int32_t* x_rowsum;    /* (M) */
+  tesm_hip_linear gate_proj, up_proj, down_proj;
+  void* y;                    /* (M, ld_y) in dt */
+  int64_t ld_y;
+} tesm_hip_ffn;
+
+int64_t tesm_hip_ffn_ws_bytes(const tesm_hip_ffn* p);
+int tesm_hip_ffn_forward(const tesm_hip_ffn* p, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -123,6 +123,35 @@ class MimoStep(ctypes.Structure):
     ]
 
 
+class RmsNorm(ctypes.Structure):
+    """``tesm_hip_rmsnorm``."""
+    _fields_ = [
+        ("dt", I32),
+        ("M", I64), ("D", I64),
+        ("eps", F32),
+        ("x", P), ("ld_x", I64),
+        ("residual", P), ("residual_dt", I32), ("ld_res", I64),
+        ("residual_out", P), ("residual_out_dt", I32), ("ld_res_out", I64),
+        ("weight", P),
+        ("y", P), ("ld_y", I64),
+        ("q", P), ("ldq", I64), ("s_x", P), ("rowsum", P),
+        ("bit_eps", F32),
+    ]
+
+
+class Ffn(ctypes.Structure):
+    """``tesm_hip_ffn``."""
+    _fields_ = [
+        ("dt", I32),
+        ("M", I64), ("d_model", I64), ("d_inter", I64),
+        ("bit_eps", F32),
+        ("x", P), ("ld_x", I64),
+        ("x_codes", P), ("ldq_x", I64), ("x_scale", P), ("x_rowsum", P),
+        ("gate_proj", Linear), ("up_proj", Linear), ("down_proj", Linear),
+        ("y", P), ("ld_y", I64),
+    ]
+
+
 _SIGNATURES = {
     "tesm_hip_abi_version": ([], I32),
     "tesm_hip_last_error": ([], ctypes.c_char_p),
@@ -147,6 +176,9 @@ _SIGNATURES = {
     "tesm_hip_siso_decode": ([ctypes.POINTER(SisoStep), P, I64, P], I32),
     "tesm_hip_mimo_decode_ws_bytes": ([ctypes.POINTER(MimoStep)], I64),
     "tesm_hip_mimo_decode": ([ctypes.POINTER(MimoStep), P, I64, P], I32),
+    "tesm_hip_add_rmsnorm": ([ctypes.POINTER(RmsNorm), P], I32),
+    "tesm_hip_ffn_ws_bytes": ([ctypes.POINTER(Ffn)], I64),
+    "tesm_hip_ffn_forward": ([ctypes.POINTER(Ffn), P, I64, P], I32),
     "tesm_hip_mimo_coef": ([P, P, I32, I64, I64, I64, P, P, P], I32),
     "tesm_hip_mimo_prefill_ws_bytes": ([ctypes.POINTER(MimoLayer)], I64),
     "tesm_hip_mimo_prefill": ([ctypes.POINTER(MimoLayer), P, I64, P], I32),

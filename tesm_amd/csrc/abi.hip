@@ -8,6 +8,7 @@
 #include "entangle.h"
 #include "global.h"
 #include "mimo.h"
+#include "norm.h"
 #include "scan.h"
 #include "tesm_hip_internal.h"
 #include "../../include/tesm_hip.h"
@@ -310,6 +311,26 @@ MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
   s.xc = take_codes(c, M, HD);
   s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(M * p.d_model * es);
   s.xy = take_codes(c, M, p.d_model);
+  s.total = c.off;
+  return s;
+}
+
+// Workspace layout of the feed-forward; with base == nullptr it only measures.
+struct FfnPlan {
+  CodeBuf xq, hq;
+  void* h;
+  int64_t total;
+};
+
+FfnPlan plan_ffn(const tesm_hip_ffn& p, void* base) {
+  Carve c(base);
+  FfnPlan s;
+  if (p.x_codes)
+    s.xq = CodeBuf{nullptr, nullptr, nullptr, 0};
+  else
+    s.xq = take_codes(c, p.M, p.d_model);
+  s.h = c.take<void>(p.M * p.d_inter * esize(p.dt));
+  s.hq = take_codes(c, p.M, p.d_inter);
   s.total = c.off;
   return s;
 }
@@ -1158,6 +1179,87 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   op.ld = n_in;
   op.y = p.y;
   return run_output_path(op, st);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm and FeedForward of the TESM block
+// ---------------------------------------------------------------------------
+int tesm_hip_add_rmsnorm(const tesm_hip_rmsnorm* pp, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "rmsnorm: null descriptor");
+  const tesm_hip_rmsnorm& p = *pp;
+  NormArgs a;
+  a.dt = p.dt;
+  a.M = p.M;
+  a.D = p.D;
+  a.eps = p.eps;
+  a.x = p.x;
+  a.ld_x = p.ld_x > 0 ? p.ld_x : p.D;
+  a.res = p.residual;
+  a.res_dt = p.residual_dt;
+  a.ld_res = p.ld_res > 0 ? p.ld_res : p.D;
+  a.res_out = p.residual_out;
+  a.res_out_dt = p.residual_out_dt;
+  a.ld_res_out = p.ld_res_out > 0 ? p.ld_res_out : p.D;
+  a.weight = p.weight;
+  a.y = p.y;
+  a.ld_y = p.ld_y > 0 ? p.ld_y : p.D;
+  a.q = p.q;
+  a.ldq = p.ldq;
+  a.s_x = p.s_x;
+  a.rowsum = p.rowsum;
+  a.bit_eps = p.bit_eps;
+  return launch_add_rmsnorm(a, static_cast<hipStream_t>(stream));
+}
+
+
+int64_t tesm_hip_ffn_ws_bytes(const tesm_hip_ffn* p) {
+  if (!p) return -1;
+  return plan_ffn(*p, nullptr).total;
+}
+
+int tesm_hip_ffn_forward(const tesm_hip_ffn* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "ffn: null descriptor");
+  const tesm_hip_ffn& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "ffn: dtype must be 0 or 1");
+  TESM_REQUIRE(p.M >= 0 && p.d_model >= 1 && p.d_inter >= 1, kErrInvalidArg, "ffn: bad sizes");
+  TESM_REQUIRE(p.y && p.ld_y >= p.d_model, kErrInvalidArg, "ffn: need y with ld_y >= d_model");
+  if (p.x_codes)
+    TESM_REQUIRE(p.x_scale && p.x_rowsum && p.ldq_x >= kpad(p.d_model) && p.ldq_x % 16 == 0, kErrInvalidArg,
+                 "ffn: x codes need x_scale, x_rowsum and ldq_x >= kpad(d_model), a multiple of 16");
+  else
+    TESM_REQUIRE(p.x && p.ld_x >= p.d_model, kErrInvalidArg, "ffn: need x (ld_x >= d_model) or x codes");
+  if (int rc = check_linear(p.gate_proj, p.d_model, "gate_proj")) return rc;
+  if (int rc = check_linear(p.up_proj, p.d_model, "up_proj")) return rc;
+  if (int rc = check_linear(p.down_proj, p.d_inter, "down_proj")) return rc;
+  const FfnPlan s = plan_ffn(p, ws);
+  TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "ffn: workspace too small");
+  if (p.M == 0) return kOk;
+  int rc;
+  CodeBuf xq = s.xq;
+  if (p.x_codes) {
+    xq = CodeBuf{const_cast<int8_t*>(p.x_codes), const_cast<float*>(p.x_scale), const_cast<int32_t*>(p.x_rowsum),
+                 p.ldq_x};
+  } else if ((rc = launch_quant_act(p.x, p.dt, p.M, p.d_model, p.ld_x, p.bit_eps, 1, xq.q, xq.ldq, xq.s, xq.rs, st))) {
+    return rc;
+  }
+  // gate and up products on the same codes, h = silu(gate) * up (mixer_seq_simple.py:57-64)
+  LinearArgs g;
+  g.op[0] = operand(xq, p.gate_proj);
+  g.op[1] = operand(xq, p.up_proj);
+  g.M = p.M;
+  g.N = p.d_inter;
+  g.Kp = kpad(p.d_model);
+  g.out = s.h;
+  g.ldo = p.d_inter;
+  g.out_dt = p.dt;
+  g.epilogue = kEpiSwiGLU;
+  if ((rc = launch_linear(g, st))) return rc;
+  // down_proj(h) (mixer_seq_simple.py:65)
+  if ((rc = launch_quant_act(s.h, p.dt, p.M, p.d_inter, p.d_inter, p.bit_eps, 1, s.hq.q, s.hq.ldq, s.hq.s, s.hq.rs,
+                             st)))
+    return rc;
+  return run_linear(s.hq, p.down_proj, p.M, p.d_model, p.d_inter, p.y, p.dt, p.ld_y, st);
 }
 
 }  // extern "C"

@@ -342,6 +342,19 @@ __device__ __forceinline__ bool vec4_ok(const void* p, int64_t ld) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0 && (ld * (DT == kBF16 ? 2 : 4)) % bytes == 0;
 }
 
+// Two-product epilogues on the rounded products p0 = rnd(v0), p1 = rnd(v1):
+//   output gate  y = rnd(rnd(local + rnd(sigmoid(gate) * p0)) + p1)      (tesm.py:1256-1261)
+//   SwiGLU       h = rnd(rnd(silu(p0)) * p1), silu(x) = x * sigmoid(x)  (mixer_seq_simple.py:63-64)
+template <int EPI, int OUT_DT>
+__device__ __forceinline__ float dual_epi(float p0, float p1, float local, float gate) {
+  if constexpr (EPI == kEpiOutputGate) {
+    const float g = rnd<OUT_DT>(sigmoidf_(gate));
+    return rnd<OUT_DT>(rnd<OUT_DT>(local + rnd<OUT_DT>(g * p0)) + p1);
+  } else {
+    return rnd<OUT_DT>(rnd<OUT_DT>(p0 * sigmoidf_(p0)) * p1);
+  }
+}
+
 // General epilogue of the 16 x 16 tiles of one wave (tile rows wm*TM.., columns wn*TN..): scale the
 // exact accumulators, optional bias / accumulator dump, or the output gate
 // y = local + sigmoid(gate) * state_proj + ent_proj in the module dtype's op order.
@@ -361,7 +374,7 @@ __device__ __forceinline__ void epilogue16(const LinearArgs& a, const v4i (&acc0
     const int32_t rs0 = o0.rowsum[m];
     float inv1 = 0.0f;
     int32_t rs1 = 0;
-    if constexpr (EPI == kEpiOutputGate) {
+    if constexpr (epi_dual(EPI)) {
       inv1 = 1.0f / o1.s_x[m];
       rs1 = o1.rowsum[m];
     }
@@ -370,7 +383,7 @@ __device__ __forceinline__ void epilogue16(const LinearArgs& a, const v4i (&acc0
       const int64_t nb = n0 + (wn * TN + j) * 16 + 4 * (lane >> 4);
       if (nb >= a.N) continue;
       const bool full = nb + 3 < a.N;
-      float v[4], lo[4], gt[4];
+      float v[4], lo[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (EPI == kEpiOutputGate) {
         if (full) {
           load4<OUT_DT>(a.local, m * a.ld_local + nb, vin, lo);
@@ -395,10 +408,8 @@ __device__ __forceinline__ void epilogue16(const LinearArgs& a, const v4i (&acc0
           v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n) : v0;
         } else {
           const float cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
-          const float sp = rnd<OUT_DT>(v0);
-          const float ep = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1) * inv1) * cw1);
-          const float g = rnd<OUT_DT>(sigmoidf_(gt[r]));
-          v[r] = rnd<OUT_DT>(rnd<OUT_DT>(lo[r] + rnd<OUT_DT>(g * sp)) + ep);
+          const float v1 = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1) * inv1) * cw1);
+          v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, lo[r], gt[r]);
         }
       }
       if (full) {
@@ -443,7 +454,7 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_kernel(LinearArgs a) {
   }
   const float cws = o0.c_w[0];
   mfma_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-  if constexpr (EPI == kEpiOutputGate) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+  if constexpr (epi_dual(EPI)) mfma_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
 
   if (plain) {
     const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));  // columns of this tile
@@ -557,7 +568,7 @@ __device__ __forceinline__ void skinny_loop(const LinearOperand& o, int64_t M, i
 
 template <int NW, int TM, int TN, int EPI, int OUT_DT>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
-  constexpr int NOP = EPI == kEpiOutputGate ? 2 : 1;
+  constexpr int NOP = epi_dual(EPI) ? 2 : 1;
   __shared__ v4i red[(NW - 1) * NOP * TM * TN * 64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t ntn = (a.N + 16 * TN - 1) / (16 * TN);
@@ -572,7 +583,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
       acc1[i][j] = v4i{0, 0, 0, 0};
     }
   skinny_loop<NW, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, w, lane, acc0);
-  if constexpr (EPI == kEpiOutputGate) skinny_loop<NW, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, w, lane, acc1);
+  if constexpr (epi_dual(EPI)) skinny_loop<NW, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, w, lane, acc1);
   if (w > 0) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -855,7 +866,7 @@ __device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
   const bool full = nb + 3 < a.N;
-  float v[4], lo[4], gt[4];
+  float v[4], lo[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (EPI == kEpiOutputGate) {
     if (full) {
       load4<OUT_DT>(a.local, m * a.ld_local + nb, vin, lo);
@@ -880,10 +891,8 @@ __device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64
       v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n) : v0;
     } else {
       const float cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
-      const float sp = rnd<OUT_DT>(v0);
-      const float ep = rnd<OUT_DT>((static_cast<float>(q1[r] - rs1) * inv1) * cw1);
-      const float g = rnd<OUT_DT>(sigmoidf_(gt[r]));
-      v[r] = rnd<OUT_DT>(rnd<OUT_DT>(lo[r] + rnd<OUT_DT>(g * sp)) + ep);
+      const float v1 = rnd<OUT_DT>((static_cast<float>(q1[r] - rs1) * inv1) * cw1);
+      v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, lo[r], gt[r]);
     }
   }
   if (full) {
@@ -1000,10 +1009,10 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   const float cws = o0.c_w[0];
   if constexpr (NS == 0) {
     mfma32_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-    if constexpr (EPI == kEpiOutputGate) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
+    if constexpr (epi_dual(EPI)) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
   } else {
     mfma32d_mainloop<C, WN, TM, TN, NS>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
-    if constexpr (EPI == kEpiOutputGate)
+    if constexpr (epi_dual(EPI))
       mfma32d_mainloop<C, WN, TM, TN, NS>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
   }
 
@@ -1048,7 +1057,7 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
     const float inv0 = 1.0f / sx[i];
     float inv1 = 0.0f;
     int32_t rs1 = 0;
-    if constexpr (EPI == kEpiOutputGate) {
+    if constexpr (epi_dual(EPI)) {
       inv1 = 1.0f / o1.s_x[m];
       rs1 = o1.rowsum[m];
     }
@@ -1749,20 +1758,33 @@ int check_operand(const LinearOperand& o, int64_t Kp, const char* which) {
 
 }  // namespace
 
+// Two-product epilogues: split-K for decode-size batches, else the 32x32 kernels as for plain products.
+template <int EPI>
+int dispatch_dual(const LinearArgs& a, hipStream_t st) {
+  if (a.M <= 16) return run_skinny<4, 1, 1, EPI>(a, st);
+  if (a.M <= 32) return run_skinny<4, 2, 1, EPI>(a, st);
+  const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, EPI, 3>(a, st);
+  if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, EPI>(a, st);
+  return run_mfma32<1, 4, 2, 1, EPI>(a, st);
+}
+
 int launch_linear(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.M >= 0 && a.N >= 0, kErrInvalidArg, "bitlinear: negative size");
   TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "bitlinear: Kp must be a positive multiple of 128");
   TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "bitlinear: out dtype must be 0 or 1");
-  TESM_REQUIRE(a.epilogue == kEpiStore || a.epilogue == kEpiOutputGate, kErrInvalidArg, "bitlinear: bad epilogue");
+  TESM_REQUIRE(a.epilogue == kEpiStore || a.epilogue == kEpiOutputGate || a.epilogue == kEpiSwiGLU, kErrInvalidArg,
+               "bitlinear: bad epilogue");
   if (a.M == 0 || a.N == 0) return kOk;
   TESM_REQUIRE(a.out && a.ldo >= a.N, kErrInvalidArg, "bitlinear: need out and ldo >= N");
   if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
-  if (a.epilogue == kEpiOutputGate) {
+  if (a.epilogue != kEpiStore) {
     if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
+    TESM_REQUIRE(a.bias == nullptr, kErrInvalidArg, "bitlinear two-product epilogue: bias unsupported");
+  }
+  if (a.epilogue == kEpiOutputGate)
     TESM_REQUIRE(a.local && a.gate && a.ld_local >= a.N && a.ld_gate >= a.N, kErrInvalidArg,
                  "bitlinear output gate: need local and gate operands");
-    TESM_REQUIRE(a.bias == nullptr, kErrInvalidArg, "bitlinear output gate: bias unsupported");
-  }
   const int64_t nch = a.Kp / 64;
   if (a.epilogue == kEpiStore && a.M <= 4 && nch <= 256) {
     if (a.M == 1) return dispatch_gemv<1>(a, nch, st);
@@ -1787,12 +1809,8 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
   }
-  if (a.M <= 16) return run_skinny<4, 1, 1, kEpiOutputGate>(a, st);
-  if (a.M <= 32) return run_skinny<4, 2, 1, kEpiOutputGate>(a, st);
-  const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiOutputGate, 3>(a, st);
-  if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiOutputGate>(a, st);
-  return run_mfma32<1, 4, 2, 1, kEpiOutputGate>(a, st);
+  if (a.epilogue == kEpiOutputGate) return dispatch_dual<kEpiOutputGate>(a, st);
+  return dispatch_dual<kEpiSwiGLU>(a, st);
 }
 
 int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {

@@ -33,10 +33,14 @@ struct LinearOperand {
 enum Epilogue : int {
   kEpiStore = 0,       // out = rnd(v (+ bias))
   kEpiOutputGate = 1,  // out = rnd(rnd(local + rnd(sigmoid(gate) * sp)) + ep), two products (sp, ep)
+  kEpiSwiGLU = 2,      // out = rnd(rnd(silu(rnd(g))) * rnd(u)), two products (g, u) of one activation
 };
 
+// Epilogues that combine two products (op[0], op[1]) computed over the same output tile.
+constexpr bool epi_dual(int epi) { return epi != kEpiStore; }
+
 struct LinearArgs {
-  LinearOperand op[2];  // op[1] used only by kEpiOutputGate
+  LinearOperand op[2];  // op[1] used only by the two-product epilogues
   int64_t M = 0, N = 0, Kp = 0;
   const void* bias = nullptr;  // (N) in out dtype, kEpiStore only
   void* out = nullptr;

@@ -60,7 +60,7 @@ def test_struct_layout_matches_header(tmp_path):
     structs = {"tesm_hip_linear": _lib.Linear, "tesm_hip_ent_quant": _lib.EntQuant,
                "tesm_hip_output_gate": _lib.OutputGate, "tesm_hip_siso_layer": _lib.SisoLayer,
                "tesm_hip_siso_step": _lib.SisoStep, "tesm_hip_mimo_layer": _lib.MimoLayer,
-               "tesm_hip_mimo_step": _lib.MimoStep}
+               "tesm_hip_mimo_step": _lib.MimoStep, "tesm_hip_rmsnorm": _lib.RmsNorm, "tesm_hip_ffn": _lib.Ffn}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "tesm_hip.h"', "int main(void) {"]
     for cname, py in structs.items():
         fields = _c_struct_fields(text, cname)
@@ -134,3 +134,29 @@ def test_host_tensors_are_rejected_before_any_launch():
         hip_ops.scan(torch.rand(1, 4, 8), torch.rand(1, 4, 8))
     with pytest.raises(RuntimeError, match="ROCm device"):
         hip_ops.quant_act(torch.randn(2, 8))
+
+
+def test_lm_construction_matches_reference():
+    """TESMLMHeadModel(tiny()) from seed 0 holds the reference's parameters (the fingerprints the
+    reference wrote: shape, first values, sum), and a small model equals the oracle's state_dict."""
+    from conftest import golden_meta
+    from tesm_amd import TESMConfig, TESMLMHeadModel
+    meta = golden_meta("tiny_model")
+    torch.manual_seed(meta["seed"])
+    sd = TESMLMHeadModel(TESMConfig.tiny()).state_dict()
+    for k, fp in meta["fingerprints"].items():
+        if k not in sd:  # co-occurrence buffers of the reference: zero-filled, no RNG
+            assert fp["abs_sum"] == 0.0, k
+            continue
+        v = sd[k].detach()
+        assert list(v.shape) == fp["shape"], k
+        assert [float(a) for a in v.flatten()[:8]] == fp["head"], k
+        assert abs(float(v.double().sum()) - fp["sum"]) <= 1e-9 * max(1.0, abs(fp["abs_sum"])), k
+    cfg = TESMConfig(d_model=64, n_layer=2, d_intermediate=128, vocab_size=100, max_seq_len=32, d_state=16,
+                     ent_rank=8, entanglement_window=4, use_mimo=True, n_heads=2, tie_embeddings=False)
+    torch.manual_seed(2)
+    ref = ot.TESMLMHeadModel(cfg).state_dict()
+    torch.manual_seed(2)
+    mine = TESMLMHeadModel(cfg).state_dict()
+    assert set(ref) == set(mine)
+    assert all(torch.equal(ref[k], mine[k]) for k in ref)
