@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel measurements")
     p.add_argument("--no-mimo", action="store_true", help="skip the configs[4] MIMO layer measurement")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
+    p.add_argument("--workload", default="all", choices=["all", "layer", "decode", "mimo", "global", "lm"],
+                   help="run one measurement alone and print its JSON (for per-workload profiles)")
     p.add_argument("--copy-calib", action="store_true",
                    help="run one 256 MiB device-to-device copy first (a known-size reference for "
                         "FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -335,6 +337,29 @@ def main():
     m = TESM_SISO(**LAYER).to(dev).to(torch.bfloat16).eval()
     u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
 
+    if args.workload != "all":
+        with torch.no_grad():
+            if args.workload == "layer":
+                for _ in range(args.warmup):
+                    m(u)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(args.steps):
+                    m(u)
+                e1.record()
+                torch.cuda.synchronize()
+                res = {"ms_per_forward": e0.elapsed_time(e1) / args.steps}
+            elif args.workload == "decode":
+                res = measure_decode(torch, m)
+            elif args.workload == "mimo":
+                res = measure_mimo(torch)
+            elif args.workload == "global":
+                res = measure_global(torch)
+            else:
+                res = measure_lm(torch)
+        print(json.dumps({"workload": args.workload, "result": res}))
+        return
     if args.copy_calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
