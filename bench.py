@@ -337,6 +337,12 @@ def main():
     m = TESM_SISO(**LAYER).to(dev).to(torch.bfloat16).eval()
     u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
 
+    if args.copy_calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.workload != "all":
         with torch.no_grad():
             if args.workload == "layer":
@@ -360,12 +366,6 @@ def main():
                 res = measure_lm(torch)
         print(json.dumps({"workload": args.workload, "result": res}))
         return
-    if args.copy_calib:
-        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     with torch.no_grad():
         for _ in range(args.warmup):
             m(u)
