@@ -59,21 +59,6 @@ def busy(torch, ms: float = 20.0):
         torch.cuda._sleep(int(ms * 2.0e6))
 
 
-def time_launches(torch, fn, n: int, warm: int = 3):
-    """Average device duration of fn() over n launches, one event pair per launch on the current stream."""
-    for _ in range(warm):
-        fn(0)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    busy(torch)
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        fn(i)
-        b.record()
-    torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in evs) / n * 1e-3  # seconds
-
-
 def time_back_to_back(torch, fn, n: int, warm: int = 3):
     """Average device time per launch of n back-to-back fn() launches between one event pair on the
     current stream (the launches are queued behind a device-side wait first, so host launch latency
@@ -120,7 +105,7 @@ def measure_kernels(torch, only):
         q, s, rs = hip_ops.quant_act(x)
         c_w = torch.full((1,), 0.05, device=dev)
         out = torch.empty(M, N, device=dev)
-        t = time_launches(torch, lambda i: hip_ops.bitlinear(q, s, rs, packs[i % nrot], c_w, N, K, torch.float32,
+        t = time_back_to_back(torch, lambda i: hip_ops.bitlinear(q, s, rs, packs[i % nrot], c_w, N, K, torch.float32,
                                                              out=out), 200 if M == 1 else 50)
         if M == 1:
             nbytes = N * K // 4 + M * K + M * N * 4 + 8 * M + 4
@@ -137,7 +122,7 @@ def measure_kernels(torch, only):
         nrot = 80
         sets = [(torch.sigmoid(torch.randn(Bs, Ls, D, device=dev, generator=gen)).to(torch.bfloat16),
                  torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
-        t = time_launches(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100)
+        t = time_back_to_back(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100)
         nbytes = Bs * Ls * D * (2 + 2 + 2)
         res["scan_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
                              "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
@@ -149,7 +134,7 @@ def measure_kernels(torch, only):
         sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
                  torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
                  torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
-        t = time_launches(torch, lambda i: hip_ops.local_ent(sets[i % nrot][0], sets[i % nrot][1], rope,
+        t = time_back_to_back(torch, lambda i: hip_ops.local_ent(sets[i % nrot][0], sets[i % nrot][1], rope,
                                                              sets[i % nrot][2], bias, W, 0.08, 0.2), 100)
         nbytes = Bs * Ls * (2 * R + 2 * D) * 2
         res["local_ent_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
@@ -162,7 +147,7 @@ def measure_kernels(torch, only):
         sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
                  torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
                  torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
-        t = time_launches(torch, lambda i: hip_ops.local_ent_quant(sets[i % nrot][0], sets[i % nrot][1], rope,
+        t = time_back_to_back(torch, lambda i: hip_ops.local_ent_quant(sets[i % nrot][0], sets[i % nrot][1], rope,
                                                                    sets[i % nrot][2], bias, W, 0.08, 0.2), 100)
         # q, k, states in; int8 codes + scale + rowsum of tanh(E) and C out
         nbytes = Bs * Ls * (2 * R * 2 + D * 2 + 2 * (D + 8))

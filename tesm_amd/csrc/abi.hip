@@ -121,7 +121,9 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   const int es = esize(p.dt);
   const bool global = p.window == 0;
   s.fuse_ent = !global && ent_fused_ok(siso_ent_shape(p));
-  s.rowq = p.d_model <= 1024;
+  // the row-complete gate keeps both weight matrices in LDS, one workgroup per CU streaming 16-row
+  // tiles: it pays with many tiles; short prefills (fewer than 256 tiles) take the tiled gate
+  s.rowq = p.d_model <= 1024 && M >= 4096;
   s.xu = take_codes(c, M, p.d_model);
   s.proj = c.take<void>(M * n_in * es);
   s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
@@ -309,7 +311,7 @@ MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
   s.cc = c.take<void>(M * HD * es);
   s.xe = take_codes(c, M, HD);
   s.xc = take_codes(c, M, HD);
-  s.yg = p.d_model <= 1024 ? nullptr : c.take<void>(M * p.d_model * es);
+  s.yg = p.d_model <= 1024 && M >= 4096 ? nullptr : c.take<void>(M * p.d_model * es);
   s.xy = take_codes(c, M, p.d_model);
   s.total = c.off;
   return s;

@@ -32,9 +32,9 @@ __device__ __forceinline__ void store_plain(const LinearArgs& a, int64_t m, int6
 // ---------------------------------------------------------------------------
 // GEMV
 // ---------------------------------------------------------------------------
-template <int LPR, int MR, int NCH, int OUT_DT>
+// RPG: output rows per lane group (independent loads in flight per lane).
+template <int LPR, int MR, int NCH, int OUT_DT, int RPG = 4>
 __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
-  constexpr int RPG = 4;          // output rows per lane group (independent loads in flight)
   constexpr int GPW = 64 / LPR;   // lane groups per wave
   const LinearOperand& o = a.op[0];
   const int lane = threadIdx.x & 63;
@@ -1723,16 +1723,16 @@ int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
   return check_launch("output gate rowq");
 }
 
-template <int LPR, int MR, int NCH>
+template <int LPR, int MR, int NCH, int RPG = 4>
 int run_gemv(const LinearArgs& a, hipStream_t st) {
   constexpr int GPW = 64 / LPR;
-  const int64_t groups = (a.N + 3) / 4;
+  const int64_t groups = (a.N + RPG - 1) / RPG;
   const int64_t waves = (groups + GPW - 1) / GPW;
   const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
   if (a.out_dt == kBF16)
-    gemv_kernel<LPR, MR, NCH, kBF16><<<blocks, 256, 0, st>>>(a);
+    gemv_kernel<LPR, MR, NCH, kBF16, RPG><<<blocks, 256, 0, st>>>(a);
   else
-    gemv_kernel<LPR, MR, NCH, kF32><<<blocks, 256, 0, st>>>(a);
+    gemv_kernel<LPR, MR, NCH, kF32, RPG><<<blocks, 256, 0, st>>>(a);
   return check_launch("bitlinear gemv");
 }
 
@@ -1742,9 +1742,10 @@ int dispatch_gemv(const LinearArgs& a, int64_t nch, hipStream_t st) {
   if (nch <= 8) return run_gemv<8, MR, 1>(a, st);
   if (nch <= 16) return run_gemv<16, MR, 1>(a, st);
   if (nch <= 32) return run_gemv<32, MR, 1>(a, st);
-  if (nch <= 64) return run_gemv<64, MR, 1>(a, st);
-  if (nch <= 128) return run_gemv<64, MR, 2>(a, st);
-  return run_gemv<64, MR, 4>(a, st);
+  // two rows per lane group: twice the waves of four, 3-7 % faster at K = 4096 (N 4096 / 11008)
+  if (nch <= 64) return run_gemv<64, MR, 1, 2>(a, st);
+  if (nch <= 128) return run_gemv<64, MR, 2, 2>(a, st);
+  return run_gemv<64, MR, 4, 2>(a, st);
 }
 
 int check_operand(const LinearOperand& o, int64_t Kp, const char* which) {
