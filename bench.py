@@ -302,8 +302,32 @@ def cpu_baseline(torch, seconds: float):
             if el >= seconds:
                 break
     return {"value": n * B * L / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"oracle TESM_SISO.forward (torch restatement of the reference torch path), bf16, "
                       f"{B}x{L} tokens, {n} forwards in {el:.1f} s"}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def copy_bandwidth(torch) -> float:
+    """Device-to-device copy of 1 GiB (read + write bytes per second, GB/s): the measured ceiling that the
+    HBM-bound kernels' fractions are also given against."""
+    dev = torch.device("cuda:0")
+    src = torch.empty(256 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    t = time_back_to_back(torch, lambda i: dst.copy_(src), 20)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * (1 << 30) / t / 1e9
 
 
 def main():
@@ -379,6 +403,12 @@ def main():
         glob = measure_global(torch)
         lm = measure_lm(torch)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
+        if kernels:
+            copy_gbs = copy_bandwidth(torch)
+            kernels["copy_1GiB_GBps"] = copy_gbs
+            for v in kernels.values():
+                if isinstance(v, dict) and v.get("unit") == "GB/s":
+                    v["frac_of_copy"] = v["achieved"] / copy_gbs
         if args.only:
             print(json.dumps({"kernels": kernels}))
             return

@@ -258,6 +258,240 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
   if (seg == NSEG - 1 && a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(h);
 }
 
+// ---------------------------------------------------------------------------
+// Single pass with decoupled look-back.  A tile is (batch row b, span c of TL positions, group g of
+// 256 channels, one per thread); TL is a multiple of the thread-chunk length, so the clamp's running
+// product restarts inside the tile.  Tiles take a ticket when they start and map it to span-major
+// order ((c * B + b) * G + g), so every tile a tile waits on took an earlier ticket and is already
+// running; ticket 0 waits on nothing, so every wait ends.  A tile loads its span and gates once,
+// scans it from h = 0 (the span's aggregate (prod d, h_end)), publishes the aggregate (flag 1), and
+// finds the state entering the span by looking back over earlier spans of the same (b, g), 64 at a
+// time in one wave: the nearest span whose end state is published (flag 2) ends the walk and the
+// aggregates in between are composed, nearest first.  Span 0 publishes its end state directly, so a
+// walk never passes it.  The tile then publishes its own end state (flag 2) and rescans the span
+// from the carry in registers, writing the states.  A reset kernel clears the flags and the ticket
+// before each pass.
+//
+// Cross-workgroup visibility without cache maintenance: the published values and the flags are
+// written and read only with agent-scope atomic accesses (coherent at agent scope, across the XCDs'
+// L2s, without the whole-L2 write-back and invalidate an agent-scope release / acquire costs).  A
+// writer waits for its value stores to complete (s_waitcnt) before the workgroup barrier after which
+// one thread stores the flag; a reader polls flags in one wave, and the other waves read values
+// only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds (the tile then
+// treats what it could not see as a zero state), so the launch completes whatever happens.
+// ---------------------------------------------------------------------------
+constexpr int kScanLbThreads = 256;
+constexpr int kScanLbTM = 32;  // positions per tile (at most)
+constexpr int kScanSpinLimit = 1 << 20;
+
+struct ScanLb {
+  float2* agg;       // (B, nc, C): (prod d, h_end from 0) of every span
+  float* incl;       // (B, nc, C): state at the end of every span
+  int* flags;        // (B, nc, G): 0 nothing yet, 1 aggregate published, 2 end state published
+  unsigned* ticket;  // tile counter
+};
+
+__global__ __launch_bounds__(256) void scan_lb_reset_kernel(int* flags, int64_t n, unsigned* ticket) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) flags[i] = 0;
+  if (i == 0) *ticket = 0u;
+}
+
+__device__ __forceinline__ int scan_flag_load(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void scan_flag_store(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void scan_agg_store(float2* p, float x, float y) {
+  const unsigned long long v = (static_cast<unsigned long long>(__float_as_uint(y)) << 32) | __float_as_uint(x);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 scan_agg_load(const float2* p) {
+  const unsigned long long v = __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(static_cast<unsigned>(v)), __uint_as_float(static_cast<unsigned>(v >> 32)));
+}
+__device__ __forceinline__ void scan_val_store(float* p, float x) {
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float scan_val_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int OUT_DT, int MODE>
+__global__ __launch_bounds__(kScanLbThreads) void scan_lb_kernel(ScanArgs a, int64_t TL, int64_t nc, int64_t G,
+                                                                 ScanLb s) {
+  constexpr int TM = kScanLbTM;
+  __shared__ unsigned s_tile;
+  __shared__ int s_m, s_stop;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_tile = atomicAdd(s.ticket, 1u);
+  __syncthreads();
+  const int64_t tile = s_tile;
+  const int64_t g = tile % G, rest = tile / G;
+  const int64_t b = rest % a.B, c = rest / a.B;
+  const int64_t ch = g * kScanLbThreads + tid;
+  const bool on = ch < a.C;
+  const int64_t chc = on ? ch : a.C - 1;  // idle threads read a valid channel and store nothing
+  const int64_t t0 = c * TL;
+  const int n = static_cast<int>((t0 + TL < a.L ? t0 + TL : a.L) - t0);
+
+  // 1. the span's inputs (all loads in flight at once; positions past the end re-read the last one)
+  float x0[TM], x1[TM], x2[TM], bias = 0.0f;
+  if constexpr (MODE == 1) bias = ld<DT>(a.decay_bias, chc);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
+    x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
+    x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
+    if constexpr (MODE == 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
+  }
+  // gates and the scan from h = 0; positions past the end become d = 1, u = 0
+  float d[TM], u[TM];
+  const int cs = static_cast<int>(a.cs);
+  float h = 0.0f, P = 1.0f, A = 1.0f;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    float dd, uu;
+    if constexpr (MODE == 0) {
+      dd = x0[i];
+      uu = x1[i];
+    } else {
+      const float sv = rnd<DT>(tanhf_(x2[i]));
+      dd = rnd<DT>(sigmoidf_(rnd<DT>(x0[i] + bias)));
+      const float w = rnd<DT>(sigmoidf_(x1[i]));
+      uu = a.round_update ? rnd<DT>(w * sv) : w * sv;
+    }
+    if (a.clamp) {
+      dd = fmaxf(dd, kScanEps);
+      A = (i % cs) == 0 ? dd : A * dd;
+      if (A < kScanEps) uu *= A * kScanInvEps;  // the clamp factor, folded into the update
+    }
+    if (i >= n) {
+      dd = 1.0f;
+      uu = 0.0f;
+    }
+    d[i] = dd;
+    u[i] = uu;
+    h = dd * h + uu;
+    P *= dd;
+  }
+
+  // 2. the state entering the span
+  const int64_t fb = b * nc * G + g;      // flag of span k: fb + k * G
+  const int64_t vb = b * nc * a.C + chc;  // values of span k: vb + k * C
+  float carry;
+  if (c == 0) {
+    carry = a.h0 ? static_cast<float>(a.h0[b * a.C + chc]) : 0.0f;
+  } else {
+    if (on) scan_agg_store(&s.agg[vb + c * a.C], P, h);
+    __builtin_amdgcn_s_waitcnt(0);  // the value stores are complete before the flag can be stored
+    __syncthreads();
+    if (tid == 0) scan_flag_store(&s.flags[fb + c * G], 1);
+    float accP = 1.0f, accH = 0.0f;
+    int64_t k0 = c - 1;  // nearest span not composed yet; k0 >= 0 (span 0 ends every walk)
+    for (;;) {
+      if (wave == 0) {
+        // lane l watches span k0 - l; lanes before span 0 never report
+        const int64_t k = k0 - lane;
+        int m = 0, stop = 2;
+        for (int it = 0;; ++it) {
+          const int f = k >= 0 ? scan_flag_load(&s.flags[fb + k * G]) : 0;
+          const unsigned long long incl = __ballot(f == 2), ready = __ballot(f >= 1);
+          if (incl) {
+            m = __ffsll(static_cast<long long>(incl)) - 1;    // aggregates to compose before it
+            const unsigned long long need = (2ull << m) - 1;  // lanes 0..m (all ones for m = 63)
+            if ((ready & need) == need) {
+              stop = 1;
+              break;
+            }
+          } else if (ready == ~0ull) {  // 64 aggregates, no end state among them: compose, go on
+            m = 64;
+            stop = 0;
+            break;
+          }
+          if (it >= kScanSpinLimit) {
+            m = 0;
+            stop = 2;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) {
+          s_m = m;
+          s_stop = stop;
+        }
+      }
+      __syncthreads();
+      const int m = s_m, stop = s_stop;
+      // compose spans k0, k0 - 1, .., k0 - m + 1 (all >= 0), 32 loads in flight at a time
+      for (int j0 = 0; j0 < m; j0 += 32) {
+        float2 v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          const int jj = j0 + j < m ? j0 + j : m - 1;
+          v[j] = scan_agg_load(&s.agg[vb + (k0 - jj) * a.C]);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+          if (j0 + j < m) {
+            accH += accP * v[j].y;
+            accP *= v[j].x;
+          }
+        }
+      }
+      if (stop == 1) {
+        carry = accH + accP * scan_val_load(&s.incl[vb + (k0 - m) * a.C]);
+        break;
+      }
+      if (stop == 2) {  // gave up waiting: the spans not seen count as a zero state
+        carry = accH;
+        break;
+      }
+      k0 -= 64;
+      __syncthreads();  // s_m / s_stop are rewritten by the next round
+    }
+  }
+  const float hend = P * carry + h;
+  if (on) scan_val_store(&s.incl[vb + c * a.C], hend);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) scan_flag_store(&s.flags[fb + c * G], 2);
+
+  // 3. rescan from the carry and store the states
+  if (!on) return;
+  float hh = carry;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    if (i < n) {
+      hh = d[i] * hh + u[i];
+      st<OUT_DT>(a.states, (b * a.L + t0 + i) * a.ld_states + ch, hh);
+    }
+  }
+  if (c == nc - 1 && a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(hend);
+}
+
+// Span length for the look-back pass: the largest multiple of the thread-chunk length T within
+// kScanLbTM (T itself when T > kScanLbTM / 2).
+int64_t scan_lb_span(int64_t T) { return T * std::max<int64_t>(1, kScanLbTM / T); }
+
+template <int DT, int OUT_DT, int MODE>
+int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
+  const int64_t TL = scan_lb_span(T);
+  const int64_t nc = (a.L + TL - 1) / TL;
+  const int64_t G = (a.C + kScanLbThreads - 1) / kScanLbThreads;
+  const int64_t tiles = a.B * nc * G;
+  ScanLb s;
+  s.agg = reinterpret_cast<float2*>(summ);
+  s.incl = summ + 2 * a.B * nc * a.C;
+  s.flags = flags;
+  s.ticket = reinterpret_cast<unsigned*>(flags + tiles);
+  scan_lb_reset_kernel<<<static_cast<unsigned>((tiles + 1 + 255) / 256), 256, 0, st>>>(flags, tiles, s.ticket);
+  scan_lb_kernel<DT, OUT_DT, MODE><<<static_cast<unsigned>(tiles), kScanLbThreads, 0, st>>>(a, TL, nc, G, s);
+  return check_launch("scan look-back");
+}
+
 template <int DT, int OUT_DT, int MODE, int TM, int CPT>
 int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
   const int64_t threads = a.B * nc * (a.C / CPT);
@@ -321,7 +555,11 @@ int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
   if (L <= 0) return 0;
   const int64_t T = scan_chunk_len(L, cs);
   const int64_t nc = (L + T - 1) / T;
-  return round_up(B * nc * C * 3 * static_cast<int64_t>(sizeof(float)), 256);
+  const int64_t G = (C + kScanLbThreads - 1) / kScanLbThreads;
+  // chunk aggregates (2 floats) and end states (1 float) per (b, chunk, channel), then the look-back
+  // flags per (b, chunk, channel group) and the tile ticket
+  return round_up(B * nc * C * 3 * static_cast<int64_t>(sizeof(float)), 256) +
+         round_up((B * nc * G + 64) * static_cast<int64_t>(sizeof(int)), 256);
 }
 
 int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
@@ -343,6 +581,8 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   TESM_REQUIRE(nc <= 65535 && a.B <= 65535, kErrUnsupported, "scan: too many chunks or batch rows");
   float* summ = static_cast<float*>(ws);
   float* carry = summ + 2 * a.B * nc * a.C;
+  int* flags = reinterpret_cast<int*>(static_cast<char*>(ws) +
+                                      round_up(a.B * nc * a.C * 3 * static_cast<int64_t>(sizeof(float)), 256));
   // the reference chunk grid starts at 0 with chunk = min(cs, L); pass the effective value
   ScanArgs e = a;
   e.cs = std::max<int64_t>(1, std::min(a.cs, a.L));
@@ -350,6 +590,22 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
                      aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
                      aligned(a.states, 4) && (!a.gated || aligned(a.gated, 4));
+  if (T <= kScanLbTM && aligned(ws, 8) && a.B * nc * ((a.C + kScanLbThreads - 1) / kScanLbThreads) < (1 << 23)) {
+    // single pass with decoupled look-back (the gate buffer of the three-pass path is not needed);
+    // its spans are at least T long, so the summary, end-state and flag regions sized for T suffice
+    const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
+    switch (key) {
+      case 0: return run_scan_lb<kF32, kF32, 0>(e, T, summ, flags, st);
+      case 1: return run_scan_lb<kF32, kF32, 1>(e, T, summ, flags, st);
+      case 110: return run_scan_lb<kBF16, kBF16, 0>(e, T, summ, flags, st);
+      case 111: return run_scan_lb<kBF16, kBF16, 1>(e, T, summ, flags, st);
+      case 100: return run_scan_lb<kBF16, kF32, 0>(e, T, summ, flags, st);
+      case 101: return run_scan_lb<kBF16, kF32, 1>(e, T, summ, flags, st);
+      case 10: return run_scan_lb<kF32, kBF16, 0>(e, T, summ, flags, st);
+      case 11: return run_scan_lb<kF32, kBF16, 1>(e, T, summ, flags, st);
+      default: return fail(kErrInvalidArg, "scan: unsupported dtype combination");
+    }
+  }
   if (T <= 32) {
     if (a.dt == kBF16) {
       if (a.out_dt == kBF16) {

@@ -1,4 +1,6 @@
 """GPU parity of the state scan, the RoPE table and the local-window entanglement against the oracle."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -57,6 +59,67 @@ def test_scan_random_vs_oracle(dtype, B, L, C, cs):
     tol = 1e-5 if dtype == torch.float32 else 2 ** -8
     assert normwise(to_np(states), to_np(ref)) <= tol
     np.testing.assert_allclose(h_final.cpu().numpy(), m._last_scan_state_f64.numpy(), rtol=1e-4, atol=1e-5)
+
+
+def _scan_inputs(B, L, C, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    decay = torch.sigmoid(torch.randn(B, L, C, generator=g) + 2.0).to(dtype)
+    update = (torch.sigmoid(torch.randn(B, L, C, generator=g)) * torch.tanh(torch.randn(B, L, C, generator=g))).to(dtype)
+    h0 = torch.randn(B, C, generator=g, dtype=torch.float64)
+    return decay, update, h0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,L,C,cs", [(2, 5000, 300, 16), (1, 4097, 520, 8), (3, 2048, 256, 16)])
+def test_scan_lookback_many_spans_vs_oracle(dtype, B, L, C, cs):
+    """Long sequences (more than 64 spans of 32 positions: the look-back walks several windows) and
+    several 256-channel groups per row; decays near 1 carry the state across many spans."""
+    decay, update, h0 = _scan_inputs(B, L, C, dtype, B * L + C)
+    m = _oracle_module(C, cs)
+    with torch.no_grad():
+        ref = m._parallel_state_scan(decay, update, prev_state=h0)
+    states, h_final = hip_ops.scan(decay.to(DEV), update.to(DEV), cs, h0=h0.to(DEV))
+    # bf16: states reach [1, 2) here, where one bf16 step of the output rounding is 2^-7 of the value
+    tol = 1e-5 if dtype == torch.float32 else 2 ** -7
+    assert normwise(to_np(states), to_np(ref)) <= tol
+    np.testing.assert_allclose(h_final.cpu().numpy(), m._last_scan_state_f64.numpy(), rtol=1e-4, atol=1e-5)
+
+
+def _scan_abi(decay, update, cs, h0, ws, nbytes):
+    """tesm_hip_scan through the C-ABI with a caller-chosen workspace pointer."""
+    from tesm_amd import _lib
+    from tesm_amd.hip_ops import _p, _stream, dt_code
+    lib = _lib.load()
+    B, L, C = decay.shape
+    states = torch.empty_like(decay)
+    h_final = torch.empty((B, C), dtype=torch.float64, device=decay.device)
+    _lib.check(lib.tesm_hip_scan(_p(decay), C, _p(update), C, dt_code(decay.dtype), B, L, C, cs, _p(h0), _p(states), C,
+                                 dt_code(decay.dtype), _p(h_final), ctypes.c_void_p(ws), nbytes, _stream(decay)))
+    return states, h_final
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scan_workspace_reuse_and_three_pass_path(dtype):
+    """One workspace across calls of different sizes (the look-back flags are cleared per call), and the
+    three-pass path (taken for a workspace that is not 8-byte aligned) against the same oracle."""
+    from tesm_amd import _lib
+    lib = _lib.load()
+    cs = 16
+    shapes = [(2, 3000, 300), (1, 700, 64), (2, 3000, 300)]
+    nbytes = max(int(lib.tesm_hip_scan_ws_bytes(B, L, C, cs)) for B, L, C in shapes)
+    ws = torch.full((nbytes + 4,), 0x7f, dtype=torch.uint8, device=DEV)  # stale bytes in the flag region
+    for i, (B, L, C) in enumerate(shapes):
+        decay, update, h0 = _scan_inputs(B, L, C, dtype, 100 + i)
+        m = _oracle_module(C, cs)
+        with torch.no_grad():
+            ref = m._parallel_state_scan(decay, update, prev_state=h0)
+        d, u, h = decay.to(DEV), update.to(DEV), h0.to(DEV)
+        tol = 1e-5 if dtype == torch.float32 else 2 ** -7  # one bf16 step of the output rounding
+        for offset in (0, 4):
+            states, h_final = _scan_abi(d, u, cs, h, ws.data_ptr() + offset, nbytes)
+            torch.cuda.synchronize()
+            assert normwise(to_np(states), to_np(ref)) <= tol, (B, L, C, offset)
+            np.testing.assert_allclose(h_final.cpu().numpy(), m._last_scan_state_f64.numpy(), rtol=1e-4, atol=1e-5)
 
 
 def test_scan_reproduces_closed_form_clamp():
