@@ -259,18 +259,24 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 }
 
 // ---------------------------------------------------------------------------
-// Single pass with decoupled look-back.  A tile is (batch row b, span c of TL positions, group g of
-// 256 channels, one per thread); TL is a multiple of the thread-chunk length, so the clamp's running
-// product restarts inside the tile.  Tiles take a ticket when they start and map it to span-major
-// order ((c * B + b) * G + g), so every tile a tile waits on took an earlier ticket and is already
-// running; ticket 0 waits on nothing, so every wait ends.  A tile loads its span and gates once,
-// scans it from h = 0 (the span's aggregate (prod d, h_end)), publishes the aggregate (flag 1), and
-// finds the state entering the span by looking back over earlier spans of the same (b, g), 64 at a
-// time in one wave: the nearest span whose end state is published (flag 2) ends the walk and the
-// aggregates in between are composed, nearest first.  Span 0 publishes its end state directly, so a
-// walk never passes it.  The tile then publishes its own end state (flag 2) and rescans the span
-// from the carry in registers, writing the states.  A reset kernel clears the flags and the ticket
-// before each pass.
+// Single pass with decoupled look-back.  A tile is (batch row b, span c of 4 T positions, group g of
+// 64 channels); its 4 waves take one sub-span of T positions each (T is a multiple of the
+// reference chunk, so the clamp's running product restarts inside a wave) and its lanes one channel
+// each.  The workgroup index fixes the chain (b, g); the span c is the ticket the workgroup takes
+// from its chain's counter when it starts, so every tile a tile waits on (earlier spans of its
+// chain) took an earlier ticket and is already running; ticket 0 waits on nothing, so every wait
+// ends.  One counter per chain, each on its own 256-byte line, keeps the ticket atomics from
+// queueing on one cache line.
+//
+// A wave loads its sub-span and gates once and scans it from h = 0; the four sub-span aggregates
+// (prod d, h_end) meet in LDS, giving each wave the state entering its sub-span as a function of
+// the tile's carry, and the tile's aggregate, which the tile publishes (flag 1).  It then finds
+// its carry by looking back over earlier spans of the same (b, g), 64 at a time: wave 0 polls the
+// flags, the nearest span whose end state is published (flag 2) ends the walk, and the aggregates
+// in between are composed nearest first (a quarter of the window per wave, the quarters combined
+// through LDS).  Span 0 publishes its end state directly, so a walk never passes it.  The tile
+// publishes its own end state (flag 2) and every wave rescans its sub-span from registers, writing
+// the states.  A reset kernel clears the flags and the ticket before each pass.
 //
 // Cross-workgroup visibility without cache maintenance: the published values and the flags are
 // written and read only with agent-scope atomic accesses (coherent at agent scope, across the XCDs'
@@ -280,21 +286,23 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 // only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds (the tile then
 // treats what it could not see as a zero state), so the launch completes whatever happens.
 // ---------------------------------------------------------------------------
-constexpr int kScanLbThreads = 256;
-constexpr int kScanLbTM = 32;  // positions per tile (at most)
+constexpr int kScanLbCh = 64;    // channels per tile (one per lane)
+constexpr int kScanLbSub = 4;    // sub-spans per tile (one per wave)
 constexpr int kScanSpinLimit = 1 << 20;
 
 struct ScanLb {
   float2* agg;       // (B, nc, C): (prod d, h_end from 0) of every span
   float* incl;       // (B, nc, C): state at the end of every span
   int* flags;        // (B, nc, G): 0 nothing yet, 1 aggregate published, 2 end state published
-  unsigned* ticket;  // tile counter
+  unsigned* ticket;  // span counter of chain x at ticket[x * kScanLbTicketStride]
 };
+constexpr int kScanLbTicketStride = 64;  // ints: one 256-byte line per counter
 
-__global__ __launch_bounds__(256) void scan_lb_reset_kernel(int* flags, int64_t n, unsigned* ticket) {
+// Clears the flags (n ints) and the chain counters (nt, strided) that follow them.
+__global__ __launch_bounds__(256) void scan_lb_reset_kernel(int* p, int64_t n, int64_t nt) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) flags[i] = 0;
-  if (i == 0) *ticket = 0u;
+  if (i < n) p[i] = 0;
+  else if (i < n + nt) p[n + (i - n) * kScanLbTicketStride] = 0;
 }
 
 __device__ __forceinline__ int scan_flag_load(const int* p) {
@@ -319,80 +327,104 @@ __device__ __forceinline__ float scan_val_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int OUT_DT, int MODE>
-__global__ __launch_bounds__(kScanLbThreads) void scan_lb_kernel(ScanArgs a, int64_t TL, int64_t nc, int64_t G,
-                                                                 ScanLb s) {
-  constexpr int TM = kScanLbTM;
+template <int DT, int OUT_DT, int MODE, int TM>
+__global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArgs a, int64_t T, int64_t nc, int64_t G,
+                                                                         ScanLb s) {
   __shared__ unsigned s_tile;
   __shared__ int s_m, s_stop;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid == 0) s_tile = atomicAdd(s.ticket, 1u);
+  __shared__ float2 s_sub[kScanLbSub][kScanLbCh];  // sub-span aggregates, then window quarters
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t chain = blockIdx.x % (a.B * G);  // grid = nc workgroups per chain
+  if (tid == 0) s_tile = atomicAdd(&s.ticket[chain * kScanLbTicketStride], 1u);
   __syncthreads();
-  const int64_t tile = s_tile;
-  const int64_t g = tile % G, rest = tile / G;
-  const int64_t b = rest % a.B, c = rest / a.B;
-  const int64_t ch = g * kScanLbThreads + tid;
+  const int64_t c = s_tile;
+  const int64_t b = chain / G, g = chain % G;
+  const int64_t ch = g * kScanLbCh + lane;
   const bool on = ch < a.C;
-  const int64_t chc = on ? ch : a.C - 1;  // idle threads read a valid channel and store nothing
-  const int64_t t0 = c * TL;
-  const int n = static_cast<int>((t0 + TL < a.L ? t0 + TL : a.L) - t0);
+  const int64_t chc = on ? ch : a.C - 1;  // idle lanes read a valid channel and store nothing
+  const int64_t t0 = (c * kScanLbSub + w) * T;  // this wave's first position
+  const int n = t0 >= a.L ? 0 : static_cast<int>(t0 + T < a.L ? T : a.L - t0);  // wave-uniform
 
-  // 1. the span's inputs (all loads in flight at once; positions past the end re-read the last one)
-  float x0[TM], x1[TM], x2[TM], bias = 0.0f;
-  if constexpr (MODE == 1) bias = ld<DT>(a.decay_bias, chc);
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
-    x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
-    x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
-    if constexpr (MODE == 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
-  }
-  // gates and the scan from h = 0; positions past the end become d = 1, u = 0
+  // 1. the sub-span's inputs and gates (all loads in flight at once; positions past the end re-read
+  //    the last one and become d = 1, u = 0), then its scan from h = 0
   float d[TM], u[TM];
-  const int cs = static_cast<int>(a.cs);
-  float h = 0.0f, P = 1.0f, A = 1.0f;
+  float h = 0.0f, P = 1.0f;
+  if (n > 0) {
+    float x0[TM], x1[TM], x2[TM], bias = 0.0f;
+    if constexpr (MODE == 1) bias = ld<DT>(a.decay_bias, chc);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    float dd, uu;
-    if constexpr (MODE == 0) {
-      dd = x0[i];
-      uu = x1[i];
-    } else {
-      const float sv = rnd<DT>(tanhf_(x2[i]));
-      dd = rnd<DT>(sigmoidf_(rnd<DT>(x0[i] + bias)));
-      const float w = rnd<DT>(sigmoidf_(x1[i]));
-      uu = a.round_update ? rnd<DT>(w * sv) : w * sv;
+    for (int i = 0; i < TM; ++i) {
+      const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
+      x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
+      x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
+      if constexpr (MODE == 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
     }
-    if (a.clamp) {
-      dd = fmaxf(dd, kScanEps);
-      A = (i % cs) == 0 ? dd : A * dd;
-      if (A < kScanEps) uu *= A * kScanInvEps;  // the clamp factor, folded into the update
+    const int cs = static_cast<int>(a.cs);
+    float A = 1.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float dd, uu;
+      if constexpr (MODE == 0) {
+        dd = x0[i];
+        uu = x1[i];
+      } else {
+        const float sv = rnd<DT>(tanhf_(x2[i]));
+        dd = rnd<DT>(sigmoidf_(rnd<DT>(x0[i] + bias)));
+        const float wr = rnd<DT>(sigmoidf_(x1[i]));
+        uu = a.round_update ? rnd<DT>(wr * sv) : wr * sv;
+      }
+      if (a.clamp) {
+        dd = fmaxf(dd, kScanEps);
+        A = (i % cs) == 0 ? dd : A * dd;
+        if (A < kScanEps) uu *= A * kScanInvEps;  // the clamp factor, folded into the update
+      }
+      if (i >= n) {
+        dd = 1.0f;
+        uu = 0.0f;
+      }
+      d[i] = dd;
+      u[i] = uu;
+      h = dd * h + uu;
+      P *= dd;
     }
-    if (i >= n) {
-      dd = 1.0f;
-      uu = 0.0f;
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      d[i] = 1.0f;
+      u[i] = 0.0f;
     }
-    d[i] = dd;
-    u[i] = uu;
-    h = dd * h + uu;
-    P *= dd;
   }
 
-  // 2. the state entering the span
+  // 2. sub-spans -> the state entering this wave's sub-span (pp * carry + ph) and the tile aggregate
+  s_sub[w][lane] = make_float2(P, h);
+  __syncthreads();
+  float pp = 1.0f, ph = 0.0f, tp = 1.0f, th = 0.0f;
+#pragma unroll
+  for (int v = 0; v < kScanLbSub; ++v) {
+    const float2 e = s_sub[v][lane];
+    if (v == w) {
+      pp = tp;
+      ph = th;
+    }
+    th = e.x * th + e.y;
+    tp *= e.x;
+  }
+
+  // 3. the tile's carry
   const int64_t fb = b * nc * G + g;      // flag of span k: fb + k * G
   const int64_t vb = b * nc * a.C + chc;  // values of span k: vb + k * C
   float carry;
   if (c == 0) {
     carry = a.h0 ? static_cast<float>(a.h0[b * a.C + chc]) : 0.0f;
   } else {
-    if (on) scan_agg_store(&s.agg[vb + c * a.C], P, h);
+    if (w == 0 && on) scan_agg_store(&s.agg[vb + c * a.C], tp, th);
     __builtin_amdgcn_s_waitcnt(0);  // the value stores are complete before the flag can be stored
-    __syncthreads();
+    __syncthreads();                // (and every wave has read s_sub)
     if (tid == 0) scan_flag_store(&s.flags[fb + c * G], 1);
     float accP = 1.0f, accH = 0.0f;
     int64_t k0 = c - 1;  // nearest span not composed yet; k0 >= 0 (span 0 ends every walk)
     for (;;) {
-      if (wave == 0) {
+      if (w == 0) {
         // lane l watches span k0 - l; lanes before span 0 never report
         const int64_t k = k0 - lane;
         int m = 0, stop = 2;
@@ -425,21 +457,31 @@ __global__ __launch_bounds__(kScanLbThreads) void scan_lb_kernel(ScanArgs a, int
       }
       __syncthreads();
       const int m = s_m, stop = s_stop;
-      // compose spans k0, k0 - 1, .., k0 - m + 1 (all >= 0), 32 loads in flight at a time
-      for (int j0 = 0; j0 < m; j0 += 32) {
-        float2 v[32];
+      // wave w composes window entries j0 .. j1 - 1 (spans k0 - j, all >= 0), nearest first
+      const int j0 = w * 16, j1 = m < j0 + 16 ? m : j0 + 16;
+      float qP = 1.0f, qH = 0.0f;
+      if (j0 < j1) {
+        float2 v[16];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-          const int jj = j0 + j < m ? j0 + j : m - 1;
+        for (int j = 0; j < 16; ++j) {
+          const int jj = j0 + j < j1 ? j0 + j : j1 - 1;
           v[j] = scan_agg_load(&s.agg[vb + (k0 - jj) * a.C]);
         }
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-          if (j0 + j < m) {
-            accH += accP * v[j].y;
-            accP *= v[j].x;
+        for (int j = 0; j < 16; ++j) {
+          if (j0 + j < j1) {
+            qH += qP * v[j].y;
+            qP *= v[j].x;
           }
         }
+      }
+      s_sub[w][lane] = make_float2(qP, qH);
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kScanLbSub; ++q) {
+        const float2 e = s_sub[q][lane];
+        accH += accP * e.y;
+        accP *= e.x;
       }
       if (stop == 1) {
         carry = accH + accP * scan_val_load(&s.incl[vb + (k0 - m) * a.C]);
@@ -450,18 +492,22 @@ __global__ __launch_bounds__(kScanLbThreads) void scan_lb_kernel(ScanArgs a, int
         break;
       }
       k0 -= 64;
-      __syncthreads();  // s_m / s_stop are rewritten by the next round
+      __syncthreads();  // s_m, s_stop and s_sub are rewritten by the next round
     }
   }
-  const float hend = P * carry + h;
-  if (on) scan_val_store(&s.incl[vb + c * a.C], hend);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) scan_flag_store(&s.flags[fb + c * G], 2);
+  const float hend = tp * carry + th;
+  if (c < nc - 1) {  // publish the end state for later spans
+    if (w == 0 && on) scan_val_store(&s.incl[vb + c * a.C], hend);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) scan_flag_store(&s.flags[fb + c * G], 2);
+  } else if (w == 0 && on && a.h_final) {
+    a.h_final[b * a.C + ch] = static_cast<double>(hend);
+  }
 
-  // 3. rescan from the carry and store the states
-  if (!on) return;
-  float hh = carry;
+  // 4. rescan the sub-span from its entering state and store the states
+  if (!on || n <= 0) return;
+  float hh = pp * carry + ph;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     if (i < n) {
@@ -469,26 +515,37 @@ __global__ __launch_bounds__(kScanLbThreads) void scan_lb_kernel(ScanArgs a, int
       st<OUT_DT>(a.states, (b * a.L + t0 + i) * a.ld_states + ch, hh);
     }
   }
-  if (c == nc - 1 && a.h_final) a.h_final[b * a.C + ch] = static_cast<double>(hend);
 }
 
-// Span length for the look-back pass: the largest multiple of the thread-chunk length T within
-// kScanLbTM (T itself when T > kScanLbTM / 2).
-int64_t scan_lb_span(int64_t T) { return T * std::max<int64_t>(1, kScanLbTM / T); }
+// Look-back launch geometry for thread-chunk length T: spans of kScanLbSub * T positions, groups of
+// kScanLbCh channels.
+struct ScanLbShape {
+  int64_t nc, G, tiles;
+};
+ScanLbShape scan_lb_shape(int64_t B, int64_t L, int64_t C, int64_t T) {
+  ScanLbShape g;
+  g.nc = (L + kScanLbSub * T - 1) / (kScanLbSub * T);
+  g.G = (C + kScanLbCh - 1) / kScanLbCh;
+  g.tiles = B * g.nc * g.G;
+  return g;
+}
 
 template <int DT, int OUT_DT, int MODE>
 int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
-  const int64_t TL = scan_lb_span(T);
-  const int64_t nc = (a.L + TL - 1) / TL;
-  const int64_t G = (a.C + kScanLbThreads - 1) / kScanLbThreads;
-  const int64_t tiles = a.B * nc * G;
+  const ScanLbShape sh = scan_lb_shape(a.B, a.L, a.C, T);
   ScanLb s;
   s.agg = reinterpret_cast<float2*>(summ);
-  s.incl = summ + 2 * a.B * nc * a.C;
+  s.incl = summ + 2 * a.B * sh.nc * a.C;
   s.flags = flags;
-  s.ticket = reinterpret_cast<unsigned*>(flags + tiles);
-  scan_lb_reset_kernel<<<static_cast<unsigned>((tiles + 1 + 255) / 256), 256, 0, st>>>(flags, tiles, s.ticket);
-  scan_lb_kernel<DT, OUT_DT, MODE><<<static_cast<unsigned>(tiles), kScanLbThreads, 0, st>>>(a, TL, nc, G, s);
+  s.ticket = reinterpret_cast<unsigned*>(flags + sh.tiles);
+  const int64_t nchain = a.B * sh.G;
+  scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, st>>>(flags, sh.tiles,
+                                                                                               nchain);
+  const unsigned grid = static_cast<unsigned>(sh.tiles);
+  if (T <= 16)
+    scan_lb_kernel<DT, OUT_DT, MODE, 16><<<grid, kScanLbCh * kScanLbSub, 0, st>>>(a, T, sh.nc, sh.G, s);
+  else
+    scan_lb_kernel<DT, OUT_DT, MODE, 32><<<grid, kScanLbCh * kScanLbSub, 0, st>>>(a, T, sh.nc, sh.G, s);
   return check_launch("scan look-back");
 }
 
@@ -555,11 +612,13 @@ int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
   if (L <= 0) return 0;
   const int64_t T = scan_chunk_len(L, cs);
   const int64_t nc = (L + T - 1) / T;
-  const int64_t G = (C + kScanLbThreads - 1) / kScanLbThreads;
-  // chunk aggregates (2 floats) and end states (1 float) per (b, chunk, channel), then the look-back
-  // flags per (b, chunk, channel group) and the tile ticket
+  const int64_t G = (C + kScanLbCh - 1) / kScanLbCh;
+  // chunk summaries and carries (3 floats per (b, chunk, channel); the look-back pass's spans are
+  // longer than chunks, so its aggregates and end states fit too), then the look-back flags per
+  // (b, span, channel group) (at most one span per chunk) and a span counter per (b, channel group),
+  // one 256-byte line each
   return round_up(B * nc * C * 3 * static_cast<int64_t>(sizeof(float)), 256) +
-         round_up((B * nc * G + 64) * static_cast<int64_t>(sizeof(int)), 256);
+         round_up((B * nc * G + B * G * kScanLbTicketStride) * static_cast<int64_t>(sizeof(int)), 256);
 }
 
 int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
@@ -590,9 +649,8 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
                      aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
                      aligned(a.states, 4) && (!a.gated || aligned(a.gated, 4));
-  if (T <= kScanLbTM && aligned(ws, 8) && a.B * nc * ((a.C + kScanLbThreads - 1) / kScanLbThreads) < (1 << 23)) {
-    // single pass with decoupled look-back (the gate buffer of the three-pass path is not needed);
-    // its spans are at least T long, so the summary, end-state and flag regions sized for T suffice
+  if (T <= 32 && aligned(ws, 8) && scan_lb_shape(a.B, a.L, a.C, T).tiles < (1 << 23)) {
+    // single pass with decoupled look-back (the gate buffer of the three-pass path is not needed)
     const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
     switch (key) {
       case 0: return run_scan_lb<kF32, kF32, 0>(e, T, summ, flags, st);
