@@ -128,7 +128,7 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   s.proj = c.take<void>(M * n_in * es);
   s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
   s.scan_ws = c.take<void>(s.scan_bytes);
-  s.gated = c.take<void>(2 * M * p.d_state * es);
+  s.gated = nullptr;  // the plan's scan workspace is aligned, so the single-pass scan runs: no gate buffer
   s.wts = nullptr;
   s.e_tanh = s.c_mix = nullptr;
   s.g_tern = nullptr;
