@@ -579,7 +579,13 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
                 o_q = 2 * dm + 3 * D, o_k = 2 * dm + 3 * D + R;
   int rc;
   // 1. in_proj
-  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  // the u quantization also clears the single-pass scan's flags, saving the scan its reset launch
+  int* scan_zero = nullptr;
+  int64_t scan_zero_n = 0;
+  scan_lb_clear_range(p.B, p.L, D, p.chunk_size, s.scan_ws, &scan_zero, &scan_zero_n);
+  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st, scan_zero,
+                             scan_zero_n)))
+    return rc;
   if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
   if (p.proj_out) {
     if (hipMemcpyAsync(p.proj_out, proj, M * n_in * es, hipMemcpyDeviceToDevice, st) != hipSuccess)
@@ -614,6 +620,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   sa.ld_states = D;
   sa.h_final = p.h_final;
   sa.gated = s.gated;
+  sa.flags_clear = scan_zero_n > 0;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   // 4. local entanglement + mix (tesm.py:853-952, 1231-1232), quantized for state_proj / ent_proj
   EntArgs ea = siso_ent_shape(p);
@@ -1020,7 +1027,13 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
                 o_q = 2 * dm + 3 * HD, o_k = 2 * dm + 3 * HD + HR;
   int rc;
   // 1. in_proj
-  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
+  // the u quantization also clears the single-pass scan's flags, saving the scan its reset launch
+  int* scan_zero = nullptr;
+  int64_t scan_zero_n = 0;
+  scan_lb_clear_range(p.B, p.L, HD, 16, s.scan_ws, &scan_zero, &scan_zero_n);
+  if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st, scan_zero,
+                             scan_zero_n)))
+    return rc;
   if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
   // 2. gates + rank-free state scan: sequential float32 recurrence h = d h + w tanh(sv) per channel
   ScanArgs sa;
@@ -1042,6 +1055,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   sa.decay_bias = p.decay_bias;
   sa.states = s.S;
   sa.ld_states = HD;
+  sa.flags_clear = scan_zero_n > 0;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   if ((rc = launch_mimo_final(s.S, p.mimo_x0sq, p.B, p.L, HD, p.h_final, p.last_state, st))) return rc;
   const void* q_raw = proj + o_q * es;

@@ -77,8 +77,13 @@ template <int DT, bool VEC, int LPR, int G>
 __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__ x, int64_t M, int64_t K,
                                                         int64_t ldx, float eps, int layout, int8_t* __restrict__ q,
                                                         int64_t ldq, float* __restrict__ s_out,
-                                                        int32_t* __restrict__ rowsum) {
+                                                        int32_t* __restrict__ rowsum, int* __restrict__ zero_p,
+                                                        int64_t zero_n) {
   constexpr int RPW = 64 / LPR;
+  // side job for a later kernel of the same stream: clear zero_n ints (a fill launch saved)
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < zero_n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    zero_p[i] = 0;
   const int lane = threadIdx.x & 63;
   const int g0 = lane & (LPR - 1);
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
@@ -132,44 +137,45 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__
 
 template <int DT, bool VEC, int LPR, int G>
 void run_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
-               float* s_x, int32_t* rowsum, hipStream_t st) {
+               float* s_x, int32_t* rowsum, int* zero_p, int64_t zero_n, hipStream_t st) {
   constexpr int RPB = 4 * (64 / LPR);
-  const unsigned nb = static_cast<unsigned>((M + RPB - 1) / RPB);
-  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum);
+  const unsigned nb = static_cast<unsigned>(std::max<int64_t>((M + RPB - 1) / RPB, zero_n > 0 ? 1 : 0));
+  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n);
 }
 
 template <int DT, bool VEC>
 void dispatch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
-                    float* s_x, int32_t* rowsum, hipStream_t st) {
+                    float* s_x, int32_t* rowsum, int* zp, int64_t zn, hipStream_t st) {
   const int64_t ng = ldq / 16;
-  if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 8) return run_quant<DT, VEC, 8, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 16) return run_quant<DT, VEC, 16, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 32) return run_quant<DT, VEC, 32, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 64) return run_quant<DT, VEC, 64, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 128) return run_quant<DT, VEC, 64, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 256) return run_quant<DT, VEC, 64, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  if (ng <= 512) return run_quant<DT, VEC, 64, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-  return run_quant<DT, VEC, 64, 0>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+  if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 8) return run_quant<DT, VEC, 8, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 16) return run_quant<DT, VEC, 16, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 32) return run_quant<DT, VEC, 32, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 64) return run_quant<DT, VEC, 64, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 128) return run_quant<DT, VEC, 64, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 256) return run_quant<DT, VEC, 64, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 512) return run_quant<DT, VEC, 64, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  return run_quant<DT, VEC, 64, 0>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
 }
 
 int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
-                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st) {
+                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p, int64_t zero_n) {
   TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "quant_act: dtype must be 0 (f32) or 1 (bf16)");
   TESM_REQUIRE(M >= 0 && K >= 1 && ldx >= K, kErrInvalidArg, "quant_act: need M >= 0, K >= 1, ldx >= K");
   TESM_REQUIRE(ldq >= K && ldq % 16 == 0, kErrInvalidArg, "quant_act: ldq must be >= K and a multiple of 16");
   TESM_REQUIRE(layout == 0 || layout == 1, kErrInvalidArg, "quant_act: layout must be 0 or 1");
   TESM_REQUIRE(M == 0 || (x && q && s_x), kErrInvalidArg, "quant_act: null pointer");
   TESM_REQUIRE(aligned(q, 16), kErrAlignment, "quant_act: code buffer must be 16-byte aligned");
-  if (M == 0) return kOk;
+  TESM_REQUIRE(zero_n == 0 || zero_p, kErrInvalidArg, "quant_act: null range to clear");
+  if (M == 0 && zero_n == 0) return kOk;  // with M == 0 one workgroup still clears the side range
   const int esz = dt == kBF16 ? 2 : 4;
   const bool vec = aligned(x, 16) && (ldx * esz) % 16 == 0;
   if (dt == kBF16) {
-    if (vec) dispatch_quant<kBF16, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-    else dispatch_quant<kBF16, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+    if (vec) dispatch_quant<kBF16, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
+    else dispatch_quant<kBF16, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
   } else {
-    if (vec) dispatch_quant<kF32, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
-    else dispatch_quant<kF32, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st);
+    if (vec) dispatch_quant<kF32, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
+    else dispatch_quant<kF32, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
   }
   return check_launch("quant_act");
 }

@@ -29,10 +29,16 @@ struct ScanArgs {
   // mode 1 with round_update: optional (2, B*L, C) dt buffer; the summary pass stores the gated
   // decay and update there and the apply pass reads them instead of recomputing the gates
   void* gated = nullptr;
+  // 1: the single-pass scan's flags and span counters in the workspace are already zero (the caller
+  // cleared the range scan_lb_clear_range names, in an earlier kernel of the same stream)
+  int flags_clear = 0;
 };
 
 int64_t scan_chunk_len(int64_t L, int64_t cs);
 int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs);
 int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st);
+// The int range of the workspace the single-pass scan needs zero at its start (*n = 0 when that
+// pass will not run for these sizes and this workspace).
+void scan_lb_clear_range(int64_t B, int64_t L, int64_t C, int64_t cs, void* ws, int** p, int64_t* n);
 
 }  // namespace tesm

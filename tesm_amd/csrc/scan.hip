@@ -539,8 +539,9 @@ int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream
   s.flags = flags;
   s.ticket = reinterpret_cast<unsigned*>(flags + sh.tiles);
   const int64_t nchain = a.B * sh.G;
-  scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, st>>>(flags, sh.tiles,
-                                                                                               nchain);
+  if (!a.flags_clear)
+    scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, st>>>(flags, sh.tiles,
+                                                                                                 nchain);
   const unsigned grid = static_cast<unsigned>(sh.tiles);
   if (T <= 16)
     scan_lb_kernel<DT, OUT_DT, MODE, 16><<<grid, kScanLbCh * kScanLbSub, 0, st>>>(a, T, sh.nc, sh.G, s);
@@ -608,6 +609,27 @@ int64_t scan_chunk_len(int64_t L, int64_t cs) {
   return cse >= 16 ? cse : cse * (16 / cse);
 }
 
+namespace {
+bool scan_lb_eligible(int64_t B, int64_t L, int64_t C, int64_t T, const void* ws) {
+  return T <= 32 && aligned(ws, 8) && scan_lb_shape(B, L, C, T).tiles < (1 << 23);
+}
+// the flag region follows the chunk summaries and carries (nc = chunks of the thread-chunk length)
+int* scan_lb_flags(int64_t B, int64_t C, int64_t nc, void* ws) {
+  return reinterpret_cast<int*>(static_cast<char*>(ws) + round_up(B * nc * C * 3 * static_cast<int64_t>(sizeof(float)), 256));
+}
+}  // namespace
+
+void scan_lb_clear_range(int64_t B, int64_t L, int64_t C, int64_t cs, void* ws, int** p, int64_t* n) {
+  *p = nullptr;
+  *n = 0;
+  if (B <= 0 || L <= 0 || C <= 0 || !ws) return;
+  const int64_t T = scan_chunk_len(L, cs);
+  if (!scan_lb_eligible(B, L, C, T, ws)) return;
+  const ScanLbShape sh = scan_lb_shape(B, L, C, T);
+  *p = scan_lb_flags(B, C, (L + T - 1) / T, ws);
+  *n = sh.tiles + B * sh.G * kScanLbTicketStride;  // flags, then the strided chain counters
+}
+
 int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
   if (L <= 0) return 0;
   const int64_t T = scan_chunk_len(L, cs);
@@ -640,8 +662,7 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   TESM_REQUIRE(nc <= 65535 && a.B <= 65535, kErrUnsupported, "scan: too many chunks or batch rows");
   float* summ = static_cast<float*>(ws);
   float* carry = summ + 2 * a.B * nc * a.C;
-  int* flags = reinterpret_cast<int*>(static_cast<char*>(ws) +
-                                      round_up(a.B * nc * a.C * 3 * static_cast<int64_t>(sizeof(float)), 256));
+  int* flags = scan_lb_flags(a.B, a.C, nc, ws);
   // the reference chunk grid starts at 0 with chunk = min(cs, L); pass the effective value
   ScanArgs e = a;
   e.cs = std::max<int64_t>(1, std::min(a.cs, a.L));
@@ -649,7 +670,7 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
                      aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
                      aligned(a.states, 4) && (!a.gated || aligned(a.gated, 4));
-  if (T <= 32 && aligned(ws, 8) && scan_lb_shape(a.B, a.L, a.C, T).tiles < (1 << 23)) {
+  if (scan_lb_eligible(a.B, a.L, a.C, T, ws)) {
     // single pass with decoupled look-back (the gate buffer of the three-pass path is not needed)
     const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
     switch (key) {

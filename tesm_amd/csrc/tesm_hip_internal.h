@@ -9,8 +9,10 @@ namespace tesm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// zero_p / zero_n: an int range the kernel also clears (for a later kernel of the same stream).
 int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
-                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st);
+                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p = nullptr,
+                     int64_t zero_n = 0);
 int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, float* s_w, float* c_w, hipStream_t st);
 int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
                 uint8_t* packed, int64_t ldp, hipStream_t st);
