@@ -85,7 +85,10 @@ int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const 
  * TESM_SISO._parallel_state_scan (tesm.py:1091-1164, torch branch; chunk_size = state_scan_chunk_size
  * reproduces its 1e-12 clamp semantics) and chunk_state_scan (ops/cuda/__init__.py:140-150).
  * decay/update: element (b,t,c) at ptr[(b*L+t)*ld + c], dt; states likewise in out_dt.
- * h0, h_final: (B, C) float64, nullable.  ws: tesm_hip_scan_ws_bytes() bytes. */
+ * h0, h_final: (B, C) float64, nullable.  ws: tesm_hip_scan_ws_bytes() bytes, any contents (each call
+ * clears what it uses); with ws 8-byte aligned and chunk_size <= 32 the scan is one pass (decoupled
+ * look-back across workgroups), otherwise three passes.  Calls that share a workspace must be ordered
+ * (same stream). */
 int64_t tesm_hip_scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t chunk_size);
 int tesm_hip_scan(const void* decay, int64_t ld_decay, const void* update, int64_t ld_update, int dt, int64_t B,
                   int64_t L, int64_t C, int64_t chunk_size, const double* h0, void* states, int64_t ld_states,
