@@ -86,7 +86,6 @@ struct SisoPlan {
   void* proj;
   void* scan_ws;
   int64_t scan_bytes;
-  void* gated;  // gated decay / update handed from the scan's summary pass to its apply pass
   float* wts;
   void* e_tanh;
   void* c_mix;
@@ -128,7 +127,6 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   s.proj = c.take<void>(M * n_in * es);
   s.scan_bytes = scan_ws_bytes(p.B, p.L, p.d_state, p.chunk_size);
   s.scan_ws = c.take<void>(s.scan_bytes);
-  s.gated = nullptr;  // the plan's scan workspace is aligned, so the single-pass scan runs: no gate buffer
   s.wts = nullptr;
   s.e_tanh = s.c_mix = nullptr;
   s.g_tern = nullptr;
@@ -619,7 +617,6 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   sa.states = p.states;
   sa.ld_states = D;
   sa.h_final = p.h_final;
-  sa.gated = s.gated;
   sa.flags_clear = scan_zero_n > 0;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   // 4. local entanglement + mix (tesm.py:853-952, 1231-1232), quantized for state_proj / ent_proj

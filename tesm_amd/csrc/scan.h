@@ -26,9 +26,6 @@ struct ScanArgs {
   void* states = nullptr;        // (b, t, c) at states[(b*L + t)*ld_states + c], out_dt
   int64_t ld_states = 0;
   double* h_final = nullptr;     // (B, C) final state or null
-  // mode 1 with round_update: optional (2, B*L, C) dt buffer; the summary pass stores the gated
-  // decay and update there and the apply pass reads them instead of recomputing the gates
-  void* gated = nullptr;
   // 1: the single-pass scan's flags and span counters in the workspace are already zero (the caller
   // cleared the range scan_lb_clear_range names, in an earlier kernel of the same stream)
   int flags_clear = 0;

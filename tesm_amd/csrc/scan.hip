@@ -9,7 +9,9 @@
 // falls below 1e-12; the kernels reproduce that factor ("clamp" mode) and run the recurrence in
 // fp32 registers.
 //
-// Three launches, all channel-parallel (lanes along C, coalesced):
+// Default: one pass with decoupled look-back across workgroups (scan_lb_kernel, below), which reads
+// the inputs once.  Fallback (chunks longer than 32 positions, or a workspace that is not 8-byte
+// aligned): three launches, all channel-parallel (lanes along C, coalesced):
 //   1. summary: each (b, chunk of T positions, channel) scans its chunk from h = 0 and stores
 //      (prod d, h_end);
 //   2. carry:   each (b, channel) folds the chunk summaries in order -> carry into every chunk
@@ -152,26 +154,6 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
       if (i >= n) {
         d[i][j] = 1.0f;
         u[i][j] = 0.0f;
-      }
-    }
-  }
-  if constexpr (MODE == 1 && PHASE == 1) {
-    if (a.gated) {  // the gated decay and update, for the apply pass (dt values, (B*L, C) each)
-      const int64_t plane = a.B * a.L * a.C;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        if (i >= n) continue;
-        const int64_t o = (b * a.L + t0 + i) * a.C + ch;
-        if constexpr (DT == kBF16 && CPT == 2) {
-          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.gated) + o) = pack_bf16x2(d[i][0], d[i][1]);
-          *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.gated) + plane + o) = pack_bf16x2(u[i][0], u[i][1]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < CPT; ++j) {
-            st<DT>(a.gated, o + j, d[i][j]);
-            st<DT>(a.gated, plane + o + j, u[i][j]);
-          }
-        }
       }
     }
   }
@@ -563,18 +545,7 @@ int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* 
     scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, st>>>(a, nc, summ, carry);
   else
     scan_carry_seg_kernel<4><<<g2, 4 * 64, 0, st>>>(a, nc, summ, carry);
-  if (MODE == 1 && a.gated) {
-    // apply pass on the stored gates: a plain decay / update scan
-    ScanArgs g = a;
-    g.mode = 0;
-    g.decay = a.gated;
-    g.ld_decay = a.C;
-    g.update = static_cast<const char*>(a.gated) + a.B * a.L * a.C * (DT == kBF16 ? 2 : 4);
-    g.ld_update = a.C;
-    scan_fast_kernel<DT, OUT_DT, 0, 3, TM, CPT><<<nb, 256, 0, st>>>(g, T, nc, summ, carry);
-  } else {
-    scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
-  }
+  scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
   return check_launch("scan");
 }
 
@@ -653,8 +624,6 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   TESM_REQUIRE(a.ld_decay >= a.C && a.ld_update >= a.C && a.ld_states >= a.C, kErrInvalidArg, "scan: ld < C");
   if (a.mode == 1)
     TESM_REQUIRE(a.sv && a.decay_bias && a.ld_sv >= a.C, kErrInvalidArg, "scan mode 1: need sv and decay_bias");
-  TESM_REQUIRE(!a.gated || (a.mode == 1 && a.round_update && a.out_dt == a.dt), kErrInvalidArg,
-               "scan: a gate buffer needs mode 1 with rounded updates");
   const int64_t need = scan_ws_bytes(a.B, a.L, a.C, a.cs);
   TESM_REQUIRE(ws && ws_bytes >= need, kErrWorkspace, "scan: workspace too small");
   const int64_t T = scan_chunk_len(a.L, a.cs);
@@ -669,9 +638,9 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   const bool pairs = a.dt == kBF16 && a.C % 2 == 0 && a.ld_decay % 2 == 0 && a.ld_update % 2 == 0 &&
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
                      aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
-                     aligned(a.states, 4) && (!a.gated || aligned(a.gated, 4));
+                     aligned(a.states, 4);
   if (scan_lb_eligible(a.B, a.L, a.C, T, ws)) {
-    // single pass with decoupled look-back (the gate buffer of the three-pass path is not needed)
+    // single pass with decoupled look-back
     const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
     switch (key) {
       case 0: return run_scan_lb<kF32, kF32, 0>(e, T, summ, flags, st);
