@@ -241,8 +241,8 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 }
 
 // ---------------------------------------------------------------------------
-// Single pass with decoupled look-back.  A tile is (batch row b, span c of 4 T positions, group g of
-// 64 channels); its 4 waves take one sub-span of T positions each (T is a multiple of the
+// Single pass with decoupled look-back.  A tile is (batch row b, span c of SUB T positions, group g
+// of 64 channels); its SUB waves (4 or 8) take one sub-span of T positions each (T is a multiple of the
 // reference chunk, so the clamp's running product restarts inside a wave) and its lanes one channel
 // each.  The workgroup index fixes the chain (b, g); the span c is the ticket the workgroup takes
 // from its chain's counter when it starts, so every tile a tile waits on (earlier spans of its
@@ -250,13 +250,13 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 // ends.  One counter per chain, each on its own 256-byte line, keeps the ticket atomics from
 // queueing on one cache line.
 //
-// A wave loads its sub-span and gates once and scans it from h = 0; the four sub-span aggregates
+// A wave loads its sub-span and gates once and scans it from h = 0; the sub-span aggregates
 // (prod d, h_end) meet in LDS, giving each wave the state entering its sub-span as a function of
 // the tile's carry, and the tile's aggregate, which the tile publishes (flag 1).  It then finds
 // its carry by looking back over earlier spans of the same (b, g), 64 at a time: wave 0 polls the
 // flags, the nearest span whose end state is published (flag 2) ends the walk, and the aggregates
-// in between are composed nearest first (a quarter of the window per wave, the quarters combined
-// through LDS).  Span 0 publishes its end state directly, so a walk never passes it.  The tile
+// in between are composed nearest first (an equal share of the window per wave, the shares
+// combined through LDS).  Span 0 publishes its end state directly, so a walk never passes it.  The tile
 // publishes its own end state (flag 2) and every wave rescans its sub-span from registers, writing
 // the states.  A reset kernel clears the flags and the ticket before each pass.
 //
@@ -269,7 +269,8 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 // treats what it could not see as a zero state), so the launch completes whatever happens.
 // ---------------------------------------------------------------------------
 constexpr int kScanLbCh = 64;    // channels per tile (one per lane)
-constexpr int kScanLbSub = 4;    // sub-spans per tile (one per wave)
+// sub-spans per tile (one per wave): 4, or 8 for long chains (fewer spans to chain; with few spans
+// per chain the shorter tile keeps more workgroups in flight)
 constexpr int kScanSpinLimit = 1 << 20;
 
 struct ScanLb {
@@ -309,12 +310,13 @@ __device__ __forceinline__ float scan_val_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int OUT_DT, int MODE, int TM>
-__global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArgs a, int64_t T, int64_t nc, int64_t G,
-                                                                         ScanLb s) {
+template <int DT, int OUT_DT, int MODE, int TM, int SUB>
+__global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, int64_t T, int64_t nc, int64_t G,
+                                                                  ScanLb s) {
+  constexpr int WIN = 64 / SUB;  // look-back window entries composed per wave
   __shared__ unsigned s_tile;
   __shared__ int s_m, s_stop;
-  __shared__ float2 s_sub[kScanLbSub][kScanLbCh];  // sub-span aggregates, then window quarters
+  __shared__ float2 s_sub[SUB][kScanLbCh];  // sub-span aggregates, then window shares
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t chain = blockIdx.x % (a.B * G);  // grid = nc workgroups per chain
   if (tid == 0) s_tile = atomicAdd(&s.ticket[chain * kScanLbTicketStride], 1u);
@@ -324,7 +326,7 @@ __global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArg
   const int64_t ch = g * kScanLbCh + lane;
   const bool on = ch < a.C;
   const int64_t chc = on ? ch : a.C - 1;  // idle lanes read a valid channel and store nothing
-  const int64_t t0 = (c * kScanLbSub + w) * T;  // this wave's first position
+  const int64_t t0 = (c * SUB + w) * T;  // this wave's first position
   const int n = t0 >= a.L ? 0 : static_cast<int>(t0 + T < a.L ? T : a.L - t0);  // wave-uniform
 
   // 1. the sub-span's inputs and gates (all loads in flight at once; positions past the end re-read
@@ -382,7 +384,7 @@ __global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArg
   __syncthreads();
   float pp = 1.0f, ph = 0.0f, tp = 1.0f, th = 0.0f;
 #pragma unroll
-  for (int v = 0; v < kScanLbSub; ++v) {
+  for (int v = 0; v < SUB; ++v) {
     const float2 e = s_sub[v][lane];
     if (v == w) {
       pp = tp;
@@ -440,17 +442,17 @@ __global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArg
       __syncthreads();
       const int m = s_m, stop = s_stop;
       // wave w composes window entries j0 .. j1 - 1 (spans k0 - j, all >= 0), nearest first
-      const int j0 = w * 16, j1 = m < j0 + 16 ? m : j0 + 16;
+      const int j0 = w * WIN, j1 = m < j0 + WIN ? m : j0 + WIN;
       float qP = 1.0f, qH = 0.0f;
       if (j0 < j1) {
-        float2 v[16];
+        float2 v[WIN];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < WIN; ++j) {
           const int jj = j0 + j < j1 ? j0 + j : j1 - 1;
           v[j] = scan_agg_load(&s.agg[vb + (k0 - jj) * a.C]);
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < WIN; ++j) {
           if (j0 + j < j1) {
             qH += qP * v[j].y;
             qP *= v[j].x;
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArg
       s_sub[w][lane] = make_float2(qP, qH);
       __syncthreads();
 #pragma unroll
-      for (int q = 0; q < kScanLbSub; ++q) {
+      for (int q = 0; q < SUB; ++q) {
         const float2 e = s_sub[q][lane];
         accH += accP * e.y;
         accP *= e.x;
@@ -499,14 +501,16 @@ __global__ __launch_bounds__(kScanLbCh * kScanLbSub) void scan_lb_kernel(ScanArg
   }
 }
 
-// Look-back launch geometry for thread-chunk length T: spans of kScanLbSub * T positions, groups of
+// Look-back launch geometry for thread-chunk length T: spans of sub * T positions, groups of
 // kScanLbCh channels.
 struct ScanLbShape {
   int64_t nc, G, tiles;
+  int sub;
 };
 ScanLbShape scan_lb_shape(int64_t B, int64_t L, int64_t C, int64_t T) {
   ScanLbShape g;
-  g.nc = (L + kScanLbSub * T - 1) / (kScanLbSub * T);
+  g.sub = (L + 4 * T - 1) / (4 * T) > 16 ? 8 : 4;
+  g.nc = (L + g.sub * T - 1) / (g.sub * T);
   g.G = (C + kScanLbCh - 1) / kScanLbCh;
   g.tiles = B * g.nc * g.G;
   return g;
@@ -525,10 +529,17 @@ int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream
     scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, st>>>(flags, sh.tiles,
                                                                                                  nchain);
   const unsigned grid = static_cast<unsigned>(sh.tiles);
-  if (T <= 16)
-    scan_lb_kernel<DT, OUT_DT, MODE, 16><<<grid, kScanLbCh * kScanLbSub, 0, st>>>(a, T, sh.nc, sh.G, s);
-  else
-    scan_lb_kernel<DT, OUT_DT, MODE, 32><<<grid, kScanLbCh * kScanLbSub, 0, st>>>(a, T, sh.nc, sh.G, s);
+  if (sh.sub == 8) {
+    if (T <= 16)
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 8><<<grid, kScanLbCh * 8, 0, st>>>(a, T, sh.nc, sh.G, s);
+    else
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 8><<<grid, kScanLbCh * 8, 0, st>>>(a, T, sh.nc, sh.G, s);
+  } else {
+    if (T <= 16)
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 4><<<grid, kScanLbCh * 4, 0, st>>>(a, T, sh.nc, sh.G, s);
+    else
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 4><<<grid, kScanLbCh * 4, 0, st>>>(a, T, sh.nc, sh.G, s);
+  }
   return check_launch("scan look-back");
 }
 
