@@ -265,8 +265,8 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 // L2s, without the whole-L2 write-back and invalidate an agent-scope release / acquire costs).  A
 // writer waits for its value stores to complete (s_waitcnt) before the workgroup barrier after which
 // one thread stores the flag; a reader polls flags in one wave, and the other waves read values
-// only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds (the tile then
-// treats what it could not see as a zero state), so the launch completes whatever happens.
+// only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds (the tile's
+// states are then NaN, so the failure shows in the outputs), so the launch completes whatever happens.
 // ---------------------------------------------------------------------------
 constexpr int kScanLbCh = 64;    // channels per tile (one per lane)
 // sub-spans per tile (one per wave): 4, or 8 for long chains (fewer spans to chain; with few spans
@@ -471,8 +471,8 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
         carry = accH + accP * scan_val_load(&s.incl[vb + (k0 - m) * a.C]);
         break;
       }
-      if (stop == 2) {  // gave up waiting: the spans not seen count as a zero state
-        carry = accH;
+      if (stop == 2) {  // gave up waiting: NaN states make the failure visible instead of plausible
+        carry = __builtin_nanf("");
         break;
       }
       k0 -= 64;
