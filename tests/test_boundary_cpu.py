@@ -160,3 +160,20 @@ def test_lm_construction_matches_reference():
     mine = TESMLMHeadModel(cfg).state_dict()
     assert set(ref) == set(mine)
     assert all(torch.equal(ref[k], mine[k]) for k in ref)
+
+
+@pytest.mark.parametrize("B,L,C,cs", [(4, 2048, 256, 16), (1, 5, 16, 16), (2, 129, 33, 7), (32, 64, 256, 16),
+                                      (1, 32768, 8192, 16), (3, 77, 40, 64)])
+def test_scan_workspace_size(B, L, C, cs):
+    """Host logic only: the scan workspace holds the chunk summaries and carries (12 B per batch row,
+    chunk and channel), then the look-back flags (one int per row, chunk and 64-channel group) and one
+    256-byte counter line per (row, 64-channel group), each region rounded up to 256 bytes."""
+    lib = _lib.load()
+    cse = max(1, min(cs, L))
+    T = cse if cse >= 16 else cse * (16 // cse)
+    nc = -(-L // T)
+    G = -(-C // 64)
+    up = lambda n: -(-n // 256) * 256
+    want = up(B * nc * C * 12) + up((B * nc * G + B * G * 64) * 4)
+    assert int(lib.tesm_hip_scan_ws_bytes(B, L, C, cs)) == want
+    assert int(lib.tesm_hip_scan_ws_bytes(B, 0, C, cs)) == 0
