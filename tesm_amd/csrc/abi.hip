@@ -767,8 +767,29 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   // 1. in_proj on the B new tokens
   const int64_t ld_u = p.ld_u > 0 ? p.ld_u : dm;
   TESM_REQUIRE(ld_u >= dm, kErrInvalidArg, "decode step: ld_u must be >= d_model");
-  if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
-  if ((rc = run_linear(s.xu, p.in_proj, Bn, n_in, dm, proj, dt, n_in, st))) return rc;
+  {
+    LinearArgs la;
+    la.op[0] = operand(s.xu, p.in_proj);
+    la.M = Bn;
+    la.N = n_in;
+    la.Kp = kpad(dm);
+    la.out = proj;
+    la.out_dt = dt;
+    la.ldo = n_in;
+    if (linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
+      FusedQuantIn f;
+      f.x = p.u;
+      f.ldx = ld_u;
+      f.K = dm;
+      f.eps = p.bit_eps;
+      f.dt = dt;
+      if ((rc = launch_linear_fq(la, f, st))) return rc;
+    } else {
+      if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st)))
+        return rc;
+      if ((rc = launch_linear(la, st))) return rc;
+    }
+  }
   // 2. cross-layer query (tesm.py:1302-1305)
   if (p.cross_state) {
     if ((rc = launch_quant_act(p.cross_state, dt, Bn, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs, st)))
@@ -911,8 +932,29 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
   // 1. in_proj on the B new tokens (tesm_mimo.py:765-781)
   const int64_t ld_u = p.ld_u > 0 ? p.ld_u : dm;
   TESM_REQUIRE(ld_u >= dm, kErrInvalidArg, "mimo decode: ld_u must be >= d_model");
-  if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st))) return rc;
-  if ((rc = run_linear(s.xu, p.in_proj, Bn, n_in, dm, proj, dt, n_in, st))) return rc;
+  {
+    LinearArgs la;
+    la.op[0] = operand(s.xu, p.in_proj);
+    la.M = Bn;
+    la.N = n_in;
+    la.Kp = kpad(dm);
+    la.out = proj;
+    la.out_dt = dt;
+    la.ldo = n_in;
+    if (linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
+      FusedQuantIn f;
+      f.x = p.u;
+      f.ldx = ld_u;
+      f.K = dm;
+      f.eps = p.bit_eps;
+      f.dt = dt;
+      if ((rc = launch_linear_fq(la, f, st))) return rc;
+    } else {
+      if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st)))
+        return rc;
+      if ((rc = launch_linear(la, st))) return rc;
+    }
+  }
   // 2. cross-layer query per head: cross_q_proj over the B * n_heads state rows (tesm_mimo.py:818-826)
   if (p.cross_state) {
     if ((rc = launch_quant_act(p.cross_state, dt, Bn * H, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs,

@@ -567,13 +567,10 @@ __device__ __forceinline__ void skinny_loop(const LinearOperand& o, int64_t M, i
 }
 
 template <int NW, int TM, int TN, int EPI, int OUT_DT>
-__global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
+__device__ __forceinline__ void skinny_body(const LinearArgs& a, int64_t m0, int64_t n0) {
   constexpr int NOP = epi_dual(EPI) ? 2 : 1;
   __shared__ v4i red[(NW - 1) * NOP * TM * TN * 64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t ntn = (a.N + 16 * TN - 1) / (16 * TN);
-  const int64_t tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
-  const int64_t m0 = tm * 16 * TM, n0 = tn * 16 * TN;
   v4i acc0[TM][TN], acc1[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -604,6 +601,72 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
         if constexpr (NOP == 2) acc1[i][j] += red[(((src * NOP + 1) * TM + i) * TN + j) * 64 + lane];
       }
   epilogue16<TM, TN, EPI, OUT_DT>(a, acc0, acc1, m0, n0, 0, 0, lane);
+}
+
+template <int NW, int TM, int TN, int EPI, int OUT_DT>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
+  const int64_t ntn = (a.N + 16 * TN - 1) / (16 * TN);
+  const int64_t tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
+  skinny_body<NW, TM, TN, EPI, OUT_DT>(a, tm * 16 * TM, tn * 16 * TN);
+}
+
+// The same product with the activation quantization fused (decode-size batches): the workgroup
+// quantizes its 16 TM rows of x into LDS exactly as quant_act_kernel does (absmax scale per row,
+// int8 codes in layout 1, code sums), then runs the split-K body on them.  Every workgroup of a row
+// tile repeats the quantization (a few KB of L2 reads each) in exchange for one launch fewer.  LDS
+// rows are Kp + 16 bytes apart, so the 16 rows a K-step reads fall on distinct banks.
+template <int NW, int TM, int TN, int OUT_DT, int DT, bool VEC>
+__global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQuantIn f) {
+  extern __shared__ __attribute__((aligned(16))) char lds_fq[];
+  constexpr int R = 16 * TM, LPR = NW * 64 / R;  // rows of the tile, lanes per row
+  const int64_t ntn = (a.N + 16 * TN - 1) / (16 * TN);
+  const int64_t tm = blockIdx.x / ntn, tn = blockIdx.x - tm * ntn;
+  const int64_t m0 = tm * 16 * TM, n0 = tn * 16 * TN;
+  const int64_t lstride = a.Kp + 16;
+  int8_t* codes = reinterpret_cast<int8_t*>(lds_fq);
+  float* sc_l = reinterpret_cast<float*>(lds_fq + R * lstride);
+  int32_t* rs_l = reinterpret_cast<int32_t*>(sc_l + R);
+  {
+    const int r = threadIdx.x / LPR, g0 = threadIdx.x % LPR;  // LPR consecutive lanes per row
+    const int64_t m = m0 + r, ngroups = a.Kp / 16;
+    int8_t* crow = codes + r * lstride;
+    if (m < a.M) {
+      const int64_t base = m * f.ldx;
+      float amax = 0.0f;
+      for (int64_t g = g0; g < ngroups; g += LPR) {
+        float v[16];
+        load_group<DT, VEC>(f.x, base, f.K, g, v);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      }
+      amax = wave_max<LPR>(amax);
+      const float sc = act_scale<DT>(amax, f.eps);
+      int32_t rs = 0;
+      for (int64_t g = g0; g < ngroups; g += LPR) {
+        float v[16];
+        load_group<DT, VEC>(f.x, base, f.K, g, v);
+        *reinterpret_cast<uint4*>(crow + 16 * g) = group_codes<DT>(v, sc, 1, rs);
+      }
+      rs = wave_sum_i<LPR>(rs);
+      if (g0 == 0) {
+        sc_l[r] = sc;
+        rs_l[r] = rs;
+      }
+    } else {  // rows past M: zero codes (never stored)
+      for (int64_t g = g0; g < ngroups; g += LPR) *reinterpret_cast<uint4*>(crow + 16 * g) = make_uint4(0, 0, 0, 0);
+      if (g0 == 0) {
+        sc_l[r] = 1.0f;
+        rs_l[r] = 0;
+      }
+    }
+  }
+  __syncthreads();
+  LinearArgs b = a;  // operand 0 now reads the LDS copy, indexed by global row as before
+  b.op[0].q = codes - m0 * lstride;
+  b.op[0].ldq = lstride;
+  b.op[0].s_x = sc_l - m0;
+  b.op[0].rowsum = rs_l - m0;
+  skinny_body<NW, TM, TN, kEpiStore, OUT_DT>(b, m0, n0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1768,6 +1831,51 @@ int dispatch_dual(const LinearArgs& a, hipStream_t st) {
   if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, EPI, 3>(a, st);
   if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, EPI>(a, st);
   return run_mfma32<1, 4, 2, 1, EPI>(a, st);
+}
+
+bool linear_fq_ok(const LinearArgs& a) {
+  return a.epilogue == kEpiStore && a.M > 4 && a.M <= 32 && a.N >= 1 && a.N < 16384 && a.Kp >= kKTile &&
+         a.Kp % kKTile == 0 && a.Kp <= 1920;  // LDS: 32 rows of Kp + 16 bytes within 64 KB
+}
+
+namespace {
+template <int TM, int DT, bool VEC>
+void run_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
+  const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 15) / 16);
+  const size_t lds = static_cast<size_t>(16 * TM * (a.Kp + 16) + 16 * TM * 8);
+  if (a.out_dt == kBF16)
+    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+  else
+    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+}
+template <int TM>
+void dispatch_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, bool vec, hipStream_t st) {
+  if (f.dt == kBF16) {
+    if (vec) run_skinny_fq<TM, kBF16, true>(a, f, st);
+    else run_skinny_fq<TM, kBF16, false>(a, f, st);
+  } else {
+    if (vec) run_skinny_fq<TM, kF32, true>(a, f, st);
+    else run_skinny_fq<TM, kF32, false>(a, f, st);
+  }
+}
+}  // namespace
+
+int launch_linear_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
+  TESM_REQUIRE(linear_fq_ok(a), kErrUnsupported, "bitlinear fused quant: needs 4 < M <= 32, N < 16384, Kp <= 1920");
+  TESM_REQUIRE(f.dt == kF32 || f.dt == kBF16, kErrInvalidArg, "bitlinear fused quant: x dtype must be 0 or 1");
+  TESM_REQUIRE(f.x && f.K >= 1 && f.K <= a.Kp && f.ldx >= f.K, kErrInvalidArg, "bitlinear fused quant: bad x");
+  TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "bitlinear: out dtype must be 0 or 1");
+  TESM_REQUIRE(a.out && a.ldo >= a.N, kErrInvalidArg, "bitlinear: need out and ldo >= N");
+  const LinearOperand& o = a.op[0];
+  TESM_REQUIRE(o.w && o.c_w && o.ldw >= a.Kp / 4 && o.ldw % 16 == 0 && aligned(o.w, 16), kErrInvalidArg,
+               "bitlinear fused quant: bad packed weights");
+  const int esz = f.dt == kBF16 ? 2 : 4;
+  const bool vec = aligned(f.x, 16) && (f.ldx * esz) % 16 == 0;
+  if (a.M <= 16)
+    dispatch_skinny_fq<1>(a, f, vec, st);
+  else
+    dispatch_skinny_fq<2>(a, f, vec, st);
+  return check_launch("bitlinear skinny (fused quant)");
 }
 
 int launch_linear(const LinearArgs& a, hipStream_t st) {

@@ -13,62 +13,6 @@
 
 namespace tesm {
 
-// Load the 16 values of code group g (codes 16g..16g+15) of one row, zero past K.
-template <int DT, bool VEC>
-__device__ __forceinline__ void load_group(const void* __restrict__ x, int64_t base, int64_t K, int64_t g,
-                                           float (&v)[16]) {
-  const int64_t k0 = g * 16;
-  if (VEC && k0 + 16 <= K) {
-    if constexpr (DT == kBF16) {
-      const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + k0);
-      const uint4 a = p[0], b = p[1];
-      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        v[2 * i] = __uint_as_float(w[i] << 16);
-        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-      }
-    } else {
-      const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + k0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 f = p[i];
-        v[4 * i] = f.x;
-        v[4 * i + 1] = f.y;
-        v[4 * i + 2] = f.z;
-        v[4 * i + 3] = f.w;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (k0 + i < K) ? ld<DT>(x, base + k0 + i) : 0.0f;
-  }
-}
-
-// Codes of one group, packed in the requested layout; adds the codes to rs.
-template <int DT>
-__device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int layout, int32_t& rs) {
-  uint32_t c[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int ci = act_code<DT>(v[i], sc);
-    rs += ci;
-    c[i] = static_cast<uint32_t>(ci) & 0xffu;
-  }
-  uint4 out;
-  if (layout == 1) {
-    out.x = c[0] | (c[4] << 8) | (c[8] << 16) | (c[12] << 24);
-    out.y = c[1] | (c[5] << 8) | (c[9] << 16) | (c[13] << 24);
-    out.z = c[2] | (c[6] << 8) | (c[10] << 16) | (c[14] << 24);
-    out.w = c[3] | (c[7] << 8) | (c[11] << 16) | (c[15] << 24);
-  } else {
-    out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    out.z = c[8] | (c[9] << 8) | (c[10] << 16) | (c[11] << 24);
-    out.w = c[12] | (c[13] << 8) | (c[14] << 16) | (c[15] << 24);
-  }
-  return out;
-}
 
 // LPR lanes per row (64 / LPR rows per wave, 4 waves per workgroup).  Each lane owns code groups
 // lane, lane + LPR, ... ; with G > 0 its G groups stay in registers between the amax and the code

@@ -58,6 +58,19 @@ struct LinearArgs {
 
 int launch_linear(const LinearArgs& a, hipStream_t st);
 
+// Raw activations for a product that quantizes them itself (x: (M, ldx) in dt, K values per row).
+struct FusedQuantIn {
+  const void* x = nullptr;
+  int64_t ldx = 0, K = 0;
+  float eps = 0.0f;
+  int dt = 0;
+};
+// Store-epilogue product with the per-token activation quantization fused in (one launch instead
+// of quant_act + product); linear_fq_ok tells whether the sizes allow it.  Operand 0's q / s_x /
+// rowsum are not read.
+bool linear_fq_ok(const LinearArgs& a);
+int launch_linear_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st);
+
 // Per-token int8 codes of the output-gate result y (the out_proj input), written instead of y.
 struct RowQuant {
   int8_t* q = nullptr;   // (M, ldq) layout-1 codes

@@ -111,6 +111,43 @@ def test_decode_random_vs_oracle(dtype, P, steps, W, cross):
         assert got[f"step{s}_seq_pos"] == want[f"step{s}_seq_pos"]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [20, 32])
+def test_decode_batch_tiles_vs_oracle(dtype, B):
+    """Batches of 17-32 sequences: the in_proj product runs on 32-row tiles with the activation
+    quantization inside it."""
+    P, steps, W, cross = 12, 4, 8, True
+    dm, D, R = 96, 48, 16
+    meta = dict(seed=11 + P + W, dm=dm, D=D, R=R, W=W)
+    ref = _module(ot.TESM_SISO, meta).to(dtype)
+    m = _module(TESM_SISO, meta).to(DEV).to(dtype)
+    gen = torch.Generator().manual_seed(5 + P)
+    u = torch.randn(B, P + steps, dm, generator=gen).to(dtype)
+    cs = torch.randn(B, P + steps, D, generator=gen).to(dtype) if cross else None
+    want = _run(ref, u, cs, P, steps, B, "cpu")
+    got = _run(m, u.to(DEV), cs.to(DEV) if cs is not None else None, P, steps, B, DEV)
+    tol = TOL[dtype]
+    for s in range(steps):
+        a, b = to_np(got[f"step{s}_y"]).reshape(B, -1), to_np(want[f"step{s}_y"]).reshape(B, -1)
+        if dtype == torch.float32:
+            flip_aware(a, b, row_tol=1e-4, max_flip_frac=0.2, bound=2e-2)
+        else:
+            flip_aware(a, b, row_tol=tol, max_flip_frac=0.4, bound=0.1)
+        if dtype == torch.float32:
+            np.testing.assert_allclose(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy(),
+                                       rtol=1e-4, atol=1e-5)
+        else:
+            # bf16 gates: a one-ulp difference of an in_proj output moves decay / write / tanh(sv) by
+            # one bf16 ulp, which the float64 state then carries; the bar is normwise
+            assert normwise(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy()) <= tol
+        assert normwise(to_np(got[f"step{s}_kcache"]), to_np(want[f"step{s}_kcache"])) <= (
+            1e-5 if dtype == torch.float32 else tol)
+        assert normwise(to_np(got[f"step{s}_vcache"]), to_np(want[f"step{s}_vcache"])) <= (
+            1e-5 if dtype == torch.float32 else tol)
+        assert got[f"step{s}_cache_idx"] == want[f"step{s}_cache_idx"]
+        assert got[f"step{s}_seq_pos"] == want[f"step{s}_seq_pos"]
+
+
 def test_decode_matches_prefill_state_and_cross_state():
     """The float64 state a decode step returns is the cache's; the layer's cross-layer state is
     that state rounded to the layer dtype (tesm.py:1395-1399)."""
