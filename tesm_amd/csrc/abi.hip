@@ -223,8 +223,26 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     ga.out = o.yg;
     ga.ldo = o.dm;
     if ((rc = launch_linear(ga, st))) return rc;
+    LinearArgs la;
+    la.op[0] = operand(o.xy, *o.out_proj);
+    la.M = o.M;
+    la.N = o.dm;
+    la.Kp = kpad(o.dm);
+    la.out = o.y;
+    la.out_dt = o.dt;
+    la.ldo = o.dm;
+    if (linear_fq_ok(la)) {  // decode-size batches: y's quantization inside out_proj, one launch fewer
+      FusedQuantIn f;
+      f.x = o.yg;
+      f.ldx = o.dm;
+      f.K = o.dm;
+      f.eps = o.eps;
+      f.dt = o.dt;
+      return launch_linear_fq(la, f, st);
+    }
     if ((rc = launch_quant_act(o.yg, o.dt, o.M, o.dm, o.dm, o.eps, 1, o.xy.q, o.xy.ldq, o.xy.s, o.xy.rs, st)))
       return rc;
+    return launch_linear(la, st);
   }
   return run_linear(o.xy, *o.out_proj, o.M, o.dm, o.dm, o.y, o.dt, o.dm, st);
 }
