@@ -615,7 +615,9 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
 // int8 codes in layout 1, code sums), then runs the split-K body on them.  Every workgroup of a row
 // tile repeats the quantization (a few KB of L2 reads each) in exchange for one launch fewer.  LDS
 // rows are Kp + 16 bytes apart, so the 16 rows a K-step reads fall on distinct banks.
-template <int NW, int TM, int TN, int OUT_DT, int DT, bool VEC>
+// G > 0: a lane's at most G groups stay in registers between the amax and the code pass (one read
+// of the row); G == 0: the row is read twice.
+template <int NW, int TM, int TN, int OUT_DT, int DT, bool VEC, int G>
 __global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQuantIn f) {
   extern __shared__ __attribute__((aligned(16))) char lds_fq[];
   constexpr int R = 16 * TM, LPR = NW * 64 / R;  // rows of the tile, lanes per row
@@ -630,7 +632,36 @@ __global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQ
     const int r = threadIdx.x / LPR, g0 = threadIdx.x % LPR;  // LPR consecutive lanes per row
     const int64_t m = m0 + r, ngroups = a.Kp / 16;
     int8_t* crow = codes + r * lstride;
-    if (m < a.M) {
+    if (m < a.M && G > 0) {
+      const int64_t base = m * f.ldx;
+      float v[G > 0 ? G : 1][16];
+      float amax = 0.0f;
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const int64_t g = g0 + LPR * gi;
+        if (g < ngroups) {
+          load_group<DT, VEC>(f.x, base, f.K, g, v[gi]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) v[gi][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[gi][i]));
+      }
+      amax = wave_max<LPR>(amax);
+      const float sc = act_scale<DT>(amax, f.eps);
+      int32_t rs = 0;
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const int64_t g = g0 + LPR * gi;
+        if (g < ngroups) *reinterpret_cast<uint4*>(crow + 16 * g) = group_codes<DT>(v[gi], sc, 1, rs);
+      }
+      rs = wave_sum_i<LPR>(rs);
+      if (g0 == 0) {
+        sc_l[r] = sc;
+        rs_l[r] = rs;
+      }
+    } else if (m < a.M) {
       const int64_t base = m * f.ldx;
       float amax = 0.0f;
       for (int64_t g = g0; g < ngroups; g += LPR) {
@@ -1839,24 +1870,31 @@ bool linear_fq_ok(const LinearArgs& a) {
 }
 
 namespace {
-template <int TM, int DT, bool VEC>
+template <int TM, int DT, bool VEC, int G>
 void run_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
   const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 15) / 16);
   const size_t lds = static_cast<size_t>(16 * TM * (a.Kp + 16) + 16 * TM * 8);
   if (a.out_dt == kBF16)
-    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
   else
-    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
 }
 template <int TM>
 void dispatch_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, bool vec, hipStream_t st) {
   if (f.dt == kBF16) {
-    if (vec) run_skinny_fq<TM, kBF16, true>(a, f, st);
-    else run_skinny_fq<TM, kBF16, false>(a, f, st);
-  } else {
-    if (vec) run_skinny_fq<TM, kF32, true>(a, f, st);
-    else run_skinny_fq<TM, kF32, false>(a, f, st);
+    if (vec) {
+      // groups per lane: Kp / 16 over 256 / (16 TM) lanes per row
+      const int64_t gpl = (a.Kp / 16 + 256 / (16 * TM) - 1) / (256 / (16 * TM));
+      if (gpl <= 2) return run_skinny_fq<TM, kBF16, true, 2>(a, f, st);
+      if (gpl <= 4) return run_skinny_fq<TM, kBF16, true, 4>(a, f, st);
+      if (gpl <= 6) return run_skinny_fq<TM, kBF16, true, 6>(a, f, st);
+      if (gpl <= 8) return run_skinny_fq<TM, kBF16, true, 8>(a, f, st);
+      return run_skinny_fq<TM, kBF16, true, 0>(a, f, st);
+    }
+    return run_skinny_fq<TM, kBF16, false, 0>(a, f, st);
   }
+  if (vec) return run_skinny_fq<TM, kF32, true, 0>(a, f, st);
+  return run_skinny_fq<TM, kF32, false, 0>(a, f, st);
 }
 }  // namespace
 
