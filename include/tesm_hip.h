@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 7
+#define TESM_HIP_ABI_VERSION 8
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -43,6 +43,62 @@ extern "C" {
 int tesm_hip_abi_version(void);
 const char* tesm_hip_last_error(void);
 int64_t tesm_hip_kpad(int64_t K);
+
+/* Launch log, a test and profiling aid with no reference counterpart: it names the kernel
+ * instantiations a call selects.  tesm_hip_launch_log(1) clears the log and starts recording
+ * "name<template args>\n" for every kernel launch of the process; (0) clears it and stops.
+ * tesm_hip_launch_log_read copies the log into buf (NUL-terminated, cut to cap - 1 bytes), returns
+ * its full length in bytes, and empties it when clear != 0.  Host-side only; thread-safe. */
+int tesm_hip_launch_log(int enable);
+int64_t tesm_hip_launch_log_read(char* buf, int64_t cap, int clear);
+
+/* Device status word of the library's bounded waits on the current device, no reference
+ * counterpart (the reference's kernels never wait on one another).  Bit 0 (TESM_STATUS_SCAN_GAVE_UP):
+ * a single-pass scan's look-back poll gave up; the states of that span are NaN.  The kernels still
+ * return, so a caller that wants certainty checks this word after its work.  Synchronises with the
+ * device (a diagnostic, not for the hot path); clear != 0 zeroes the word after reading it.
+ * tesm_hip_debug_scan_spin_limit sets the poll limit of later scans (default 1 << 20 rounds; a
+ * negative limit gives up at once, which tests use to exercise the report). */
+#define TESM_STATUS_SCAN_GAVE_UP 1u
+int tesm_hip_device_status(uint32_t* status, int clear);
+int tesm_hip_debug_scan_spin_limit(int limit);
+
+/* Decision taps, a parity-test aid.  The reference's eval forward keeps its ternary decisions
+ * (last_entanglement_map, tesm.py:716-744); its int8 codes are internal to BitLinear
+ * (tesm.py:206-209).  While taps are set, each later call of tesm_hip_siso_prefill,
+ * tesm_hip_siso_decode, tesm_hip_mimo_prefill and tesm_hip_mimo_decode also copies its discrete
+ * decisions to these device buffers (any may be NULL):
+ *   q_u/s_u, q_cs/s_cs, q_te/s_te, q_c/s_c, q_y/s_y: layout-1 int8 codes (M, kpad(K)) and scales (M)
+ *     of the inputs of in_proj (u), cross_layer_q_proj (the cross-layer state; MIMO decode: B*n_heads
+ *     rows), state_proj (tanh E), ent_proj (C) and out_proj (y); M = B*L (prefill) or B (decode),
+ *     K = d_model for u and y, d_state for cs, d_state (SISO) or n_heads*d_state (MIMO) for te/c;
+ *     tesm_hip_ffn_forward: q_u/s_u the codes of x (gate_proj / up_proj), q_h/s_h those of h
+ *     (down_proj);
+ *   tern: prefill with window > 0: SISO (B, L, min(window, L)), MIMO (B, L, n_heads, window), entry w
+ *     deciding key t - W + 1 + w (W the window used); decode: (B, n_heads, window) at the reference's
+ *     padded window positions, in its ring read order (SISO: n_heads = 1);
+ *   wts: MIMO prefill with window > 0: float32 window weights tern / norm, (B*L, n_heads, window).
+ * Copies are queued on the call's stream.  With taps set, u and y are quantized by their own
+ * kernels (the same codes as the products that quantize them inline).  Process-wide;
+ * tesm_hip_debug_taps(NULL) stops. */
+typedef struct tesm_hip_taps {
+  int8_t* q_u;
+  float* s_u;
+  int8_t* q_cs;
+  float* s_cs;
+  int8_t* q_te;
+  float* s_te;
+  int8_t* q_c;
+  float* s_c;
+  int8_t* q_y;
+  float* s_y;
+  int8_t* q_h;
+  float* s_h;
+  int8_t* tern;
+  float* wts;
+} tesm_hip_taps;
+
+int tesm_hip_debug_taps(const tesm_hip_taps* taps);
 
 /* Per-token int8 activation codes.  Replaces BitLinear.quantized_input
  * (tesm_ssm/modules/tesm.py:206-209): s_x[m] = 127 / max(amax_k |x[m,k]|, eps) evaluated as
@@ -80,6 +136,17 @@ int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const 
                           const uint8_t* packed, int64_t ldw, const float* c_w, int c_w_per_row, const void* bias,
                           int64_t M, int64_t N, int64_t K, void* out, int out_dt, int64_t ldo, int32_t* acc_dump,
                           void* stream);
+
+/* BitLinear forward from raw activations: the per-token int8 codes of x (tesm_hip_quant_act_i8)
+ * and the INT2 product (tesm_hip_bitlinear_i2) in one call.  Replaces BitLinear.forward
+ * (tesm.py:287-290) for a packed weight.  x: (M, ldx) in dt, K values per row; out: (M, ldo) in
+ * out_dt.  With fuse != 0 and 4 < M <= 32, N < 16384, kpad(K) <= 1920 the quantization runs inside
+ * the product (one launch); otherwise, or with fuse == 0, the codes go through ws (same result bit
+ * for bit).  ws: tesm_hip_bitlinear_fwd_ws_bytes(M, K) bytes. */
+int64_t tesm_hip_bitlinear_fwd_ws_bytes(int64_t M, int64_t K);
+int tesm_hip_bitlinear_fwd(const void* x, int dt, int64_t ldx, float eps, const uint8_t* packed, int64_t ldw,
+                           const float* c_w, int c_w_per_row, const void* bias, int64_t M, int64_t N, int64_t K,
+                           void* out, int out_dt, int64_t ldo, int fuse, void* ws, int64_t ws_bytes, void* stream);
 
 /* State scan h_t = d_t h_{t-1} + u_t over (B, L, C), C contiguous.  Replaces
  * TESM_SISO._parallel_state_scan (tesm.py:1091-1164, torch branch; chunk_size = state_scan_chunk_size

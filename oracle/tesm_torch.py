@@ -62,6 +62,11 @@ class BitLinear(nn.Module):
             lim = 1 / math.sqrt(self.in_features)
             nn.init.uniform_(self.bias, -lim, lim)
 
+    # Test hook (None by default): ``code_hook(x, v, codes, scale) -> (codes, scale)`` sees the
+    # pre-rounding values v = x * scale and the codes before they are dequantized; parity tests use
+    # it to feed in another implementation's codes where those differ from these only at near-ties.
+    code_hook = None
+
     def quantized_input(self, x):
         """Per-token absmax int8 fake quant (tesm.py:206-209).
 
@@ -69,7 +74,11 @@ class BitLinear(nn.Module):
         """
         amax = x.detach().abs().max(dim=-1, keepdim=True).values
         scale = 127 / amax.clamp_min(self.bit_eps)
-        deq = (x * scale).round().clamp(-128, 127) / scale
+        v = x * scale
+        codes = v.round().clamp(-128, 127)
+        if self.code_hook is not None:
+            codes, scale = self.code_hook(x, v, codes, scale)
+        deq = codes / scale
         return x + (deq - x).detach()
 
     def quantized_weight(self):
@@ -188,17 +197,24 @@ class TESM_SISO(nn.Module):
             T = self.T_start
         return max(T, self.T_end)
 
-    def _hard_ternary(self, scores):
+    # Test hook (None by default): ``tern_hook(scores, tern, where) -> tern`` sees every hard
+    # ternary decision with its place (``where``: ("local", t0, t1), ("global",), ("decode",),
+    # ("mimo", t, w)); parity tests use it like BitLinear.code_hook.
+    tern_hook = None
+
+    def _hard_ternary(self, scores, where=None):
         thr = self.entanglement_threshold
         one = torch.ones_like(scores)
-        return torch.where(scores > thr, one,
-                           torch.where(scores < -thr, -one, torch.zeros_like(scores)))
+        tern = torch.where(scores > thr, one, torch.where(scores < -thr, -one, torch.zeros_like(scores)))
+        if self.tern_hook is not None:
+            tern = self.tern_hook(scores, tern, where)
+        return tern
 
-    def ternary_entanglement(self, scores):
+    def ternary_entanglement(self, scores, where=None):
         T = self.get_temperature()
         if T > 1.0:
             return F.softmax(scores / T, dim=-1)
-        hard = self._hard_ternary(scores)
+        hard = self._hard_ternary(scores, where)
         return scores + (hard - scores).detach()
 
     # -- RoPE (tesm.py:783-793) --------------------------------------------------
@@ -262,7 +278,7 @@ class TESM_SISO(nn.Module):
             kb, vb = k[:, gpos, :], values[:, gpos, :]
             scores = torch.einsum("bqr,bqwr->bqw", q[:, t0:t1, :], kb) / math.sqrt(self.ent_rank)
             scores = scores + rel_bias[:, :, -W:].masked_fill(~valid, 0.0)
-            tern = self.ternary_entanglement(scores).masked_fill(~valid, 0.0)
+            tern = self.ternary_entanglement(scores, ("local", t0, t1)).masked_fill(~valid, 0.0)
             norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)
             out[:, t0:t1, :] = torch.einsum("bqw,bqwd->bqd", tern / norm, vb)
             maps.append(tern.detach())
@@ -286,7 +302,7 @@ class TESM_SISO(nn.Module):
         scores = torch.matmul(q, k.transpose(-2, -1)) / math.sqrt(self.ent_rank)
         scores = scores + rel_bias.unsqueeze(0)
         causal = torch.tril(torch.ones(L, L, dtype=torch.bool, device=q.device))
-        tern = self.ternary_entanglement(scores) * causal.unsqueeze(0).to(scores.dtype)
+        tern = self.ternary_entanglement(scores, ("global",)) * causal.unsqueeze(0).to(scores.dtype)
         norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)
         self._record_map(tern)
         return torch.matmul(tern / norm, values)
@@ -402,7 +418,7 @@ class TESM_SISO(nn.Module):
             full = torch.zeros(B, W, device=scores.device, dtype=zdt)
             full[:, W - valid:] = scores
             scores = full
-        tern = self.ternary_entanglement(scores)
+        tern = self.ternary_entanglement(scores, ("decode",))
         if valid < W:
             tern[:, :W - valid] = 0.0
         norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)
@@ -496,7 +512,7 @@ class TESMMIMO_Optimized(TESM_SISO):
                 if j < 0:
                     continue
                 s = (q[:, t] * k[:, j]).sum(dim=-1) / math.sqrt(R) + bias[:, w]
-                terms.append(s if T > 1.0 else self.ternary_entanglement(s))
+                terms.append(s if T > 1.0 else self.ternary_entanglement(s, ("mimo", t, w)))
                 vals.append(v[:, j])
             if not terms:
                 continue
@@ -516,7 +532,7 @@ class TESMMIMO_Optimized(TESM_SISO):
         scores = torch.matmul(q.reshape(B, L, H * R), k.reshape(B, L, H * R).transpose(-2, -1)) / math.sqrt(H * R)
         scores = scores + rel_bias.unsqueeze(0)
         causal = torch.tril(torch.ones(L, L, dtype=torch.bool, device=q.device))
-        tern = self.ternary_entanglement(scores) * causal.unsqueeze(0).to(scores.dtype)
+        tern = self.ternary_entanglement(scores, ("global",)) * causal.unsqueeze(0).to(scores.dtype)
         norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)
         w = tern / norm
         if self.amend_bf16 and w.dtype != states.dtype:  # bf16 weights against float32 rank states
@@ -678,7 +694,7 @@ class TESMMIMO_Optimized(TESM_SISO):
             full = scores.new_zeros(B, H, W)
             full[:, :, W - valid:] = scores
             scores = full
-        tern = self.ternary_entanglement(scores)
+        tern = self.ternary_entanglement(scores, ("decode",))
         if valid < W:
             tern[:, :, :W - valid] = 0.0
         norm = tern.abs().sum(dim=-1, keepdim=True).clamp_min(1.0)

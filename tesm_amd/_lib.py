@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -152,10 +152,23 @@ class Ffn(ctypes.Structure):
     ]
 
 
+class Taps(ctypes.Structure):
+    """``tesm_hip_taps``."""
+    _fields_ = [("q_u", P), ("s_u", P), ("q_cs", P), ("s_cs", P), ("q_te", P), ("s_te", P), ("q_c", P), ("s_c", P),
+                ("q_y", P), ("s_y", P), ("q_h", P), ("s_h", P), ("tern", P), ("wts", P)]
+
+
 _SIGNATURES = {
     "tesm_hip_abi_version": ([], I32),
     "tesm_hip_last_error": ([], ctypes.c_char_p),
     "tesm_hip_kpad": ([I64], I64),
+    "tesm_hip_launch_log": ([I32], I32),
+    "tesm_hip_launch_log_read": ([ctypes.c_char_p, I64, I32], I64),
+    "tesm_hip_device_status": ([ctypes.POINTER(ctypes.c_uint32), I32], I32),
+    "tesm_hip_debug_scan_spin_limit": ([I32], I32),
+    "tesm_hip_debug_taps": ([ctypes.POINTER(Taps)], I32),
+    "tesm_hip_bitlinear_fwd_ws_bytes": ([I64, I64], I64),
+    "tesm_hip_bitlinear_fwd": ([P, I32, I64, F32, P, I64, P, I32, P, I64, I64, I64, P, I32, I64, I32, P, I64, P], I32),
     "tesm_hip_quant_act_i8": ([P, I32, I64, I64, I64, F32, I32, P, I64, P, P, P], I32),
     "tesm_hip_absmean_ws_bytes": ([], I64),
     "tesm_hip_absmean_scale": ([P, I32, I64, F32, P, P, P, P], I32),

@@ -201,9 +201,8 @@ class BitLinear(nn.Module):
         pw = self.packed_weight()
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.in_features)
-        q, s, rs = hip_ops.quant_act(x2, self.bit_eps)
-        out = hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, self.out_features, self.in_features, x.dtype,
-                                bias=self.bias)
+        # quantized_input + _project_quantized (tesm.py:206-209, 287-290) in one C-ABI call
+        out = hip_ops.bitlinear_fwd(x2, pw.packed, pw.c_w, self.out_features, self.bit_eps, bias=self.bias)
         return out.reshape(*lead, self.out_features)
 
     def extra_repr(self):

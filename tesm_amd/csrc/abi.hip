@@ -2,6 +2,8 @@
 // layer drivers.  The drivers only queue kernels on the caller's stream; every buffer comes
 // from the caller (outputs) or from one caller-provided workspace carved up here.
 #include <cstring>
+#include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "decode.h"
@@ -24,6 +26,29 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
   return code;
+}
+
+int g_launch_log_on = 0;
+
+namespace {
+std::mutex g_log_mu;
+std::string g_log;
+}  // namespace
+
+// `pretty` is kernel_pretty<K>()'s text, "... [K = &ns::name<args>]": keep "name<args>".
+void log_kernel(const char* pretty) {
+  const char* p = std::strstr(pretty, "K = &");
+  std::string s = p ? p + 5 : pretty;
+  if (!s.empty() && s.back() == ']') s.pop_back();
+  const size_t lt = s.find('<');
+  const size_t cut = s.rfind("::", lt);
+  if (cut != std::string::npos) s = s.substr(cut + 2);
+  std::string name;
+  for (char c : s)
+    if (c != ' ') name += c;
+  std::lock_guard<std::mutex> g(g_log_mu);
+  g_log += name;
+  g_log += '\n';
 }
 
 int check_launch(const char* what) {
@@ -77,6 +102,173 @@ LinearOperand operand(const CodeBuf& x, const tesm_hip_linear& w) {
 }
 
 int esize(int dt) { return dt == kBF16 ? 2 : 4; }
+
+// Every pointer an entry point hands to a kernel must be memory the GPU can address: a device or
+// managed allocation, or pinned host memory.  A pageable host pointer would make the kernel fault,
+// so it is refused here, before anything is queued.  Device allocations that passed are remembered
+// per thread by address range, so later calls with the same buffers cost a range lookup.
+struct PtrRange {
+  uintptr_t lo = 0, hi = 0;
+};
+thread_local PtrRange t_known[32];
+thread_local int t_known_next = 0;
+
+int check_ptr(const void* p, const char* what, const char* who) {
+  if (p == nullptr) return kOk;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  for (const PtrRange& r : t_known)
+    if (a >= r.lo && a < r.hi) return kOk;
+  hipPointerAttribute_t at;
+  const hipError_t e = hipPointerGetAttributes(&at, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // the query's error must not be reported by a later launch check
+    return fail(kErrInvalidArg, std::string(who) + ": " + what +
+                                    " is not GPU-addressable memory (a host pointer? pass device tensors)");
+  }
+  if (at.type == hipMemoryTypeHost) return kOk;  // pinned host memory: addressable, not cached here
+  if (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged && at.type != hipMemoryTypeUnified)
+    return fail(kErrInvalidArg, std::string(who) + ": " + what +
+                                    " is not GPU-addressable memory (a host pointer? pass device tensors)");
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) == hipSuccess && size > 0) {
+    PtrRange& r = t_known[t_known_next];
+    t_known_next = (t_known_next + 1) % 32;
+    r.lo = reinterpret_cast<uintptr_t>(base);
+    r.hi = r.lo + size;
+  } else {
+    (void)hipGetLastError();
+  }
+  return kOk;
+}
+
+struct NamedPtr {
+  const void* p;
+  const char* name;
+};
+
+int check_ptrs(const char* who, std::initializer_list<NamedPtr> ps) {
+  for (const NamedPtr& n : ps)
+    if (int rc = check_ptr(n.p, n.name, who)) return rc;
+  return kOk;
+}
+
+int check_linear_ptrs(const char* who, const char* name, const tesm_hip_linear& w) {
+  if (int rc = check_ptr(w.packed, name, who)) return rc;
+  return check_ptr(w.c_w, name, who);
+}
+
+int check_desc_ptrs(const tesm_hip_ent_quant& p) {
+  return check_ptrs("local_ent_quant", {{p.q, "q"}, {p.k, "k"}, {p.rope, "rope"}, {p.q_add, "q_add"}, {p.bias, "bias"},
+                                        {p.S, "S"}, {p.q_te, "q_te"}, {p.s_te, "s_te"}, {p.rs_te, "rs_te"},
+                                        {p.q_c, "q_c"}, {p.s_c, "s_c"}, {p.rs_c, "rs_c"}, {p.e_tanh, "e_tanh"},
+                                        {p.c_out, "c_out"}, {p.tern, "tern"}});
+}
+
+int check_desc_ptrs(const tesm_hip_output_gate& p) {
+  if (int rc = check_ptrs("output_gate", {{p.q_te, "q_te"}, {p.s_te, "s_te"}, {p.rs_te, "rs_te"}, {p.q_c, "q_c"},
+                                          {p.s_c, "s_c"}, {p.rs_c, "rs_c"}, {p.local, "local"}, {p.gate, "gate"},
+                                          {p.y, "y"}, {p.q_y, "q_y"}, {p.s_y, "s_y"}, {p.rs_y, "rs_y"}}))
+    return rc;
+  if (int rc = check_linear_ptrs("output_gate", "state_proj", p.state_proj)) return rc;
+  return check_linear_ptrs("output_gate", "ent_proj", p.ent_proj);
+}
+
+int check_desc_ptrs(const tesm_hip_siso_layer& p) {
+  if (int rc = check_ptrs("siso prefill",
+                          {{p.u, "u"}, {p.decay_bias, "decay_bias"}, {p.local_bias, "local_bias"}, {p.rope, "rope"},
+                           {p.cross_state, "cross_state"}, {p.h0, "h0"}, {p.y, "y"}, {p.states, "states"},
+                           {p.h_final, "h_final"}, {p.proj_out, "proj_out"}, {p.k_cache, "k_cache"},
+                           {p.v_cache, "v_cache"}, {p.global_embed, "global_embed"}, {p.global_scale, "global_scale"},
+                           {p.global_bias, "global_bias"}}))
+    return rc;
+  for (const auto& w : {std::make_pair(&p.in_proj, "in_proj"), std::make_pair(&p.state_proj, "state_proj"),
+                        std::make_pair(&p.ent_proj, "ent_proj"), std::make_pair(&p.out_proj, "out_proj"),
+                        std::make_pair(&p.cross_q_proj, "cross_q_proj")})
+    if (int rc = check_linear_ptrs("siso prefill", w.second, *w.first)) return rc;
+  return kOk;
+}
+
+int check_desc_ptrs(const tesm_hip_siso_step& p) {
+  if (int rc = check_ptrs("siso decode",
+                          {{p.u, "u"}, {p.decay_bias, "decay_bias"}, {p.local_bias, "local_bias"}, {p.rope, "rope"},
+                           {p.cross_state, "cross_state"}, {p.state, "state"}, {p.state_out, "state_out"},
+                           {p.k_cache, "k_cache"}, {p.v_cache, "v_cache"}, {p.y, "y"}, {p.new_state, "new_state"}}))
+    return rc;
+  for (const auto& w : {std::make_pair(&p.in_proj, "in_proj"), std::make_pair(&p.state_proj, "state_proj"),
+                        std::make_pair(&p.ent_proj, "ent_proj"), std::make_pair(&p.out_proj, "out_proj"),
+                        std::make_pair(&p.cross_q_proj, "cross_q_proj")})
+    if (int rc = check_linear_ptrs("siso decode", w.second, *w.first)) return rc;
+  return kOk;
+}
+
+int check_desc_ptrs(const tesm_hip_mimo_layer& p) {
+  if (int rc = check_ptrs("mimo prefill",
+                          {{p.u, "u"}, {p.decay_bias, "decay_bias"}, {p.local_bias, "local_bias"}, {p.rope, "rope"},
+                           {p.mimo_coef, "mimo_coef"}, {p.mimo_x0sq, "mimo_x0sq"}, {p.y, "y"}, {p.h_final, "h_final"},
+                           {p.last_state, "last_state"}, {p.k_cache, "k_cache"}, {p.v_cache, "v_cache"},
+                           {p.stats_ternary, "stats_ternary"}, {p.stats_counts, "stats_counts"},
+                           {p.global_embed, "global_embed"}, {p.global_scale, "global_scale"},
+                           {p.global_bias, "global_bias"}}))
+    return rc;
+  for (const auto& w : {std::make_pair(&p.in_proj, "in_proj"), std::make_pair(&p.state_proj, "state_proj"),
+                        std::make_pair(&p.ent_proj, "ent_proj"), std::make_pair(&p.out_proj, "out_proj")})
+    if (int rc = check_linear_ptrs("mimo prefill", w.second, *w.first)) return rc;
+  return kOk;
+}
+
+int check_desc_ptrs(const tesm_hip_mimo_step& p) {
+  if (int rc = check_ptrs("mimo decode",
+                          {{p.u, "u"}, {p.decay_bias, "decay_bias"}, {p.local_bias, "local_bias"}, {p.rope, "rope"},
+                           {p.cross_state, "cross_state"}, {p.state, "state"}, {p.state_out, "state_out"},
+                           {p.k_cache, "k_cache"}, {p.v_cache, "v_cache"}, {p.y, "y"}, {p.new_state, "new_state"}}))
+    return rc;
+  for (const auto& w : {std::make_pair(&p.in_proj, "in_proj"), std::make_pair(&p.state_proj, "state_proj"),
+                        std::make_pair(&p.ent_proj, "ent_proj"), std::make_pair(&p.out_proj, "out_proj"),
+                        std::make_pair(&p.cross_q_proj, "cross_q_proj")})
+    if (int rc = check_linear_ptrs("mimo decode", w.second, *w.first)) return rc;
+  return kOk;
+}
+
+int check_desc_ptrs(const tesm_hip_rmsnorm& p) {
+  return check_ptrs("add_rmsnorm", {{p.x, "x"}, {p.residual, "residual"}, {p.residual_out, "residual_out"},
+                                    {p.weight, "weight"}, {p.y, "y"}, {p.q, "q"}, {p.s_x, "s_x"},
+                                    {p.rowsum, "rowsum"}});
+}
+
+int check_desc_ptrs(const tesm_hip_ffn& p) {
+  if (int rc = check_ptrs("ffn", {{p.x, "x"}, {p.x_codes, "x_codes"}, {p.x_scale, "x_scale"},
+                                  {p.x_rowsum, "x_rowsum"}, {p.y, "y"}}))
+    return rc;
+  for (const auto& w : {std::make_pair(&p.gate_proj, "gate_proj"), std::make_pair(&p.up_proj, "up_proj"),
+                        std::make_pair(&p.down_proj, "down_proj")})
+    if (int rc = check_linear_ptrs("ffn", w.second, *w.first)) return rc;
+  return kOk;
+}
+
+// Decision taps (tesm_hip_debug_taps): process-wide copy targets for the discrete decisions of
+// the layer and step drivers; a driver takes a snapshot when it is called.
+std::mutex g_taps_mu;
+tesm_hip_taps g_taps{};
+bool g_taps_on = false;
+
+bool snapshot_taps(tesm_hip_taps* t) {
+  std::lock_guard<std::mutex> g(g_taps_mu);
+  *t = g_taps;
+  return g_taps_on;
+}
+
+int tap_copy(void* dst, const void* src, int64_t bytes, hipStream_t st) {
+  if (!dst || !src || bytes <= 0) return kOk;
+  if (hipMemcpyAsync(dst, src, static_cast<size_t>(bytes), hipMemcpyDeviceToDevice, st) != hipSuccess)
+    return fail(kErrLaunch, "decision tap: copy failed");
+  return kOk;
+}
+
+int tap_codes(int8_t* q, float* sc, const CodeBuf& b, int64_t M, hipStream_t st) {
+  if (int rc = tap_copy(q, b.q, M * b.ldq, st)) return rc;
+  return tap_copy(sc, b.s, M * 4, st);
+}
 
 // Workspace layout of the SISO prefill; with base == nullptr it only measures.
 struct SisoPlan {
@@ -195,6 +387,7 @@ struct OutputPath {
   const void* gate;
   int64_t ld;
   void* y;
+  const tesm_hip_taps* taps = nullptr;  // set: copy out y's codes (quantized apart from out_proj)
 };
 
 int run_output_path(const OutputPath& o, hipStream_t st) {
@@ -219,6 +412,7 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     rq.rs = o.xy.rs;
     rq.eps = o.eps;
     if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
+    if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
   } else {
     ga.out = o.yg;
     ga.ldo = o.dm;
@@ -231,7 +425,7 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     la.out = o.y;
     la.out_dt = o.dt;
     la.ldo = o.dm;
-    if (linear_fq_ok(la)) {  // decode-size batches: y's quantization inside out_proj, one launch fewer
+    if (!o.taps && linear_fq_ok(la)) {  // decode-size batches: y's quantization inside out_proj, one launch fewer
       FusedQuantIn f;
       f.x = o.yg;
       f.ldx = o.dm;
@@ -242,6 +436,7 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     }
     if ((rc = launch_quant_act(o.yg, o.dt, o.M, o.dm, o.dm, o.eps, 1, o.xy.q, o.xy.ldq, o.xy.s, o.xy.rs, st)))
       return rc;
+    if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
     return launch_linear(la, st);
   }
   return run_linear(o.xy, *o.out_proj, o.M, o.dm, o.dm, o.y, o.dt, o.dm, st);
@@ -362,12 +557,51 @@ extern "C" {
 
 int tesm_hip_abi_version(void) { return TESM_HIP_ABI_VERSION; }
 
+int tesm_hip_launch_log(int enable) {
+  std::lock_guard<std::mutex> g(g_log_mu);
+  g_log.clear();
+  __atomic_store_n(&g_launch_log_on, enable ? 1 : 0, __ATOMIC_RELAXED);
+  return kOk;
+}
+
+int tesm_hip_device_status(uint32_t* status, int clear) {
+  unsigned v = 0;
+  if (int rc = scan_status(&v, clear)) return rc;
+  if (status) *status = v;
+  return kOk;
+}
+
+int tesm_hip_debug_taps(const tesm_hip_taps* t) {
+  std::lock_guard<std::mutex> g(g_taps_mu);
+  g_taps_on = t != nullptr;
+  g_taps = t ? *t : tesm_hip_taps{};
+  return kOk;
+}
+
+int tesm_hip_debug_scan_spin_limit(int limit) {
+  scan_set_spin_limit(limit);
+  return kOk;
+}
+
+int64_t tesm_hip_launch_log_read(char* buf, int64_t cap, int clear) {
+  std::lock_guard<std::mutex> g(g_log_mu);
+  const int64_t n = static_cast<int64_t>(g_log.size());
+  if (buf && cap > 0) {
+    const int64_t k = std::min<int64_t>(n, cap - 1);
+    std::memcpy(buf, g_log.data(), static_cast<size_t>(k));
+    buf[k] = '\0';
+  }
+  if (clear) g_log.clear();
+  return n;
+}
+
 const char* tesm_hip_last_error(void) { return g_last_error.c_str(); }
 
 int64_t tesm_hip_kpad(int64_t K) { return kpad(K); }
 
 int tesm_hip_quant_act_i8(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
                           int64_t ldq, float* s_x, int32_t* rowsum, void* stream) {
+  if (int rc = check_ptrs("quant_act", {{x, "x"}, {q, "q"}, {s_x, "s_x"}, {rowsum, "rowsum"}})) return rc;
   return launch_quant_act(x, dt, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, static_cast<hipStream_t>(stream));
 }
 
@@ -375,16 +609,19 @@ int64_t tesm_hip_absmean_ws_bytes(void) { return 512 * static_cast<int64_t>(size
 
 int tesm_hip_absmean_scale(const void* w, int dt, int64_t n, float eps, void* ws, float* s_w, float* c_w,
                            void* stream) {
+  if (int rc = check_ptrs("absmean", {{w, "w"}, {ws, "ws"}, {s_w, "s_w"}, {c_w, "c_w"}})) return rc;
   return launch_absmean(w, dt, n, eps, static_cast<double*>(ws), s_w, c_w, static_cast<hipStream_t>(stream));
 }
 
 int tesm_hip_pack_w_i2(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
                        uint8_t* packed, int64_t ldp, void* stream) {
+  if (int rc = check_ptrs("pack_w_i2", {{w, "w"}, {s_w, "s_w"}, {packed, "packed"}})) return rc;
   return launch_pack(w, dt, N, K, ldw, s_w, per_row, packed, ldp, static_cast<hipStream_t>(stream));
 }
 
 int tesm_hip_unpack_w_i2(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
                          void* stream) {
+  if (int rc = check_ptrs("unpack_w_i2", {{packed, "packed"}, {codes, "codes"}})) return rc;
   return launch_unpack(packed, N, K, ldp, codes, ldc, static_cast<hipStream_t>(stream));
 }
 
@@ -392,6 +629,9 @@ int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const 
                           const uint8_t* packed, int64_t ldw, const float* c_w, int c_w_per_row, const void* bias,
                           int64_t M, int64_t N, int64_t K, void* out, int out_dt, int64_t ldo, int32_t* acc_dump,
                           void* stream) {
+  if (int rc = check_ptrs("bitlinear", {{q, "q"}, {s_x, "s_x"}, {rowsum, "rowsum"}, {packed, "packed"}, {c_w, "c_w"},
+                                         {bias, "bias"}, {out, "out"}, {acc_dump, "acc_dump"}}))
+    return rc;
   TESM_REQUIRE(K >= 1, kErrInvalidArg, "bitlinear: K must be >= 1");
   LinearArgs a;
   a.op[0].q = q;
@@ -413,6 +653,55 @@ int tesm_hip_bitlinear_i2(const int8_t* q, int64_t ldq, const float* s_x, const 
   return launch_linear(a, static_cast<hipStream_t>(stream));
 }
 
+int64_t tesm_hip_bitlinear_fwd_ws_bytes(int64_t M, int64_t K) {
+  Carve c(nullptr);
+  take_codes(c, std::max<int64_t>(M, 1), K);
+  return c.off;
+}
+
+int tesm_hip_bitlinear_fwd(const void* x, int dt, int64_t ldx, float eps, const uint8_t* packed, int64_t ldw,
+                           const float* c_w, int c_w_per_row, const void* bias, int64_t M, int64_t N, int64_t K,
+                           void* out, int out_dt, int64_t ldo, int fuse, void* ws, int64_t ws_bytes, void* stream) {
+  if (int rc = check_ptrs("bitlinear fwd", {{x, "x"}, {packed, "packed"}, {c_w, "c_w"}, {bias, "bias"}, {out, "out"},
+                                            {ws, "ws"}}))
+    return rc;
+  TESM_REQUIRE(K >= 1 && M >= 0 && N >= 0, kErrInvalidArg, "bitlinear fwd: bad sizes");
+  TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "bitlinear fwd: x dtype must be 0 or 1");
+  TESM_REQUIRE(ldx >= K, kErrInvalidArg, "bitlinear fwd: ldx must be >= K");
+  if (M == 0 || N == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  LinearArgs la;
+  la.op[0].w = packed;
+  la.op[0].ldw = ldw;
+  la.op[0].c_w = c_w;
+  la.op[0].c_w_per_row = c_w_per_row;
+  la.M = M;
+  la.N = N;
+  la.Kp = kpad(K);
+  la.bias = bias;
+  la.out = out;
+  la.out_dt = out_dt;
+  la.ldo = ldo;
+  if (fuse && linear_fq_ok(la)) {
+    FusedQuantIn f;
+    f.x = x;
+    f.ldx = ldx;
+    f.K = K;
+    f.eps = eps;
+    f.dt = dt;
+    return launch_linear_fq(la, f, st);
+  }
+  Carve c(ws);
+  const CodeBuf cb = take_codes(c, M, K);
+  TESM_REQUIRE(ws && ws_bytes >= c.off, kErrWorkspace, "bitlinear fwd: workspace too small");
+  if (int rc = launch_quant_act(x, dt, M, K, ldx, eps, 1, cb.q, cb.ldq, cb.s, cb.rs, st)) return rc;
+  la.op[0].q = cb.q;
+  la.op[0].ldq = cb.ldq;
+  la.op[0].s_x = cb.s;
+  la.op[0].rowsum = cb.rs;
+  return launch_linear(la, st);
+}
+
 int64_t tesm_hip_scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t chunk_size) {
   return scan_ws_bytes(B, L, C, chunk_size);
 }
@@ -420,6 +709,9 @@ int64_t tesm_hip_scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t chunk_si
 int tesm_hip_scan(const void* decay, int64_t ld_decay, const void* update, int64_t ld_update, int dt, int64_t B,
                   int64_t L, int64_t C, int64_t chunk_size, const double* h0, void* states, int64_t ld_states,
                   int out_dt, double* h_final, void* ws, int64_t ws_bytes, void* stream) {
+  if (int rc = check_ptrs("scan", {{decay, "decay"}, {update, "update"}, {h0, "h0"}, {states, "states"},
+                                    {h_final, "h_final"}, {ws, "ws"}}))
+    return rc;
   ScanArgs a;
   a.mode = 0;
   a.dt = dt;
@@ -441,6 +733,7 @@ int tesm_hip_scan(const void* decay, int64_t ld_decay, const void* update, int64
 }
 
 int tesm_hip_rope_table(void* tab, int64_t L, int64_t R, int64_t pos_offset, double base, int dt, void* stream) {
+  if (int rc = check_ptrs("rope_table", {{tab, "tab"}})) return rc;
   return launch_rope_table(static_cast<float2*>(tab), L, R, pos_offset, base, dt, static_cast<hipStream_t>(stream));
 }
 
@@ -451,6 +744,10 @@ int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k,
                        int64_t L, int64_t H, int64_t R, int64_t D, int64_t W, float thr, float ent_scale, void* avg,
                        void* e_out, void* c_out, void* e_tanh, int64_t ld_out, int8_t* tern, void* ws,
                        int64_t ws_bytes, void* stream) {
+  if (int rc = check_ptrs("local_ent", {{q, "q"}, {k, "k"}, {rope, "rope"}, {q_add, "q_add"}, {bias, "bias"}, {S, "S"},
+                                         {avg, "avg"}, {e_out, "e_out"}, {c_out, "c_out"}, {e_tanh, "e_tanh"},
+                                         {tern, "tern"}, {ws, "ws"}}))
+    return rc;
   EntArgs a;
   a.dt = dt;
   a.mimo = mimo;
@@ -486,6 +783,7 @@ int tesm_hip_local_ent(const void* q, int64_t ld_q, const void* k, int64_t ld_k,
 
 int tesm_hip_local_ent_quant(const tesm_hip_ent_quant* p, void* stream) {
   TESM_REQUIRE(p != nullptr, kErrInvalidArg, "local_ent_quant: null descriptor");
+  if (int rc = check_desc_ptrs(*p)) return rc;
   EntArgs a;
   a.dt = p->dt;
   a.mimo = 0;
@@ -525,6 +823,7 @@ int tesm_hip_local_ent_quant(const tesm_hip_ent_quant* p, void* stream) {
 
 int tesm_hip_output_gate_i2(const tesm_hip_output_gate* p, void* stream) {
   TESM_REQUIRE(p != nullptr, kErrInvalidArg, "output_gate: null descriptor");
+  if (int rc = check_desc_ptrs(*p)) return rc;
   CodeBuf te{const_cast<int8_t*>(p->q_te), const_cast<float*>(p->s_te), const_cast<int32_t*>(p->rs_te), p->ldq_te};
   CodeBuf cc{const_cast<int8_t*>(p->q_c), const_cast<float*>(p->s_c), const_cast<int32_t*>(p->rs_c), p->ldq_c};
   LinearArgs ga;
@@ -564,6 +863,7 @@ int64_t tesm_hip_siso_prefill_ws_bytes(const tesm_hip_siso_layer* p) {
 
 int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_bytes, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso layer: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_siso_layer& p = *pp;
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso layer: dtype must be 0 or 1");
@@ -584,6 +884,8 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     if (int rc = check_linear(p.cross_q_proj, p.d_state, "cross_q_proj")) return rc;
   const SisoPlan s = plan_siso(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "siso layer: workspace too small");
+  tesm_hip_taps tp;
+  const bool tapping = snapshot_taps(&tp);
 
   const int dt = p.dt;
   const int es = esize(dt);
@@ -602,6 +904,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st, scan_zero,
                              scan_zero_n)))
     return rc;
+  if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, s.xu, M, st))) return rc;
   if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
   if (p.proj_out) {
     if (hipMemcpyAsync(p.proj_out, proj, M * n_in * es, hipMemcpyDeviceToDevice, st) != hipSuccess)
@@ -611,6 +914,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   if (p.cross_state) {
     if ((rc = launch_quant_act(p.cross_state, dt, M, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs, st)))
       return rc;
+    if (tapping && (rc = tap_codes(tp.q_cs, tp.s_cs, s.xs, M, st))) return rc;
     if ((rc = run_linear(s.xs, p.cross_q_proj, M, R, D, s.cq, dt, R, st))) return rc;
   }
   // 3. gates + state scan (tesm.py:1202-1205, 1222-1223)
@@ -652,6 +956,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   ea.S = p.states;
   ea.ld_s = D;
   ea.eps = p.bit_eps;
+  if (tapping) ea.tern = tp.tern;
   if (p.window == 0) {  // global causal entanglement (tesm.py:963-1063), then the same quantizations
     if ((rc = launch_global_bias_table(dt, 2 * p.L, p.global_embed, p.global_dim, p.global_scale, p.global_bias,
                                        s.g_table, st)))
@@ -709,6 +1014,10 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
       return rc;
   }
+  if (tapping) {
+    if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, M, st))) return rc;
+    if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, M, st))) return rc;
+  }
   // 5. decode caches (tesm.py:1235-1253)
   if (p.k_cache || p.v_cache) {
     CacheFillArgs cf;
@@ -746,6 +1055,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   op.gate = proj + o_gate * es;
   op.ld = n_in;
   op.y = p.y;
+  op.taps = tapping ? &tp : nullptr;
   return run_output_path(op, st);
 }
 
@@ -756,6 +1066,7 @@ int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p) {
 
 int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_bytes, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso decode: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_siso_step& p = *pp;
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso decode: dtype must be 0 or 1");
@@ -773,6 +1084,8 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
     if (int rc = check_linear(p.cross_q_proj, p.d_state, "cross_q_proj")) return rc;
   const DecodePlan s = plan_decode(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "siso decode: workspace too small");
+  tesm_hip_taps tp;
+  const bool tapping = snapshot_taps(&tp);
 
   const int dt = p.dt;
   const int es = esize(dt);
@@ -794,7 +1107,7 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
     la.out = proj;
     la.out_dt = dt;
     la.ldo = n_in;
-    if (linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
+    if (!tapping && linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
       FusedQuantIn f;
       f.x = p.u;
       f.ldx = ld_u;
@@ -805,6 +1118,7 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
     } else {
       if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st)))
         return rc;
+      if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, s.xu, Bn, st))) return rc;
       if ((rc = launch_linear(la, st))) return rc;
     }
   }
@@ -812,6 +1126,7 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   if (p.cross_state) {
     if ((rc = launch_quant_act(p.cross_state, dt, Bn, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs, st)))
       return rc;
+    if (tapping && (rc = tap_codes(tp.q_cs, tp.s_cs, s.xs, Bn, st))) return rc;
     if ((rc = run_linear(s.xs, p.cross_q_proj, Bn, R, D, s.cq, dt, R, st))) return rc;
   }
   // 3. state update, ring write, window entanglement, codes of tanh(E) and C
@@ -853,7 +1168,12 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   da.s_c = s.xc.s;
   da.rs_c = s.xc.rs;
   da.ldq = s.xe.ldq;
+  if (tapping) da.tern = tp.tern;
   if ((rc = launch_decode_ent(da, st))) return rc;
+  if (tapping) {
+    if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, Bn, st))) return rc;
+    if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, Bn, st))) return rc;
+  }
   // 4. output gate and out_proj
   OutputPath op;
   op.xe = s.xe;
@@ -872,6 +1192,7 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   op.gate = proj + o_gate * es;
   op.ld = n_in;
   op.y = p.y;
+  op.taps = tapping ? &tp : nullptr;
   return run_output_path(op, st);
 }
 
@@ -918,6 +1239,7 @@ int64_t tesm_hip_mimo_decode_ws_bytes(const tesm_hip_mimo_step* p) {
 
 int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_bytes, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "mimo decode: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_mimo_step& p = *pp;
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "mimo decode: dtype must be 0 or 1");
@@ -939,6 +1261,8 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
     if (int rc = check_linear(p.cross_q_proj, D, "cross_q_proj")) return rc;
   const MimoDecodePlan s = plan_mimo_decode(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "mimo decode: workspace too small");
+  tesm_hip_taps tp;
+  const bool tapping = snapshot_taps(&tp);
 
   const int dt = p.dt;
   const int es = esize(dt);
@@ -959,7 +1283,7 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
     la.out = proj;
     la.out_dt = dt;
     la.ldo = n_in;
-    if (linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
+    if (!tapping && linear_fq_ok(la)) {  // quantization of u inside the product: one launch fewer per step
       FusedQuantIn f;
       f.x = p.u;
       f.ldx = ld_u;
@@ -970,6 +1294,7 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
     } else {
       if ((rc = launch_quant_act(p.u, dt, Bn, dm, ld_u, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st)))
         return rc;
+      if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, s.xu, Bn, st))) return rc;
       if ((rc = launch_linear(la, st))) return rc;
     }
   }
@@ -978,6 +1303,7 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
     if ((rc = launch_quant_act(p.cross_state, dt, Bn * H, D, D, p.bit_eps, 1, s.xs.q, s.xs.ldq, s.xs.s, s.xs.rs,
                                st)))
       return rc;
+    if (tapping && (rc = tap_codes(tp.q_cs, tp.s_cs, s.xs, Bn * H, st))) return rc;
     if ((rc = run_linear(s.xs, p.cross_q_proj, Bn * H, R, D, s.cq, dt, R, st))) return rc;
   }
   // 3. per-head state update, ring write, window entanglement (tesm_mimo.py:838-887)
@@ -1016,10 +1342,15 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
   da.te_out = s.te;
   da.c_out = s.cc;
   da.ld_out = HD;
+  if (tapping) da.tern = tp.tern;
   if ((rc = launch_decode_ent(da, st))) return rc;
   // 4. per-token codes of tanh(E) and C over the flattened heads (tesm_mimo.py:895-900)
   if ((rc = launch_quant_act(s.te, dt, Bn, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
   if ((rc = launch_quant_act(s.cc, dt, Bn, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  if (tapping) {
+    if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, Bn, st))) return rc;
+    if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, Bn, st))) return rc;
+  }
   // 5. output gate and out_proj (tesm_mimo.py:902-906)
   OutputPath op;
   op.xe = s.xe;
@@ -1038,11 +1369,13 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
   op.gate = proj + o_gate * es;
   op.ld = n_in;
   op.y = p.y;
+  op.taps = tapping ? &tp : nullptr;
   return run_output_path(op, st);
 }
 
 int tesm_hip_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t n_heads, int64_t mimo_rank,
                        int64_t d_state, float* coef, float* x0sq, void* stream) {
+  if (int rc = check_ptrs("mimo_coef", {{mimo_x, "mimo_x"}, {mimo_o, "mimo_o"}, {coef, "coef"}, {x0sq, "x0sq"}})) return rc;
   return launch_mimo_coef(mimo_x, mimo_o, dt, n_heads, mimo_rank, d_state, coef, x0sq,
                           static_cast<hipStream_t>(stream));
 }
@@ -1054,6 +1387,7 @@ int64_t tesm_hip_mimo_prefill_ws_bytes(const tesm_hip_mimo_layer* p) {
 
 int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_bytes, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "mimo layer: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_mimo_layer& p = *pp;
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "mimo layer: dtype must be 0 or 1");
@@ -1073,6 +1407,8 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   if (int rc = check_linear(p.out_proj, dm, "out_proj")) return rc;
   const MimoPlan s = plan_mimo(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "mimo layer: workspace too small");
+  tesm_hip_taps tp;
+  const bool tapping = snapshot_taps(&tp);
 
   const int dt = p.dt;
   const int es = esize(dt);
@@ -1091,6 +1427,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st, scan_zero,
                              scan_zero_n)))
     return rc;
+  if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, s.xu, M, st))) return rc;
   if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
   // 2. gates + rank-free state scan: sequential float32 recurrence h = d h + w tanh(sv) per channel
   ScanArgs sa;
@@ -1139,6 +1476,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
     ea.S = s.S;
     ea.ld_s = HD;
     ea.wts = s.wts;
+    if (tapping) ea.tern = tp.tern;
     if ((rc = launch_local_ent(ea, st))) return rc;
     // 4. window mix, entangled state, rank merge; tanh(E c) and C c in dt for the projections
     MimoMixArgs ma;
@@ -1155,6 +1493,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
     ma.te = s.te;
     ma.cc = s.cc;
     if ((rc = launch_mimo_mix(ma, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.wts, s.wts, M * H * p.window * 4, st))) return rc;
   } else {
     // 3-4. global causal entanglement over the flattened heads (tesm_mimo.py:655-687), E = A, merged
     if ((rc = launch_global_bias_table(dt, 2 * p.L, p.global_embed, p.global_dim, p.global_scale, p.global_bias,
@@ -1211,6 +1550,10 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   }
   if ((rc = launch_quant_act(s.te, dt, M, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
   if ((rc = launch_quant_act(s.cc, dt, M, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  if (tapping) {
+    if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, M, st))) return rc;
+    if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, M, st))) return rc;
+  }
   // 5. decode caches
   if (p.k_cache || p.v_cache) {
     CacheFillArgs cf;
@@ -1251,6 +1594,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   op.gate = proj + o_gate * es;
   op.ld = n_in;
   op.y = p.y;
+  op.taps = tapping ? &tp : nullptr;
   return run_output_path(op, st);
 }
 
@@ -1259,6 +1603,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
 // ---------------------------------------------------------------------------
 int tesm_hip_add_rmsnorm(const tesm_hip_rmsnorm* pp, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "rmsnorm: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_rmsnorm& p = *pp;
   NormArgs a;
   a.dt = p.dt;
@@ -1292,6 +1637,7 @@ int64_t tesm_hip_ffn_ws_bytes(const tesm_hip_ffn* p) {
 
 int tesm_hip_ffn_forward(const tesm_hip_ffn* pp, void* ws, int64_t ws_bytes, void* stream) {
   TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "ffn: null descriptor");
+  if (int rc = check_desc_ptrs(*pp)) return rc;
   const tesm_hip_ffn& p = *pp;
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "ffn: dtype must be 0 or 1");
@@ -1308,6 +1654,8 @@ int tesm_hip_ffn_forward(const tesm_hip_ffn* pp, void* ws, int64_t ws_bytes, voi
   const FfnPlan s = plan_ffn(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "ffn: workspace too small");
   if (p.M == 0) return kOk;
+  tesm_hip_taps tp;
+  const bool tapping = snapshot_taps(&tp);
   int rc;
   CodeBuf xq = s.xq;
   if (p.x_codes) {
@@ -1316,6 +1664,7 @@ int tesm_hip_ffn_forward(const tesm_hip_ffn* pp, void* ws, int64_t ws_bytes, voi
   } else if ((rc = launch_quant_act(p.x, p.dt, p.M, p.d_model, p.ld_x, p.bit_eps, 1, xq.q, xq.ldq, xq.s, xq.rs, st))) {
     return rc;
   }
+  if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, xq, p.M, st))) return rc;
   // gate and up products on the same codes, h = silu(gate) * up (mixer_seq_simple.py:57-64)
   LinearArgs g;
   g.op[0] = operand(xq, p.gate_proj);
@@ -1332,6 +1681,7 @@ int tesm_hip_ffn_forward(const tesm_hip_ffn* pp, void* ws, int64_t ws_bytes, voi
   if ((rc = launch_quant_act(s.h, p.dt, p.M, p.d_inter, p.d_inter, p.bit_eps, 1, s.hq.q, s.hq.ldq, s.hq.s, s.hq.rs,
                              st)))
     return rc;
+  if (tapping && (rc = tap_codes(tp.q_h, tp.s_h, s.hq, p.M, st))) return rc;
   return run_linear(s.hq, p.down_proj, p.M, p.d_model, p.d_inter, p.y, p.dt, p.ld_y, st);
 }
 

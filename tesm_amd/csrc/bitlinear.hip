@@ -1714,9 +1714,9 @@ int run_mfma32(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
   const unsigned grid = static_cast<unsigned>(tiles);
   if (a.out_dt == kBF16)
-    mfma32_kernel<WM, WN, TM, TN, EPI, kBF16, NS><<<grid, C::NT, 0, st>>>(a);
+    mfma32_kernel<WM, WN, TM, TN, EPI, kBF16, NS><<<grid, C::NT, 0, TESM_LOGGED(st, mfma32_kernel<WM, WN, TM, TN, EPI, kBF16, NS>)>>>(a);
   else
-    mfma32_kernel<WM, WN, TM, TN, EPI, kF32, NS><<<grid, C::NT, 0, st>>>(a);
+    mfma32_kernel<WM, WN, TM, TN, EPI, kF32, NS><<<grid, C::NT, 0, TESM_LOGGED(st, mfma32_kernel<WM, WN, TM, TN, EPI, kF32, NS>)>>>(a);
   return check_launch("bitlinear mfma32");
 }
 
@@ -1747,9 +1747,9 @@ int run_skinny(const LinearArgs& a, hipStream_t st) {
   const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 16 * TN - 1) / (16 * TN));
   TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
   if (a.out_dt == kBF16)
-    skinny_kernel<NW, TM, TN, EPI, kBF16><<<static_cast<unsigned>(tiles), NW * 64, 0, st>>>(a);
+    skinny_kernel<NW, TM, TN, EPI, kBF16><<<static_cast<unsigned>(tiles), NW * 64, 0, TESM_LOGGED(st, skinny_kernel<NW, TM, TN, EPI, kBF16>)>>>(a);
   else
-    skinny_kernel<NW, TM, TN, EPI, kF32><<<static_cast<unsigned>(tiles), NW * 64, 0, st>>>(a);
+    skinny_kernel<NW, TM, TN, EPI, kF32><<<static_cast<unsigned>(tiles), NW * 64, 0, TESM_LOGGED(st, skinny_kernel<NW, TM, TN, EPI, kF32>)>>>(a);
   return check_launch("bitlinear skinny");
 }
 
@@ -1760,9 +1760,9 @@ int run_mfma(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(tiles <= 0x7fffffff, kErrUnsupported, "bitlinear: too many tiles");
   const unsigned grid = static_cast<unsigned>(tiles);
   if (a.out_dt == kBF16)
-    mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, st>>>(a);
+    mfma_kernel<WM, WN, TM, TN, EPI, kBF16><<<grid, C::NT, 0, TESM_LOGGED(st, mfma_kernel<WM, WN, TM, TN, EPI, kBF16>)>>>(a);
   else
-    mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, st>>>(a);
+    mfma_kernel<WM, WN, TM, TN, EPI, kF32><<<grid, C::NT, 0, TESM_LOGGED(st, mfma_kernel<WM, WN, TM, TN, EPI, kF32>)>>>(a);
   return check_launch("bitlinear mfma");
 }
 
@@ -1776,9 +1776,9 @@ void launch_rowq_lds(const LinearArgs& a, const RowQuant& o, int64_t ntiles, int
   const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / lds));
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ntiles, cus * per_cu));
   if (a.out_dt == kBF16)
-    gate_rowq_lds_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, st>>>(a, o, ntiles);
+    gate_rowq_lds_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_lds_kernel<NW, NCT, kBF16, NKS>)>>>(a, o, ntiles);
   else
-    gate_rowq_lds_kernel<NW, NCT, kF32, NKS><<<grid, NW * 64, lds, st>>>(a, o, ntiles);
+    gate_rowq_lds_kernel<NW, NCT, kF32, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_lds_kernel<NW, NCT, kF32, NKS>)>>>(a, o, ntiles);
 }
 
 template <int NW, int NCT>
@@ -1805,14 +1805,14 @@ int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(ntiles);
   if (a.out_dt == kBF16) {
     if (vec)
-      gate_rowq_kernel<NW, NCT, kBF16, true, 0><<<grid, NW * 64, lds, st>>>(a, o);
+      gate_rowq_kernel<NW, NCT, kBF16, true, 0><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_kernel<NW, NCT, kBF16, true, 0>)>>>(a, o);
     else
-      gate_rowq_kernel<NW, NCT, kBF16, false, 0><<<grid, NW * 64, lds, st>>>(a, o);
+      gate_rowq_kernel<NW, NCT, kBF16, false, 0><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_kernel<NW, NCT, kBF16, false, 0>)>>>(a, o);
   } else {
     if (vec)
-      gate_rowq_kernel<NW, NCT, kF32, true, 0><<<grid, NW * 64, lds, st>>>(a, o);
+      gate_rowq_kernel<NW, NCT, kF32, true, 0><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_kernel<NW, NCT, kF32, true, 0>)>>>(a, o);
     else
-      gate_rowq_kernel<NW, NCT, kF32, false, 0><<<grid, NW * 64, lds, st>>>(a, o);
+      gate_rowq_kernel<NW, NCT, kF32, false, 0><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_kernel<NW, NCT, kF32, false, 0>)>>>(a, o);
   }
   return check_launch("output gate rowq");
 }
@@ -1824,9 +1824,9 @@ int run_gemv(const LinearArgs& a, hipStream_t st) {
   const int64_t waves = (groups + GPW - 1) / GPW;
   const unsigned blocks = static_cast<unsigned>((waves + 3) / 4);
   if (a.out_dt == kBF16)
-    gemv_kernel<LPR, MR, NCH, kBF16, RPG><<<blocks, 256, 0, st>>>(a);
+    gemv_kernel<LPR, MR, NCH, kBF16, RPG><<<blocks, 256, 0, TESM_LOGGED(st, gemv_kernel<LPR, MR, NCH, kBF16, RPG>)>>>(a);
   else
-    gemv_kernel<LPR, MR, NCH, kF32, RPG><<<blocks, 256, 0, st>>>(a);
+    gemv_kernel<LPR, MR, NCH, kF32, RPG><<<blocks, 256, 0, TESM_LOGGED(st, gemv_kernel<LPR, MR, NCH, kF32, RPG>)>>>(a);
   return check_launch("bitlinear gemv");
 }
 
@@ -1875,9 +1875,9 @@ void run_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
   const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 15) / 16);
   const size_t lds = static_cast<size_t>(16 * TM * (a.Kp + 16) + 16 * TM * 8);
   if (a.out_dt == kBF16)
-    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, TESM_LOGGED(st, skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G>)>>>(a, f);
   else
-    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, st>>>(a, f);
+    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, TESM_LOGGED(st, skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G>)>>>(a, f);
 }
 template <int TM>
 void dispatch_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, bool vec, hipStream_t st) {

@@ -264,6 +264,20 @@ void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
+// Launch log: while enabled (tesm_hip_launch_log), every kernel launch appends the kernel's name
+// with its template arguments.  The launch sites pass their stream through TESM_LOGGED, so a
+// disabled log costs one relaxed load per launch.
+extern int g_launch_log_on;
+void log_kernel(const char* pretty);
+template <auto K>
+inline const char* kernel_pretty() {
+  return __PRETTY_FUNCTION__;  // "... [K = &ns::name<args>]"
+}
+template <auto K>
+inline void note_kernel() {
+  if (__atomic_load_n(&g_launch_log_on, __ATOMIC_RELAXED)) log_kernel(kernel_pretty<K>());
+}
+
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -278,3 +292,7 @@ inline int64_t kpad(int64_t K) { return round_up(K < 1 ? 1 : K, kKTile); }
   do {                                       \
     if (!(cond)) return ::tesm::fail((code), (msg)); \
   } while (0)
+
+// Stream argument of a kernel launch that also records the kernel in the launch log:
+//   kern<A, B><<<grid, block, lds, TESM_LOGGED(st, kern<A, B>)>>>(args);
+#define TESM_LOGGED(st, ...) (::tesm::note_kernel<&__VA_ARGS__>(), (st))

@@ -46,6 +46,8 @@ struct DecodeArgs {
   float* s_c = nullptr;
   int32_t* rs_c = nullptr;
   int64_t ldq = 0;
+  // optional (B, H, W) int8 ternary decisions at the padded window positions (reference read order)
+  int8_t* tern = nullptr;
 };
 
 int64_t decode_lds_bytes(int64_t R, int64_t CW);

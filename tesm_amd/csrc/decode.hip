@@ -211,6 +211,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
     const float tern = lane < W ? wn[lane] : 0.0f;
     const float n = fmaxf(wave_sum_f<64>(fabsf(tern)), 1.0f);
     if (lane < W) wn[lane] = rnd<DT>(tern / n);
+    if (a.tern && blockIdx.z == 0 && lane < W) a.tern[bh * a.W + lane] = static_cast<int8_t>(tern);
   }
   __syncthreads();
 
@@ -408,11 +409,11 @@ int launch_decode_ent(const DecodeArgs& a, hipStream_t st) {
 #define TESM_DEC_LAUNCH3(DT_, CDT_, FUSE_, CPT_)                                        \
   do {                                                                                 \
     if (ni == 1)                                                                       \
-      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 1><<<grid, 256, lds, st>>>(k);         \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 1><<<grid, 256, lds, TESM_LOGGED(st, decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 1>)>>>(k);         \
     else if (ni == 2)                                                                  \
-      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 2><<<grid, 256, lds, st>>>(k);         \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 2><<<grid, 256, lds, TESM_LOGGED(st, decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 2>)>>>(k);         \
     else                                                                               \
-      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 4><<<grid, 256, lds, st>>>(k);         \
+      decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 4><<<grid, 256, lds, TESM_LOGGED(st, decode_ent_kernel<DT_, CDT_, FUSE_, CPT_, 4>)>>>(k);         \
   } while (0)
 #define TESM_DEC_LAUNCH2(DT_, CDT_, FUSE_)                                             \
   do {                                                                                 \
@@ -458,20 +459,20 @@ int launch_cache_fill(const CacheFillArgs& a, hipStream_t st) {
   if (a.dt == kBF16) {
     if (sdt == kF32) {
       if (a.cdt == kBF16)
-        cache_fill_kernel<kBF16, kBF16, kF32><<<grid, 256, 0, st>>>(a);
+        cache_fill_kernel<kBF16, kBF16, kF32><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kBF16, kBF16, kF32>)>>>(a);
       else
-        cache_fill_kernel<kBF16, kF32, kF32><<<grid, 256, 0, st>>>(a);
+        cache_fill_kernel<kBF16, kF32, kF32><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kBF16, kF32, kF32>)>>>(a);
     } else {
       if (a.cdt == kBF16)
-        cache_fill_kernel<kBF16, kBF16, kBF16><<<grid, 256, 0, st>>>(a);
+        cache_fill_kernel<kBF16, kBF16, kBF16><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kBF16, kBF16, kBF16>)>>>(a);
       else
-        cache_fill_kernel<kBF16, kF32, kBF16><<<grid, 256, 0, st>>>(a);
+        cache_fill_kernel<kBF16, kF32, kBF16><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kBF16, kF32, kBF16>)>>>(a);
     }
   } else {
     if (a.cdt == kBF16)
-      cache_fill_kernel<kF32, kBF16, kF32><<<grid, 256, 0, st>>>(a);
+      cache_fill_kernel<kF32, kBF16, kF32><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kF32, kBF16, kF32>)>>>(a);
     else
-      cache_fill_kernel<kF32, kF32, kF32><<<grid, 256, 0, st>>>(a);
+      cache_fill_kernel<kF32, kF32, kF32><<<grid, 256, 0, TESM_LOGGED(st, cache_fill_kernel<kF32, kF32, kF32>)>>>(a);
   }
   return check_launch("cache fill");
 }

@@ -586,15 +586,15 @@ int run_scores(const EntArgs& a, int64_t weff, hipStream_t st) {
   if (MIMO && a.q_add == nullptr) {
     const size_t lds = static_cast<size_t>((kScTP + kScTP + a.W - 1) * kScPitch) * sizeof(float);
     dim3 grid(static_cast<unsigned>((a.L + kScTP - 1) / kScTP), static_cast<unsigned>(a.B * a.H));
-    ent_scores_mimo_kernel<DT><<<grid, 256, lds, st>>>(a);
+    ent_scores_mimo_kernel<DT><<<grid, 256, lds, TESM_LOGGED(st, ent_scores_mimo_kernel<DT>)>>>(a);
     return check_launch("entanglement scores (MIMO, tiled)");
   }
   const int64_t groups = a.B * a.L * a.H;
   auto blocks = [&](int wp) { return static_cast<unsigned>((groups * wp + 255) / 256); };
-  if (weff <= 8) ent_scores_kernel<DT, MIMO, 8><<<blocks(8), 256, 0, st>>>(a, weff, 0.f);
-  else if (weff <= 16) ent_scores_kernel<DT, MIMO, 16><<<blocks(16), 256, 0, st>>>(a, weff, 0.f);
-  else if (weff <= 32) ent_scores_kernel<DT, MIMO, 32><<<blocks(32), 256, 0, st>>>(a, weff, 0.f);
-  else ent_scores_kernel<DT, MIMO, 64><<<blocks(64), 256, 0, st>>>(a, weff, 0.f);
+  if (weff <= 8) ent_scores_kernel<DT, MIMO, 8><<<blocks(8), 256, 0, TESM_LOGGED(st, ent_scores_kernel<DT, MIMO, 8>)>>>(a, weff, 0.f);
+  else if (weff <= 16) ent_scores_kernel<DT, MIMO, 16><<<blocks(16), 256, 0, TESM_LOGGED(st, ent_scores_kernel<DT, MIMO, 16>)>>>(a, weff, 0.f);
+  else if (weff <= 32) ent_scores_kernel<DT, MIMO, 32><<<blocks(32), 256, 0, TESM_LOGGED(st, ent_scores_kernel<DT, MIMO, 32>)>>>(a, weff, 0.f);
+  else ent_scores_kernel<DT, MIMO, 64><<<blocks(64), 256, 0, TESM_LOGGED(st, ent_scores_kernel<DT, MIMO, 64>)>>>(a, weff, 0.f);
   return check_launch("entanglement scores");
 }
 
@@ -603,7 +603,7 @@ int run_mix(const EntArgs& a, int64_t weff, hipStream_t st) {
   dim3 grid(static_cast<unsigned>((a.D + kMixDS - 1) / kMixDS), static_cast<unsigned>((a.L + kMixTP - 1) / kMixTP),
             static_cast<unsigned>(a.B * a.H));
   const size_t lds = static_cast<size_t>((kMixTP + weff - 1) * kMixDS + kMixTP * weff) * sizeof(float);
-  ent_mix_kernel<DT><<<grid, 256, lds, st>>>(a, weff);
+  ent_mix_kernel<DT><<<grid, 256, lds, TESM_LOGGED(st, ent_mix_kernel<DT>)>>>(a, weff);
   return check_launch("entanglement mix");
 }
 
@@ -617,9 +617,9 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
   TESM_REQUIRE(tab != nullptr, kErrInvalidArg, "rope_table: null pointer");
   const unsigned nb = static_cast<unsigned>((L * (R / 2) + 255) / 256);
   if (dt == kBF16)
-    rope_table_kernel<kBF16><<<nb, 256, 0, st>>>(tab, L, R, pos_offset, base);
+    rope_table_kernel<kBF16><<<nb, 256, 0, TESM_LOGGED(st, rope_table_kernel<kBF16>)>>>(tab, L, R, pos_offset, base);
   else
-    rope_table_kernel<kF32><<<nb, 256, 0, st>>>(tab, L, R, pos_offset, base);
+    rope_table_kernel<kF32><<<nb, 256, 0, TESM_LOGGED(st, rope_table_kernel<kF32>)>>>(tab, L, R, pos_offset, base);
   return check_launch("rope_table");
 }
 
@@ -658,9 +658,9 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
     const FusedLds f = fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4);
     dim3 grid(static_cast<unsigned>((a.L + kFusedTP - 1) / kFusedTP), static_cast<unsigned>(a.B));
     if (a.dt == kBF16)
-      ent_fused_kernel<kBF16><<<grid, 256, f.total, st>>>(a, weff, f);
+      ent_fused_kernel<kBF16><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16>)>>>(a, weff, f);
     else
-      ent_fused_kernel<kF32><<<grid, 256, f.total, st>>>(a, weff, f);
+      ent_fused_kernel<kF32><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kF32>)>>>(a, weff, f);
     return check_launch("entanglement fused");
   }
   int rc;

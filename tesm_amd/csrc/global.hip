@@ -203,9 +203,9 @@ int launch_global_bias_table(int dt, int64_t n, const float* embed, int64_t P, c
   TESM_REQUIRE(embed && scale && bias && table && P >= 1 && n >= 1, kErrInvalidArg, "global bias: bad arguments");
   const unsigned nb = static_cast<unsigned>((n + 255) / 256);
   if (dt == kBF16)
-    global_bias_table_kernel<kBF16><<<nb, 256, 0, st>>>(n, embed, P, scale, bias, table);
+    global_bias_table_kernel<kBF16><<<nb, 256, 0, TESM_LOGGED(st, global_bias_table_kernel<kBF16>)>>>(n, embed, P, scale, bias, table);
   else
-    global_bias_table_kernel<kF32><<<nb, 256, 0, st>>>(n, embed, P, scale, bias, table);
+    global_bias_table_kernel<kF32><<<nb, 256, 0, TESM_LOGGED(st, global_bias_table_kernel<kF32>)>>>(n, embed, P, scale, bias, table);
   return check_launch("global bias table");
 }
 
@@ -237,16 +237,16 @@ int launch_global_ent(const GlobalArgs& a, hipStream_t st) {
   const dim3 gs(static_cast<unsigned>(nqb), static_cast<unsigned>(nqb), static_cast<unsigned>(a.B));
   const dim3 gm(static_cast<unsigned>(ncb), static_cast<unsigned>(nqb), static_cast<unsigned>(a.B));
   if (a.dt == kBF16) {
-    global_rope_kernel<kBF16><<<nbr, 256, 0, st>>>(a, a.qr, a.kr);
-    global_scores_kernel<kBF16><<<gs, 256, 0, st>>>(a, a.qr, a.kr, ldt, a.count, nqb);
+    global_rope_kernel<kBF16><<<nbr, 256, 0, TESM_LOGGED(st, global_rope_kernel<kBF16>)>>>(a, a.qr, a.kr);
+    global_scores_kernel<kBF16><<<gs, 256, 0, TESM_LOGGED(st, global_scores_kernel<kBF16>)>>>(a, a.qr, a.kr, ldt, a.count, nqb);
     if (a.mimo)
-      global_mix_kernel<kBF16, kF32><<<gm, 256, 0, st>>>(a, ldt, nqb);
+      global_mix_kernel<kBF16, kF32><<<gm, 256, 0, TESM_LOGGED(st, global_mix_kernel<kBF16, kF32>)>>>(a, ldt, nqb);
     else
-      global_mix_kernel<kBF16, kBF16><<<gm, 256, 0, st>>>(a, ldt, nqb);
+      global_mix_kernel<kBF16, kBF16><<<gm, 256, 0, TESM_LOGGED(st, global_mix_kernel<kBF16, kBF16>)>>>(a, ldt, nqb);
   } else {
-    global_rope_kernel<kF32><<<nbr, 256, 0, st>>>(a, a.qr, a.kr);
-    global_scores_kernel<kF32><<<gs, 256, 0, st>>>(a, a.qr, a.kr, ldt, a.count, nqb);
-    global_mix_kernel<kF32, kF32><<<gm, 256, 0, st>>>(a, ldt, nqb);
+    global_rope_kernel<kF32><<<nbr, 256, 0, TESM_LOGGED(st, global_rope_kernel<kF32>)>>>(a, a.qr, a.kr);
+    global_scores_kernel<kF32><<<gs, 256, 0, TESM_LOGGED(st, global_scores_kernel<kF32>)>>>(a, a.qr, a.kr, ldt, a.count, nqb);
+    global_mix_kernel<kF32, kF32><<<gm, 256, 0, TESM_LOGGED(st, global_mix_kernel<kF32, kF32>)>>>(a, ldt, nqb);
   }
   return check_launch("global ent");
 }

@@ -250,9 +250,9 @@ int launch_mimo_stats(const MimoStatsArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.R >= 2 && a.R % 2 == 0 && a.H >= 1, kErrInvalidArg, "mimo stats: need an even R");
   TESM_REQUIRE((a.S - a.W + 1) * a.H * a.W <= 0x7fffffff, kErrUnsupported, "mimo stats: too many scores");
   if (a.dt == kBF16)
-    mimo_stats_kernel<kBF16><<<static_cast<unsigned>(a.B), 256, 0, st>>>(a);
+    mimo_stats_kernel<kBF16><<<static_cast<unsigned>(a.B), 256, 0, TESM_LOGGED(st, mimo_stats_kernel<kBF16>)>>>(a);
   else
-    mimo_stats_kernel<kF32><<<static_cast<unsigned>(a.B), 256, 0, st>>>(a);
+    mimo_stats_kernel<kF32><<<static_cast<unsigned>(a.B), 256, 0, TESM_LOGGED(st, mimo_stats_kernel<kF32>)>>>(a);
   return check_launch("mimo stats");
 }
 
@@ -263,9 +263,9 @@ int launch_mimo_coef(const void* mimo_x, const void* mimo_o, int dt, int64_t H, 
   TESM_REQUIRE(mimo_x && mimo_o && coef && x0sq, kErrInvalidArg, "mimo coef: null pointer");
   const unsigned nb = static_cast<unsigned>((H * D + 255) / 256);
   if (dt == kBF16)
-    mimo_coef_kernel<kBF16><<<nb, 256, 0, st>>>(mimo_x, mimo_o, H, Rm, D, coef, x0sq);
+    mimo_coef_kernel<kBF16><<<nb, 256, 0, TESM_LOGGED(st, mimo_coef_kernel<kBF16>)>>>(mimo_x, mimo_o, H, Rm, D, coef, x0sq);
   else
-    mimo_coef_kernel<kF32><<<nb, 256, 0, st>>>(mimo_x, mimo_o, H, Rm, D, coef, x0sq);
+    mimo_coef_kernel<kF32><<<nb, 256, 0, TESM_LOGGED(st, mimo_coef_kernel<kF32>)>>>(mimo_x, mimo_o, H, Rm, D, coef, x0sq);
   return check_launch("mimo coef");
 }
 
@@ -285,13 +285,13 @@ int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st) {
                    reinterpret_cast<uintptr_t>(a.te) % (a.dt == kBF16 ? 8 : 16) == 0 &&
                    reinterpret_cast<uintptr_t>(a.cc) % (a.dt == kBF16 ? 8 : 16) == 0;
   if (a.dt == kBF16) {
-    if (vec && a.W == 64) mimo_mix_kernel<kBF16, true, 64><<<grid, 256, lds, st>>>(a);
-    else if (vec) mimo_mix_kernel<kBF16, true, 0><<<grid, 256, lds, st>>>(a);
-    else mimo_mix_kernel<kBF16, false, 0><<<grid, 256, lds, st>>>(a);
+    if (vec && a.W == 64) mimo_mix_kernel<kBF16, true, 64><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 64>)>>>(a);
+    else if (vec) mimo_mix_kernel<kBF16, true, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 0>)>>>(a);
+    else mimo_mix_kernel<kBF16, false, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, false, 0>)>>>(a);
   } else {
-    if (vec && a.W == 64) mimo_mix_kernel<kF32, true, 64><<<grid, 256, lds, st>>>(a);
-    else if (vec) mimo_mix_kernel<kF32, true, 0><<<grid, 256, lds, st>>>(a);
-    else mimo_mix_kernel<kF32, false, 0><<<grid, 256, lds, st>>>(a);
+    if (vec && a.W == 64) mimo_mix_kernel<kF32, true, 64><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 64>)>>>(a);
+    else if (vec) mimo_mix_kernel<kF32, true, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 0>)>>>(a);
+    else mimo_mix_kernel<kF32, false, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, false, 0>)>>>(a);
   }
   return check_launch("mimo mix");
 }
@@ -301,7 +301,7 @@ int launch_mimo_final(const float* S, const float* x0sq, int64_t B, int64_t L, i
   if (B == 0 || L == 0 || (!h_final && !last)) return kOk;
   TESM_REQUIRE(S && x0sq, kErrInvalidArg, "mimo final: null pointer");
   const unsigned nb = static_cast<unsigned>((B * C + 255) / 256);
-  mimo_final_kernel<<<nb, 256, 0, st>>>(S, x0sq, B, L, C, h_final, last);
+  mimo_final_kernel<<<nb, 256, 0, TESM_LOGGED(st, mimo_final_kernel)>>>(S, x0sq, B, L, C, h_final, last);
   return check_launch("mimo final");
 }
 

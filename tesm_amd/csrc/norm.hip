@@ -108,9 +108,9 @@ int launch_add_rmsnorm(const NormArgs& a, hipStream_t st) {
   const size_t lds = static_cast<size_t>(a.D + 8) * sizeof(float);
   const dim3 grid(static_cast<unsigned>(a.M));
   if (a.dt == kBF16)
-    add_rmsnorm_kernel<kBF16><<<grid, kNormThreads, lds, st>>>(a);
+    add_rmsnorm_kernel<kBF16><<<grid, kNormThreads, lds, TESM_LOGGED(st, add_rmsnorm_kernel<kBF16>)>>>(a);
   else
-    add_rmsnorm_kernel<kF32><<<grid, kNormThreads, lds, st>>>(a);
+    add_rmsnorm_kernel<kF32><<<grid, kNormThreads, lds, TESM_LOGGED(st, add_rmsnorm_kernel<kF32>)>>>(a);
   return check_launch("rmsnorm");
 }
 

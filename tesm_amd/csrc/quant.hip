@@ -84,7 +84,7 @@ void run_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int 
                float* s_x, int32_t* rowsum, int* zero_p, int64_t zero_n, hipStream_t st) {
   constexpr int RPB = 4 * (64 / LPR);
   const unsigned nb = static_cast<unsigned>(std::max<int64_t>((M + RPB - 1) / RPB, zero_n > 0 ? 1 : 0));
-  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, st>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n);
+  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, TESM_LOGGED(st, quant_act_kernel<DT, VEC, LPR, G>)>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n);
 }
 
 template <int DT, bool VEC>
@@ -166,11 +166,11 @@ int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, floa
   TESM_REQUIRE(n >= 1 && w && ws && s_w && c_w, kErrInvalidArg, "absmean: need n >= 1 and non-null pointers");
   const int nb = static_cast<int>(std::min<int64_t>(kAbsmeanBlocks, (n + 255) / 256));
   if (dt == kBF16) {
-    absmean_partial_kernel<kBF16><<<nb, 256, 0, st>>>(w, n, ws);
-    absmean_final_kernel<kBF16><<<1, 64, 0, st>>>(ws, nb, n, eps, s_w, c_w);
+    absmean_partial_kernel<kBF16><<<nb, 256, 0, TESM_LOGGED(st, absmean_partial_kernel<kBF16>)>>>(w, n, ws);
+    absmean_final_kernel<kBF16><<<1, 64, 0, TESM_LOGGED(st, absmean_final_kernel<kBF16>)>>>(ws, nb, n, eps, s_w, c_w);
   } else {
-    absmean_partial_kernel<kF32><<<nb, 256, 0, st>>>(w, n, ws);
-    absmean_final_kernel<kF32><<<1, 64, 0, st>>>(ws, nb, n, eps, s_w, c_w);
+    absmean_partial_kernel<kF32><<<nb, 256, 0, TESM_LOGGED(st, absmean_partial_kernel<kF32>)>>>(w, n, ws);
+    absmean_final_kernel<kF32><<<1, 64, 0, TESM_LOGGED(st, absmean_final_kernel<kF32>)>>>(ws, nb, n, eps, s_w, c_w);
   }
   return check_launch("absmean");
 }
@@ -213,9 +213,9 @@ int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const 
   const int64_t total = N * ldp;
   const unsigned nb = static_cast<unsigned>((total + 255) / 256);
   if (dt == kBF16)
-    pack_kernel<kBF16><<<nb, 256, 0, st>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
+    pack_kernel<kBF16><<<nb, 256, 0, TESM_LOGGED(st, pack_kernel<kBF16>)>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
   else
-    pack_kernel<kF32><<<nb, 256, 0, st>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
+    pack_kernel<kF32><<<nb, 256, 0, TESM_LOGGED(st, pack_kernel<kF32>)>>>(w, N, K, ldw, s_w, per_row, packed, ldp);
   return check_launch("pack_w_i2");
 }
 
@@ -235,7 +235,7 @@ int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8
   TESM_REQUIRE(N == 0 || (packed && codes), kErrInvalidArg, "unpack_w_i2: null pointer");
   if (N == 0) return kOk;
   const unsigned nb = static_cast<unsigned>((N * K + 255) / 256);
-  unpack_kernel<<<nb, 256, 0, st>>>(packed, N, K, ldp, codes, ldc);
+  unpack_kernel<<<nb, 256, 0, TESM_LOGGED(st, unpack_kernel)>>>(packed, N, K, ldp, codes, ldc);
   return check_launch("unpack_w_i2");
 }
 

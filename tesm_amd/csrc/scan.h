@@ -36,6 +36,10 @@ int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs);
 int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st);
 // The int range of the workspace the single-pass scan needs zero at its start (*n = 0 when that
 // pass will not run for these sizes and this workspace).
+// Status word of the look-back scan on the current device (bit 0: a poll gave up); synchronous.
+int scan_status(unsigned* out, int clear);
+// Poll limit of later look-back launches (< 0: give up at once; a test of the failure report).
+void scan_set_spin_limit(int limit);
 void scan_lb_clear_range(int64_t B, int64_t L, int64_t C, int64_t cs, void* ws, int** p, int64_t* n);
 
 }  // namespace tesm

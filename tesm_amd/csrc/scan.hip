@@ -265,19 +265,27 @@ __global__ __launch_bounds__(NSEG * 64) void scan_carry_seg_kernel(ScanArgs a, i
 // L2s, without the whole-L2 write-back and invalidate an agent-scope release / acquire costs).  A
 // writer waits for its value stores to complete (s_waitcnt) before the workgroup barrier after which
 // one thread stores the flag; a reader polls flags in one wave, and the other waves read values
-// only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds (the tile's
-// states are then NaN, so the failure shows in the outputs), so the launch completes whatever happens.
+// only after the barrier that follows.  A poll gives up after kScanSpinLimit rounds, so the launch
+// completes whatever happens: the tile's states are then NaN and bit 0 of the device status word
+// g_scan_status is set (tesm_hip_device_status reads and clears it).
 // ---------------------------------------------------------------------------
 constexpr int kScanLbCh = 64;    // channels per tile (one per lane)
 // sub-spans per tile (one per wave): 4, or 8 for long chains (fewer spans to chain; with few spans
 // per chain the shorter tile keeps more workgroups in flight)
 constexpr int kScanSpinLimit = 1 << 20;
 
+// Device status word of the look-back scan (one per device): bit 0 = a poll gave up.
+__device__ unsigned g_scan_status;
+// Poll limit of the next launches; a negative value makes every look-back give up at once, which
+// tests use to exercise the failure report (tesm_hip_debug_scan_spin_limit).
+int g_scan_spin_limit = kScanSpinLimit;
+
 struct ScanLb {
   float2* agg;       // (B, nc, C): (prod d, h_end from 0) of every span
   float* incl;       // (B, nc, C): state at the end of every span
   int* flags;        // (B, nc, G): 0 nothing yet, 1 aggregate published, 2 end state published
   unsigned* ticket;  // span counter of chain x at ticket[x * kScanLbTicketStride]
+  int spin_limit;    // poll rounds before giving up (< 0: give up without polling)
 };
 constexpr int kScanLbTicketStride = 64;  // ints: one 256-byte line per counter
 
@@ -413,6 +421,11 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
         const int64_t k = k0 - lane;
         int m = 0, stop = 2;
         for (int it = 0;; ++it) {
+          if (s.spin_limit < 0) {
+            m = 0;
+            stop = 2;
+            break;
+          }
           const int f = k >= 0 ? scan_flag_load(&s.flags[fb + k * G]) : 0;
           const unsigned long long incl = __ballot(f == 2), ready = __ballot(f >= 1);
           if (incl) {
@@ -427,7 +440,7 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
             stop = 0;
             break;
           }
-          if (it >= kScanSpinLimit) {
+          if (it >= s.spin_limit) {
             m = 0;
             stop = 2;
             break;
@@ -471,8 +484,9 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
         carry = accH + accP * scan_val_load(&s.incl[vb + (k0 - m) * a.C]);
         break;
       }
-      if (stop == 2) {  // gave up waiting: NaN states make the failure visible instead of plausible
+      if (stop == 2) {  // gave up waiting: NaN states and the status bit report the failure
         carry = __builtin_nanf("");
+        if (tid == 0) __hip_atomic_fetch_or(&g_scan_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       k0 -= 64;
@@ -524,21 +538,22 @@ int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream
   s.incl = summ + 2 * a.B * sh.nc * a.C;
   s.flags = flags;
   s.ticket = reinterpret_cast<unsigned*>(flags + sh.tiles);
+  s.spin_limit = __atomic_load_n(&g_scan_spin_limit, __ATOMIC_RELAXED);
   const int64_t nchain = a.B * sh.G;
   if (!a.flags_clear)
-    scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, st>>>(flags, sh.tiles,
+    scan_lb_reset_kernel<<<static_cast<unsigned>((sh.tiles + nchain + 255) / 256), 256, 0, TESM_LOGGED(st, scan_lb_reset_kernel)>>>(flags, sh.tiles,
                                                                                                  nchain);
   const unsigned grid = static_cast<unsigned>(sh.tiles);
   if (sh.sub == 8) {
     if (T <= 16)
-      scan_lb_kernel<DT, OUT_DT, MODE, 16, 8><<<grid, kScanLbCh * 8, 0, st>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 8><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 8>)>>>(a, T, sh.nc, sh.G, s);
     else
-      scan_lb_kernel<DT, OUT_DT, MODE, 32, 8><<<grid, kScanLbCh * 8, 0, st>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 8><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 8>)>>>(a, T, sh.nc, sh.G, s);
   } else {
     if (T <= 16)
-      scan_lb_kernel<DT, OUT_DT, MODE, 16, 4><<<grid, kScanLbCh * 4, 0, st>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 4><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 4>)>>>(a, T, sh.nc, sh.G, s);
     else
-      scan_lb_kernel<DT, OUT_DT, MODE, 32, 4><<<grid, kScanLbCh * 4, 0, st>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 4><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 4>)>>>(a, T, sh.nc, sh.G, s);
   }
   return check_launch("scan look-back");
 }
@@ -550,13 +565,13 @@ int run_scan_fast(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* 
   // the gate pass is VALU-heavy: one channel per thread for twice the waves
   constexpr int CPT1 = MODE == 1 ? 1 : CPT;
   const unsigned nb1 = static_cast<unsigned>((a.B * nc * (a.C / CPT1) + 255) / 256);
-  scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT1><<<nb1, 256, 0, st>>>(a, T, nc, summ, carry);
+  scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT1><<<nb1, 256, 0, TESM_LOGGED(st, scan_fast_kernel<DT, OUT_DT, MODE, 1, TM, CPT1>)>>>(a, T, nc, summ, carry);
   dim3 g2(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.B));
   if (nc >= 64)
-    scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, st>>>(a, nc, summ, carry);
+    scan_carry_seg_kernel<16><<<g2, 16 * 64, 0, TESM_LOGGED(st, scan_carry_seg_kernel<16>)>>>(a, nc, summ, carry);
   else
-    scan_carry_seg_kernel<4><<<g2, 4 * 64, 0, st>>>(a, nc, summ, carry);
-  scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, st>>>(a, T, nc, summ, carry);
+    scan_carry_seg_kernel<4><<<g2, 4 * 64, 0, TESM_LOGGED(st, scan_carry_seg_kernel<4>)>>>(a, nc, summ, carry);
+  scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT><<<nb, 256, 0, TESM_LOGGED(st, scan_fast_kernel<DT, OUT_DT, MODE, 3, TM, CPT>)>>>(a, T, nc, summ, carry);
   return check_launch("scan");
 }
 
@@ -575,10 +590,10 @@ int scan_fast_dispatch(const ScanArgs& e, int64_t T, int64_t nc, float* summ, fl
 template <int DT, int OUT_DT, int MODE>
 int run_scan(const ScanArgs& a, int64_t T, int64_t nc, float* summ, float* carry, hipStream_t st) {
   dim3 g3(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(nc), static_cast<unsigned>(a.B));
-  scan_chunk_kernel<DT, OUT_DT, MODE, 1><<<g3, 64, 0, st>>>(a, T, nc, summ, carry);
+  scan_chunk_kernel<DT, OUT_DT, MODE, 1><<<g3, 64, 0, TESM_LOGGED(st, scan_chunk_kernel<DT, OUT_DT, MODE, 1>)>>>(a, T, nc, summ, carry);
   dim3 g2(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.B));
-  scan_carry_kernel<<<g2, 64, 0, st>>>(a, nc, summ, carry);
-  scan_chunk_kernel<DT, OUT_DT, MODE, 3><<<g3, 64, 0, st>>>(a, T, nc, summ, carry);
+  scan_carry_kernel<<<g2, 64, 0, TESM_LOGGED(st, scan_carry_kernel)>>>(a, nc, summ, carry);
+  scan_chunk_kernel<DT, OUT_DT, MODE, 3><<<g3, 64, 0, TESM_LOGGED(st, scan_chunk_kernel<DT, OUT_DT, MODE, 3>)>>>(a, T, nc, summ, carry);
   return check_launch("scan");
 }
 
@@ -692,5 +707,19 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
     default: return fail(kErrInvalidArg, "scan: unsupported dtype combination");
   }
 }
+
+int scan_status(unsigned* out, int clear) {
+  unsigned v = 0;
+  hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_scan_status), sizeof(v), 0, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && clear && v != 0) {
+    const unsigned zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_scan_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) return fail(kErrLaunch, std::string("device status: ") + hipGetErrorString(e));
+  if (out) *out = v;
+  return kOk;
+}
+
+void scan_set_spin_limit(int limit) { __atomic_store_n(&g_scan_spin_limit, limit, __ATOMIC_RELAXED); }
 
 }  // namespace tesm

@@ -149,6 +149,77 @@ def bitlinear(q, s_x, rowsum, packed, c_w, N: int, K: int, out_dtype: torch.dtyp
     return (out, acc) if acc_dump else out
 
 
+def bitlinear_fwd(x, packed, c_w, N: int, eps: float = 1e-5, bias=None, c_w_per_row: bool = False,
+                  fuse: bool = True, out: Optional[torch.Tensor] = None):
+    """BitLinear forward from raw activations x (M, K): codes + product in one C-ABI call (fused
+    for decode-size M when ``fuse``); out (M, N) in x's dtype."""
+    lib = _lib.load()
+    x = _rows(x)
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    require_device(x, packed, c_w, bias, out)
+    nbytes = int(lib.tesm_hip_bitlinear_fwd_ws_bytes(M, K))
+    from .tesm import workspace
+    ws = workspace(x.device, nbytes)
+    with torch.cuda.device(x.device):
+        _lib.check(lib.tesm_hip_bitlinear_fwd(_p(x), dt_code(x.dtype), x.stride(0), eps, _p(packed), packed.stride(0),
+                                              _p(c_w), int(c_w_per_row), _p(bias), M, N, K, _p(out),
+                                              dt_code(out.dtype), out.stride(0), int(fuse), _p(ws), nbytes,
+                                              _stream(x)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# diagnostics: launch log, device status, decision taps
+# ---------------------------------------------------------------------------
+class launch_log:
+    """Context manager recording the kernel instantiations launched inside it::
+
+        with hip_ops.launch_log() as log:
+            layer(u)
+        assert "scan_lb_kernel<1,1,1,16,8>" in log.kernels
+    """
+
+    def __enter__(self):
+        self.kernels = []
+        _lib.check(_lib.load().tesm_hip_launch_log(1))
+        return self
+
+    def __exit__(self, *exc):
+        lib = _lib.load()
+        n = int(lib.tesm_hip_launch_log_read(None, 0, 0))
+        buf = ctypes.create_string_buffer(n + 1)
+        lib.tesm_hip_launch_log_read(buf, n + 1, 1)
+        lib.tesm_hip_launch_log(0)
+        self.kernels = [k for k in buf.value.decode().split("\n") if k]
+        return False
+
+
+def device_status(clear: bool = True) -> int:
+    """The device status word of the current device (bit 0: a scan look-back gave up); synchronises."""
+    v = ctypes.c_uint32(0)
+    lib = _lib.load()
+    _lib.check(lib.tesm_hip_device_status(ctypes.byref(v), int(clear)))
+    return int(v.value)
+
+
+def debug_scan_spin_limit(limit: int) -> None:
+    _lib.check(_lib.load().tesm_hip_debug_scan_spin_limit(int(limit)))
+
+
+def set_taps(**bufs) -> None:
+    """Point the decision taps at device tensors (q_te, s_te, q_c, s_c, q_y, s_y, tern, wts); no
+    arguments stops tapping."""
+    lib = _lib.load()
+    if not bufs:
+        _lib.check(lib.tesm_hip_debug_taps(None))
+        return
+    require_device(*bufs.values())
+    t = _lib.Taps(**{k: (v.data_ptr() if v is not None else None) for k, v in bufs.items()})
+    _lib.check(lib.tesm_hip_debug_taps(ctypes.byref(t)))
+
+
 # ---------------------------------------------------------------------------
 # scan / RoPE / entanglement
 # ---------------------------------------------------------------------------

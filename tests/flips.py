@@ -1,0 +1,255 @@
+"""Flip-resolved parity (test infrastructure).
+
+A device layer and the oracle make the same discrete decisions -- int8 activation codes and
+ternary window decisions -- except where an upstream difference of a few ulps (exact integer vs
+float GEMM accumulation, float32 vs float64 scan, device vs torch transcendental) moves a value
+across a decision boundary.  These helpers
+
+1. run the device layer with the decision taps on (``tesm_hip_debug_taps``), collecting its codes,
+   scales and ternary decisions;
+2. run the oracle with hooks (``BitLinear.code_hook``, ``TESM_SISO.tern_hook``) that replace each
+   oracle decision by the device's, after checking that every decision that differs is a near-tie:
+   the oracle's own pre-rounding value lies within ``near`` of the boundary between the two
+   outcomes (codes: one step apart, value near the half-way point; ternary: score near +-thr);
+3. count those flips, so that the comparison of the outputs can hold *every* row to the north-star
+   tolerance (1e-3 float32, 2e-2 bfloat16).
+
+A defect that changes decisions away from a boundary (a wrong index, scale or sign) fails step 2;
+one that changes continuous values fails step 3 on the rows it touches.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from hip_helpers import DEV, normwise, to_np, unpermute_layout1
+from tesm_amd import hip_ops
+
+# near-tie width of a pre-rounding value v: REL * |v| + ABS.  float32: the paths' values differ by
+# ~1e-6 relative upstream (a 10-100x margin); bfloat16: by one or two bf16 ulps (2^-8 relative
+# each).  Codes: v = x * s on the 127-code scale; scores: q.k / sqrt(R) + bias near +-thr.
+NEAR = {torch.float32: (1e-5, 2e-3), torch.bfloat16: (2.0 ** -6, 0.05)}
+NEAR_SCORE = {torch.float32: (1e-5, 1e-4), torch.bfloat16: (2.0 ** -6, 4e-3)}
+# relative difference allowed between the two paths' per-token scales (the row's absmax)
+SCALE_REL = {torch.float32: 1e-5, torch.bfloat16: 2.0 ** -6}
+TOL = {torch.float32: 1e-3, torch.bfloat16: 2e-2}
+
+
+class Taps:
+    """Device buffers for the decision taps of one layer or feed-forward call (M tokens).
+
+    K widths: u and y d_model, cs d_state (cs_rows rows), te and c k_te, h d_inter."""
+
+    def __init__(self, M, k_te, d_model, dev, tern_shape=None, d_state=None, cs_rows=None, d_inter=None):
+        kp = hip_ops.kpad
+        self.K = {"u": d_model, "y": d_model, "te": k_te, "c": k_te, "cs": d_state or 1, "h": d_inter or 1}
+        rows = {"cs": cs_rows or M}
+        for name, K in self.K.items():
+            r = rows.get(name, M)
+            setattr(self, "q_" + name, torch.zeros((r, kp(K)), dtype=torch.int8, device=dev))
+            setattr(self, "s_" + name, torch.zeros((r,), dtype=torch.float32, device=dev))
+        self.tern = torch.full(tern_shape, 7, dtype=torch.int8, device=dev) if tern_shape else None
+
+    def __enter__(self):
+        bufs = {}
+        for name in self.K:
+            bufs["q_" + name] = getattr(self, "q_" + name)
+            bufs["s_" + name] = getattr(self, "s_" + name)
+        hip_ops.set_taps(tern=self.tern, **bufs)
+        return self
+
+    def __exit__(self, *exc):
+        hip_ops.set_taps()
+        torch.cuda.synchronize()
+        return False
+
+    def codes(self, name):
+        """(natural-order int8 codes (rows, K), float32 scales (rows,)) on the CPU."""
+        q = getattr(self, "q_" + name).cpu().numpy()
+        return unpermute_layout1(q, self.K[name]), getattr(self, "s_" + name).cpu()
+
+
+class Flips:
+    """Counts and checks the decisions fed from the device into the oracle."""
+
+    def __init__(self, dtype):
+        self.dtype = dtype
+        self.code_flips = 0
+        self.codes = 0
+        self.tern_flips = 0
+        self.terns = 0
+
+    def _near(self, v, table=NEAR):
+        rel, ab = table[self.dtype]
+        return rel * v.abs() + ab
+
+    def code_hook(self, q_dev, s_dev):
+        """A BitLinear.code_hook that substitutes the device codes (M, K) and scales (M,)."""
+        def hook(x, v, codes, scale):
+            qd = torch.as_tensor(q_dev).reshape(codes.shape).to(codes.dtype)
+            sd = torch.as_tensor(s_dev).reshape(scale.shape).to(scale.dtype)
+            rel = ((sd.double() - scale.double()).abs() / scale.double().abs()).max().item()
+            assert rel <= SCALE_REL[self.dtype], f"per-token scale differs beyond a near-tie: {rel:.3g}"
+            diff = qd != codes
+            n = int(diff.sum())
+            if n:
+                a, b, vv = codes.double()[diff], qd.double()[diff], v.double()[diff]
+                assert bool(((a - b).abs() == 1).all()), "a code differs by more than one step"
+                gap = (vv - (a + b) / 2).abs()
+                bad = gap > self._near(vv)
+                assert not bool(bad.any()), (
+                    f"{int(bad.sum())} code(s) differ away from a rounding boundary; worst gap "
+                    f"{float(gap.max()):.4g} at value {float(vv[gap.argmax()]):.6g}")
+            self.code_flips += n
+            self.codes += codes.numel()
+            return qd, sd
+        return hook
+
+    def tern_hook(self, dev_tern, thr, kind):
+        """An oracle tern_hook that substitutes the device's ternary decisions.
+
+        kind "local": dev_tern (B, L, W); "decode": (B, H, W) in ring read order; "mimo":
+        (B, L, H, W) with entry w deciding key t - W + 1 + w."""
+        dt = torch.as_tensor(dev_tern).to(torch.float32)
+
+        def hook(scores, tern, where):
+            if where is None or where[0] != kind:
+                return tern
+            if kind == "local":
+                t0, t1 = where[1], where[2]
+                td = dt[:, t0:t1, :].to(tern.dtype)
+                W = td.shape[-1]
+                pos = torch.arange(t0, t1).unsqueeze(1) - (W - 1) + torch.arange(W).unsqueeze(0)
+                valid = (pos >= 0).unsqueeze(0).expand_as(tern)
+            elif kind == "decode":
+                td = dt.reshape(tern.shape).to(tern.dtype)
+                valid = torch.ones_like(tern, dtype=torch.bool)
+            else:  # mimo
+                t, w = where[1], where[2]
+                td = dt[:, t, :, w].reshape(tern.shape).to(tern.dtype)
+                valid = torch.ones_like(tern, dtype=torch.bool)
+            diff = (td != tern) & valid
+            n = int(diff.sum())
+            if n:
+                sc = scores.double()[diff]
+                assert bool((td[diff].double() - tern[diff].double()).abs().max() == 1), "a decision jumps -1 <-> +1"
+                gap = (sc.abs() - thr).abs()
+                bad = gap > self._near(sc, NEAR_SCORE)
+                assert not bool(bad.any()), (
+                    f"{int(bad.sum())} ternary decision(s) differ away from the threshold; worst gap "
+                    f"{float(gap.max()):.4g} at score {float(sc[gap.argmax()]):.6g}")
+            self.tern_flips += n
+            self.terns += int(valid.sum())
+            return torch.where(valid, td, tern)
+        return hook
+
+    def summary(self):
+        return (f"code flips {self.code_flips}/{self.codes}, ternary flips {self.tern_flips}/{self.terns}")
+
+
+def install(ref, flips, taps, tern_kind=None, thr=None):
+    """Feed the taps' decisions into oracle layer ``ref`` (SISO or MIMO)."""
+    for mod, name in ((ref.in_proj, "u"), (ref.cross_layer_q_proj, "cs"), (ref.state_proj, "te"),
+                      (ref.ent_proj, "c"), (ref.out_proj, "y")):
+        mod.code_hook = flips.code_hook(*taps.codes(name))
+    if tern_kind is not None:
+        ref.tern_hook = flips.tern_hook(taps.tern.cpu(), ref.entanglement_threshold if thr is None else thr,
+                                        tern_kind)
+
+
+def install_ffn(ffn, flips, taps):
+    """Feed a feed-forward call's codes (x for gate/up, h for down_proj) into oracle FeedForward ``ffn``."""
+    ffn.gate_proj.code_hook = flips.code_hook(*taps.codes("u"))
+    ffn.down_proj.code_hook = flips.code_hook(*taps.codes("h"))
+
+
+def uninstall(ref):
+    for m in ref.modules():
+        if hasattr(m, "code_hook"):
+            m.code_hook = None
+        if hasattr(m, "tern_hook"):
+            m.tern_hook = None
+
+
+def row_errors(a, b, floor=0.1):
+    """Per-row error max|a - b| / max(max|b_row|, floor * max|b|) over the last axis."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    a2 = a.reshape(-1, a.shape[-1])
+    b2 = b.reshape(-1, b.shape[-1])
+    den = np.maximum(np.abs(b2).max(axis=1), floor * np.abs(b2).max())
+    return np.abs(a2 - b2).max(axis=1) / np.maximum(den, 1e-30)
+
+
+def assert_rows(a, b, dtype, what=""):
+    err = row_errors(a, b)
+    tol = TOL[dtype]
+    bad = np.flatnonzero(err > tol)
+    assert bad.size == 0, f"{what}: {bad.size}/{err.size} rows over {tol} (worst {err.max():.3g} at row {err.argmax()})"
+    return float(err.max())
+
+
+def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
+    """Prefill P tokens, then `steps` one-token steps, on the device and on the oracle call by call.
+    Each oracle call takes the device call's int8 codes and ternary decisions through the oracle's
+    hooks, after checking that every one it would decide otherwise is a near-tie (tests/flips.py).
+    Returns (device outputs, oracle outputs, Flips)."""
+    flips = Flips(dtype)
+    D, dm, W = m.d_state, m.d_model, m.entanglement_window
+    n = max(P + steps, 64)
+    caches = [m.allocate_inference_cache(B, n), ref.allocate_inference_cache(B, n)]
+    outs = [{}, {}]
+    ud, csd = u.to(DEV), cs.to(DEV) if cs is not None else None
+    with torch.no_grad():
+        if P:
+            tern = (B, P, min(W, P)) if W > 0 else None
+            with Taps(B * P, D, dm, DEV, tern, d_state=D) as tp:
+                outs[0]["prefill_y"] = m(ud[:, :P], inference_params={"state_cache": caches[0]},
+                                         cross_layer_state=csd[:, :P] if cs is not None else None)[0]
+            install(ref, flips, tp, "local" if W > 0 else None)
+            outs[1]["prefill_y"] = ref(u[:, :P], inference_params={"state_cache": caches[1]},
+                                       cross_layer_state=cs[:, :P] if cs is not None else None)[0]
+            uninstall(ref)
+        for s in range(steps):
+            t = P + s
+            with Taps(B, D, dm, DEV, (B, 1, max(W, 1)), d_state=D) as tp:
+                y, st = m(ud[:, t:t + 1], inference_params={"state_cache": caches[0]},
+                          cross_layer_state=csd[:, t] if cs is not None else None)
+            install(ref, flips, tp, "decode")
+            yr, str_ = ref(u[:, t:t + 1], inference_params={"state_cache": caches[1]},
+                           cross_layer_state=cs[:, t] if cs is not None else None)
+            uninstall(ref)
+            for o, yy, ss, c in ((outs[0], y, st, caches[0]), (outs[1], yr, str_, caches[1])):
+                o[f"step{s}_y"] = yy.clone()
+                o[f"step{s}_state"] = ss.clone()
+                o[f"step{s}_kcache"] = c["ent_k_cache"].clone()
+                o[f"step{s}_vcache"] = c["ent_v_cache"].clone()
+                o[f"step{s}_cache_idx"] = c["cache_idx"]
+                o[f"step{s}_seq_pos"] = c["seq_pos"]
+    return outs[0], outs[1], flips
+
+
+def check_siso_steps(got, want, steps, B, dtype, flips):
+    """Every row of every step's output within the north-star tolerance (decisions fed in)."""
+    tol = TOL[dtype]
+    if "prefill_y" in got:
+        assert_rows(to_np(got["prefill_y"]), to_np(want["prefill_y"]), dtype, "prefill")
+    for s in range(steps):
+        assert_rows(to_np(got[f"step{s}_y"]).reshape(B, -1), to_np(want[f"step{s}_y"]).reshape(B, -1), dtype,
+                    f"step {s} ({flips.summary()})")
+        if dtype == torch.float32:
+            np.testing.assert_allclose(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy(),
+                                       rtol=1e-4, atol=1e-5)
+        else:
+            # bf16 gates: a one-ulp difference of an in_proj output moves decay / write / tanh(sv) by
+            # one bf16 ulp, which the float64 state then carries; the bar is normwise
+            assert normwise(got[f"step{s}_state"].cpu().numpy(), want[f"step{s}_state"].numpy()) <= tol
+        assert normwise(to_np(got[f"step{s}_kcache"]), to_np(want[f"step{s}_kcache"])) <= (
+            1e-5 if dtype == torch.float32 else tol)
+        assert normwise(to_np(got[f"step{s}_vcache"]), to_np(want[f"step{s}_vcache"])) <= (
+            1e-5 if dtype == torch.float32 else tol)
+        assert got[f"step{s}_cache_idx"] == want[f"step{s}_cache_idx"]
+        assert got[f"step{s}_seq_pos"] == want[f"step{s}_seq_pos"]
+    # decisions fed in are rare near-ties, not a systematic disagreement
+    assert flips.code_flips <= max(4, 0.01 * flips.codes), flips.summary()
+    assert flips.tern_flips <= max(4, 0.02 * flips.terns), flips.summary()

@@ -60,7 +60,8 @@ def test_struct_layout_matches_header(tmp_path):
     structs = {"tesm_hip_linear": _lib.Linear, "tesm_hip_ent_quant": _lib.EntQuant,
                "tesm_hip_output_gate": _lib.OutputGate, "tesm_hip_siso_layer": _lib.SisoLayer,
                "tesm_hip_siso_step": _lib.SisoStep, "tesm_hip_mimo_layer": _lib.MimoLayer,
-               "tesm_hip_mimo_step": _lib.MimoStep, "tesm_hip_rmsnorm": _lib.RmsNorm, "tesm_hip_ffn": _lib.Ffn}
+               "tesm_hip_mimo_step": _lib.MimoStep, "tesm_hip_rmsnorm": _lib.RmsNorm, "tesm_hip_ffn": _lib.Ffn,
+               "tesm_hip_taps": _lib.Taps}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "tesm_hip.h"', "int main(void) {"]
     for cname, py in structs.items():
         fields = _c_struct_fields(text, cname)
