@@ -75,9 +75,12 @@ int tesm_hip_debug_scan_spin_limit(int limit);
  *     tesm_hip_ffn_forward: q_u/s_u the codes of x (gate_proj / up_proj), q_h/s_h those of h
  *     (down_proj);
  *   tern: prefill with window > 0: SISO (B, L, min(window, L)), MIMO (B, L, n_heads, window), entry w
- *     deciding key t - W + 1 + w (W the window used); decode: (B, n_heads, window) at the reference's
- *     padded window positions, in its ring read order (SISO: n_heads = 1);
- *   wts: MIMO prefill with window > 0: float32 window weights tern / norm, (B*L, n_heads, window).
+ *     deciding key t - W + 1 + w (W the window used); prefill with window == 0 (global): (B, L, P),
+ *     P = L rounded up to 64, entry [b, i, j] deciding key j for query i (valid for j <= i);
+ *     decode: (B, n_heads, window) at the reference's padded window positions, in its ring read
+ *     order (SISO: n_heads = 1);
+ *   wts: MIMO prefill with window > 0: float32 window weights tern / norm, (B*L, n_heads, window);
+ *   S: MIMO prefill: the float32 rank-free states (B*L, n_heads*d_state) (rank r's are S * mimo_x[r]^2).
  * Copies are queued on the call's stream.  With taps set, u and y are quantized by their own
  * kernels (the same codes as the products that quantize them inline).  Process-wide;
  * tesm_hip_debug_taps(NULL) stops. */
@@ -96,6 +99,7 @@ typedef struct tesm_hip_taps {
   float* s_h;
   int8_t* tern;
   float* wts;
+  float* S;
 } tesm_hip_taps;
 
 int tesm_hip_debug_taps(const tesm_hip_taps* taps);
@@ -325,6 +329,7 @@ typedef struct tesm_hip_siso_step {
 
 int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);
 int tesm_hip_siso_decode(const tesm_hip_siso_step* p, void* ws, int64_t ws_bytes, void* stream);
+
 
 /* MIMO rank merge factors.  TESMMIMO_Optimized expands each head's update into mimo_rank copies
  * scaled by mimo_x and merges the entangled copies with mimo_o (tesm_mimo.py:963-1017); the scan

@@ -197,6 +197,12 @@ class TESM_SISO(nn.Module):
             T = self.T_start
         return max(T, self.T_end)
 
+    # Test hook (None by default): ``state_hook(states, where) -> states`` sees the layer-dtype states
+    # the entanglement reads (``where``: ("prefill",), ("decode",), or ("mimo",) with the list of
+    # per-rank states); bf16 parity tests feed in another implementation's states, because a one-ulp
+    # difference of a state is amplified by the cancellation in C = E - S.
+    state_hook = None
+
     # Test hook (None by default): ``tern_hook(scores, tern, where) -> tern`` sees every hard
     # ternary decision with its place (``where``: ("local", t0, t1), ("global",), ("decode",),
     # ("mimo", t, w)); parity tests use it like BitLinear.code_hook.
@@ -335,6 +341,8 @@ class TESM_SISO(nn.Module):
                 cq = cq.unsqueeze(1)
             q = q + cq
         states = self._parallel_state_scan(decay, write * sv, prev_state=prev_state)
+        if self.state_hook is not None:
+            states = self.state_hook(states, ("prefill",))
         avg = self._compute_entanglement(q, k, states)
         ent = states + self.entanglement_scale * (avg - states)
         change = ent - states
@@ -401,6 +409,8 @@ class TESM_SISO(nn.Module):
             qv = qv + self.cross_layer_q_proj(cross_layer_state)
         new64 = decay[:, 0, :].double() * cache["state"] + write[:, 0, :].double() * vv.double()
         new = new64.to(decay.dtype)
+        if self.state_hook is not None:
+            new = self.state_hook(new, ("decode",))
         W = cache["ent_k_cache"].shape[1]
         slot = cache.get("cache_idx", 0)
         cache["ent_k_cache"][:, slot, :] = kv
@@ -602,6 +612,8 @@ class TESMMIMO_Optimized(TESM_SISO):
         wr_m = torch.einsum("blhd,hrd->blrhd", write.float(), self.mimo_x.float())
         upd = wr_m * sv_m
         states_r = [self._scan_mimo(decay, upd[:, :, r].contiguous()) for r in range(Rm)]
+        if self.state_hook is not None:
+            states_r = self.state_hook(states_r, ("mimo",))
         finals = [s[:, -1] for s in states_r]
         states_m = torch.stack(states_r, dim=2)
         q = self._apply_rope(q)
@@ -677,6 +689,8 @@ class TESMMIMO_Optimized(TESM_SISO):
             qr = qr + cq.unsqueeze(1)
         new64 = decay[:, 0].double() * cache["state"] + write[:, 0].double() * sv[:, 0].double()
         new = new64.to(decay.dtype)
+        if self.state_hook is not None:
+            new = self.state_hook(new, ("decode",))
         W = cache["ent_k_cache"].shape[1]
         slot = cache.get("cache_idx", 0)
         cache["ent_k_cache"][:, slot] = kr[:, 0]

@@ -1,6 +1,10 @@
 // extern "C" entry points of libtesm_hip.so (declared in include/tesm_hip.h) and the fused
 // layer drivers.  The drivers only queue kernels on the caller's stream; every buffer comes
 // from the caller (outputs) or from one caller-provided workspace carved up here.
+#include <cxxabi.h>
+
+#include <cctype>
+#include <cstdlib>
 #include <cstring>
 #include <initializer_list>
 #include <mutex>
@@ -35,17 +39,37 @@ std::mutex g_log_mu;
 std::string g_log;
 }  // namespace
 
-// `pretty` is kernel_pretty<K>()'s text, "... [K = &ns::name<args>]": keep "name<args>".
-void log_kernel(const char* pretty) {
-  const char* p = std::strstr(pretty, "K = &");
-  std::string s = p ? p + 5 : pretty;
-  if (!s.empty() && s.back() == ']') s.pop_back();
-  const size_t lt = s.find('<');
-  const size_t cut = s.rfind("::", lt);
-  if (cut != std::string::npos) s = s.substr(cut + 2);
-  std::string name;
-  for (char c : s)
-    if (c != ' ') name += c;
+// "void tesm::(anonymous namespace)::name_kernel<1, 2, true>(tesm::Args)" -> "name_kernel<1,2,true>"
+std::string short_kernel_name(const std::string& full) {
+  const size_t pos = full.find("_kernel");
+  if (pos == std::string::npos) return full;
+  size_t b = pos;
+  while (b > 0 && (std::isalnum(static_cast<unsigned char>(full[b - 1])) || full[b - 1] == '_')) --b;
+  size_t e = pos + 7;
+  if (e < full.size() && full[e] == '<') {
+    int depth = 0;
+    for (; e < full.size(); ++e) {
+      if (full[e] == '<') ++depth;
+      if (full[e] == '>' && --depth == 0) {
+        ++e;
+        break;
+      }
+    }
+  }
+  std::string out;
+  for (size_t i = b; i < e && i < full.size(); ++i)
+    if (full[i] != ' ') out += full[i];
+  return out;
+}
+
+void log_kernel(const void* host_stub) {
+  const char* mangled = hipKernelNameRefByPtr(host_stub, nullptr);
+  std::string name = mangled ? mangled : "unknown_kernel";
+  int status = 0;
+  char* dem = abi::__cxa_demangle(name.c_str(), nullptr, nullptr, &status);
+  if (status == 0 && dem) name = dem;
+  std::free(dem);
+  name = short_kernel_name(name);
   std::lock_guard<std::mutex> g(g_log_mu);
   g_log += name;
   g_log += '\n';
@@ -990,6 +1014,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     ga.qr = s.g_qr;
     ga.kr = s.g_kr;
     if ((rc = launch_global_ent(ga, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.tern, s.g_tern, M * global_tern_pitch(p.L), st))) return rc;
     if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
       return rc;
     if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
@@ -1452,6 +1477,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   sa.flags_clear = scan_zero_n > 0;
   if ((rc = launch_scan(sa, s.scan_ws, s.scan_bytes, st))) return rc;
   if ((rc = launch_mimo_final(s.S, p.mimo_x0sq, p.B, p.L, HD, p.h_final, p.last_state, st))) return rc;
+  if (tapping && (rc = tap_copy(tp.S, s.S, M * HD * 4, st))) return rc;
   const void* q_raw = proj + o_q * es;
   const void* k_raw = proj + o_k * es;
   if (p.window > 0) {
@@ -1526,6 +1552,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
     ga.qr = s.g_qr;
     ga.kr = s.g_kr;
     if ((rc = launch_global_ent(ga, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.tern, s.g_tern, M * global_tern_pitch(p.L), st))) return rc;
   }
   if (p.stats_ternary || p.stats_counts) {  // tesm_mimo.py:1019-1020 -> 458-523
     MimoStatsArgs sa2;

@@ -265,17 +265,13 @@ int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
 // Launch log: while enabled (tesm_hip_launch_log), every kernel launch appends the kernel's name
-// with its template arguments.  The launch sites pass their stream through TESM_LOGGED, so a
-// disabled log costs one relaxed load per launch.
+// with its template arguments (the runtime's name of the kernel's host stub, demangled).  The launch
+// sites pass their stream through TESM_LOGGED, so a disabled log costs one relaxed load per launch.
 extern int g_launch_log_on;
-void log_kernel(const char* pretty);
-template <auto K>
-inline const char* kernel_pretty() {
-  return __PRETTY_FUNCTION__;  // "... [K = &ns::name<args>]"
-}
+void log_kernel(const void* host_stub);
 template <auto K>
 inline void note_kernel() {
-  if (__atomic_load_n(&g_launch_log_on, __ATOMIC_RELAXED)) log_kernel(kernel_pretty<K>());
+  if (__atomic_load_n(&g_launch_log_on, __ATOMIC_RELAXED)) log_kernel(reinterpret_cast<const void*>(K));
 }
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }

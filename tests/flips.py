@@ -40,7 +40,8 @@ class Taps:
 
     K widths: u and y d_model, cs d_state (cs_rows rows), te and c k_te, h d_inter."""
 
-    def __init__(self, M, k_te, d_model, dev, tern_shape=None, d_state=None, cs_rows=None, d_inter=None):
+    def __init__(self, M, k_te, d_model, dev, tern_shape=None, d_state=None, cs_rows=None, d_inter=None,
+                 states=False):
         kp = hip_ops.kpad
         self.K = {"u": d_model, "y": d_model, "te": k_te, "c": k_te, "cs": d_state or 1, "h": d_inter or 1}
         rows = {"cs": cs_rows or M}
@@ -49,13 +50,14 @@ class Taps:
             setattr(self, "q_" + name, torch.zeros((r, kp(K)), dtype=torch.int8, device=dev))
             setattr(self, "s_" + name, torch.zeros((r,), dtype=torch.float32, device=dev))
         self.tern = torch.full(tern_shape, 7, dtype=torch.int8, device=dev) if tern_shape else None
+        self.S = torch.full((M, k_te), float("nan"), device=dev) if states else None
 
     def __enter__(self):
         bufs = {}
         for name in self.K:
             bufs["q_" + name] = getattr(self, "q_" + name)
             bufs["s_" + name] = getattr(self, "s_" + name)
-        hip_ops.set_taps(tern=self.tern, **bufs)
+        hip_ops.set_taps(tern=self.tern, S=self.S, **bufs)
         return self
 
     def __exit__(self, *exc):
@@ -109,7 +111,8 @@ class Flips:
         """An oracle tern_hook that substitutes the device's ternary decisions.
 
         kind "local": dev_tern (B, L, W); "decode": (B, H, W) in ring read order; "mimo":
-        (B, L, H, W) with entry w deciding key t - W + 1 + w."""
+        (B, L, H, W) with entry w deciding key t - W + 1 + w; "global": (B, L, P >= L), key j of
+        query i at [b, i, j] for j <= i."""
         dt = torch.as_tensor(dev_tern).to(torch.float32)
 
         def hook(scores, tern, where):
@@ -124,6 +127,10 @@ class Flips:
             elif kind == "decode":
                 td = dt.reshape(tern.shape).to(tern.dtype)
                 valid = torch.ones_like(tern, dtype=torch.bool)
+            elif kind == "global":
+                L = tern.shape[-1]
+                td = dt[:, :L, :L].to(tern.dtype)
+                valid = torch.ones(L, L, dtype=torch.bool).tril().unsqueeze(0).expand_as(tern)
             else:  # mimo
                 t, w = where[1], where[2]
                 td = dt[:, t, :, w].reshape(tern.shape).to(tern.dtype)
@@ -143,18 +150,46 @@ class Flips:
             return torch.where(valid, td, tern)
         return hook
 
+    def state_hook(self, dev_states, mimo_x=None):
+        """An oracle state_hook that substitutes the device's layer-dtype states (bfloat16 runs: a one-ulp
+        difference of a bf16 state is amplified by the cancellation in C = E - S far beyond a rounding
+        tie).  The device's states must agree with the oracle's own to the bf16 tolerance, normwise;
+        MIMO: the device's rank-free float32 states S give rank r's as S * mimo_x[:, r]^2."""
+        d = torch.as_tensor(dev_states)
+
+        def hook(states, where):
+            if where[0] == "mimo":
+                B, L, H, D = states[0].shape
+                S = d.reshape(B, L, H, D).float()
+                out = []
+                for r, sr in enumerate(states):
+                    cand = (S * mimo_x[:, r, :].float() ** 2).to(sr.dtype)
+                    err = normwise(cand.numpy(), sr.float().numpy())
+                    assert err <= TOL[self.dtype], f"rank {r} states differ: {err:.3g}"
+                    out.append(cand)
+                return out
+            dd = d.reshape(states.shape).to(states.dtype)
+            err = normwise(dd.float().numpy(), states.float().numpy())
+            assert err <= TOL[self.dtype], f"states differ: {err:.3g}"
+            return dd
+        return hook
+
     def summary(self):
         return (f"code flips {self.code_flips}/{self.codes}, ternary flips {self.tern_flips}/{self.terns}")
 
 
-def install(ref, flips, taps, tern_kind=None, thr=None):
-    """Feed the taps' decisions into oracle layer ``ref`` (SISO or MIMO)."""
+def install(ref, flips, taps, tern_kind=None, thr=None, states=None):
+    """Feed the taps' decisions into oracle layer ``ref`` (SISO or MIMO); in bfloat16 runs also the
+    device's ``states`` (SISO: the layer-dtype states or decode state; MIMO: the rank-free float32
+    states, or the decode state)."""
     for mod, name in ((ref.in_proj, "u"), (ref.cross_layer_q_proj, "cs"), (ref.state_proj, "te"),
                       (ref.ent_proj, "c"), (ref.out_proj, "y")):
         mod.code_hook = flips.code_hook(*taps.codes(name))
     if tern_kind is not None:
         ref.tern_hook = flips.tern_hook(taps.tern.cpu(), ref.entanglement_threshold if thr is None else thr,
                                         tern_kind)
+    if states is not None and flips.dtype == torch.bfloat16:
+        ref.state_hook = flips.state_hook(states.detach().cpu(), getattr(ref, "mimo_x", None))
 
 
 def install_ffn(ffn, flips, taps):
@@ -165,10 +200,9 @@ def install_ffn(ffn, flips, taps):
 
 def uninstall(ref):
     for m in ref.modules():
-        if hasattr(m, "code_hook"):
-            m.code_hook = None
-        if hasattr(m, "tern_hook"):
-            m.tern_hook = None
+        for hook in ("code_hook", "tern_hook", "state_hook"):
+            if hasattr(m, hook):
+                setattr(m, hook, None)
 
 
 def row_errors(a, b, floor=0.1):
@@ -202,11 +236,11 @@ def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
     ud, csd = u.to(DEV), cs.to(DEV) if cs is not None else None
     with torch.no_grad():
         if P:
-            tern = (B, P, min(W, P)) if W > 0 else None
+            tern = (B, P, min(W, P)) if W > 0 else (B, P, (P + 63) // 64 * 64)
             with Taps(B * P, D, dm, DEV, tern, d_state=D) as tp:
                 outs[0]["prefill_y"] = m(ud[:, :P], inference_params={"state_cache": caches[0]},
                                          cross_layer_state=csd[:, :P] if cs is not None else None)[0]
-            install(ref, flips, tp, "local" if W > 0 else None)
+            install(ref, flips, tp, "local" if W > 0 else "global", states=m._last_cross_layer_state)
             outs[1]["prefill_y"] = ref(u[:, :P], inference_params={"state_cache": caches[1]},
                                        cross_layer_state=cs[:, :P] if cs is not None else None)[0]
             uninstall(ref)
@@ -215,7 +249,7 @@ def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
             with Taps(B, D, dm, DEV, (B, 1, max(W, 1)), d_state=D) as tp:
                 y, st = m(ud[:, t:t + 1], inference_params={"state_cache": caches[0]},
                           cross_layer_state=csd[:, t] if cs is not None else None)
-            install(ref, flips, tp, "decode")
+            install(ref, flips, tp, "decode", states=m._last_cross_layer_state)
             yr, str_ = ref(u[:, t:t + 1], inference_params={"state_cache": caches[1]},
                            cross_layer_state=cs[:, t] if cs is not None else None)
             uninstall(ref)
@@ -253,3 +287,95 @@ def check_siso_steps(got, want, steps, B, dtype, flips):
     # decisions fed in are rare near-ties, not a systematic disagreement
     assert flips.code_flips <= max(4, 0.01 * flips.codes), flips.summary()
     assert flips.tern_flips <= max(4, 0.02 * flips.terns), flips.summary()
+
+
+class ModelTaps:
+    """Per-call taps on every block of a device model (TESMLMHeadModel / MixerModel) or on one Block:
+    each mixer call and each feed-forward call runs with its own taps, and ``install`` feeds them
+    into the oracle's corresponding modules.  ``decode``: the next call is a one-token step."""
+
+    def __init__(self, blocks, B, L, decode=False):
+        self.blocks = list(blocks)
+        self.entries = []
+        for blk in self.blocks:
+            mixer, mlp = blk.mixer, blk.mlp
+            H = getattr(mixer, "n_heads", 1)
+            mimo = hasattr(mixer, "n_heads")
+            D, W, dm = mixer.d_state, mixer.entanglement_window, mixer.d_model
+            M = B * L
+            if decode:
+                tern = (B, H, max(W, 1))
+            elif W > 0:
+                tern = (B, L, H, W) if mimo else (B, L, min(W, L))
+            else:
+                tern = (B, L, (L + 63) // 64 * 64)
+            mt = Taps(M, H * D, dm, DEV, tern, d_state=D, cs_rows=B * H if (decode and mimo) else M,
+                      states=mimo and not decode)
+            ft = Taps(M, 1, dm, DEV, d_inter=mlp.down_proj.in_features)
+            ent = {"mixer": mt, "ffn": ft, "mimo": mimo, "states": None,
+                   "orig": (mixer.forward, mlp.forward, getattr(mlp, "forward_codes", None))}
+            self.entries.append(ent)
+            self._wrap(blk, ent)
+        self.decode = decode
+
+    @staticmethod
+    def _wrap(blk, ent):
+        mixer, mlp = blk.mixer, blk.mlp
+        fwd, mfwd, mcodes = ent["orig"]
+
+        def mixer_forward(*a, **k):
+            with ent["mixer"]:
+                out = fwd(*a, **k)
+            ent["states"] = mixer._last_cross_layer_state
+            return out
+
+        def mlp_forward(*a, **k):
+            with ent["ffn"]:
+                return mfwd(*a, **k)
+
+        mixer.forward = mixer_forward
+        mlp.forward = mlp_forward
+        if mcodes is not None:
+            def mlp_codes(*a, **k):
+                with ent["ffn"]:
+                    return mcodes(*a, **k)
+            mlp.forward_codes = mlp_codes
+
+    def restore(self):
+        for blk, ent in zip(self.blocks, self.entries):
+            for mod, name in ((blk.mixer, "forward"), (blk.mlp, "forward"), (blk.mlp, "forward_codes")):
+                mod.__dict__.pop(name, None)
+
+    def install(self, ref_blocks, flips):
+        for rb, ent in zip(ref_blocks, self.entries):
+            W = rb.mixer.entanglement_window
+            if self.decode:
+                kind = "decode"
+            elif W > 0:
+                kind = "mimo" if ent["mimo"] else "local"
+            else:
+                kind = "global"
+            states = ent["mixer"].S if ent["mimo"] and not self.decode else ent["states"]
+            install(rb.mixer, flips, ent["mixer"], kind, states=states)
+            install_ffn(rb.mlp, flips, ent["ffn"])
+
+
+def siso_prefill_check(ref, m, u, dtype, cs=None, h0=None):
+    """One TESM_SISO prefill on the device (decision taps on) and on oracle ``ref`` with the device's
+    decisions fed in; every row of y within the north-star tolerance.  Returns (y, final state,
+    oracle y, oracle final state)."""
+    B, L, dm = u.shape
+    D, W = m.d_state, m.entanglement_window
+    tern = (B, L, min(W, L)) if W > 0 else (B, L, (L + 63) // 64 * 64)
+    flips = Flips(dtype)
+    with torch.no_grad():
+        with Taps(B * L, D, dm, DEV, tern, d_state=D) as tp:
+            y, f = m(u.to(DEV), cross_layer_state=cs.to(DEV) if cs is not None else None,
+                     prev_state=h0.to(DEV) if h0 is not None else None)
+        install(ref, flips, tp, "local" if W > 0 else "global", states=m._last_cross_layer_state)
+        yr, fr = ref(u, cross_layer_state=cs, prev_state=h0)
+        uninstall(ref)
+    assert_rows(to_np(y), to_np(yr), dtype, f"prefill ({flips.summary()})")
+    assert flips.code_flips <= max(4, 0.01 * flips.codes), flips.summary()
+    assert flips.tern_flips <= max(4, 0.01 * flips.terns), flips.summary()
+    return y, f, yr, fr

@@ -207,7 +207,7 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
     with torch.no_grad():
         with hip_ops.launch_log() as log, Taps(B * L, D, cfg["d_model"], DEV, (B, L, W), d_state=D) as tp:
             y, f = m(u.to(DEV))
-        install(ref, flips, tp, "local")
+        install(ref, flips, tp, "local", states=m._last_cross_layer_state)
         yr, fr = ref(u)
         uninstall(ref)
     dc = DT_CODE[dtype]
@@ -287,9 +287,9 @@ def test_cfg4_mimo_long_vs_oracle(dtype):
     H, D, W = 2, 64, 64
     flips = Flips(dtype)
     with torch.no_grad():
-        with hip_ops.launch_log() as log, Taps(1100, H * D, 128, DEV, (1, 1100, H, W)) as tp:
+        with hip_ops.launch_log() as log, Taps(1100, H * D, 128, DEV, (1, 1100, H, W), states=True) as tp:
             y, f = m(u.to(DEV))
-        install(ref, flips, tp, "mimo")
+        install(ref, flips, tp, "mimo", states=tp.S)
         yr, fr = ref(u)
         uninstall(ref)
     dc = DT_CODE[dtype]
@@ -316,7 +316,7 @@ def test_cfg4_mimo_full_size():
     u = torch.randn(1, L, dm, generator=torch.Generator().manual_seed(0)).to(dtype)
     hip_ops.device_status(clear=True)
     with torch.no_grad():
-        with hip_ops.launch_log() as log, Taps(L, H * D, dm, DEV, (1, L, H, W)) as tp:
+        with hip_ops.launch_log() as log, Taps(L, H * D, dm, DEV, (1, L, H, W), states=True) as tp:
             y, f = m(u.to(DEV))
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
@@ -336,6 +336,7 @@ def test_cfg4_mimo_full_size():
     ref.ent_proj.code_hook = flips.code_hook(*codes("c", H * D))
     ref.out_proj.code_hook = flips.code_hook(*codes("y", dm))
     ref.tern_hook = flips.tern_hook(tp.tern[:, :M].cpu(), cfg["entanglement_threshold"], "mimo")
+    ref.state_hook = flips.state_hook(tp.S[:M].cpu(), ref.mimo_x)
     with torch.no_grad():
         yr, _ = ref(u[:, :Lp])
     uninstall(ref)

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 import torch
 
-from hip_helpers import DEV, TOL, bf16_bits, flip_aware, need_gpu, normwise, rel_l2, to_np
+from flips import Flips, Taps, assert_rows, install, uninstall
+from hip_helpers import DEV, TOL, bf16_bits, need_gpu, normwise, to_np
 from oracle import int2_export as oe
 from oracle import int_ref
 from oracle import tesm_torch as ot
@@ -143,15 +144,20 @@ def test_siso_from_oracle_export_matches_float_model(dtype):
     m = _scramble(TESM_SISO(**SISO_CFG).eval()).to(DEV).to(dtype)
     hi.load_int2_weights_to_model(m, oe.export_model_to_int2(ref), keep_float_weights=False)
     u = torch.randn(2, 300, 128, generator=torch.Generator().manual_seed(7)).to(dtype)
+    flips = Flips(dtype)
+    D, W = SISO_CFG["d_state"], SISO_CFG["entanglement_window"]
     with torch.no_grad():
+        with Taps(600, D, 128, DEV, (2, 300, min(W, 300)), d_state=D) as tp:
+            y, f = m(u.to(DEV))
+        install(ref, flips, tp, "local", states=m._last_cross_layer_state)
         yr, fr = ref(u)
-        y, f = m(u.to(DEV))
+        uninstall(ref)
+    assert_rows(to_np(y), to_np(yr), dtype, f"INT2-loaded layer ({flips.summary()})")
+    assert flips.code_flips <= max(4, 0.01 * flips.codes), flips.summary()
     if dtype == torch.float32:
-        flip_aware(to_np(y), to_np(yr), row_tol=1e-5, max_flip_frac=0.01, bound=1e-2)
         np.testing.assert_allclose(f.cpu().numpy(), fr.numpy(), rtol=1e-4, atol=1e-5)
     else:
-        assert rel_l2(to_np(y), to_np(yr)) <= TOL[dtype]
-        flip_aware(to_np(y), to_np(yr), row_tol=TOL[dtype], max_flip_frac=0.05, bound=0.1)
+        assert normwise(f.cpu().numpy(), fr.numpy()) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

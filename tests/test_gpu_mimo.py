@@ -80,9 +80,9 @@ def _prefill_lockstep(ref, m, u, dtype):
     H, D, W = m.n_heads, m.d_state, m.entanglement_window
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(B * L, H * D, m.d_model, DEV, (B, L, H, W)) as tp:
+        with Taps(B * L, H * D, m.d_model, DEV, (B, L, H, W), states=True) as tp:
             y, f = m(u.to(DEV))
-        install(ref, flips, tp, "mimo")
+        install(ref, flips, tp, "mimo", states=tp.S)
         yr, fr = ref(u)
         uninstall(ref)
     assert_rows(to_np(y), to_np(yr), dtype, f"mimo prefill ({flips.summary()})")
@@ -119,9 +119,10 @@ def _decode_lockstep(ref, m, u, cs, P, steps, B, dtype):
     ud, csd = u.to(DEV), cs.to(DEV) if cs is not None else None
     with torch.no_grad():
         if P:
-            with Taps(B * P, H * D, m.d_model, DEV, (B, P, H, W) if W > 0 else None) as tp:
+            tern = (B, P, H, W) if W > 0 else (B, P, (P + 63) // 64 * 64)
+            with Taps(B * P, H * D, m.d_model, DEV, tern, states=True) as tp:
                 outs[0]["prefill_y"] = m(ud[:, :P], inference_params={"state_cache": caches[0]})[0]
-            install(ref, flips, tp, "mimo" if W > 0 else None)
+            install(ref, flips, tp, "mimo" if W > 0 else "global", states=tp.S)
             outs[1]["prefill_y"] = ref(u[:, :P], inference_params={"state_cache": caches[1]})[0]
             uninstall(ref)
         for s in range(steps):
@@ -129,7 +130,7 @@ def _decode_lockstep(ref, m, u, cs, P, steps, B, dtype):
             with Taps(B, H * D, m.d_model, DEV, (B, H, max(W, 1)), d_state=D, cs_rows=B * H) as tp:
                 y, st = m(ud[:, t:t + 1], inference_params={"state_cache": caches[0]},
                           cross_layer_state=csd[:, t] if cs is not None else None)
-            install(ref, flips, tp, "decode")
+            install(ref, flips, tp, "decode", states=m._last_cross_layer_state)
             yr, str_ = ref(u[:, t:t + 1], inference_params={"state_cache": caches[1]},
                            cross_layer_state=cs[:, t] if cs is not None else None)
             uninstall(ref)
