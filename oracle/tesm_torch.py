@@ -66,6 +66,12 @@ class BitLinear(nn.Module):
     # pre-rounding values v = x * scale and the codes before they are dequantized; parity tests use
     # it to feed in another implementation's codes where those differ from these only at near-ties.
     code_hook = None
+    # Test switch (False by default): evaluate the product exactly -- float64 sums of the unrounded
+    # dequantized operands codes / scale, rounded once to the output dtype -- which is the arithmetic of
+    # an int32-accumulator implementation, instead of F.linear on dtype-rounded operands.  bf16 parity
+    # tests set it so that two implementations' BitLinear outputs differ only at rounding boundaries.
+    exact_products = False
+    _exact_input = None
 
     def quantized_input(self, x):
         """Per-token absmax int8 fake quant (tesm.py:206-209).
@@ -78,6 +84,8 @@ class BitLinear(nn.Module):
         codes = v.round().clamp(-128, 127)
         if self.code_hook is not None:
             codes, scale = self.code_hook(x, v, codes, scale)
+        if self.exact_products:
+            self._exact_input = codes.double() / scale.double()
         deq = codes / scale
         return x + (deq - x).detach()
 
@@ -102,6 +110,10 @@ class BitLinear(nn.Module):
         return self.quantized_weight()
 
     def _project_quantized(self, qinput, qweight, bias=None):  # tesm.py:273-276
+        ex, self._exact_input = self._exact_input, None
+        if self.exact_products and ex is not None and ex.shape == qinput.shape:
+            b = bias.double() if bias is not None else None
+            return F.linear(ex, qweight.double(), b).to(qinput.dtype)
         return F.linear(qinput, qweight, bias)
 
     def forward(self, x):  # tesm.py:287-290
