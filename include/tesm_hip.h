@@ -330,6 +330,16 @@ typedef struct tesm_hip_siso_step {
 int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);
 int tesm_hip_siso_decode(const tesm_hip_siso_step* p, void* ws, int64_t ws_bytes, void* stream);
 
+/* The same decode step with no workspace argument and no allocation anywhere: the step's scratch
+ * (activation codes, the in_proj output, the gate output) lives in a fixed array of
+ * TESM_HIP_NOALLOC_SCRATCH_BYTES per device inside the library, held until the process ends.  No
+ * reference counterpart: it is for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that forbid allocation).  A step whose tesm_hip_siso_decode_ws_bytes exceeds the
+ * array is refused (TESM_ERR_WORKSPACE).  Every call on one device shares that device's array:
+ * calls that overlap on one device (different streams, or threads) race and must be serialised by
+ * the caller.  Results are bit-identical to tesm_hip_siso_decode. */
+#define TESM_HIP_NOALLOC_SCRATCH_BYTES (8 << 20)
+int tesm_hip_siso_decode_noalloc(const tesm_hip_siso_step* p, void* stream);
 
 /* MIMO rank merge factors.  TESMMIMO_Optimized expands each head's update into mimo_rank copies
  * scaled by mimo_x and merges the entangled copies with mimo_o (tesm_mimo.py:963-1017); the scan

@@ -22,6 +22,9 @@ F32 = ctypes.c_float
 F64 = ctypes.c_double
 
 
+NOALLOC_SCRATCH_BYTES = 8 << 20  # TESM_HIP_NOALLOC_SCRATCH_BYTES
+
+
 class HipBackendUnavailable(RuntimeError):
     pass
 
@@ -187,6 +190,7 @@ _SIGNATURES = {
     "tesm_hip_siso_prefill": ([ctypes.POINTER(SisoLayer), P, I64, P], I32),
     "tesm_hip_siso_decode_ws_bytes": ([ctypes.POINTER(SisoStep)], I64),
     "tesm_hip_siso_decode": ([ctypes.POINTER(SisoStep), P, I64, P], I32),
+    "tesm_hip_siso_decode_noalloc": ([ctypes.POINTER(SisoStep), P], I32),
     "tesm_hip_mimo_decode_ws_bytes": ([ctypes.POINTER(MimoStep)], I64),
     "tesm_hip_mimo_decode": ([ctypes.POINTER(MimoStep), P, I64, P], I32),
     "tesm_hip_add_rmsnorm": ([ctypes.POINTER(RmsNorm), P], I32),

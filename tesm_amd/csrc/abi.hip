@@ -573,6 +573,40 @@ FfnPlan plan_ffn(const tesm_hip_ffn& p, void* base) {
 }
 
 }  // namespace
+
+// Scratch memory of the allocation-free decode entry point (tesm_hip_siso_decode_noalloc): one
+// array per device, held until the process ends.  Host code never passes the array's name to a
+// kernel (in host code it is only a stand-in for the symbol): it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device.
+constexpr int64_t kNoAllocScratchBytes = TESM_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// The current device's scratch address (nullptr and an error message if it cannot be found).
+void* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    set_error("no-alloc decode: no current device (or more than 64 devices)");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      (void)hipGetLastError();
+      set_error(std::string("no-alloc decode: hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
 }  // namespace tesm
 
 using namespace tesm;
@@ -1219,6 +1253,19 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   op.y = p.y;
   op.taps = tapping ? &tp : nullptr;
   return run_output_path(op, st);
+}
+
+int tesm_hip_siso_decode_noalloc(const tesm_hip_siso_step* p, void* stream) {
+  TESM_REQUIRE(p != nullptr, kErrInvalidArg, "no-alloc decode: null descriptor");
+  const int64_t need = plan_decode(*p, nullptr).total;
+  TESM_REQUIRE(need <= kNoAllocScratchBytes, kErrWorkspace,
+               "no-alloc decode: the step needs " + std::to_string(need) + " bytes of scratch, more than the " +
+                   std::to_string(kNoAllocScratchBytes) + " of TESM_HIP_NOALLOC_SCRATCH_BYTES (use "
+                   "tesm_hip_siso_decode with a workspace)");
+  void* ptr = scratch_ptr();
+  if (ptr == nullptr) return kErrLaunch;
+  // every scratch byte the step reads is written earlier in the same step: nothing to clear
+  return tesm_hip_siso_decode(p, ptr, kNoAllocScratchBytes, stream);
 }
 
 // Workspace layout of the MIMO decode step; with base == nullptr it only measures.
