@@ -80,7 +80,10 @@ int tesm_hip_debug_scan_spin_limit(int limit);
  *     decode: (B, n_heads, window) at the reference's padded window positions, in its ring read
  *     order (SISO: n_heads = 1);
  *   wts: MIMO prefill with window > 0: float32 window weights tern / norm, (B*L, n_heads, window);
- *   S: MIMO prefill: the float32 rank-free states (B*L, n_heads*d_state) (rank r's are S * mimo_x[r]^2).
+ *   S: MIMO prefill: the float32 rank-free states (B*L, n_heads*d_state) (rank r's are S * mimo_x[r]^2);
+ *   te, c: the layer-dtype values of tanh(E) and C = E - S that state_proj / ent_proj quantize
+ *     (MIMO: merged over the ranks), (M, K_te) row-major; set both or neither;
+ *   yv: the layer-dtype output-gate values y that out_proj quantizes, (M, d_model).
  * Copies are queued on the call's stream.  With taps set, u and y are quantized by their own
  * kernels (the same codes as the products that quantize them inline).  Process-wide;
  * tesm_hip_debug_taps(NULL) stops. */
@@ -100,6 +103,9 @@ typedef struct tesm_hip_taps {
   int8_t* tern;
   float* wts;
   float* S;
+  void* te;
+  void* c;
+  void* yv;
 } tesm_hip_taps;
 
 int tesm_hip_debug_taps(const tesm_hip_taps* taps);

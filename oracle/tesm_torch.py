@@ -215,6 +215,15 @@ class TESM_SISO(nn.Module):
     # difference of a state is amplified by the cancellation in C = E - S.
     state_hook = None
 
+    # Test hook (None by default): ``mix_hook(te, c, ent, states, where) -> (te, c)`` sees the inputs of
+    # state_proj (tanh E) and ent_proj (C = E - S) with the E and S they came from; bf16 parity tests feed
+    # in another implementation's values after bounding their difference by a rounding of E.
+    mix_hook = None
+
+    # Test hook (None by default): ``gate_hook(y, terms, where) -> y`` sees the out_proj input
+    # y = local + gate * sp + ep with its three terms; used like mix_hook.
+    gate_hook = None
+
     # Test hook (None by default): ``tern_hook(scores, tern, where) -> tern`` sees every hard
     # ternary decision with its place (``where``: ("local", t0, t1), ("global",), ("decode",),
     # ("mimo", t, w)); parity tests use it like BitLinear.code_hook.
@@ -372,7 +381,13 @@ class TESM_SISO(nn.Module):
                     cache["ent_k_cache"][:, -L:, :] = k.detach().float()
                     cache["ent_v_cache"][:, -L:, :] = states.detach().float()
                 cache["cache_idx"] = 0
-        y = local + gate * self.state_proj(torch.tanh(ent)) + self.ent_proj(change)
+        te = torch.tanh(ent)
+        if self.mix_hook is not None:
+            te, change = self.mix_hook(te, change, ent, states, ("prefill",))
+        sp, ep = self.state_proj(te), self.ent_proj(change)
+        y = local + gate * sp + ep
+        if self.gate_hook is not None:
+            y = self.gate_hook(y, (local, gate * sp, ep), ("prefill",))
         y = self.out_proj(self.dropout(y))
         self._last_cross_layer_state = states.detach()
         if self.training and self.annealing_enabled:
@@ -453,7 +468,13 @@ class TESM_SISO(nn.Module):
         change = ent - new
         cache["state"] = new64.detach()
         cache["seq_pos"] += 1
-        y = local[:, 0, :] + gate[:, 0, :] * self.state_proj(torch.tanh(ent)) + self.ent_proj(change)
+        te = torch.tanh(ent)
+        if self.mix_hook is not None:
+            te, change = self.mix_hook(te, change, ent, new, ("decode",))
+        sp, ep = self.state_proj(te), self.ent_proj(change)
+        y = local[:, 0, :] + gate[:, 0, :] * sp + ep
+        if self.gate_hook is not None:
+            y = self.gate_hook(y, (local[:, 0, :], gate[:, 0, :] * sp, ep), ("decode",))
         y = self.out_proj(y.unsqueeze(1))
         self._last_cross_layer_state = new.detach()
         return y, new64.detach()
@@ -660,9 +681,16 @@ class TESMMIMO_Optimized(TESM_SISO):
         HD = self.n_heads * self.d_state
         ent_flat = ent.reshape(B, L, HD).contiguous()
         chg_flat = chg.reshape(B, L, HD).contiguous()
-        sp = self.state_proj(self._to_proj_dtype(torch.tanh(ent_flat), self.state_proj))
-        ep = self.ent_proj(self._to_proj_dtype(chg_flat, self.ent_proj))
-        y = self.out_proj(self.dropout(local + gate * sp + ep))
+        te = self._to_proj_dtype(torch.tanh(ent_flat), self.state_proj)
+        ce = self._to_proj_dtype(chg_flat, self.ent_proj)
+        if self.mix_hook is not None:
+            te, ce = self.mix_hook(te, ce, ent_flat, None, ("mimo",))
+        sp = self.state_proj(te)
+        ep = self.ent_proj(ce)
+        yg = local + gate * sp + ep
+        if self.gate_hook is not None:
+            yg = self.gate_hook(yg, (local, gate * sp, ep), ("mimo",))
+        y = self.out_proj(self.dropout(yg))
         self._last_cross_layer_state = states_m[:, -1, 0].detach()
         if self.training and self.annealing_enabled:
             self.annealing_step.add_(1)
@@ -733,9 +761,16 @@ class TESMMIMO_Optimized(TESM_SISO):
         change = ent - new
         cache["state"] = new64.detach()
         cache["seq_pos"] += 1
-        sp = self.state_proj(torch.tanh(ent.reshape(B, H * D)))
-        ep = self.ent_proj(change.reshape(B, H * D))
-        y = self.out_proj((local[:, 0] + gate[:, 0] * sp + ep).unsqueeze(1))
+        te = torch.tanh(ent.reshape(B, H * D))
+        ce = change.reshape(B, H * D)
+        if self.mix_hook is not None:
+            te, ce = self.mix_hook(te, ce, ent.reshape(B, H * D), new.reshape(B, H * D), ("decode",))
+        sp = self.state_proj(te)
+        ep = self.ent_proj(ce)
+        yg = local[:, 0] + gate[:, 0] * sp + ep
+        if self.gate_hook is not None:
+            yg = self.gate_hook(yg, (local[:, 0], gate[:, 0] * sp, ep), ("decode",))
+        y = self.out_proj(yg.unsqueeze(1))
         self._last_cross_layer_state = new.detach()
         return y, new64.detach()
 

@@ -158,7 +158,8 @@ class Ffn(ctypes.Structure):
 class Taps(ctypes.Structure):
     """``tesm_hip_taps``."""
     _fields_ = [("q_u", P), ("s_u", P), ("q_cs", P), ("s_cs", P), ("q_te", P), ("s_te", P), ("q_c", P), ("s_c", P),
-                ("q_y", P), ("s_y", P), ("q_h", P), ("s_h", P), ("tern", P), ("wts", P), ("S", P)]
+                ("q_y", P), ("s_y", P), ("q_h", P), ("s_h", P), ("tern", P), ("wts", P), ("S", P),
+                ("te", P), ("c", P), ("yv", P)]
 
 
 _SIGNATURES = {

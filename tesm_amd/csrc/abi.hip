@@ -435,6 +435,10 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     rq.s = o.xy.s;
     rq.rs = o.xy.rs;
     rq.eps = o.eps;
+    if (o.taps && o.taps->yv) {  // the row-complete gate also writes y itself
+      rq.y = o.taps->yv;
+      rq.ldy = o.dm;
+    }
     if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
     if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
   } else {
@@ -461,6 +465,7 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
     if ((rc = launch_quant_act(o.yg, o.dt, o.M, o.dm, o.dm, o.eps, 1, o.xy.q, o.xy.ldq, o.xy.s, o.xy.rs, st)))
       return rc;
     if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
+    if (o.taps && (rc = tap_copy(o.taps->yv, o.yg, o.M * o.dm * esize(o.dt), st))) return rc;
     return launch_linear(la, st);
   }
   return run_linear(o.xy, *o.out_proj, o.M, o.dm, o.dm, o.y, o.dt, o.dm, st);
@@ -1049,6 +1054,8 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     ga.kr = s.g_kr;
     if ((rc = launch_global_ent(ga, st))) return rc;
     if (tapping && (rc = tap_copy(tp.tern, s.g_tern, M * global_tern_pitch(p.L), st))) return rc;
+    if (tapping && (rc = tap_copy(tp.te, s.e_tanh, M * D * es, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.c, s.c_mix, M * D * es, st))) return rc;
     if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
       return rc;
     if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
@@ -1061,6 +1068,11 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     ea.s_c = s.xc.s;
     ea.rs_c = s.xc.rs;
     ea.ldq = s.xe.ldq;
+    if (tapping && tp.te && tp.c) {  // the fused kernel also writes the float values it quantizes
+      ea.e_tanh = tp.te;
+      ea.c_out = tp.c;
+      ea.ld_out = D;
+    }
     if ((rc = launch_local_ent(ea, st))) return rc;
   } else {
     ea.e_tanh = s.e_tanh;
@@ -1068,6 +1080,8 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     ea.ld_out = D;
     ea.wts = s.wts;
     if ((rc = launch_local_ent(ea, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.te, s.e_tanh, M * D * es, st))) return rc;
+    if (tapping && (rc = tap_copy(tp.c, s.c_mix, M * D * es, st))) return rc;
     if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
       return rc;
     if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
@@ -1228,7 +1242,18 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   da.rs_c = s.xc.rs;
   da.ldq = s.xe.ldq;
   if (tapping) da.tern = tp.tern;
+  const bool tap_floats = tapping && tp.te && tp.c;
+  if (tap_floats) {  // tanh(E) and C in dt to the taps, then quantized by their own kernels (same codes)
+    da.q_te = nullptr;
+    da.te_out = tp.te;
+    da.c_out = tp.c;
+    da.ld_out = D;
+  }
   if ((rc = launch_decode_ent(da, st))) return rc;
+  if (tap_floats) {
+    if ((rc = launch_quant_act(tp.te, dt, Bn, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
+    if ((rc = launch_quant_act(tp.c, dt, Bn, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  }
   if (tapping) {
     if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, Bn, st))) return rc;
     if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, Bn, st))) return rc;
@@ -1420,6 +1445,8 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
   if ((rc = launch_quant_act(s.te, dt, Bn, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
   if ((rc = launch_quant_act(s.cc, dt, Bn, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
   if (tapping) {
+    if ((rc = tap_copy(tp.te, s.te, Bn * HD * es, st))) return rc;
+    if ((rc = tap_copy(tp.c, s.cc, Bn * HD * es, st))) return rc;
     if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, Bn, st))) return rc;
     if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, Bn, st))) return rc;
   }
@@ -1625,6 +1652,8 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   if ((rc = launch_quant_act(s.te, dt, M, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
   if ((rc = launch_quant_act(s.cc, dt, M, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
   if (tapping) {
+    if ((rc = tap_copy(tp.te, s.te, M * HD * es, st))) return rc;
+    if ((rc = tap_copy(tp.c, s.cc, M * HD * es, st))) return rc;
     if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, M, st))) return rc;
     if ((rc = tap_codes(tp.q_c, tp.s_c, s.xc, M, st))) return rc;
   }

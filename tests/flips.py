@@ -18,8 +18,11 @@ In bfloat16 two more things are fed in, because bf16 rounding turns sub-ulp diff
 whole-ulp ones everywhere: the oracle evaluates BitLinear products exactly (``exact_products``: the
 int32-accumulator arithmetic that the device implements and the north star prescribes, instead of
 F.linear on bf16-rounded dequantized operands, which differs by about half an ulp per output), and
-it takes the device's layer-dtype states, checked normwise against its own (a one-ulp difference of a
-state is amplified by the cancellation in C = E - S, tesm.py:1231-1232).
+it takes the device's layer-dtype values at the three places where bf16 sums cancel -- the states
+(checked normwise), tanh(E) and C = E - S (tesm.py:1231-1232), and the output gate
+y = local + gate * sp + ep (tesm.py:1256-1260) -- each checked elementwise to within a couple of ulps of
+the terms it is formed from.  Each stage is thus checked against the oracle's computation from the
+device's previous stage.
 
 A defect that changes decisions away from a boundary (a wrong index, scale or sign) fails step 2;
 one that changes continuous values fails step 3 on the rows it touches.
@@ -48,7 +51,7 @@ class Taps:
     K widths: u and y d_model, cs d_state (cs_rows rows), te and c k_te, h d_inter."""
 
     def __init__(self, M, k_te, d_model, dev, tern_shape=None, d_state=None, cs_rows=None, d_inter=None,
-                 states=False):
+                 states=False, dtype=torch.float32):
         kp = hip_ops.kpad
         self.K = {"u": d_model, "y": d_model, "te": k_te, "c": k_te, "cs": d_state or 1, "h": d_inter or 1}
         rows = {"cs": cs_rows or M}
@@ -58,13 +61,17 @@ class Taps:
             setattr(self, "s_" + name, torch.zeros((r,), dtype=torch.float32, device=dev))
         self.tern = torch.full(tern_shape, 7, dtype=torch.int8, device=dev) if tern_shape else None
         self.S = torch.full((M, k_te), float("nan"), device=dev) if states else None
+        # the values state_proj / ent_proj quantize, in the layer dtype
+        self.te = torch.full((M, k_te), float("nan"), device=dev).to(dtype)
+        self.c = torch.full((M, k_te), float("nan"), device=dev).to(dtype)
+        self.yv = torch.full((M, d_model), float("nan"), device=dev).to(dtype)
 
     def __enter__(self):
         bufs = {}
         for name in self.K:
             bufs["q_" + name] = getattr(self, "q_" + name)
             bufs["s_" + name] = getattr(self, "s_" + name)
-        hip_ops.set_taps(tern=self.tern, S=self.S, **bufs)
+        hip_ops.set_taps(tern=self.tern, S=self.S, te=self.te, c=self.c, yv=self.yv, **bufs)
         return self
 
     def __exit__(self, *exc):
@@ -72,10 +79,10 @@ class Taps:
         torch.cuda.synchronize()
         return False
 
-    def codes(self, name):
-        """(natural-order int8 codes (rows, K), float32 scales (rows,)) on the CPU."""
-        q = getattr(self, "q_" + name).cpu().numpy()
-        return unpermute_layout1(q, self.K[name]), getattr(self, "s_" + name).cpu()
+    def codes(self, name, rows=None):
+        """(natural-order int8 codes (rows, K), float32 scales (rows,)) on the CPU (the first ``rows``)."""
+        q = getattr(self, "q_" + name)[:rows].cpu().numpy()
+        return unpermute_layout1(q, self.K[name]), getattr(self, "s_" + name)[:rows].cpu()
 
 
 class Flips:
@@ -87,12 +94,13 @@ class Flips:
         self.codes = 0
         self.tern_flips = 0
         self.terns = 0
+        self.mix_fed = 0
 
     def _near(self, v, table=NEAR):
         rel, ab = table[self.dtype]
         return rel * v.abs() + ab
 
-    def code_hook(self, q_dev, s_dev):
+    def code_hook(self, q_dev, s_dev, name="?"):
         """A BitLinear.code_hook that substitutes the device codes (M, K) and scales (M,)."""
         def hook(x, v, codes, scale):
             qd = torch.as_tensor(q_dev).reshape(codes.shape).to(codes.dtype)
@@ -106,11 +114,12 @@ class Flips:
                 # (float32: one step, and only next to a rounding boundary; bfloat16: up to the few ulps
                 # by which a bf16 value may differ, so two steps at the top of the code range)
                 b, vv = qd.double()[diff], v.double()[diff]
-                gap = (b - vv).abs() - 0.5
-                bad = gap > self._near(vv)
+                excess = (b - vv).abs() - 0.5 - self._near(vv)
+                bad = excess > 0
+                i = int(excess.argmax())
                 assert not bool(bad.any()), (
-                    f"{int(bad.sum())} of {n} differing code(s) lie away from a rounding boundary; worst: "
-                    f"device code {float(b[gap.argmax()]):.0f} for value {float(vv[gap.argmax()]):.6g}")
+                    f"{name}: {int(bad.sum())} of {n} differing code(s) lie away from a rounding boundary; "
+                    f"worst: device code {float(b[i]):.0f} for value {float(vv[i]):.6g}")
             self.code_flips += n
             self.codes += codes.numel()
             return qd, sd
@@ -183,36 +192,90 @@ class Flips:
             return dd
         return hook
 
+    def mix_hook(self, te_dev, c_dev):
+        """An oracle mix_hook that substitutes the device's tanh(E) and C (bfloat16 runs), each element
+        within what one rounding of E (and of S, and of the value itself) can move it: |d tanh E| <=
+        2 ulp(tanh E) + ulp(E); |d C| <= 2 ulp(E) + 2 ulp(S) + ulp(C) (MIMO, where C is formed in float32
+        and then rounded: 2 ulp(C) + 1e-5 |E|)."""
+        td = torch.as_tensor(te_dev)
+        cd = torch.as_tensor(c_dev)
+
+        def ulp(x):
+            a = x.double().abs().clamp_min(2.0 ** -126)
+            return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+        def hook(te, c, ent, states, where):
+            t2 = td.reshape(te.shape).to(te.dtype)
+            c2 = cd.reshape(c.shape).to(c.dtype)
+            e = ent.double()
+            tiny = 2.0 ** -24  # values this small quantize to code 0 beside any O(1) entry of their row
+            lim_t = 2 * ulp(te) + ulp(e) + tiny
+            if states is not None:
+                lim_c = 2 * ulp(e) + 2 * ulp(states.reshape(e.shape)) + ulp(c) + tiny
+            else:
+                lim_c = 2 * ulp(c) + 1e-5 * e.abs() + tiny
+            dt = (t2.double() - te.double()).abs()
+            dc = (c2.double() - c.double()).abs()
+            assert bool((dt <= lim_t).all()), f"tanh(E) differs beyond a rounding of E: {float((dt - lim_t).max()):.3g}"
+            assert bool((dc <= lim_c).all()), f"C differs beyond a rounding of E and S: {float((dc - lim_c).max()):.3g}"
+            self.mix_fed += 1
+            return t2, c2
+        return hook
+
+    def gate_hook(self, y_dev):
+        """An oracle gate_hook that substitutes the device's output-gate values y = local + gate*sp + ep
+        (bfloat16 runs: the sum can cancel), each within two ulps of each of its terms and of itself."""
+        yd = torch.as_tensor(y_dev)
+
+        def ulp(x):
+            a = x.double().abs().clamp_min(2.0 ** -126)
+            return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+        def hook(y, terms, where):
+            y2 = yd.reshape(y.shape).to(y.dtype)
+            lim = 2 * ulp(y) + 2.0 ** -24
+            for t in terms:
+                lim = lim + 2 * ulp(t.reshape(y.shape))
+            d = (y2.double() - y.double()).abs()
+            assert bool((d <= lim).all()), f"output gate y differs beyond its terms' rounding: {float((d - lim).max()):.3g}"
+            self.mix_fed += 1
+            return y2
+        return hook
+
     def summary(self):
         return (f"code flips {self.code_flips}/{self.codes}, ternary flips {self.tern_flips}/{self.terns}")
 
 
-def install(ref, flips, taps, tern_kind=None, thr=None, states=None):
+def install(ref, flips, taps, tern_kind=None, thr=None, states=None, rows=None):
     """Feed the taps' decisions into oracle layer ``ref`` (SISO or MIMO); in bfloat16 runs also the
     device's ``states`` (SISO: the layer-dtype states or decode state; MIMO: the rank-free float32
-    states, or the decode state)."""
+    states, or the decode state) and its tanh(E) / C.  ``rows``: only the first rows (tokens) of a
+    batch-1 device run, for an oracle run on that causal prefix."""
     for mod, name in ((ref.in_proj, "u"), (ref.cross_layer_q_proj, "cs"), (ref.state_proj, "te"),
                       (ref.ent_proj, "c"), (ref.out_proj, "y")):
-        mod.code_hook = flips.code_hook(*taps.codes(name))
+        mod.code_hook = flips.code_hook(*taps.codes(name, rows), name=name)
         mod.exact_products = flips.dtype == torch.bfloat16
     if tern_kind is not None:
-        ref.tern_hook = flips.tern_hook(taps.tern.cpu(), ref.entanglement_threshold if thr is None else thr,
-                                        tern_kind)
+        tern = taps.tern if rows is None else taps.tern[:, :rows]
+        ref.tern_hook = flips.tern_hook(tern.cpu(), ref.entanglement_threshold if thr is None else thr, tern_kind)
     if states is not None and flips.dtype == torch.bfloat16:
-        ref.state_hook = flips.state_hook(states.detach().cpu(), getattr(ref, "mimo_x", None))
+        ref.state_hook = flips.state_hook(states[:rows].detach().cpu(), getattr(ref, "mimo_x", None))
+    if flips.dtype == torch.bfloat16:
+        ref.mix_hook = flips.mix_hook(taps.te[:rows].cpu(), taps.c[:rows].cpu())
+        ref.gate_hook = flips.gate_hook(taps.yv[:rows].cpu())
 
 
 def install_ffn(ffn, flips, taps):
     """Feed a feed-forward call's codes (x for gate/up, h for down_proj) into oracle FeedForward ``ffn``."""
-    ffn.gate_proj.code_hook = flips.code_hook(*taps.codes("u"))
-    ffn.down_proj.code_hook = flips.code_hook(*taps.codes("h"))
+    ffn.gate_proj.code_hook = flips.code_hook(*taps.codes("u"), name="ffn x")
+    ffn.down_proj.code_hook = flips.code_hook(*taps.codes("h"), name="ffn h")
     for mod in (ffn.gate_proj, ffn.down_proj):
         mod.exact_products = flips.dtype == torch.bfloat16
 
 
 def uninstall(ref):
     for m in ref.modules():
-        for hook in ("code_hook", "tern_hook", "state_hook"):
+        for hook in ("code_hook", "tern_hook", "state_hook", "mix_hook", "gate_hook"):
             if hasattr(m, hook):
                 setattr(m, hook, None)
         if hasattr(m, "exact_products"):
@@ -251,7 +314,7 @@ def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
     with torch.no_grad():
         if P:
             tern = (B, P, min(W, P)) if W > 0 else (B, P, (P + 63) // 64 * 64)
-            with Taps(B * P, D, dm, DEV, tern, d_state=D) as tp:
+            with Taps(B * P, D, dm, DEV, tern, d_state=D, dtype=dtype) as tp:
                 outs[0]["prefill_y"] = m(ud[:, :P], inference_params={"state_cache": caches[0]},
                                          cross_layer_state=csd[:, :P] if cs is not None else None)[0]
             install(ref, flips, tp, "local" if W > 0 else "global", states=m._last_cross_layer_state)
@@ -260,7 +323,7 @@ def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
             uninstall(ref)
         for s in range(steps):
             t = P + s
-            with Taps(B, D, dm, DEV, (B, 1, max(W, 1)), d_state=D) as tp:
+            with Taps(B, D, dm, DEV, (B, 1, max(W, 1)), d_state=D, dtype=dtype) as tp:
                 y, st = m(ud[:, t:t + 1], inference_params={"state_cache": caches[0]},
                           cross_layer_state=csd[:, t] if cs is not None else None)
             install(ref, flips, tp, "decode", states=m._last_cross_layer_state)
@@ -323,9 +386,10 @@ class ModelTaps:
                 tern = (B, L, H, W) if mimo else (B, L, min(W, L))
             else:
                 tern = (B, L, (L + 63) // 64 * 64)
+            dtype = mixer.in_proj.weight.dtype
             mt = Taps(M, H * D, dm, DEV, tern, d_state=D, cs_rows=B * H if (decode and mimo) else M,
-                      states=mimo and not decode)
-            ft = Taps(M, 1, dm, DEV, d_inter=mlp.down_proj.in_features)
+                      states=mimo and not decode, dtype=dtype)
+            ft = Taps(M, 1, dm, DEV, d_inter=mlp.down_proj.in_features, dtype=dtype)
             ent = {"mixer": mt, "ffn": ft, "mimo": mimo, "states": None,
                    "orig": (mixer.forward, mlp.forward, getattr(mlp, "forward_codes", None))}
             self.entries.append(ent)
@@ -383,7 +447,7 @@ def siso_prefill_check(ref, m, u, dtype, cs=None, h0=None):
     tern = (B, L, min(W, L)) if W > 0 else (B, L, (L + 63) // 64 * 64)
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(B * L, D, dm, DEV, tern, d_state=D) as tp:
+        with Taps(B * L, D, dm, DEV, tern, d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV), cross_layer_state=cs.to(DEV) if cs is not None else None,
                      prev_state=h0.to(DEV) if h0 is not None else None)
         install(ref, flips, tp, "local" if W > 0 else "global", states=m._last_cross_layer_state)

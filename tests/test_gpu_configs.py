@@ -205,7 +205,7 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
     D, W = cfg["d_state"], cfg["entanglement_window"]
     flips = Flips(dtype)
     with torch.no_grad():
-        with hip_ops.launch_log() as log, Taps(B * L, D, cfg["d_model"], DEV, (B, L, W), d_state=D) as tp:
+        with hip_ops.launch_log() as log, Taps(B * L, D, cfg["d_model"], DEV, (B, L, W), d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
         install(ref, flips, tp, "local", states=m._last_cross_layer_state)
         yr, fr = ref(u)
@@ -252,7 +252,7 @@ def test_cfg3_decode_b32_at_size(dtype):
             torch.cuda.synchronize()
         c1 = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in cache.items()}
         cache.update({k: (v.clone() if torch.is_tensor(v) else v) for k, v in snap.items()})
-        with Taps(B, cfg["d_state"], cfg["d_model"], DEV, (B, 1, cfg["entanglement_window"]), d_state=cfg["d_state"]):
+        with Taps(B, cfg["d_state"], cfg["d_model"], DEV, (B, 1, cfg["entanglement_window"]), d_state=cfg["d_state"], dtype=dtype):
             y2, s2 = m(u[:, P:P + 1].to(DEV), inference_params={"state_cache": cache})
     assert sum(k.startswith("skinny_fq_kernel<") for k in log.kernels) == 2, log.kernels
     assert torch.equal(y1, y2) and torch.equal(s1, s2)
@@ -287,7 +287,7 @@ def test_cfg4_mimo_long_vs_oracle(dtype):
     H, D, W = 2, 64, 64
     flips = Flips(dtype)
     with torch.no_grad():
-        with hip_ops.launch_log() as log, Taps(1100, H * D, 128, DEV, (1, 1100, H, W), states=True) as tp:
+        with hip_ops.launch_log() as log, Taps(1100, H * D, 128, DEV, (1, 1100, H, W), states=True, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
         install(ref, flips, tp, "mimo", states=tp.S)
         yr, fr = ref(u)
@@ -316,27 +316,17 @@ def test_cfg4_mimo_full_size():
     u = torch.randn(1, L, dm, generator=torch.Generator().manual_seed(0)).to(dtype)
     hip_ops.device_status(clear=True)
     with torch.no_grad():
-        with hip_ops.launch_log() as log, Taps(L, H * D, dm, DEV, (1, L, H, W), states=True) as tp:
+        with hip_ops.launch_log() as log, Taps(L, H * D, dm, DEV, (1, L, H, W), states=True, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
     for k in ("mfma32_kernel<2,4,2,2,0,1,3>", "mfma32_kernel<2,4,2,2,1,1,3>", "scan_lb_kernel<1,0,1,16,8>",
               "mimo_mix_kernel<1,true,64>", "ent_scores_mimo_kernel<1>"):
         assert _has(log.kernels, k), (k, log.kernels)
-    # the oracle on the causal prefix, fed the device's decisions for those rows
+    # the oracle on the causal prefix, fed the device's decisions (and, bf16, states and tanh(E) / C) for
+    # those rows
     flips = Flips(dtype)
-    M = Lp
-
-    def codes(name, K):
-        q = getattr(tp, "q_" + name)[:M].cpu().numpy()
-        return unpermute_layout1(q, K), getattr(tp, "s_" + name)[:M].cpu()
-
-    ref.in_proj.code_hook = flips.code_hook(*codes("u", dm))
-    ref.state_proj.code_hook = flips.code_hook(*codes("te", H * D))
-    ref.ent_proj.code_hook = flips.code_hook(*codes("c", H * D))
-    ref.out_proj.code_hook = flips.code_hook(*codes("y", dm))
-    ref.tern_hook = flips.tern_hook(tp.tern[:, :M].cpu(), cfg["entanglement_threshold"], "mimo")
-    ref.state_hook = flips.state_hook(tp.S[:M].cpu(), ref.mimo_x)
+    install(ref, flips, tp, "mimo", states=tp.S, rows=Lp)
     with torch.no_grad():
         yr, _ = ref(u[:, :Lp])
     uninstall(ref)

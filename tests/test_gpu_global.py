@@ -47,7 +47,7 @@ def _siso_lockstep(ref, m, u, cs, dtype):
     D = m.d_state
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(B * L, D, dm, DEV, (B, L, (L + 63) // 64 * 64), d_state=D) as tp:
+        with Taps(B * L, D, dm, DEV, (B, L, (L + 63) // 64 * 64), d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV), cross_layer_state=cs.to(DEV) if cs is not None else None)
         install(ref, flips, tp, "global", states=m._last_cross_layer_state)
         yr, fr = ref(u, cross_layer_state=cs)
@@ -125,7 +125,7 @@ def test_mimo_global_random_vs_oracle(dtype, B, L):
     u = torch.randn(B, L, 64, generator=torch.Generator().manual_seed(3)).to(dtype)
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(B * L, 32, 64, DEV, (B, L, (L + 63) // 64 * 64), states=True) as tp:
+        with Taps(B * L, 32, 64, DEV, (B, L, (L + 63) // 64 * 64), states=True, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
         install(ref, flips, tp, "global", states=tp.S)
         yr, fr = ref(u)

@@ -147,7 +147,7 @@ def test_siso_from_oracle_export_matches_float_model(dtype):
     flips = Flips(dtype)
     D, W = SISO_CFG["d_state"], SISO_CFG["entanglement_window"]
     with torch.no_grad():
-        with Taps(600, D, 128, DEV, (2, 300, min(W, 300)), d_state=D) as tp:
+        with Taps(600, D, 128, DEV, (2, 300, min(W, 300)), d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
         install(ref, flips, tp, "local", states=m._last_cross_layer_state)
         yr, fr = ref(u)

@@ -77,7 +77,7 @@ def test_ffn_vs_oracle(dtype, M):
     x = torch.randn(M, cfg.d_model, generator=torch.Generator().manual_seed(3)).to(dtype)
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(M, 1, cfg.d_model, DEV, d_inter=cfg.d_intermediate) as tp:
+        with Taps(M, 1, cfg.d_model, DEV, d_inter=cfg.d_intermediate, dtype=dtype) as tp:
             y = m(x.to(DEV))
         # the codes path (as after norm2) gives the same bits
         q, s, rs = hip_ops.quant_act(x.to(DEV), m.gate_proj.bit_eps)

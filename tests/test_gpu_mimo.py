@@ -80,7 +80,7 @@ def _prefill_lockstep(ref, m, u, dtype):
     H, D, W = m.n_heads, m.d_state, m.entanglement_window
     flips = Flips(dtype)
     with torch.no_grad():
-        with Taps(B * L, H * D, m.d_model, DEV, (B, L, H, W), states=True) as tp:
+        with Taps(B * L, H * D, m.d_model, DEV, (B, L, H, W), states=True, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
         install(ref, flips, tp, "mimo", states=tp.S)
         yr, fr = ref(u)
@@ -120,14 +120,15 @@ def _decode_lockstep(ref, m, u, cs, P, steps, B, dtype):
     with torch.no_grad():
         if P:
             tern = (B, P, H, W) if W > 0 else (B, P, (P + 63) // 64 * 64)
-            with Taps(B * P, H * D, m.d_model, DEV, tern, states=True) as tp:
+            with Taps(B * P, H * D, m.d_model, DEV, tern, states=True, dtype=dtype) as tp:
                 outs[0]["prefill_y"] = m(ud[:, :P], inference_params={"state_cache": caches[0]})[0]
             install(ref, flips, tp, "mimo" if W > 0 else "global", states=tp.S)
             outs[1]["prefill_y"] = ref(u[:, :P], inference_params={"state_cache": caches[1]})[0]
             uninstall(ref)
         for s in range(steps):
             t = P + s
-            with Taps(B, H * D, m.d_model, DEV, (B, H, max(W, 1)), d_state=D, cs_rows=B * H) as tp:
+            with Taps(B, H * D, m.d_model, DEV, (B, H, max(W, 1)), d_state=D, cs_rows=B * H,
+                      dtype=dtype) as tp:
                 y, st = m(ud[:, t:t + 1], inference_params={"state_cache": caches[0]},
                           cross_layer_state=csd[:, t] if cs is not None else None)
             install(ref, flips, tp, "decode", states=m._last_cross_layer_state)
