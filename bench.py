@@ -43,8 +43,11 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-kernels", action="store_true", help="skip the isolated-kernel measurements")
     p.add_argument("--no-mimo", action="store_true", help="skip the configs[4] MIMO layer measurement")
+    p.add_argument("--cpu-all", action="store_true",
+                   help="time every config's CPU baseline (configs[1]-[4], the MIMO layer at L 1024/2048/4096) at "
+                        "the affinity core count and on one thread, print their JSON and exit (slow)")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
-    p.add_argument("--workload", default="all", choices=["all", "layer", "decode", "mimo", "global", "lm"],
+    p.add_argument("--workload", default="all", choices=["all", "layer", "decode", "mimo", "global", "lm", "base"],
                    help="run one measurement alone and print its JSON (for per-workload profiles)")
     p.add_argument("--copy-calib", action="store_true",
                    help="run one 256 MiB device-to-device copy first (a known-size reference for "
@@ -218,6 +221,31 @@ def measure_lm(torch, steps: int = 10):
     return out
 
 
+def measure_true_base(torch, steps: int = 20):
+    """The base() preset's own layer (d_state 384, window 32; BASELINE's headline overrides them to 256 / 16),
+    B4 x L2048 prefill, bf16: per-forward time."""
+    from tesm_amd import TESM_SISO
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = dict(LAYER, d_state=384, entanglement_window=32)
+    m = TESM_SISO(**cfg).to(dev).to(torch.bfloat16).eval()
+    u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        for _ in range(3):
+            m(u)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            m(u)
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": "TESM_SISO prefill at the base() preset's own d_state 384 / window 32, B4 x L2048, bf16",
+            "ms_per_forward": ms, "tokens_per_s": B * L / (ms * 1e-3)}
+
+
 def measure_global(torch, steps: int = 10):
     """TESM_SISO with global causal entanglement (entanglement_window = 0, the next row after the
     local-window layer) at configs[3]'s dims, B4 x L2048 prefill, bf16: per-forward time."""
@@ -285,26 +313,160 @@ def gemm_traffic():
         return None
 
 
+def progress(msg: str) -> None:
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
+def affinity_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def time_cpu(fn, seconds: float, min_reps: int = 1):
+    """Median-free wall rate: one warm-up call, then calls until `seconds` have passed (at least
+    min_reps); returns (calls, elapsed seconds)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= min_reps:
+            return n, el
+
+
 def cpu_baseline(torch, seconds: float):
-    """The oracle's torch path (restating the reference's kernel_backend='torch') on host cores."""
+    """The oracle's torch path (restating the reference's kernel_backend='torch') on host cores:
+    configs[3]'s layer forward with as many threads as this process may run on, and a shorter
+    one-thread sample."""
     from oracle import tesm_torch as ot
 
+    cores = affinity_cores()
     torch.manual_seed(0)
     m = ot.TESM_SISO(**LAYER).eval().to(torch.bfloat16)
     u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
-    with torch.no_grad():
-        m(u)
-        n, t0 = 0, time.perf_counter()
-        while True:
-            m(u)
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= seconds:
-                break
-    return {"value": n * B * L / el, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "cpu": cpu_model(),
+    prev = torch.get_num_threads()
+    try:
+        with torch.no_grad():
+            torch.set_num_threads(cores)
+            n, el = time_cpu(lambda: m(u), seconds)
+            torch.set_num_threads(1)
+            n1, el1 = time_cpu(lambda: m(u), seconds / 4)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": n * B * L / el, "unit": "tokens/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
             "sample": f"oracle TESM_SISO.forward (torch restatement of the reference torch path), bf16, "
-                      f"{B}x{L} tokens, {n} forwards in {el:.1f} s"}
+                      f"{B}x{L} tokens, {n} forwards in {el:.1f} s on {cores} threads (the process's affinity set)",
+            "one_thread": {"value": n1 * B * L / el1, "unit": "tokens/s", "cores": 1,
+                           "sample": f"{n1} forwards in {el1:.1f} s on 1 thread"}}
+
+
+def cpu_suite(torch, seconds: float):
+    """CPU baselines of every config (the oracle's torch path on this host), at the affinity core count
+    and on one thread: configs[1] BitLinear (fake-quant F.linear, cached ternary weight, fp32),
+    configs[2] scan + local entanglement (bf16 and fp32), configs[3] layer forward (bf16 and fp32) and
+    B32 decode step, configs[4] MIMO layer at L 1024 / 2048 / 4096 with a linear extrapolation to the
+    32768-token prefill (the full length would take hours: the reference loops over ranks, positions
+    and window slots in Python)."""
+    import math
+
+    from oracle import tesm_torch as ot
+
+    cores = affinity_cores()
+    out = {"cpu": cpu_model(), "cores": cores, "kind": "port", "configs": {}}
+    prev = torch.get_num_threads()
+
+    def both(fn, secs):
+        res = {}
+        for th in (cores, 1):
+            torch.set_num_threads(th)
+            n, el = time_cpu(fn, secs if th == cores else secs / 2)
+            res[f"threads_{th}"] = {"s_per_call": el / n, "calls": n}
+        return res
+
+    try:
+        with torch.no_grad():
+            c1 = {}
+            for (M, K, N) in [(1, 4096, 4096), (1, 4096, 11008), (2048, 4096, 4096)]:
+                torch.manual_seed(0)
+                bl = ot.BitLinear(K, N).eval()
+                x = torch.randn(M, K, generator=torch.Generator().manual_seed(0))
+                r = both(lambda: bl(x), seconds)
+                nbytes = N * K // 4 + M * K + M * N * 4
+                for v in r.values():
+                    if M == 1:
+                        v["GB_per_s_of_int2_bytes"] = nbytes / v["s_per_call"] / 1e9
+                    else:
+                        v["TOP_per_s"] = 2 * M * N * K / v["s_per_call"] / 1e12
+                c1[f"M{M}_K{K}_N{N}"] = r
+                progress(f"cpu configs[1] M{M} K{K} N{N} done")
+            out["configs"]["1_bitlinear_fp32"] = c1
+            c2 = {}
+            for dt in (torch.bfloat16, torch.float32):
+                g = torch.Generator().manual_seed(0)
+                Bs, Ls, D, R, W = 8, 512, 256, 48, 16
+                m = ot.TESM_SISO(d_model=512, d_state=D, ent_rank=R, entanglement_window=W,
+                                 entanglement_threshold=0.08, entanglement_scale=0.2, max_seq_len=Ls).eval().to(dt)
+                decay = torch.sigmoid(torch.randn(Bs, Ls, D, generator=g)).to(dt)
+                upd = (torch.sigmoid(torch.randn(Bs, Ls, D, generator=g) / math.sqrt(512)) *
+                       torch.tanh(torch.randn(Bs, Ls, D, generator=g) / math.sqrt(512))).to(dt)
+                q = torch.randn(Bs, Ls, R, generator=g).to(dt)
+                k = torch.randn(Bs, Ls, R, generator=g).to(dt)
+                S = m._parallel_state_scan(decay, upd)
+                c2[str(dt).split(".")[-1]] = {
+                    "scan": both(lambda: m._parallel_state_scan(decay, upd), seconds / 2),
+                    "local_entanglement": both(lambda: m._compute_local_entanglement(q, k, S), seconds / 2)}
+                progress(f"cpu configs[2] {dt} done")
+            out["configs"]["2_scan_local_ent_B8xL512"] = c2
+            c3 = {}
+            for dt in (torch.bfloat16, torch.float32):
+                torch.manual_seed(0)
+                m = ot.TESM_SISO(**LAYER).eval().to(dt)
+                u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(dt)
+                r = both(lambda: m(u), seconds)
+                for v in r.values():
+                    v["tokens_per_s"] = B * L / v["s_per_call"]
+                c3[f"prefill_{str(dt).split('.')[-1]}"] = r
+                ud = torch.randn(32, 65, LAYER["d_model"], generator=torch.Generator().manual_seed(1)).to(dt)
+                cache = m.allocate_inference_cache(32, 128)
+                m(ud[:, :64], inference_params={"state_cache": cache})
+
+                def one_step():  # keeps stepping the same cache (positions past the prefill)
+                    m(ud[:, 64:65], inference_params={"state_cache": cache})
+                r = both(one_step, seconds / 2)
+                for v in r.values():
+                    v["tokens_per_s"] = 32 / v["s_per_call"]
+                c3[f"decode_B32_{str(dt).split('.')[-1]}"] = r
+                progress(f"cpu configs[3] {dt} done")
+            out["configs"]["3_siso_layer_base_B4xL2048"] = c3
+            c4 = {}
+            mimo_cfg = dict(MIMO)
+            for Lm in (1024, 2048, 4096):
+                torch.manual_seed(0)
+                m = ot.TESMMIMO_Optimized(**dict(mimo_cfg, max_seq_len=Lm)).eval().to(torch.bfloat16)
+                u = torch.randn(1, Lm, MIMO["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+                torch.set_num_threads(cores)
+                t0 = time.perf_counter()
+                m(u)
+                el = time.perf_counter() - t0
+                c4[f"L{Lm}"] = {"threads": cores, "s_per_forward": el, "tokens_per_s": Lm / el}
+                progress(f"cpu configs[4] L{Lm} done ({el:.1f} s)")
+                del m
+            # least-squares line t = a + b L through the three lengths, evaluated at 32768
+            xs = [1024.0, 2048.0, 4096.0]
+            ys = [c4[f"L{int(x)}"]["s_per_forward"] for x in xs]
+            mx, my = sum(xs) / 3, sum(ys) / 3
+            b = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+            a = my - b * mx
+            t32 = a + b * 32768
+            c4["extrapolated_L32768"] = {"s_per_forward": t32, "tokens_per_s": 32768 / t32,
+                                         "note": "linear fit t = a + b*L through L 1024/2048/4096 (not measured)"}
+            out["configs"]["4_mimo_large40b_bf16"] = c4
+    finally:
+        torch.set_num_threads(prev)
+    return out
 
 
 def cpu_model() -> str:
@@ -318,20 +480,29 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def copy_bandwidth(torch) -> float:
-    """Device-to-device copy of 1 GiB (read + write bytes per second, GB/s): the measured ceiling that the
-    HBM-bound kernels' fractions are also given against."""
+def copy_bandwidth(torch):
+    """1 GiB device-to-device copies (read + write bytes per second, GB/s): the library's streaming copy
+    kernel (16-byte nontemporal loads and stores, the measured ceiling that the HBM-bound kernels'
+    fractions are also given against) and torch's copy_ for comparison."""
+    from tesm_amd import hip_ops
+
     dev = torch.device("cuda:0")
     src = torch.empty(256 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
-    t = time_back_to_back(torch, lambda i: dst.copy_(src), 20)
+    t = time_back_to_back(torch, lambda i: hip_ops.stream_copy(dst, src), 20)
+    t_torch = time_back_to_back(torch, lambda i: dst.copy_(src), 20)
     del src, dst
     torch.cuda.empty_cache()
-    return 2 * (1 << 30) / t / 1e9
+    return 2 * (1 << 30) / t / 1e9, 2 * (1 << 30) / t_torch / 1e9
 
 
 def main():
     args = parse()
+    if args.cpu_all:
+        import torch
+
+        print(json.dumps({"cpu_baselines": cpu_suite(torch, args.cpu_seconds)}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); multi-GPU sharding is "
               f"design-only", file=sys.stderr)
@@ -371,6 +542,8 @@ def main():
                 res = measure_mimo(torch)
             elif args.workload == "global":
                 res = measure_global(torch)
+            elif args.workload == "base":
+                res = measure_true_base(torch)
             else:
                 res = measure_lm(torch)
         print(json.dumps({"workload": args.workload, "result": res}))
@@ -401,11 +574,13 @@ def main():
         decode = measure_decode(torch, m)
         mimo = None if args.no_mimo else measure_mimo(torch)
         glob = measure_global(torch)
+        true_base = measure_true_base(torch)
         lm = measure_lm(torch)
         kernels = {} if args.no_kernels else measure_kernels(torch, args.only)
         if kernels:
-            copy_gbs = copy_bandwidth(torch)
+            copy_gbs, copy_torch = copy_bandwidth(torch)
             kernels["copy_1GiB_GBps"] = copy_gbs
+            kernels["copy_1GiB_GBps_torch"] = copy_torch
             for v in kernels.values():
                 if isinstance(v, dict) and v.get("unit") == "GB/s":
                     v["frac_of_copy"] = v["achieved"] / copy_gbs
@@ -432,14 +607,15 @@ def main():
                    "batch": B, "seq_len": L, "d_model": 768, "d_state": 256, "ent_rank": 64, "window": 16,
                    "weights": "INT2 ternary", "activations": "bf16"},
         "roofline": {"kernel": "in_proj INT2xINT8 MFMA GEMM (M=8192, K=768, N=2432)", "bound": "mfma",
-                     "achieved": ops / t_gemm / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "achieved": ops / t_gemm / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                      "frac": ops / t_gemm / 1e12 / INT8_PEAK_TOPS, "traffic": gemm_traffic(), "us": t_gemm * 1e6,
                      "algorithmic_bytes": M * K + N * (K // 4) + 8 * M + 2 * M * N,
-                     "note": "int8 ops/s against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes per "
-                             "launch from profiles/in_proj_gemm_traffic.json"},
+                     "note": "int8 ops/s (TOP/s) against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes "
+                             "per launch from profiles/in_proj_gemm_traffic.json"},
         "decode": decode,
         "mimo_layer": mimo,
         "global_layer": glob,
+        "layer_true_base": true_base,
         "lm_tiny": lm,
         "kernels": kernels,
     }

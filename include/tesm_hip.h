@@ -52,6 +52,11 @@ int64_t tesm_hip_kpad(int64_t K);
 int tesm_hip_launch_log(int enable);
 int64_t tesm_hip_launch_log_read(char* buf, int64_t cap, int clear);
 
+/* Streaming device copy of `bytes` bytes (16-byte vector loads and stores when both pointers are
+ * 16-byte aligned), a measurement aid with no reference counterpart: the HBM bandwidth ceiling that
+ * the bandwidth-bound kernels are compared with, and a known-size reference for byte counters. */
+int tesm_hip_stream_copy(void* dst, const void* src, int64_t bytes, void* stream);
+
 /* Device status word of the library's bounded waits on the current device, no reference
  * counterpart (the reference's kernels never wait on one another).  Bit 0 (TESM_STATUS_SCAN_GAVE_UP):
  * a single-pass scan's look-back poll gave up; the states of that span are NaN.  The kernels still

@@ -169,6 +169,7 @@ _SIGNATURES = {
     "tesm_hip_launch_log": ([I32], I32),
     "tesm_hip_launch_log_read": ([ctypes.c_char_p, I64, I32], I64),
     "tesm_hip_device_status": ([ctypes.POINTER(ctypes.c_uint32), I32], I32),
+    "tesm_hip_stream_copy": ([P, P, I64, P], I32),
     "tesm_hip_debug_scan_spin_limit": ([I32], I32),
     "tesm_hip_debug_taps": ([ctypes.POINTER(Taps)], I32),
     "tesm_hip_bitlinear_fwd_ws_bytes": ([I64, I64], I64),

@@ -627,6 +627,11 @@ int tesm_hip_launch_log(int enable) {
   return kOk;
 }
 
+int tesm_hip_stream_copy(void* dst, const void* src, int64_t bytes, void* stream) {
+  if (int rc = check_ptrs("stream copy", {{dst, "dst"}, {src, "src"}})) return rc;
+  return launch_stream_copy(dst, src, bytes, static_cast<hipStream_t>(stream));
+}
+
 int tesm_hip_device_status(uint32_t* status, int clear) {
   unsigned v = 0;
   if (int rc = scan_status(&v, clear)) return rc;

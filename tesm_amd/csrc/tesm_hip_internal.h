@@ -16,6 +16,7 @@ int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, f
 int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, float* s_w, float* c_w, hipStream_t st);
 int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
                 uint8_t* packed, int64_t ldp, hipStream_t st);
+int launch_stream_copy(void* dst, const void* src, int64_t bytes, hipStream_t st);
 int launch_unpack(const uint8_t* packed, int64_t N, int64_t K, int64_t ldp, int8_t* codes, int64_t ldc,
                   hipStream_t st);
 

@@ -196,6 +196,18 @@ class launch_log:
         return False
 
 
+def stream_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """Copy src's bytes into dst with the library's streaming copy kernel (a bandwidth reference)."""
+    require_device(dst, src)
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("stream_copy: tensors must be contiguous")
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() < n:
+        raise ValueError("stream_copy: destination too small")
+    with torch.cuda.device(src.device):
+        _lib.check(_lib.load().tesm_hip_stream_copy(_p(dst), _p(src), n, _stream(src)))
+
+
 def device_status(clear: bool = True) -> int:
     """The device status word of the current device (bit 0: a scan look-back gave up); synchronises."""
     v = ctypes.c_uint32(0)

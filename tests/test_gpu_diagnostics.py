@@ -137,3 +137,20 @@ def test_bitlinear_module_one_call():
         y2 = hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, 96, 256, torch.float32)
     assert torch.equal(y.reshape(-1, 96), y2)
     assert np.isfinite(y.cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("nbytes,off", [(0, 0), (1, 0), (4095, 0), (1 << 20, 0), ((1 << 20) + 7, 3),
+                                        (64 * 1024 * 1024 + 48, 0)])
+def test_stream_copy(nbytes, off):
+    """The streaming copy (the bandwidth reference of the measurements) copies every byte, aligned or
+    not, and touches nothing past the end."""
+    g = torch.Generator().manual_seed(nbytes)
+    src = torch.randint(0, 256, (nbytes + off + 16,), dtype=torch.uint8, generator=g).to(DEV)
+    dst = torch.zeros(nbytes + off + 16, dtype=torch.uint8, device=DEV)
+    with hip_ops.launch_log() as log:
+        hip_ops.stream_copy(dst[off:off + nbytes], src[off:off + nbytes])
+        torch.cuda.synchronize()
+    assert torch.equal(dst[off:off + nbytes], src[off:off + nbytes])
+    assert not dst[:off].any() and not dst[off + nbytes:].any()
+    if nbytes >= 16 and off == 0:
+        assert "stream_copy_kernel" in log.kernels, log.kernels
