@@ -307,8 +307,9 @@ struct SisoPlan {
   void* c_mix;
   void* yg;
   void* cq;
-  int8_t* g_tern;   // global entanglement (window == 0): decisions, counts, bias table, RoPE'd q / k
-  int32_t* g_count;
+  int8_t* g_tern;   // global entanglement (window == 0): decisions, counts, bias table, RoPE'd q / k,
+  int32_t* g_count; // bf16 states transposed
+  uint16_t* g_st;
   float* g_table;
   float *g_qr, *g_kr;
   int64_t total;
@@ -347,15 +348,17 @@ SisoPlan plan_siso(const tesm_hip_siso_layer& p, void* base) {
   s.e_tanh = s.c_mix = nullptr;
   s.g_tern = nullptr;
   s.g_count = nullptr;
+  s.g_st = nullptr;
   s.g_table = nullptr;
   s.g_qr = s.g_kr = nullptr;
   if (!s.fuse_ent) {
     if (global) {
       s.g_tern = c.take<int8_t>(p.B * p.L * global_tern_pitch(p.L));
-      s.g_count = c.take<int32_t>(p.B * p.L * ((p.L + 63) / 64) * 4);
+      s.g_count = c.take<int32_t>(p.B * p.L * 4);
       s.g_table = c.take<float>(2 * p.L * 4);
       s.g_qr = c.take<float>(p.B * p.L * p.ent_rank * 4);
       s.g_kr = c.take<float>(p.B * p.L * p.ent_rank * 4);
+      s.g_st = p.dt == kBF16 ? c.take<uint16_t>(global_states_t_bytes(p.dt, 0, p.B, p.L, p.d_state)) : nullptr;
     } else {
       s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, 1, std::min(p.window, p.L)));
     }
@@ -542,7 +545,7 @@ MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
     s.wts = c.take<float>(ent_ws_bytes(p.B, p.L, p.n_heads, p.window));
   } else {
     s.g_tern = c.take<int8_t>(p.B * p.L * global_tern_pitch(p.L));
-    s.g_count = c.take<int32_t>(p.B * p.L * ((p.L + 63) / 64) * 4);
+    s.g_count = c.take<int32_t>(p.B * p.L * 4);
     s.g_table = c.take<float>(2 * p.L * 4);
     s.g_qr = c.take<float>(p.B * p.L * p.n_heads * p.ent_rank * 4);
     s.g_kr = c.take<float>(p.B * p.L * p.n_heads * p.ent_rank * 4);
@@ -1055,6 +1058,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     ga.ld_out = D;
     ga.tern = s.g_tern;
     ga.count = s.g_count;
+    ga.states_t = s.g_st;
     ga.qr = s.g_qr;
     ga.kr = s.g_kr;
     if ((rc = launch_global_ent(ga, st))) return rc;

@@ -38,14 +38,17 @@ struct GlobalArgs {
   void* e_tanh = nullptr;        // (b, t, c) at [(b*L + t)*ld_out + c], dt: tanh(E) (MIMO: tanh(E * coef))
   void* c_out = nullptr;         // E - S (MIMO: (E - S) * coef)
   int64_t ld_out = 0;
-  int8_t* tern = nullptr;        // workspace (B, L, ldt) ternary decisions, ldt = round_up(L, 64)
-  int32_t* count = nullptr;      // workspace (B, L, ceil(L/64)) nonzero decisions per query and key tile
+  int8_t* tern = nullptr;        // workspace (B, L, ldt) ternary decisions, ldt = round_up(L, 64); a row's
+                                 // columns past its 64-key diagonal tile are left unwritten
+  int32_t* count = nullptr;      // workspace (B, L) nonzero decisions per query
+  uint16_t* states_t = nullptr;  // workspace (B, H*D, ldt) bf16 states transposed (bf16 SISO layers only)
   float* qr = nullptr;           // workspace (B, L, H*R) RoPE'd queries (+ cross-layer bias)
   float* kr = nullptr;           // workspace (B, L, H*R) RoPE'd keys
 };
 
 int64_t global_tern_pitch(int64_t L);
-int64_t global_ws_bytes(int64_t B, int64_t L, int64_t RQ);  // tern + counts + table + RoPE'd q / k
+// bytes of the transposed-states workspace (zero where the states are float32)
+int64_t global_states_t_bytes(int dt, int mimo, int64_t B, int64_t L, int64_t C);
 int launch_global_ent(const GlobalArgs& a, hipStream_t st);
 
 }  // namespace tesm
