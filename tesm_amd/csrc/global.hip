@@ -214,14 +214,43 @@ __global__ __launch_bounds__(256) void global_transpose_kernel(const uint16_t* _
   }
 }
 
+template <int DT, int SDT, int NWV>
+__device__ __forceinline__ void global_mix_finish(const GlobalArgs& a, const float (&part)[NWV][kMQ][kMC + 4],
+                                                  int64_t b, int64_t i, int q, int64_t c0, int cc, int64_t C) {
+  if (i >= a.L) return;
+  const int n = a.count[b * a.L + i];
+  const float winv = rnd<DT>(1.0f / rnd<DT>(static_cast<float>(n > 1 ? n : 1)));  // dt(t / dt(n)) for t = 1
+#pragma unroll
+  for (int y = 0; y < 8; ++y) {
+    const int64_t c = c0 + cc + y;
+    if (c >= C) break;
+    float A0 = part[0][q][cc + y];
+#pragma unroll
+    for (int v = 1; v < NWV; ++v) A0 += part[v][q][cc + y];
+    const float s = ld<SDT>(a.S, (b * a.L + i) * a.ld_s + c);
+    const int64_t o = (b * a.L + i) * a.ld_out + c;
+    if (a.mimo) {
+      const float A = A0 * winv;
+      const float cf = a.coef[c];
+      st<DT>(a.e_tanh, o, tanhf_(A * cf));
+      st<DT>(a.c_out, o, (A - s) * cf);
+    } else {
+      const float avg = rnd<DT>(A0 * winv);
+      const float e = rnd<DT>(s + rnd<DT>(a.ent_scale * rnd<DT>(avg - s)));
+      st<DT>(a.e_tanh, o, tanhf_(e));
+      st<DT>(a.c_out, o, e - s);
+    }
+  }
+}
+
 // Decisions x states for one (32-query block, 64-channel block, batch row), the query blocks in
 // descending order over the flattened grid.  Wave w takes key steps w, w + 4, ... of kMK keys; the
 // partial accumulators meet in LDS and every thread finishes 8 consecutive channels of one query.
 // SDT: states dtype; bf16 states come transposed in s_t (pitch ldst).
-template <int DT, int SDT>
-__global__ __launch_bounds__(256) void global_mix_kernel(GlobalArgs a, int64_t ldt, const uint16_t* s_t, int64_t ldst,
-                                                         int64_t nqb, int64_t ncb) {
-  __shared__ float part[4][kMQ][kMC + 4];
+template <int DT, int SDT, int NWV = 4, int PF = 2>
+__global__ __launch_bounds__(NWV * 64) void global_mix_kernel(GlobalArgs a, int64_t ldt, const uint16_t* s_t,
+                                                               int64_t ldst, int64_t nqb, int64_t ncb) {
+  __shared__ float part[NWV][kMQ][kMC + 4];
   const int64_t flat = blockIdx.x;
   const int64_t b = flat % a.B, cb = (flat / a.B) % ncb, qb = nqb - 1 - flat / (a.B * ncb);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -237,34 +266,52 @@ __global__ __launch_bounds__(256) void global_mix_kernel(GlobalArgs a, int64_t l
     const int64_t ca = c0 + l32 < C ? c0 + l32 : C - 1, cbb = c0 + 32 + l32 < C ? c0 + 32 + l32 : C - 1;
     const uint16_t* s0 = s_t + (b * C + ca) * ldst;
     const uint16_t* s1 = s_t + (b * C + cbb) * ldst;
-    int64_t ks = w;
-    uint2 ta[2];
-    uint4 sa[2], sb[2];
-    auto fetch = [&](int64_t k) {
+    // PF steps of loads in flight: slot p holds step ks + p * NWV of the current round
+    uint2 ta[PF][2];
+    uint4 sa[PF][2], sb[PF][2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int64_t kk = k * kMK + 16 * u + 8 * h;
-        ta[u] = *reinterpret_cast<const uint2*>(trow + kk);
-        sa[u] = *reinterpret_cast<const uint4*>(s0 + kk);
-        sb[u] = *reinterpret_cast<const uint4*>(s1 + kk);
+    for (int p = 0; p < PF; ++p) {
+      const int64_t k = w + p * NWV;
+      if (k < nks) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t kk = k * kMK + 16 * u + 8 * h;
+          ta[p][u] = *reinterpret_cast<const uint2*>(trow + kk);
+          sa[p][u] = *reinterpret_cast<const uint4*>(s0 + kk);
+          sb[p][u] = *reinterpret_cast<const uint4*>(s1 + kk);
+        }
       }
-    };
-    if (ks < nks) fetch(ks);
-    for (; ks < nks; ks += 4) {
-      const uint2 t0 = ta[0], t1 = ta[1];
-      const uint4 a0 = sa[0], a1 = sa[1], b0 = sb[0], b1 = sb[1];
-      if (ks + 4 < nks) fetch(ks + 4);
-      const bf16x8_t x0 = tern_bf16x8(t0), x1 = tern_bf16x8(t1);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, __builtin_bit_cast(bf16x8_t, a0), acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, __builtin_bit_cast(bf16x8_t, b0), acc1, 0, 0, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, __builtin_bit_cast(bf16x8_t, a1), acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, __builtin_bit_cast(bf16x8_t, b1), acc1, 0, 0, 0);
+    }
+    for (int64_t ks = w; ks < nks; ks += PF * NWV) {
+#pragma unroll
+      for (int p = 0; p < PF; ++p) {
+        const int64_t k = ks + p * NWV;
+        if (k < nks) {
+          const uint2 t0 = ta[p][0], t1 = ta[p][1];
+          const uint4 a0 = sa[p][0], a1 = sa[p][1], b0 = sb[p][0], b1 = sb[p][1];
+          const int64_t kn = k + PF * NWV;
+          if (kn < nks) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int64_t kk = kn * kMK + 16 * u + 8 * h;
+              ta[p][u] = *reinterpret_cast<const uint2*>(trow + kk);
+              sa[p][u] = *reinterpret_cast<const uint4*>(s0 + kk);
+              sb[p][u] = *reinterpret_cast<const uint4*>(s1 + kk);
+            }
+          }
+          const bf16x8_t x0 = tern_bf16x8(t0), x1 = tern_bf16x8(t1);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, __builtin_bit_cast(bf16x8_t, a0), acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, __builtin_bit_cast(bf16x8_t, b0), acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, __builtin_bit_cast(bf16x8_t, a1), acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, __builtin_bit_cast(bf16x8_t, b1), acc1, 0, 0, 0);
+        }
+      }
     }
   } else {
     // step (g, s) pairs the lanes of half h with key 8 g + 4 h + s: one dword of decisions per g
     const int64_t ca = c0 + l32 < C ? c0 + l32 : C - 1, cbb = c0 + 32 + l32 < C ? c0 + 32 + l32 : C - 1;
     const float* Sf = static_cast<const float*>(a.S);
-    for (int64_t ks = w; ks < nks; ks += 4) {
+    for (int64_t ks = w; ks < nks; ks += NWV) {
 #pragma unroll
       for (int g = 0; g < kMK / 8; ++g) {
         const int64_t kk = ks * kMK + 8 * g + 4 * h;
@@ -292,29 +339,9 @@ __global__ __launch_bounds__(256) void global_mix_kernel(GlobalArgs a, int64_t l
     part[w][q][32 + l32] = acc1[r];
   }
   __syncthreads();
-  const int q = tid >> 3, cc = 8 * (tid & 7);
-  const int64_t i = i0 + q;
-  if (i >= a.L) return;
-  const int n = a.count[b * a.L + i];
-  const float winv = rnd<DT>(1.0f / rnd<DT>(static_cast<float>(n > 1 ? n : 1)));  // dt(t / dt(n)) for t = 1
-#pragma unroll
-  for (int y = 0; y < 8; ++y) {
-    const int64_t c = c0 + cc + y;
-    if (c >= C) break;
-    const float A0 = part[0][q][cc + y] + part[1][q][cc + y] + part[2][q][cc + y] + part[3][q][cc + y];
-    const float s = ld<SDT>(a.S, (b * a.L + i) * a.ld_s + c);
-    const int64_t o = (b * a.L + i) * a.ld_out + c;
-    if (a.mimo) {
-      const float A = A0 * winv;
-      const float cf = a.coef[c];
-      st<DT>(a.e_tanh, o, tanhf_(A * cf));
-      st<DT>(a.c_out, o, (A - s) * cf);
-    } else {
-      const float avg = rnd<DT>(A0 * winv);
-      const float e = rnd<DT>(s + rnd<DT>(a.ent_scale * rnd<DT>(avg - s)));
-      st<DT>(a.e_tanh, o, tanhf_(e));
-      st<DT>(a.c_out, o, e - s);
-    }
+  for (int e = tid; e < kMQ * kMC / 8; e += NWV * 64) {
+    const int q = e >> 3, cc = 8 * (e & 7);
+    global_mix_finish<DT, SDT, NWV>(a, part, b, i0 + q, q, c0, cc, C);
   }
 }
 

@@ -11,7 +11,8 @@ struct ScanArgs {
   int dt = 0;          // input dtype (0 f32, 1 bf16)
   int out_dt = 0;      // states dtype
   int clamp = 1;       // 1: SISO closed-form clamp semantics (1e-12); 0: plain recurrence (MIMO)
-  int round_update = 1;  // mode 1: round write*tanh(sv) to dt (SISO) or keep fp32 (MIMO)
+  int round_update = 1;  // mode 1: round write*tanh(sv) to dt (SISO) or keep fp32 (MIMO); in mode 1
+                         // clamp and round_update must agree (the SISO and MIMO semantics)
   int64_t B = 0, L = 0, C = 0;
   int64_t cs = 16;     // reference chunk size (state_scan_chunk_size)
   // token-major inputs: element (b, t, c) at ptr[(b*L + t)*ld + c]

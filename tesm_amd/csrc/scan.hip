@@ -318,14 +318,18 @@ __device__ __forceinline__ float scan_val_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int OUT_DT, int MODE, int TM, int SUB>
+// CR: the clamp / update-rounding semantics, 1 = both (SISO), 0 = neither (MIMO), 2 = read from a.
+template <int DT, int OUT_DT, int MODE, int TM, int SUB, int CR>
 __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, int64_t T, int64_t nc, int64_t G,
                                                                   ScanLb s) {
+  const bool clamp = CR == 2 ? a.clamp != 0 : CR == 1;
+  const bool round_update = CR == 2 ? a.round_update != 0 : CR == 1;
   constexpr int WIN = 64 / SUB;  // look-back window entries composed per wave
   __shared__ unsigned s_tile;
   __shared__ int s_m, s_stop;
   __shared__ float2 s_sub[SUB][kScanLbCh];  // sub-span aggregates, then window shares
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the wave index is uniform: read it into a scalar register so that position offsets are scalar math
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t chain = blockIdx.x % (a.B * G);  // grid = nc workgroups per chain
   if (tid == 0) s_tile = atomicAdd(&s.ticket[chain * kScanLbTicketStride], 1u);
   __syncthreads();
@@ -363,9 +367,9 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
         const float sv = rnd<DT>(tanhf_(x2[i]));
         dd = rnd<DT>(sigmoidf_(rnd<DT>(x0[i] + bias)));
         const float wr = rnd<DT>(sigmoidf_(x1[i]));
-        uu = a.round_update ? rnd<DT>(wr * sv) : wr * sv;
+        uu = round_update ? rnd<DT>(wr * sv) : wr * sv;
       }
-      if (a.clamp) {
+      if (clamp) {
         dd = fmaxf(dd, kScanEps);
         A = (i % cs) == 0 ? dd : A * dd;
         if (A < kScanEps) uu *= A * kScanInvEps;  // the clamp factor, folded into the update
@@ -530,8 +534,8 @@ ScanLbShape scan_lb_shape(int64_t B, int64_t L, int64_t C, int64_t T) {
   return g;
 }
 
-template <int DT, int OUT_DT, int MODE>
-int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
+template <int DT, int OUT_DT, int MODE, int CR>
+int run_scan_lb_cr(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
   const ScanLbShape sh = scan_lb_shape(a.B, a.L, a.C, T);
   ScanLb s;
   s.agg = reinterpret_cast<float2*>(summ);
@@ -546,16 +550,28 @@ int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream
   const unsigned grid = static_cast<unsigned>(sh.tiles);
   if (sh.sub == 8) {
     if (T <= 16)
-      scan_lb_kernel<DT, OUT_DT, MODE, 16, 8><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 8>)>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 8, CR><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 8, CR>)>>>(a, T, sh.nc, sh.G, s);
     else
-      scan_lb_kernel<DT, OUT_DT, MODE, 32, 8><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 8>)>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 8, CR><<<grid, kScanLbCh * 8, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 8, CR>)>>>(a, T, sh.nc, sh.G, s);
   } else {
     if (T <= 16)
-      scan_lb_kernel<DT, OUT_DT, MODE, 16, 4><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 4>)>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 16, 4, CR><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 16, 4, CR>)>>>(a, T, sh.nc, sh.G, s);
     else
-      scan_lb_kernel<DT, OUT_DT, MODE, 32, 4><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 4>)>>>(a, T, sh.nc, sh.G, s);
+      scan_lb_kernel<DT, OUT_DT, MODE, 32, 4, CR><<<grid, kScanLbCh * 4, 0, TESM_LOGGED(st, scan_lb_kernel<DT, OUT_DT, MODE, 32, 4, CR>)>>>(a, T, sh.nc, sh.G, s);
   }
   return check_launch("scan look-back");
+}
+
+// Gate mode fixes the clamp / rounding semantics at compile time (both or neither); the
+// decay / update mode reads them.
+template <int DT, int OUT_DT, int MODE>
+int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
+  if constexpr (MODE == 1) {
+    if (a.clamp) return run_scan_lb_cr<DT, OUT_DT, MODE, 1>(a, T, summ, flags, st);
+    return run_scan_lb_cr<DT, OUT_DT, MODE, 0>(a, T, summ, flags, st);
+  } else {
+    return run_scan_lb_cr<DT, OUT_DT, MODE, 2>(a, T, summ, flags, st);
+  }
 }
 
 template <int DT, int OUT_DT, int MODE, int TM, int CPT>
@@ -648,8 +664,11 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   if (a.B == 0 || a.L == 0) return kOk;
   TESM_REQUIRE(a.decay && a.update && a.states, kErrInvalidArg, "scan: null pointer");
   TESM_REQUIRE(a.ld_decay >= a.C && a.ld_update >= a.C && a.ld_states >= a.C, kErrInvalidArg, "scan: ld < C");
-  if (a.mode == 1)
+  if (a.mode == 1) {
     TESM_REQUIRE(a.sv && a.decay_bias && a.ld_sv >= a.C, kErrInvalidArg, "scan mode 1: need sv and decay_bias");
+    TESM_REQUIRE((a.clamp != 0) == (a.round_update != 0), kErrUnsupported,
+                 "scan mode 1: clamp and round_update must agree (SISO: both, MIMO: neither)");
+  }
   const int64_t need = scan_ws_bytes(a.B, a.L, a.C, a.cs);
   TESM_REQUIRE(ws && ws_bytes >= need, kErrWorkspace, "scan: workspace too small");
   const int64_t T = scan_chunk_len(a.L, a.cs);

@@ -135,7 +135,7 @@ def test_cfg2_scan_at_size(dtype):
         states, hf = hip_ops.scan(decay.to(DEV), update.to(DEV), 16)
         torch.cuda.synchronize()
     dc = DT_CODE[dtype]
-    assert _has(log.kernels, f"scan_lb_kernel<{dc},{dc},0,16,4>"), log.kernels
+    assert _has(log.kernels, f"scan_lb_kernel<{dc},{dc},0,16,4,2>"), log.kernels
     ref = _cfg2_oracle_module(dtype, bias)
     with torch.no_grad():
         sr = ref._parallel_state_scan(decay, update)
@@ -215,7 +215,7 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
         # the benchmarked in_proj instantiation (128x256 tiles, three direct-to-LDS stages) and the
         # single-pass scan with the gates fused and eight sub-spans per workgroup
         assert _has(log.kernels, f"mfma32_kernel<2,4,2,2,0,{dc},3>"), log.kernels
-    assert _has(log.kernels, f"scan_lb_kernel<{dc},{dc},1,16,8>"), log.kernels
+    assert _has(log.kernels, f"scan_lb_kernel<{dc},{dc},1,16,8,1>"), log.kernels
     assert _has(log.kernels, "ent_fused_kernel<") or _has(log.kernels, "ent_scores_kernel<"), log.kernels
     err = assert_rows(to_np(y), to_np(yr), dtype, f"configs[3] {preset} y ({flips.summary()})")
     print(f"configs[3] {preset} {dtype}: worst row error {err:.3g}; {flips.summary()}")
@@ -293,7 +293,7 @@ def test_cfg4_mimo_long_vs_oracle(dtype):
         yr, fr = ref(u)
         uninstall(ref)
     dc = DT_CODE[dtype]
-    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,1,16,8>"), log.kernels
+    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,1,16,8,0>"), log.kernels
     assert _has(log.kernels, f"mimo_mix_kernel<{dc},true,64>"), log.kernels
     assert _has(log.kernels, f"ent_scores_mimo_kernel<{dc}>"), log.kernels
     assert_rows(to_np(y), to_np(yr), dtype, f"configs[4]-shaped MIMO L1100 ({flips.summary()})")
@@ -320,7 +320,7 @@ def test_cfg4_mimo_full_size():
             y, f = m(u.to(DEV))
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
-    for k in ("mfma32_kernel<2,4,2,2,0,1,3>", "mfma32_kernel<2,4,2,2,1,1,3>", "scan_lb_kernel<1,0,1,16,8>",
+    for k in ("mfma32_kernel<2,4,2,2,0,1,3>", "mfma32_kernel<2,4,2,2,1,1,3>", "scan_lb_kernel<1,0,1,16,8,0>",
               "mimo_mix_kernel<1,true,64>", "ent_scores_mimo_kernel<1>"):
         assert _has(log.kernels, k), (k, log.kernels)
     # the oracle on the causal prefix, fed the device's decisions (and, bf16, states and tanh(E) / C) for

@@ -53,7 +53,7 @@ def test_scan_give_up_sets_status_word():
             torch.cuda.synchronize()
     finally:
         hip_ops.debug_scan_spin_limit(1 << 20)
-    assert any(k.startswith("scan_lb_kernel<0,0,0,16,8>") for k in log.kernels), log.kernels
+    assert any(k.startswith("scan_lb_kernel<0,0,0,16,8,2>") for k in log.kernels), log.kernels
     assert hip_ops.device_status(clear=True) & 1
     st = st.cpu()
     span = 8 * 16                                  # eight 16-position sub-spans per workgroup
