@@ -337,99 +337,182 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
   const int rows = kFusedTP + W - 1;
   const int64_t tk0 = t0 - (W - 1);  // position of key row 0
 
-  // 1. RoPE'd keys and queries (tesm.py:783-793, 1209-1218).  Rows go over waves, RoPE pairs over
-  //    lanes; each wave loads kBatch rows (clamped into [0, L)) before it writes any of them, so the
-  //    loads of a batch are in flight together.
-  constexpr int kBatch = 8;
-  for (int c = lane; c < half; c += 64) {
-    for (int r0 = wave; r0 < rows; r0 += 4 * kBatch) {
-      float xa[kBatch], xb[kBatch];
-      float2 cs[kBatch];
-#pragma unroll
-      for (int bi = 0; bi < kBatch; ++bi) {
-        int64_t tt = tk0 + r0 + 4 * bi;
-        tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
-        const int64_t ko = (b * a.L + tt) * a.ld_k;
-        xa[bi] = ld<DT>(a.k, ko + c);
-        xb[bi] = ld<DT>(a.k, ko + half + c);
-        cs[bi] = a.rope[tt * half + c];
-      }
-#pragma unroll
-      for (int bi = 0; bi < kBatch; ++bi) {
-        const int r = r0 + 4 * bi;
-        if (r >= rows) break;
-        const int64_t tt = tk0 + r;
-        float o1 = 0.0f, o2 = 0.0f;
-        if (tt >= 0 && tt < a.L) rope_pair<DT>(xa[bi], xb[bi], cs[bi], o1, o2);
-        kr[r * krs + c] = o1;
-        kr[r * krs + half + c] = o2;
-      }
-    }
-    {
-      float xa[4], xb[4], qa[4], qb[4];
-      float2 cs[4];
-#pragma unroll
-      for (int bi = 0; bi < 4; ++bi) {  // kFusedTP / 4 rows per wave
-        const int pp = wave + 4 * bi;
-        const int64_t tt = (t0 + pp < a.L) ? t0 + pp : a.L - 1;
-        const int64_t qo = (b * a.L + tt) * a.ld_q;
-        xa[bi] = ld<DT>(a.q, qo + c);
-        xb[bi] = ld<DT>(a.q, qo + half + c);
-        cs[bi] = a.rope[tt * half + c];
-        if (a.q_add) {
-          const int64_t ao = (b * a.L + tt) * a.ld_qadd;
-          qa[bi] = ld<DT>(a.q_add, ao + c);
-          qb[bi] = ld<DT>(a.q_add, ao + half + c);
-        }
-      }
-#pragma unroll
-      for (int bi = 0; bi < 4; ++bi) {
-        const int pp = wave + 4 * bi;
-        float o1 = 0.0f, o2 = 0.0f;
-        if (t0 + pp < a.L) {
-          rope_pair<DT>(xa[bi], xb[bi], cs[bi], o1, o2);
-          if (a.q_add) {
-            o1 = rnd<DT>(o1 + qa[bi]);
-            o2 = rnd<DT>(o2 + qb[bi]);
-          }
-        }
-        qr[pp * krs + c] = o1;
-        qr[pp * krs + half + c] = o2;
-      }
-    }
-  }
-  // 2. state halo rows in the raw dtype, channels padded with zeros to a multiple of 16
   const T* S = static_cast<const T*>(a.S);
   constexpr int kVec = 16 / sizeof(T);
   const bool vec = (D % kVec) == 0 && (a.ld_s % kVec) == 0 && (reinterpret_cast<uintptr_t>(S) % 16) == 0;
-  if (vec) {
-    for (int c = lane * kVec; c < dp; c += 64 * kVec) {
+  // Single-issue path: when the tile's keys, queries and state halo fit kKPT / kQPT / kSPT items per
+  // thread, every global operand is requested before any is used (one memory round trip per tile),
+  // items numbered flat over the workgroup so that all lanes take part.
+  constexpr int kKPT = 4, kQPT = 2, kSPT = 4;
+  const int nvec = dp / kVec;
+  if (vec && rows * half <= 256 * kKPT && kFusedTP * half <= 256 * kQPT && rows * nvec <= 256 * kSPT) {
+    float kxa[kKPT], kxb[kKPT], qxa[kQPT], qxb[kQPT], qaa[kQPT], qab[kQPT];
+    float2 kcs[kKPT], qcs[kQPT];
+    v4i sv[kSPT];
+#pragma unroll
+    for (int k = 0; k < kSPT; ++k) {
+      const int i = tid + 256 * k;
+      const int r = i / nvec, c = (i - r * nvec) * kVec;
       const int cc = c < D ? c : D - kVec;
+      int64_t tt = tk0 + (r < rows ? r : rows - 1);
+      tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
+      sv[k] = *reinterpret_cast<const v4i*>(S + (b * a.L + tt) * a.ld_s + cc);
+    }
+#pragma unroll
+    for (int k = 0; k < kKPT; ++k) {
+      const int i = tid + 256 * k;
+      const int r = i / half, c = i - r * half;
+      int64_t tt = tk0 + (r < rows ? r : rows - 1);
+      tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
+      const int64_t ko = (b * a.L + tt) * a.ld_k;
+      kxa[k] = ld<DT>(a.k, ko + c);
+      kxb[k] = ld<DT>(a.k, ko + half + c);
+      kcs[k] = a.rope[tt * half + c];
+    }
+#pragma unroll
+    for (int k = 0; k < kQPT; ++k) {
+      const int i = tid + 256 * k;
+      const int pp = i / half, c = i - pp * half;
+      const int64_t tt = (t0 + pp < a.L) ? t0 + pp : a.L - 1;
+      const int64_t qo = (b * a.L + tt) * a.ld_q;
+      qxa[k] = ld<DT>(a.q, qo + c);
+      qxb[k] = ld<DT>(a.q, qo + half + c);
+      qcs[k] = a.rope[tt * half + c];
+      qaa[k] = qab[k] = 0.0f;
+      if (a.q_add) {
+        const int64_t ao = (b * a.L + tt) * a.ld_qadd;
+        qaa[k] = ld<DT>(a.q_add, ao + c);
+        qab[k] = ld<DT>(a.q_add, ao + half + c);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSPT; ++k) {
+      const int i = tid + 256 * k;
+      const int r = i / nvec, c = (i - r * nvec) * kVec;
+      if (r >= rows) break;
+      const int64_t tt = tk0 + r;
+      const bool ok = tt >= 0 && tt < a.L && c < D;
+      *reinterpret_cast<v4i*>(sx + static_cast<int64_t>(r) * dp + c) = ok ? sv[k] : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int k = 0; k < kKPT; ++k) {
+      const int i = tid + 256 * k;
+      const int r = i / half, c = i - r * half;
+      if (r >= rows) break;
+      const int64_t tt = tk0 + r;
+      float o1 = 0.0f, o2 = 0.0f;
+      if (tt >= 0 && tt < a.L) rope_pair<DT>(kxa[k], kxb[k], kcs[k], o1, o2);
+      kr[r * krs + c] = o1;
+      kr[r * krs + half + c] = o2;
+    }
+#pragma unroll
+    for (int k = 0; k < kQPT; ++k) {
+      const int i = tid + 256 * k;
+      const int pp = i / half, c = i - pp * half;
+      if (pp >= kFusedTP) break;
+      float o1 = 0.0f, o2 = 0.0f;
+      if (t0 + pp < a.L) {
+        rope_pair<DT>(qxa[k], qxb[k], qcs[k], o1, o2);
+        if (a.q_add) {
+          o1 = rnd<DT>(o1 + qaa[k]);
+          o2 = rnd<DT>(o2 + qab[k]);
+        }
+      }
+      qr[pp * krs + c] = o1;
+      qr[pp * krs + half + c] = o2;
+    }
+  } else {
+    // 1. RoPE'd keys and queries (tesm.py:783-793, 1209-1218).  Rows go over waves, RoPE pairs over
+    //    lanes; each wave loads kBatch rows (clamped into [0, L)) before it writes any of them, so the
+    //    loads of a batch are in flight together.
+    constexpr int kBatch = 8;
+    for (int c = lane; c < half; c += 64) {
       for (int r0 = wave; r0 < rows; r0 += 4 * kBatch) {
-        v4i v[kBatch];
+        float xa[kBatch], xb[kBatch];
+        float2 cs[kBatch];
 #pragma unroll
         for (int bi = 0; bi < kBatch; ++bi) {
           int64_t tt = tk0 + r0 + 4 * bi;
           tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
-          v[bi] = *reinterpret_cast<const v4i*>(S + (b * a.L + tt) * a.ld_s + cc);
+          const int64_t ko = (b * a.L + tt) * a.ld_k;
+          xa[bi] = ld<DT>(a.k, ko + c);
+          xb[bi] = ld<DT>(a.k, ko + half + c);
+          cs[bi] = a.rope[tt * half + c];
         }
 #pragma unroll
         for (int bi = 0; bi < kBatch; ++bi) {
           const int r = r0 + 4 * bi;
           if (r >= rows) break;
           const int64_t tt = tk0 + r;
-          const bool ok = tt >= 0 && tt < a.L && c < D;
-          *reinterpret_cast<v4i*>(sx + static_cast<int64_t>(r) * dp + c) = ok ? v[bi] : v4i{0, 0, 0, 0};
+          float o1 = 0.0f, o2 = 0.0f;
+          if (tt >= 0 && tt < a.L) rope_pair<DT>(xa[bi], xb[bi], cs[bi], o1, o2);
+          kr[r * krs + c] = o1;
+          kr[r * krs + half + c] = o2;
+        }
+      }
+      {
+        float xa[4], xb[4], qa[4], qb[4];
+        float2 cs[4];
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi) {  // kFusedTP / 4 rows per wave
+          const int pp = wave + 4 * bi;
+          const int64_t tt = (t0 + pp < a.L) ? t0 + pp : a.L - 1;
+          const int64_t qo = (b * a.L + tt) * a.ld_q;
+          xa[bi] = ld<DT>(a.q, qo + c);
+          xb[bi] = ld<DT>(a.q, qo + half + c);
+          cs[bi] = a.rope[tt * half + c];
+          if (a.q_add) {
+            const int64_t ao = (b * a.L + tt) * a.ld_qadd;
+            qa[bi] = ld<DT>(a.q_add, ao + c);
+            qb[bi] = ld<DT>(a.q_add, ao + half + c);
+          }
+        }
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi) {
+          const int pp = wave + 4 * bi;
+          float o1 = 0.0f, o2 = 0.0f;
+          if (t0 + pp < a.L) {
+            rope_pair<DT>(xa[bi], xb[bi], cs[bi], o1, o2);
+            if (a.q_add) {
+              o1 = rnd<DT>(o1 + qa[bi]);
+              o2 = rnd<DT>(o2 + qb[bi]);
+            }
+          }
+          qr[pp * krs + c] = o1;
+          qr[pp * krs + half + c] = o2;
         }
       }
     }
-  } else {
-    for (int r = wave; r < rows; r += 4) {
-      const int64_t tt = tk0 + r;
-      const bool ok = tt >= 0 && tt < a.L;
-      const T* src = S + (b * a.L + tt) * a.ld_s;
-      T* dst = sx + static_cast<int64_t>(r) * dp;
-      for (int c = lane; c < dp; c += 64) dst[c] = (ok && c < D) ? src[c] : T(0);
+    // 2. state halo rows in the raw dtype, channels padded with zeros to a multiple of 16
+    if (vec) {
+      for (int c = lane * kVec; c < dp; c += 64 * kVec) {
+        const int cc = c < D ? c : D - kVec;
+        for (int r0 = wave; r0 < rows; r0 += 4 * kBatch) {
+          v4i v[kBatch];
+#pragma unroll
+          for (int bi = 0; bi < kBatch; ++bi) {
+            int64_t tt = tk0 + r0 + 4 * bi;
+            tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
+            v[bi] = *reinterpret_cast<const v4i*>(S + (b * a.L + tt) * a.ld_s + cc);
+          }
+#pragma unroll
+          for (int bi = 0; bi < kBatch; ++bi) {
+            const int r = r0 + 4 * bi;
+            if (r >= rows) break;
+            const int64_t tt = tk0 + r;
+            const bool ok = tt >= 0 && tt < a.L && c < D;
+            *reinterpret_cast<v4i*>(sx + static_cast<int64_t>(r) * dp + c) = ok ? v[bi] : v4i{0, 0, 0, 0};
+          }
+        }
+      }
+    } else {
+      for (int r = wave; r < rows; r += 4) {
+        const int64_t tt = tk0 + r;
+        const bool ok = tt >= 0 && tt < a.L;
+        const T* src = S + (b * a.L + tt) * a.ld_s;
+        T* dst = sx + static_cast<int64_t>(r) * dp;
+        for (int c = lane; c < dp; c += 64) dst[c] = (ok && c < D) ? src[c] : T(0);
+      }
     }
   }
   __syncthreads();
