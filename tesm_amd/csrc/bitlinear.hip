@@ -1864,9 +1864,22 @@ int dispatch_dual(const LinearArgs& a, hipStream_t st) {
   return run_mfma32<1, 4, 2, 1, EPI>(a, st);
 }
 
+// LDS of one fused-quantization workgroup: 16 TM code rows of Kp + 16 bytes with their scales and sums
+// (dynamic), and skinny_body's static split-K reduction buffer (three waves' TM partial tiles, 16 bytes
+// per lane each).
+static int64_t linear_fq_lds_bytes(int64_t M, int64_t Kp) {
+  const int64_t TM = M <= 16 ? 1 : 2;
+  return 16 * TM * (Kp + 16) + 16 * TM * 8 + 3 * TM * 64 * 16;
+}
+
+// Kp <= 1920 keeps a workgroup at most 68 KB of LDS; the device's per-workgroup limit is checked too (a
+// build for a target with less LDS takes the two-launch path).
 bool linear_fq_ok(const LinearArgs& a) {
-  return a.epilogue == kEpiStore && a.M > 4 && a.M <= 32 && a.N >= 1 && a.N < 16384 && a.Kp >= kKTile &&
-         a.Kp % kKTile == 0 && a.Kp <= 1920;  // LDS: 32 rows of Kp + 16 bytes within 64 KB
+  if (!(a.epilogue == kEpiStore && a.M > 4 && a.M <= 32 && a.N >= 1 && a.N < 16384 && a.Kp >= kKTile &&
+        a.Kp % kKTile == 0 && a.Kp <= 1920))
+    return false;
+  const DeviceLimits dl = device_limits();
+  return dl.lds > 0 && linear_fq_lds_bytes(a.M, a.Kp) <= dl.lds;
 }
 
 namespace {
