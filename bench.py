@@ -47,7 +47,8 @@ def parse():
                    help="time every config's CPU baseline (configs[1]-[4], the MIMO layer at L 1024/2048/4096) at "
                         "the affinity core count and on one thread, print their JSON and exit (slow)")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
-    p.add_argument("--workload", default="all", choices=["all", "layer", "decode", "mimo", "global", "lm", "base"],
+    p.add_argument("--workload", default="all",
+                   choices=["all", "layer", "decode", "mimo", "global", "lm", "base", "kernels"],
                    help="run one measurement alone and print its JSON (for per-workload profiles)")
     p.add_argument("--copy-calib", action="store_true",
                    help="run one 256 MiB device-to-device copy first (a known-size reference for "
@@ -517,10 +518,10 @@ def main():
     m = TESM_SISO(**LAYER).to(dev).to(torch.bfloat16).eval()
     u = torch.randn(B, L, LAYER["d_model"], generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
 
-    if args.copy_calib:
+    if args.copy_calib:  # a known-size plain copy (256 MiB read, 256 MiB written) for the counter runs
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        hip_ops.stream_copy(dst, src)
         torch.cuda.synchronize()
         del src, dst
     if args.workload != "all":
@@ -544,6 +545,8 @@ def main():
                 res = measure_global(torch)
             elif args.workload == "base":
                 res = measure_true_base(torch)
+            elif args.workload == "kernels":
+                res = measure_kernels(torch, args.only)
             else:
                 res = measure_lm(torch)
         print(json.dumps({"workload": args.workload, "result": res}))
