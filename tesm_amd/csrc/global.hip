@@ -193,24 +193,43 @@ __global__ __launch_bounds__(256) void global_scores_kernel(GlobalArgs a, const 
   if (h == 0 && cnt) atomicAdd(a.count + b * a.L + i, cnt);
 }
 
-// bf16 states (b, t, c) -> transposed copy (b, c, key) with pitch ldst, keys L .. ldst-1 zero.
+// bf16 states (b, t, c) -> transposed copy (b, c, key) with pitch ldst, keys L .. ldst-1 zero.  A 64-key x
+// 64-channel tile goes through LDS; where the rows allow (16-byte aligned, C % 8 == 0) each thread reads
+// 8 channels of one key and writes 8 keys of one channel with single 16-byte accesses.
 __global__ __launch_bounds__(256) void global_transpose_kernel(const uint16_t* __restrict__ S, int64_t ld_s,
                                                                int64_t L, int64_t C, uint16_t* __restrict__ s_t,
                                                                int64_t ldst) {
-  __shared__ uint16_t t[64][64 + 2];
+  __shared__ uint16_t t[64][64 + 8];  // [channel][key]; rows of 144 bytes keep 16-byte reads aligned
   const int64_t k0 = static_cast<int64_t>(blockIdx.x) * 64, c0 = static_cast<int64_t>(blockIdx.y) * 64;
   const int64_t b = blockIdx.z;
   const int tid = threadIdx.x;
-  for (int e = tid; e < 64 * 64; e += 256) {
-    const int r = e >> 6, c = e & 63;  // r: key, c: channel
-    const int64_t k = k0 + r, ch = c0 + c;
-    t[c][r] = (k < L && ch < C) ? S[(b * L + k) * ld_s + ch] : uint16_t(0);
+  const bool vec = (C % 8) == 0 && (ld_s % 8) == 0 && (reinterpret_cast<uintptr_t>(S) % 16) == 0;
+  if (vec) {
+#pragma unroll
+    for (int e = tid; e < 64 * 8; e += 256) {
+      const int r = e >> 3, c = 8 * (e & 7);  // r: key, c: first of 8 channels
+      const int64_t k = k0 + r, ch = c0 + c;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (k < L && ch < C) v = *reinterpret_cast<const uint4*>(S + (b * L + k) * ld_s + ch);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[c + i][r] = static_cast<uint16_t>(w[i >> 1] >> (16 * (i & 1)));
+    }
+  } else {
+    for (int e = tid; e < 64 * 64; e += 256) {
+      const int r = e >> 6, c = e & 63;
+      const int64_t k = k0 + r, ch = c0 + c;
+      t[c][r] = (k < L && ch < C) ? S[(b * L + k) * ld_s + ch] : uint16_t(0);
+    }
   }
   __syncthreads();
-  for (int e = tid; e < 64 * 64; e += 256) {
-    const int r = e >> 6, k = e & 63;  // r: channel
+  // ldst is a multiple of 64 and the copy's base 256-byte aligned: rows of the copy take 16-byte stores
+#pragma unroll
+  for (int e = tid; e < 64 * 8; e += 256) {
+    const int r = e >> 3, k = 8 * (e & 7);  // r: channel, k: first of 8 keys
     const int64_t ch = c0 + r;
-    if (ch < C) s_t[(b * C + ch) * ldst + k0 + k] = t[r][k];
+    if (ch < C)
+      *reinterpret_cast<uint4*>(s_t + (b * C + ch) * ldst + k0 + k) = *reinterpret_cast<const uint4*>(&t[r][k]);
   }
 }
 
