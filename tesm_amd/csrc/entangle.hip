@@ -320,7 +320,8 @@ __device__ __forceinline__ void lds_row16(const void* base, float (&x)[16]) {
   }
 }
 
-template <int DT>
+// SI: items per thread of the single-issue load path (keys and state vectors; queries SI / 2).
+template <int DT, int SI>
 __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff, FusedLds f) {
   using T = typename Elem<DT>::T;
   extern __shared__ __attribute__((aligned(16))) char lds_fused[];
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
   // Single-issue path: when the tile's keys, queries and state halo fit kKPT / kQPT / kSPT items per
   // thread, every global operand is requested before any is used (one memory round trip per tile),
   // items numbered flat over the workgroup so that all lanes take part.
-  constexpr int kKPT = 4, kQPT = 2, kSPT = 4;
+  constexpr int kKPT = SI, kQPT = SI / 2, kSPT = SI;
   const int nvec = dp / kVec;
   if (vec && rows * half <= 256 * kKPT && kFusedTP * half <= 256 * kQPT && rows * nvec <= 256 * kSPT) {
     float kxa[kKPT], kxb[kKPT], qxa[kQPT], qxb[kQPT], qaa[kQPT], qab[kQPT];
@@ -738,12 +739,27 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
     TESM_REQUIRE(a.q_c && a.s_te && a.s_c && a.rs_te && a.rs_c && a.ldq >= a.D && a.ldq % 16 == 0 &&
                      aligned(a.q_te, 16) && aligned(a.q_c, 16),
                  kErrInvalidArg, "local_ent: bad quantized outputs");
-    const FusedLds f = fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4);
+    const int esz = a.dt == kBF16 ? 2 : 4;
+    const FusedLds f = fused_lds(a.R, a.D, weff, esz);
     dim3 grid(static_cast<unsigned>((a.L + kFusedTP - 1) / kFusedTP), static_cast<unsigned>(a.B));
-    if (a.dt == kBF16)
-      ent_fused_kernel<kBF16><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16>)>>>(a, weff, f);
-    else
-      ent_fused_kernel<kF32><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kF32>)>>>(a, weff, f);
+    // the single-issue load path's capacity: 4 key / state items per thread up to window 16 at the
+    // base shape, 8 beyond (the kernel falls back to its loops where neither fits)
+    const int64_t rows = kFusedTP + weff - 1, half = a.R / 2, nvec = f.dp / (16 / esz);
+    auto fits = [&](int64_t si) {
+      return rows * half <= 256 * si && kFusedTP * half <= 256 * (si / 2) && rows * nvec <= 256 * si;
+    };
+    const bool big = !fits(4) && fits(8);
+    if (a.dt == kBF16) {
+      if (big)
+        ent_fused_kernel<kBF16, 8><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16, 8>)>>>(a, weff, f);
+      else
+        ent_fused_kernel<kBF16, 4><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16, 4>)>>>(a, weff, f);
+    } else {
+      if (big)
+        ent_fused_kernel<kF32, 8><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kF32, 8>)>>>(a, weff, f);
+      else
+        ent_fused_kernel<kF32, 4><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kF32, 4>)>>>(a, weff, f);
+    }
     return check_launch("entanglement fused");
   }
   int rc;
