@@ -358,6 +358,127 @@ __device__ __forceinline__ float dual_epi(float p0, float p1, float local, float
 // General epilogue of the 16 x 16 tiles of one wave (tile rows wm*TM.., columns wn*TN..): scale the
 // exact accumulators, optional bias / accumulator dump, or the output gate
 // y = local + sigmoid(gate) * state_proj + ent_proj in the module dtype's op order.
+// Raw bits of one element: bf16 zero-extended, f32 as is (converted where used, so a load issued
+// early is not waited for until its value is needed).
+template <int DT>
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i) {
+  if constexpr (DT == kBF16)
+    return static_cast<const uint16_t*>(p)[i];
+  else
+    return static_cast<const uint32_t*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float from_bits(uint32_t b) {
+  return __uint_as_float(DT == kBF16 ? b << 16 : b);
+}
+
+// Operands of one 16·TM × 16·TN epilogue tile (activation scales and code sums, weight scales, bias,
+// output-gate inputs) for the split-K kernels, read in straight-line code with rows and columns clamped into range (values
+// at clamped positions are never stored), so they are all in flight together and can be issued
+// before the K loop.
+template <int TM, int TN, int EPI, int OUT_DT>
+struct Epi16In {
+  float sx0[TM], sx1[TM];  // activation scales and code sums of the lane's rows
+  int32_t rs0[TM], rs1[TM];
+  float cw0[TN][4], cw1[TN][4];
+  uint32_t bias[TN][4];
+  uint32_t lo[TM][TN][4], gt[TM][TN][4];
+};
+
+template <int TM, int TN, int EPI, int OUT_DT>
+__device__ __forceinline__ void epi16_load(const LinearArgs& a, Epi16In<TM, TN, EPI, OUT_DT>& e, int64_t m0,
+                                           int64_t n0, int lane) {
+  const LinearOperand& o0 = a.op[0];
+  const LinearOperand& o1 = a.op[1];
+  const void* bias = a.bias ? a.bias : static_cast<const void*>(o0.c_w);  // no bias: a valid dummy address
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t nb = n0 + j * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = nb + r < a.N ? nb + r : a.N - 1;
+      e.cw0[j][r] = o0.c_w[o0.c_w_per_row ? n : 0];
+      if constexpr (epi_dual(EPI)) e.cw1[j][r] = o1.c_w[o1.c_w_per_row ? n : 0];
+      if constexpr (EPI == kEpiStore) e.bias[j][r] = ld_bits<OUT_DT>(bias, a.bias ? n : 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + i * 16 + (lane & 15), mc = m < a.M ? m : a.M - 1;
+    e.sx0[i] = o0.s_x[mc];
+    e.rs0[i] = o0.rowsum[mc];
+    if constexpr (epi_dual(EPI)) {
+      e.sx1[i] = o1.s_x[mc];
+      e.rs1[i] = o1.rowsum[mc];
+    }
+  }
+  if constexpr (EPI == kEpiOutputGate) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = m0 + i * 16 + (lane & 15), mc = m < a.M ? m : a.M - 1;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t nb = n0 + j * 16 + 4 * (lane >> 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t n = nb + r < a.N ? nb + r : a.N - 1;
+          e.lo[i][j][r] = ld_bits<OUT_DT>(a.local, mc * a.ld_local + n);
+          e.gt[i][j][r] = ld_bits<OUT_DT>(a.gate, mc * a.ld_gate + n);
+        }
+      }
+    }
+  }
+}
+
+// The split-K kernels' epilogue (one wave owns the whole tile) on operands read by epi16_load.
+template <int TM, int TN, int EPI, int OUT_DT>
+__device__ __forceinline__ void epilogue16_pre(const LinearArgs& a, const v4i (&acc0)[TM][TN],
+                                               const v4i (&acc1)[TM][TN], const Epi16In<TM, TN, EPI, OUT_DT>& e,
+                                               int64_t m0, int64_t n0, int lane) {
+  const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m0 + i * 16 + (lane & 15);
+    if (m >= a.M) continue;
+    const float inv0 = 1.0f / e.sx0[i];
+    const int32_t rs0 = e.rs0[i];
+    float inv1 = 0.0f;
+    int32_t rs1 = 0;
+    if constexpr (epi_dual(EPI)) {
+      inv1 = 1.0f / e.sx1[i];
+      rs1 = e.rs1[i];
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t nb = n0 + j * 16 + 4 * (lane >> 4);
+      if (nb >= a.N) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = nb + r;
+        const int32_t a0 = acc0[i][j][r] - rs0;
+        if (a.acc_dump && n < a.N) a.acc_dump[m * a.N + n] = a0;
+        const float v0 = (static_cast<float>(a0) * inv0) * e.cw0[j][r];
+        if constexpr (EPI == kEpiStore) {
+          v[r] = a.bias ? v0 + from_bits<OUT_DT>(e.bias[j][r]) : v0;
+        } else {
+          const float v1 = rnd<OUT_DT>((static_cast<float>(acc1[i][j][r] - rs1) * inv1) * e.cw1[j][r]);
+          if constexpr (EPI == kEpiOutputGate)
+            v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, from_bits<OUT_DT>(e.lo[i][j][r]),
+                                         from_bits<OUT_DT>(e.gt[i][j][r]));
+          else
+            v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, 0.0f, 0.0f);
+        }
+      }
+      if (nb + 3 < a.N) {
+        store4<OUT_DT>(a.out, m * a.ldo + nb, v, vout);
+      } else {
+        for (int r = 0; r < 4 && nb + r < a.N; ++r) st<OUT_DT>(a.out, m * a.ldo + nb + r, v[r]);
+      }
+    }
+  }
+}
+
 template <int TM, int TN, int EPI, int OUT_DT>
 __device__ __forceinline__ void epilogue16(const LinearArgs& a, const v4i (&acc0)[TM][TN], const v4i (&acc1)[TM][TN],
                                            int64_t m0, int64_t n0, int wm, int wn, int lane) {
@@ -570,7 +691,9 @@ template <int NW, int TM, int TN, int EPI, int OUT_DT>
 __device__ __forceinline__ void skinny_body(const LinearArgs& a, int64_t m0, int64_t n0) {
   constexpr int NOP = epi_dual(EPI) ? 2 : 1;
   __shared__ v4i red[(NW - 1) * NOP * TM * TN * 64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Epi16In<TM, TN, EPI, OUT_DT> ein;  // wave 0's epilogue operands, in flight during the K loop
+  if (w == 0) epi16_load<TM, TN, EPI, OUT_DT>(a, ein, m0, n0, lane);
   v4i acc0[TM][TN], acc1[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -600,7 +723,7 @@ __device__ __forceinline__ void skinny_body(const LinearArgs& a, int64_t m0, int
         acc0[i][j] += red[(((src * NOP) * TM + i) * TN + j) * 64 + lane];
         if constexpr (NOP == 2) acc1[i][j] += red[(((src * NOP + 1) * TM + i) * TN + j) * 64 + lane];
       }
-  epilogue16<TM, TN, EPI, OUT_DT>(a, acc0, acc1, m0, n0, 0, 0, lane);
+  epilogue16_pre<TM, TN, EPI, OUT_DT>(a, acc0, acc1, ein, m0, n0, lane);
 }
 
 template <int NW, int TM, int TN, int EPI, int OUT_DT>
@@ -616,7 +739,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(LinearArgs a) {
 // tile repeats the quantization (a few KB of L2 reads each) in exchange for one launch fewer.  LDS
 // rows are Kp + 16 bytes apart, so the 16 rows a K-step reads fall on distinct banks.
 // G > 0: a lane's at most G groups stay in registers between the amax and the code pass (one read
-// of the row); G == 0: the row is read twice.
+// of the row, all loads issued before the first use; needs VEC rows with K % 16 == 0); G == 0: the
+// row is read twice.
 template <int NW, int TM, int TN, int OUT_DT, int DT, bool VEC, int G>
 __global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQuantIn f) {
   extern __shared__ __attribute__((aligned(16))) char lds_fq[];
@@ -632,34 +756,49 @@ __global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQ
     const int r = threadIdx.x / LPR, g0 = threadIdx.x % LPR;  // LPR consecutive lanes per row
     const int64_t m = m0 + r, ngroups = a.Kp / 16;
     int8_t* crow = codes + r * lstride;
-    if (m < a.M && G > 0) {
-      const int64_t base = m * f.ldx;
+    if (G > 0) {
+      // Straight-line code: the lane's G groups are loaded (16-byte loads, all issued before the first
+      // use) from row min(m, M - 1), groups past K re-reading the row's last group; both are zeroed
+      // or discarded below.  Needs 16-byte aligned rows and K % 16 == 0.
+      constexpr int NV = DT == kBF16 ? 2 : 4;  // 16-byte loads per 16-element group
+      const int64_t mc = m < a.M ? m : a.M - 1, nfull = f.K / 16;
+      const char* xr = static_cast<const char*>(f.x) + mc * f.ldx * (DT == kBF16 ? 2 : 4);
+      uint4 raw[G > 0 ? G : 1][NV];
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        const int64_t g = g0 + LPR * gi, gl = g < nfull ? g : nfull - 1;
+        const uint4* p = reinterpret_cast<const uint4*>(xr + gl * 16 * (DT == kBF16 ? 2 : 4));
+#pragma unroll
+        for (int q = 0; q < NV; ++q) raw[gi][q] = p[q];
+      }
       float v[G > 0 ? G : 1][16];
       float amax = 0.0f;
 #pragma unroll
       for (int gi = 0; gi < G; ++gi) {
-        const int64_t g = g0 + LPR * gi;
-        if (g < ngroups) {
-          load_group<DT, VEC>(f.x, base, f.K, g, v[gi]);
-        } else {
+        const bool in = g0 + LPR * gi < nfull;
+        const uint32_t* wd = reinterpret_cast<const uint32_t*>(&raw[gi][0]);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) v[gi][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+          const float x = DT == kBF16 ? __uint_as_float(i % 2 == 0 ? wd[i / 2] << 16 : wd[i / 2] & 0xffff0000u)
+                                      : __uint_as_float(wd[i]);
+          v[gi][i] = in ? x : 0.0f;
+          amax = fmaxf(amax, fabsf(v[gi][i]));
         }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[gi][i]));
       }
       amax = wave_max<LPR>(amax);
+      const bool live = m < a.M;  // rows past M: zero codes, scale 1, sum 0
       const float sc = act_scale<DT>(amax, f.eps);
       int32_t rs = 0;
 #pragma unroll
       for (int gi = 0; gi < G; ++gi) {
         const int64_t g = g0 + LPR * gi;
-        if (g < ngroups) *reinterpret_cast<uint4*>(crow + 16 * g) = group_codes<DT>(v[gi], sc, 1, rs);
+        const uint4 c = group_codes<DT>(v[gi], sc, 1, rs);
+        if (g < ngroups) *reinterpret_cast<uint4*>(crow + 16 * g) = live ? c : make_uint4(0, 0, 0, 0);
       }
       rs = wave_sum_i<LPR>(rs);
       if (g0 == 0) {
-        sc_l[r] = sc;
-        rs_l[r] = rs;
+        sc_l[r] = live ? sc : 1.0f;
+        rs_l[r] = live ? rs : 0;
       }
     } else if (m < a.M) {
       const int64_t base = m * f.ldx;
@@ -1894,17 +2033,23 @@ void run_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
 }
 template <int TM>
 void dispatch_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, bool vec, hipStream_t st) {
+  // groups per lane: Kp / 16 over 256 / (16 TM) lanes per row; the register-held variants (one read
+  // of the row, straight-line loads) need 16-byte aligned rows of whole 16-element groups
+  const int64_t gpl = (a.Kp / 16 + 256 / (16 * TM) - 1) / (256 / (16 * TM));
+  const bool held = vec && f.K % 16 == 0;
   if (f.dt == kBF16) {
-    if (vec) {
-      // groups per lane: Kp / 16 over 256 / (16 TM) lanes per row
-      const int64_t gpl = (a.Kp / 16 + 256 / (16 * TM) - 1) / (256 / (16 * TM));
+    if (held) {
       if (gpl <= 2) return run_skinny_fq<TM, kBF16, true, 2>(a, f, st);
       if (gpl <= 4) return run_skinny_fq<TM, kBF16, true, 4>(a, f, st);
       if (gpl <= 6) return run_skinny_fq<TM, kBF16, true, 6>(a, f, st);
       if (gpl <= 8) return run_skinny_fq<TM, kBF16, true, 8>(a, f, st);
-      return run_skinny_fq<TM, kBF16, true, 0>(a, f, st);
     }
+    if (vec) return run_skinny_fq<TM, kBF16, true, 0>(a, f, st);
     return run_skinny_fq<TM, kBF16, false, 0>(a, f, st);
+  }
+  if (held) {
+    if (gpl <= 2) return run_skinny_fq<TM, kF32, true, 2>(a, f, st);
+    if (gpl <= 4) return run_skinny_fq<TM, kF32, true, 4>(a, f, st);
   }
   if (vec) return run_skinny_fq<TM, kF32, true, 0>(a, f, st);
   return run_skinny_fq<TM, kF32, false, 0>(a, f, st);
