@@ -358,20 +358,6 @@ __device__ __forceinline__ float dual_epi(float p0, float p1, float local, float
 // General epilogue of the 16 x 16 tiles of one wave (tile rows wm*TM.., columns wn*TN..): scale the
 // exact accumulators, optional bias / accumulator dump, or the output gate
 // y = local + sigmoid(gate) * state_proj + ent_proj in the module dtype's op order.
-// Raw bits of one element: bf16 zero-extended, f32 as is (converted where used, so a load issued
-// early is not waited for until its value is needed).
-template <int DT>
-__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i) {
-  if constexpr (DT == kBF16)
-    return static_cast<const uint16_t*>(p)[i];
-  else
-    return static_cast<const uint32_t*>(p)[i];
-}
-template <int DT>
-__device__ __forceinline__ float from_bits(uint32_t b) {
-  return __uint_as_float(DT == kBF16 ? b << 16 : b);
-}
-
 // Operands of one 16·TM × 16·TN epilogue tile (activation scales and code sums, weight scales, bias,
 // output-gate inputs) for the split-K kernels, read in straight-line code with rows and columns clamped into range (values
 // at clamped positions are never stored), so they are all in flight together and can be issued

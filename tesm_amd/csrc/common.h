@@ -85,6 +85,21 @@ __device__ __forceinline__ void st(void* p, int64_t i, float v) {
   }
 }
 
+// Raw bits of one element: bf16 zero-extended, f32 as is.  Kernels that issue their loads early keep
+// the bits and convert where the value is used (from_bits), so no conversion forces a wait for the
+// load right after it is issued.
+template <int DT>
+__device__ __forceinline__ uint32_t ld_bits(const void* p, int64_t i) {
+  if constexpr (DT == kBF16)
+    return static_cast<const uint16_t*>(p)[i];
+  else
+    return static_cast<const uint32_t*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float from_bits(uint32_t b) {
+  return __uint_as_float(DT == kBF16 ? b << 16 : b);
+}
+
 // Four consecutive elements at p[i .. i+3] in one store; needs i*size 8-byte (bf16) / 16-byte (f32) aligned.
 template <int DT>
 __device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {

@@ -24,21 +24,33 @@ namespace {
 
 constexpr int kDecMaxCPT = 8;  // channels per thread: at most 2048 channels per workgroup
 
-// Four consecutive ring values at p[i .. i+3] (16-byte aligned for f32, 8-byte for bf16).
+// Raw bits of four consecutive ring values at p[i .. i+3] (16-byte aligned for f32, 8-byte for bf16):
+// f32 four words, bf16 two words of two values each (ring_val reads them back).
 template <int CDT>
-__device__ __forceinline__ void ld4v(const void* p, int64_t i, float (&v)[4]) {
+__device__ __forceinline__ void ld4_bits(const void* p, int64_t i, uint32_t (&r)[4]) {
   if constexpr (CDT == kBF16) {
     const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-    v[0] = __uint_as_float(w.x << 16);
-    v[1] = __uint_as_float(w.x & 0xffff0000u);
-    v[2] = __uint_as_float(w.y << 16);
-    v[3] = __uint_as_float(w.y & 0xffff0000u);
+    r[0] = w.x;
+    r[1] = w.y;
+    r[2] = 0;
+    r[3] = 0;
   } else {
-    const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
-    v[0] = f.x;
-    v[1] = f.y;
-    v[2] = f.z;
-    v[3] = f.w;
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const float*>(p) + i);
+    r[0] = w.x;
+    r[1] = w.y;
+    r[2] = w.z;
+    r[3] = w.w;
+  }
+}
+
+// Value e (0..3) of four ring values read by ld4_bits (vec) or as four single elements (ld_bits).
+template <int CDT>
+__device__ __forceinline__ float ring_val(const uint32_t (&r)[4], int e, bool vec) {
+  if constexpr (CDT == kBF16) {
+    if (vec) return __uint_as_float(e & 1 ? r[e >> 1] & 0xffff0000u : r[e >> 1] << 16);
+    return __uint_as_float(r[e] << 16);
+  } else {
+    return __uint_as_float(r[e]);
   }
 }
 
@@ -62,14 +74,14 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   const int R = static_cast<int>(a.R), W = static_cast<int>(a.W), CW = static_cast<int>(a.chunk);
   const int D = static_cast<int>(a.D);
   const int half = R / 2;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t b = blockIdx.x, h = blockIdx.y, H = a.H;
   const int c0 = static_cast<int>(blockIdx.z) * CW;
   const int cn = min(CW, D - c0);  // channels of this workgroup (>= 1)
   float* qv = lds_dec;       // R   RoPE'd query (+ cross query)
   float* kv = qv + R;        // R   RoPE'd key of this step
   float* nv = kv + R;        // CW  new state of this chunk in the layer dtype
-  float* wn = nv + CW;       // 64  ternary / norm per padded window position
+  float* wn = nv + CW;       // 64  window bias, then ternary / norm per padded window position
   float* red = wn + 64;      // 16  block reductions
   int* redi = reinterpret_cast<int*>(red + 8);
   float* mixp = red + 16;    // 4 x CW  per-wave partial mixes (CPT = 1)
@@ -92,60 +104,110 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
     return s >= W ? s - W : s;
   };
 
-  // 0. (CPT = 1) ring states of this thread's four channels at its window positions
+  // Ring slot the loads for window position w read: the position's slot, or for positions without a
+  // ring entry (padding, past W) and for this step's slot (its key and state come from LDS) another
+  // slot, so the loads need no branch and, with W > 1, never read the slot this step writes.
+  const int alt = W > 1 ? (slot + 1 == W ? 0 : slot + 1) : slot;
+  auto read_slot = [&](int w) -> int {
+    const int s = (w >= wlo && w < W) ? slot_of(w) : alt;
+    return s == slot ? alt : s;
+  };
+
+  // 0. Every global read of steps 1-4 (the last batches of window keys and, with CPT > 1, of ring
+  //    states aside) is issued here in straight-line code, indices clamped into range and values at
+  //    unused positions discarded, and converted where used: the workgroup waits for memory about
+  //    once instead of once per guarded load.
+  // 0a. (CPT = 1) ring states of this thread's four channels at its window positions
   const int j4 = 4 * lane;
-  float xs[CPT == 1 ? 16 : 1][4];
+  const bool vec = a.vec4 != 0;  // chunk widths are multiples of 4 and ring rows aligned
+  uint32_t xr[CPT == 1 ? 16 : 1][4];
   if constexpr (CPT == 1) {
+    if (vec) {
+      const int jc = min(j4, cn - 4);
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {  // W <= 64
-      const int w = wave + 4 * u;
-      const bool on = w < W && w >= wlo;
-      const int s = on ? slot_of(w) : slot;
+      for (int u = 0; u < 16; ++u) {  // W <= 64
+        const int w = wave + 4 * u;
+        if (w >= W) break;  // uniform in the wave
+        ld4_bits<CDT>(a.v_cache, vbase + static_cast<int64_t>(read_slot(w)) * vstep + jc, xr[u]);
+      }
+    } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) xs[u][r] = 0.0f;
-      if (on && s != slot) {
-        const int64_t vo = vbase + s * vstep + j4;
-        if (a.vec4 && j4 + 3 < cn) {
-          float v4[4];
-          ld4v<CDT>(a.v_cache, vo, v4);
+      for (int u = 0; u < 16; ++u) {
+        const int w = wave + 4 * u;
+        if (w >= W) break;
+        const int64_t vo = vbase + static_cast<int64_t>(read_slot(w)) * vstep;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) xs[u][r] = rnd<DT>(v4[r]);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (j4 + r < cn) xs[u][r] = rnd<DT>(ld<CDT>(a.v_cache, vo + r));
-        }
+        for (int r = 0; r < 4; ++r) xr[u][r] = ld_bits<CDT>(a.v_cache, vo + min(j4 + r, cn - 1));
       }
     }
   }
+  // 0b. RoPE inputs of element tid of each rank half (half <= 256)
+  const int ir = tid < half ? tid : half - 1;
+  const float2 rcs = a.rope[a.pos * half + ir];
+  const uint32_t bq1 = ld_bits<DT>(prow, o_q + ir), bq2 = ld_bits<DT>(prow, o_q + half + ir);
+  const uint32_t bk1 = ld_bits<DT>(prow, o_k + ir), bk2 = ld_bits<DT>(prow, o_k + half + ir);
+  const void* qadd = a.q_add ? a.q_add : a.proj;  // no cross query: a valid dummy address
+  const int64_t qo = a.q_add ? bh * a.ld_qadd : 0;
+  const uint32_t ba1 = ld_bits<DT>(qadd, qo + ir), ba2 = ld_bits<DT>(qadd, qo + half + ir);
+  const float wbv = wbias[tid < W ? tid : W - 1];  // window bias of position tid, parked in wn below
+  // 0c. gate inputs and float64 state of the thread's channels
+  uint32_t bdc[CPT], bdb[CPT], bwr[CPT], bsv[CPT];
+  double st64[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int j = tid + 256 * k, c = c0 + (j < cn ? j : cn - 1);
+    bdc[k] = ld_bits<DT>(prow, o_decay + c);
+    bdb[k] = ld_bits<DT>(a.decay_bias, h * a.D + c);
+    bwr[k] = ld_bits<DT>(prow, o_write + c);
+    bsv[k] = ld_bits<DT>(prow, o_sv + c);
+    st64[k] = a.state[bh * a.D + c];
+  }
+  // 0d. window keys of the wave's first four window positions (later batches in step 3)
+  uint32_t kb[4][2 * NI];
+  auto load_keys = [&](int j0) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int64_t ko = kbase + static_cast<int64_t>(read_slot(wave + 4 * (j0 + jj))) * kstep;
+#pragma unroll
+      for (int t = 0; t < NI; ++t) {
+        const int i = min(lane + 64 * t, half - 1);
+        kb[jj][2 * t] = ld_bits<CDT>(a.k_cache, ko + i);
+        kb[jj][2 * t + 1] = ld_bits<CDT>(a.k_cache, ko + half + i);
+      }
+    }
+  };
+  load_keys(0);
 
   // 1. RoPE at position pos (tesm.py:1311-1313), cross query (1302-1305), key into the ring
-  for (int i = tid; i < half; i += 256) {
-    const float2 cs = a.rope[a.pos * half + i];
+  if (tid < W) wn[tid] = wbv;  // read back (and replaced by the ternary) by the lane scoring position tid
+  if (tid < half) {
     float q1, q2, k1, k2;
-    rope_pair<DT>(ld<DT>(prow, o_q + i), ld<DT>(prow, o_q + half + i), cs, q1, q2);
-    rope_pair<DT>(ld<DT>(prow, o_k + i), ld<DT>(prow, o_k + half + i), cs, k1, k2);
+    rope_pair<DT>(from_bits<DT>(bq1), from_bits<DT>(bq2), rcs, q1, q2);
+    rope_pair<DT>(from_bits<DT>(bk1), from_bits<DT>(bk2), rcs, k1, k2);
     if (a.q_add) {
-      q1 = rnd<DT>(q1 + ld<DT>(a.q_add, bh * a.ld_qadd + i));
-      q2 = rnd<DT>(q2 + ld<DT>(a.q_add, bh * a.ld_qadd + half + i));
+      q1 = rnd<DT>(q1 + from_bits<DT>(ba1));
+      q2 = rnd<DT>(q2 + from_bits<DT>(ba2));
     }
-    qv[i] = q1;
-    qv[half + i] = q2;
-    kv[i] = k1;
-    kv[half + i] = k2;
+    qv[tid] = q1;
+    qv[half + tid] = q2;
+    kv[tid] = k1;
+    kv[half + tid] = k2;
     if (blockIdx.z == 0) {
       const int64_t ko = kbase + slot * kstep;
-      st<CDT>(a.k_cache, ko + i, k1);
-      st<CDT>(a.k_cache, ko + half + i, k2);
+      st<CDT>(a.k_cache, ko + tid, k1);
+      st<CDT>(a.k_cache, ko + half + tid, k2);
     }
   }
   // 2. gates and the float64 state update (tesm.py:1315-1322): new = decay * h + write * tanh(sv)
-  for (int j = tid; j < cn; j += 256) {
+#pragma unroll
+  for (int k = 0; k < CPT; ++k) {
+    const int j = tid + 256 * k;
+    if (j >= cn) continue;
     const int c = c0 + j;
-    const float d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(prow, o_decay + c) + ld<DT>(a.decay_bias, h * a.D + c))));
-    const float wr = rnd<DT>(sigmoidf_(ld<DT>(prow, o_write + c)));
-    const float sv = rnd<DT>(tanhf_(ld<DT>(prow, o_sv + c)));
-    const double n64 = static_cast<double>(d) * a.state[bh * a.D + c] + static_cast<double>(wr) * static_cast<double>(sv);
+    const float d = rnd<DT>(sigmoidf_(rnd<DT>(from_bits<DT>(bdc[k]) + from_bits<DT>(bdb[k]))));
+    const float wr = rnd<DT>(sigmoidf_(from_bits<DT>(bwr[k])));
+    const float sv = rnd<DT>(tanhf_(from_bits<DT>(bsv[k])));
+    const double n64 = static_cast<double>(d) * st64[k] + static_cast<double>(wr) * static_cast<double>(sv);
     a.state_out[bh * a.D + c] = n64;
     const float nf = rnd<DT>(static_cast<float>(n64));  // torch: float64 -> float -> dtype
     nv[j] = nf;
@@ -158,40 +220,21 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
   for (int j0 = 0; j0 < 16; j0 += 4) {  // W <= 64: at most 16 windows per wave
     if (wave + 4 * j0 >= W) break;       // uniform in the wave
-    float kk[4][2 * NI];
+    if (j0 > 0) load_keys(j0);
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int w = wave + 4 * (j0 + jj);
       const bool on = w < W && w >= wlo;
-      const int s = on ? slot_of(w) : slot;
-#pragma unroll
-      for (int t = 0; t < NI; ++t) {
-        const int i = lane + 64 * t;
-        float k1 = 0.0f, k2 = 0.0f;
-        if (on && i < half) {
-          if (s == slot) {
-            k1 = kv[i];
-            k2 = kv[half + i];
-          } else {
-            const int64_t ko = kbase + s * kstep;
-            k1 = rnd<DT>(ld<CDT>(a.k_cache, ko + i));
-            k2 = rnd<DT>(ld<CDT>(a.k_cache, ko + half + i));
-          }
-        }
-        kk[jj][2 * t] = k1;
-        kk[jj][2 * t + 1] = k2;
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int w = wave + 4 * (j0 + jj);
+      const bool fresh = on && slot_of(w) == slot;
       float dot = 0.0f;
 #pragma unroll
       for (int t = 0; t < NI; ++t) {
         const int i = lane + 64 * t;
-        if (i < half) {
-          dot += qv[i] * kk[jj][2 * t];
-          dot += qv[half + i] * kk[jj][2 * t + 1];
+        if (on && i < half) {
+          const float k1 = fresh ? kv[i] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t]));
+          const float k2 = fresh ? kv[half + i] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t + 1]));
+          dot += qv[i] * k1;
+          dot += qv[half + i] * k2;
         }
       }
       dot = wave_sum_f<64>(dot);
@@ -200,7 +243,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
           wn[w] = 0.0f;
         } else {
           float sc = rnd<DT>(rnd<DT>(dot) / sq);
-          sc = rnd<DT>(sc + wbias[w]);
+          sc = rnd<DT>(sc + wn[w]);  // wn[w] holds the window bias until here
           wn[w] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);  // strict ternary (1359-1368)
         }
       }
@@ -230,7 +273,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
       const float wv = wn[w];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float x = fresh ? (j4 + r < cn ? nv[j4 + r] : 0.0f) : xs[u][r];
+        const float x = fresh ? (j4 + r < cn ? nv[j4 + r] : 0.0f) : rnd<DT>(ring_val<CDT>(xr[u], r, vec));
         pm[r] += wv * x;
       }
     }
@@ -242,26 +285,28 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   } else {
     constexpr int kWB = 4;
     for (int w0 = wlo; w0 < W; w0 += kWB) {
-      float xb[kWB][CPT];
+      uint32_t xb[kWB][CPT];  // a batch's loads in straight-line code, all in flight together
 #pragma unroll
       for (int u = 0; u < kWB; ++u) {
-        const int w = w0 + u;
-        const int s = w < W ? slot_of(w) : slot;
-        const int64_t vo = vbase + s * vstep;
+        const int64_t vo = vbase + static_cast<int64_t>(read_slot(w0 + u)) * vstep;
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
           const int j = tid + 256 * k;
-          float x = 0.0f;
-          if (w < W && j < cn) x = s == slot ? nv[j] : rnd<DT>(ld<CDT>(a.v_cache, vo + j));
-          xb[u][k] = x;
+          xb[u][k] = ld_bits<CDT>(a.v_cache, vo + (j < cn ? j : cn - 1));
         }
       }
 #pragma unroll
       for (int u = 0; u < kWB; ++u) {
-        if (w0 + u >= W) break;
-        const float wv = wn[w0 + u];
+        const int w = w0 + u;
+        if (w >= W) break;
+        const bool fresh = slot_of(w) == slot;
+        const float wv = wn[w];
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) acc[k] += wv * xb[u][k];
+        for (int k = 0; k < CPT; ++k) {
+          const int j = tid + 256 * k;
+          const float x = j < cn ? (fresh ? nv[j] : rnd<DT>(from_bits<CDT>(xb[u][k]))) : 0.0f;
+          acc[k] += wv * x;
+        }
       }
     }
   }
