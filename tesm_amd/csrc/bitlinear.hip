@@ -1076,51 +1076,6 @@ __device__ __forceinline__ void mfma32d_mainloop(const LinearOperand& o, int64_t
   __syncthreads();
 }
 
-// Outputs (m, nb .. nb+3) from exact accumulators q0 (op0) and q1 (op1, output gate): per-tensor or
-// per-row scales, optional bias and accumulator dump, the output gate; columns past N skipped.
-template <int EPI, int OUT_DT>
-__device__ __forceinline__ void epi_store4(const LinearArgs& a, int64_t m, int64_t nb, const int32_t (&q0)[4],
-                                           const int32_t (&q1)[4], float inv0, int32_t rs0, float inv1, int32_t rs1,
-                                           bool vout, bool vin) {
-  const LinearOperand& o0 = a.op[0];
-  const LinearOperand& o1 = a.op[1];
-  const bool full = nb + 3 < a.N;
-  float v[4], lo[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (EPI == kEpiOutputGate) {
-    if (full) {
-      load4<OUT_DT>(a.local, m * a.ld_local + nb, vin, lo);
-      load4<OUT_DT>(a.gate, m * a.ld_gate + nb, vin, gt);
-    } else {
-      for (int r = 0; r < 4; ++r) {
-        lo[r] = nb + r < a.N ? ld<OUT_DT>(a.local, m * a.ld_local + nb + r) : 0.0f;
-        gt[r] = nb + r < a.N ? ld<OUT_DT>(a.gate, m * a.ld_gate + nb + r) : 0.0f;
-      }
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t n = nb + r;
-    v[r] = 0.0f;
-    if (n >= a.N) continue;
-    const float cw0 = o0.c_w_per_row ? o0.c_w[n] : o0.c_w[0];
-    const int32_t a0 = q0[r] - rs0;
-    if (a.acc_dump) a.acc_dump[m * a.N + n] = a0;
-    const float v0 = (static_cast<float>(a0) * inv0) * cw0;
-    if constexpr (EPI == kEpiStore) {
-      v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n) : v0;
-    } else {
-      const float cw1 = o1.c_w_per_row ? o1.c_w[n] : o1.c_w[0];
-      const float v1 = rnd<OUT_DT>((static_cast<float>(q1[r] - rs1) * inv1) * cw1);
-      v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, lo[r], gt[r]);
-    }
-  }
-  if (full) {
-    store4<OUT_DT>(a.out, m * a.ldo + nb, v, vout);
-  } else {
-    for (int r = 0; r < 4 && nb + r < a.N; ++r) st<OUT_DT>(a.out, m * a.ldo + nb + r, v[r]);
-  }
-}
-
 // Plain epilogue staged through LDS.  The accumulator layout gives each lane 4 consecutive outputs
 // of one row, so direct stores cover 32 rows x 16 bytes per instruction; instead each wave writes
 // one 32-row slab of its (already scaled and rounded) outputs into a private LDS buffer and reads
@@ -1216,16 +1171,21 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
   const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
-  float sx[TM];
-  int32_t rsum[TM];
+  float sx[TM], sx1[TM];
+  int32_t rsum[TM], rs1[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31);
     const int64_t mc = m < a.M ? m : a.M - 1;
     sx[i] = o0.s_x[mc];
     rsum[i] = o0.rowsum[mc];
+    if constexpr (epi_dual(EPI)) {
+      sx1[i] = o1.s_x[mc];
+      rs1[i] = o1.rowsum[mc];
+    }
   }
   const float cws = o0.c_w[0];
+  const float cws1 = epi_dual(EPI) ? o1.c_w[0] : 0.0f;
   if constexpr (NS == 0) {
     mfma32_mainloop<C, WN, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, acc0, smem);
     if constexpr (epi_dual(EPI)) mfma32_mainloop<C, WN, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, acc1, smem);
@@ -1267,32 +1227,84 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
     }
     return;
   }
-  bool vin = false;
-  if constexpr (EPI == kEpiOutputGate) vin = vec4_ok<OUT_DT>(a.local, a.ld_local) && vec4_ok<OUT_DT>(a.gate, a.ld_gate);
+  // Generic epilogue.  The output-gate inputs of one 32 x 32 tile (four groups of four columns per
+  // lane) are requested together in straight-line code (indices clamped into range, raw bits) before
+  // any is used, so the tile waits for memory once instead of once per group; second-operand row
+  // scales and sums and per-tensor weight scales were read before the K loop.
+  const bool vin = EPI == kEpiOutputGate && vec4_ok<OUT_DT>(a.local, a.ld_local) &&
+                   vec4_ok<OUT_DT>(a.gate, a.ld_gate) && a.N % 4 == 0;
+  constexpr int es = OUT_DT == kBF16 ? 2 : 4;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31);
-    if (m >= a.M) continue;
+    const int64_t m = m0 + (wm * TM + i) * 32 + (lane & 31), mc = m < a.M ? m : a.M - 1;
     const float inv0 = 1.0f / sx[i];
-    float inv1 = 0.0f;
-    int32_t rs1 = 0;
-    if constexpr (epi_dual(EPI)) {
-      inv1 = 1.0f / o1.s_x[m];
-      rs1 = o1.rowsum[m];
-    }
+    const float inv1 = epi_dual(EPI) ? 1.0f / sx1[i] : 0.0f;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      uint32_t lo[4][4], gt[4][4];
+      if constexpr (EPI == kEpiOutputGate) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t nb = n0 + (wn * TN + j) * 32 + 8 * g + 4 * (lane >> 5);
+          if (vin) {  // whole groups of four: a group past N re-reads the last one
+            const int64_t nv = nb < a.N ? nb : a.N - 4;
+            const char* pl = static_cast<const char*>(a.local) + (mc * a.ld_local + nv) * es;
+            const char* pg = static_cast<const char*>(a.gate) + (mc * a.ld_gate + nv) * es;
+#pragma unroll
+            for (int q = 0; q < es / 2; ++q) {  // bf16: one 8-byte load, f32: two
+              const uint2 wl = reinterpret_cast<const uint2*>(pl)[q], wg = reinterpret_cast<const uint2*>(pg)[q];
+              lo[g][2 * q] = wl.x;
+              lo[g][2 * q + 1] = wl.y;
+              gt[g][2 * q] = wg.x;
+              gt[g][2 * q + 1] = wg.y;
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int64_t n = nb + r < a.N ? nb + r : a.N - 1;
+              lo[g][r] = ld_bits<OUT_DT>(a.local, mc * a.ld_local + n);
+              gt[g][r] = ld_bits<OUT_DT>(a.gate, mc * a.ld_gate + n);
+            }
+          }
+        }
+      }
+      if (m >= a.M) continue;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t nb = n0 + (wn * TN + j) * 32 + 8 * g + 4 * (lane >> 5);
         if (nb >= a.N) continue;
-        int32_t q0[4], q1[4];
+        float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          q0[r] = acc0[i][j][4 * g + r];
-          q1[r] = acc1[i][j][4 * g + r];
+          const int64_t n = nb + r;
+          const float cw0 = o0.c_w_per_row ? o0.c_w[n < a.N ? n : a.N - 1] : cws;
+          const int32_t a0 = acc0[i][j][4 * g + r] - rsum[i];
+          if (a.acc_dump && n < a.N) a.acc_dump[m * a.N + n] = a0;
+          const float v0 = (static_cast<float>(a0) * inv0) * cw0;
+          if constexpr (EPI == kEpiStore) {
+            v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n < a.N ? n : a.N - 1) : v0;
+          } else {
+            const float cw1 = o1.c_w_per_row ? o1.c_w[n < a.N ? n : a.N - 1] : cws1;
+            const float v1 = rnd<OUT_DT>((static_cast<float>(acc1[i][j][4 * g + r] - rs1[i]) * inv1) * cw1);
+            float lv = 0.0f, gv = 0.0f;
+            if constexpr (EPI == kEpiOutputGate) {
+              if (vin && OUT_DT == kBF16) {
+                const uint32_t wl = lo[g][r >> 1], wg = gt[g][r >> 1];
+                lv = __uint_as_float(r & 1 ? wl & 0xffff0000u : wl << 16);
+                gv = __uint_as_float(r & 1 ? wg & 0xffff0000u : wg << 16);
+              } else {
+                lv = from_bits<OUT_DT>(lo[g][r]);
+                gv = from_bits<OUT_DT>(gt[g][r]);
+              }
+            }
+            v[r] = dual_epi<EPI, OUT_DT>(rnd<OUT_DT>(v0), v1, lv, gv);
+          }
         }
-        epi_store4<EPI, OUT_DT>(a, m, nb, q0, q1, inv0, rsum[i], inv1, rs1, vout, vin);
+        if (nb + 3 < a.N) {
+          store4<OUT_DT>(a.out, m * a.ldo + nb, v, vout);
+        } else {
+          for (int r = 0; r < 4 && nb + r < a.N; ++r) st<OUT_DT>(a.out, m * a.ldo + nb + r, v[r]);
+        }
       }
     }
   }
