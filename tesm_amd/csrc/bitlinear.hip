@@ -746,31 +746,14 @@ __global__ __launch_bounds__(NW * 64) void skinny_fq_kernel(LinearArgs a, FusedQ
       // Straight-line code: the lane's G groups are loaded (16-byte loads, all issued before the first
       // use) from row min(m, M - 1), groups past K re-reading the row's last group; both are zeroed
       // or discarded below.  Needs 16-byte aligned rows and K % 16 == 0.
-      constexpr int NV = DT == kBF16 ? 2 : 4;  // 16-byte loads per 16-element group
-      const int64_t mc = m < a.M ? m : a.M - 1, nfull = f.K / 16;
-      const char* xr = static_cast<const char*>(f.x) + mc * f.ldx * (DT == kBF16 ? 2 : 4);
-      uint4 raw[G > 0 ? G : 1][NV];
-#pragma unroll
-      for (int gi = 0; gi < G; ++gi) {
-        const int64_t g = g0 + LPR * gi, gl = g < nfull ? g : nfull - 1;
-        const uint4* p = reinterpret_cast<const uint4*>(xr + gl * 16 * (DT == kBF16 ? 2 : 4));
-#pragma unroll
-        for (int q = 0; q < NV; ++q) raw[gi][q] = p[q];
-      }
+      const int64_t mc = m < a.M ? m : a.M - 1;
       float v[G > 0 ? G : 1][16];
+      load_groups<DT, (G > 0 ? G : 1), LPR>(f.x, mc * f.ldx, f.K, g0, v);
       float amax = 0.0f;
 #pragma unroll
-      for (int gi = 0; gi < G; ++gi) {
-        const bool in = g0 + LPR * gi < nfull;
-        const uint32_t* wd = reinterpret_cast<const uint32_t*>(&raw[gi][0]);
+      for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float x = DT == kBF16 ? __uint_as_float(i % 2 == 0 ? wd[i / 2] << 16 : wd[i / 2] & 0xffff0000u)
-                                      : __uint_as_float(wd[i]);
-          v[gi][i] = in ? x : 0.0f;
-          amax = fmaxf(amax, fabsf(v[gi][i]));
-        }
-      }
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[gi][i]));
       amax = wave_max<LPR>(amax);
       const bool live = m < a.M;  // rows past M: zero codes, scale 1, sum 0
       const float sc = act_scale<DT>(amax, f.eps);

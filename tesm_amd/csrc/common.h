@@ -207,6 +207,37 @@ __device__ __forceinline__ void load_group(const void* __restrict__ x, int64_t b
   }
 }
 
+// A lane's G groups of 16 elements (groups g0, g0 + LPR, ...) of a row starting at element `base`,
+// for 16-byte aligned rows with K % 16 == 0: every group's 16-byte loads are issued in straight-line
+// code before the first is converted, so the lane waits for memory once.  Groups past K re-read the
+// row's last group and come back as zeros.
+template <int DT, int G, int LPR>
+__device__ __forceinline__ void load_groups(const void* __restrict__ x, int64_t base, int64_t K, int64_t g0,
+                                            float (&v)[G][16]) {
+  constexpr int ES = DT == kBF16 ? 2 : 4, NV = 16 * ES / 16;  // 16-byte loads per group
+  const int64_t nfull = K / 16;
+  const char* xr = static_cast<const char*>(x) + base * ES;
+  uint4 raw[G][NV];
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    const int64_t g = g0 + LPR * gi, gl = g < nfull ? g : nfull - 1;
+    const uint4* p = reinterpret_cast<const uint4*>(xr + gl * 16 * ES);
+#pragma unroll
+    for (int q = 0; q < NV; ++q) raw[gi][q] = p[q];
+  }
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    const bool in = g0 + LPR * gi < nfull;
+    const uint32_t* wd = reinterpret_cast<const uint32_t*>(&raw[gi][0]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float f = DT == kBF16 ? __uint_as_float(i % 2 == 0 ? wd[i / 2] << 16 : wd[i / 2] & 0xffff0000u)
+                                  : __uint_as_float(wd[i]);
+      v[gi][i] = in ? f : 0.0f;
+    }
+  }
+}
+
 // Codes of one group, packed in the requested layout; adds the codes to rs.
 template <int DT>
 __device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int layout, int32_t& rs) {

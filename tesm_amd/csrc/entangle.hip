@@ -140,26 +140,48 @@ __global__ __launch_bounds__(256) void ent_scores_mimo_kernel(EntArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) dot[i][j] = 0.0f;
+  float wb[4];  // window bias of the thread's slots, read up front
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wb[j] = a.bias[h * a.W + (w0 + j < W ? w0 + j : W - 1)];
 
   for (int i0 = 0; i0 < half; i0 += kScPairs) {
     const int np = half - i0 < kScPairs ? half - i0 : kScPairs;
-    // stage RoPE'd pairs (interleaved q1, q2 per pair) of the slice
-    for (int idx = tid; idx < (kScTP + krows) * kScPairs; idx += 256) {
-      const int r = idx / kScPairs, i = idx - r * kScPairs;
-      const bool isq = r < kScTP;
-      const int rr = isq ? r : r - kScTP;
-      int64_t tt_ = isq ? t0 + rr : tk0 + rr;
-      const bool ok = i < np && tt_ >= 0 && tt_ < a.L;
-      tt_ = tt_ < 0 ? 0 : (tt_ >= a.L ? a.L - 1 : tt_);
-      float o1 = 0.0f, o2 = 0.0f;
-      if (ok) {
+    // stage RoPE'd pairs (interleaved q1, q2 per pair) of the slice: each thread loads kSB items
+    // (clamped into range, raw bits) before it rotates and stores any of them
+    constexpr int kSB = 8;
+    const int nitems = (kScTP + krows) * kScPairs;
+    for (int base = 0; base < nitems; base += 256 * kSB) {
+      uint32_t xa[kSB], xb[kSB];
+      float2 cs[kSB];
+#pragma unroll
+      for (int u = 0; u < kSB; ++u) {
+        int idx = base + tid + 256 * u;
+        idx = idx < nitems ? idx : nitems - 1;
+        const int r = idx / kScPairs, i = idx - r * kScPairs, ic = i < np ? i : np - 1;
+        const bool isq = r < kScTP;
+        int64_t tt_ = isq ? t0 + r : tk0 + (r - kScTP);
+        tt_ = tt_ < 0 ? 0 : (tt_ >= a.L ? a.L - 1 : tt_);
         const void* src = isq ? a.q : a.k;
-        const int64_t off = (b * a.L + tt_) * (isq ? a.ld_q : a.ld_k) + h * a.R + i0 + i;
-        rope_pair<DT>(ld<DT>(src, off), ld<DT>(src, off + half), a.rope[tt_ * half + i0 + i], o1, o2);
+        const int64_t off = (b * a.L + tt_) * (isq ? a.ld_q : a.ld_k) + h * a.R + i0 + ic;
+        xa[u] = ld_bits<DT>(src, off);
+        xb[u] = ld_bits<DT>(src, off + half);
+        cs[u] = a.rope[tt_ * half + i0 + ic];
       }
-      float* dst = (isq ? qs : ks) + rr * kScPitch + 2 * i;
-      dst[0] = o1;
-      dst[1] = o2;
+#pragma unroll
+      for (int u = 0; u < kSB; ++u) {
+        const int idx = base + tid + 256 * u;
+        if (idx >= nitems) break;
+        const int r = idx / kScPairs, i = idx - r * kScPairs;
+        const bool isq = r < kScTP;
+        const int rr = isq ? r : r - kScTP;
+        const int64_t tt_ = isq ? t0 + rr : tk0 + rr;
+        const bool ok = i < np && tt_ >= 0 && tt_ < a.L;
+        float o1 = 0.0f, o2 = 0.0f;
+        if (ok) rope_pair<DT>(from_bits<DT>(xa[u]), from_bits<DT>(xb[u]), cs[u], o1, o2);
+        float* dst = (isq ? qs : ks) + rr * kScPitch + 2 * i;
+        dst[0] = o1;
+        dst[1] = o2;
+      }
     }
     __syncthreads();
     if (active) {
@@ -195,7 +217,7 @@ __global__ __launch_bounds__(256) void ent_scores_mimo_kernel(EntArgs a) {
         float tern = 0.0f;
         if (valid) {
           float sc = rnd<DT>(rnd<DT>(dot[i][j]) / sq);
-          sc = rnd<DT>(sc + a.bias[h * a.W + w]);
+          sc = rnd<DT>(sc + wb[j]);
           tern = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
         }
         tt[(p0 + i) * W + w] = tern;
@@ -337,6 +359,15 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
   const int krs = static_cast<int>(f.krs), dp = static_cast<int>(f.dp);
   const int rows = kFusedTP + W - 1;
   const int64_t tk0 = t0 - (W - 1);  // position of key row 0
+
+  // window bias of the thread's score slots w = (tid & 15) + 16 i, read before the tile's other
+  // operands (used after the LDS phase, so never waited for on its own)
+  float wbias[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int w = (tid & 15) + 16 * i;
+    wbias[i] = a.bias[a.W - W + (w < W ? w : W - 1)];
+  }
 
   const T* S = static_cast<const T*>(a.S);
   constexpr int kVec = 16 / sizeof(T);
@@ -557,7 +588,7 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
           dot += qp[half + c] * kp[half + c];
         }
         float sc = rnd<DT>(rnd<DT>(dot) / sq);
-        sc = rnd<DT>(sc + a.bias[a.W - W + w]);
+        sc = rnd<DT>(sc + wbias[i]);
         tern[i] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
       }
       n += fabsf(tern[i]);

@@ -16,7 +16,8 @@ namespace tesm {
 
 // LPR lanes per row (64 / LPR rows per wave, 4 waves per workgroup).  Each lane owns code groups
 // lane, lane + LPR, ... ; with G > 0 its G groups stay in registers between the amax and the code
-// pass, with G == 0 (very wide rows) the row is read twice.
+// pass (loaded in straight-line code, all in flight together, for 16-byte aligned rows with
+// K % 16 == 0), with G == 0 (very wide rows) the row is read twice.
 template <int DT, bool VEC, int LPR, int G>
 __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__ x, int64_t M, int64_t K,
                                                         int64_t ldx, float eps, int layout, int8_t* __restrict__ q,
@@ -39,18 +40,24 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__
   int32_t rs = 0;
   if constexpr (G > 0) {
     float v[G][16];
+    if (VEC && K % 16 == 0) {  // straight-line loads, all in flight together
+      load_groups<DT, G, LPR>(x, base, K, g0, v);
+    } else {
 #pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      const int64_t g = g0 + LPR * gi;
-      if (g < ngroups) {
-        load_group<DT, VEC>(x, base, K, g, v[gi]);
-      } else {
+      for (int gi = 0; gi < G; ++gi) {
+        const int64_t g = g0 + LPR * gi;
+        if (g < ngroups) {
+          load_group<DT, VEC>(x, base, K, g, v[gi]);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[gi][i] = 0.0f;
+          for (int i = 0; i < 16; ++i) v[gi][i] = 0.0f;
+        }
       }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
 #pragma unroll
       for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[gi][i]));
-    }
     amax = wave_max<LPR>(amax);
     const float sc = act_scale<DT>(amax, eps);
 #pragma unroll
