@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TESM_HIP_ABI_VERSION 8
+#define TESM_HIP_ABI_VERSION 9
 
 #define TESM_DT_F32 0
 #define TESM_DT_BF16 1
@@ -336,6 +336,13 @@ typedef struct tesm_hip_siso_step {
   void* y;                    /* (B, d_model) in dt */
   void* new_state;            /* optional (B, d_state) in dt: this step's state */
   int64_t ld_u;               /* row pitch of u in elements (0: d_model) */
+  /* optional device int64[2] = {seq_pos, cache_idx}.  When set, the step reads its position and ring
+   * slot there at run time (the host fields above are not used) and advances them at its end
+   * ({seq_pos + 1, (cache_idx + 1) % window}), so one captured HIP graph of this call serves every
+   * following step.  rope must then hold rope_rows >= every position the graph reaches (positions
+   * past it read the last row). */
+  int64_t* step_pos;
+  int64_t rope_rows;
 } tesm_hip_siso_step;
 
 int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p);

@@ -12,7 +12,7 @@ import ctypes
 import os
 import threading
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 _DEFAULT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_build", "libtesm_hip.so")
 
 P = ctypes.c_void_p
@@ -91,7 +91,7 @@ class SisoStep(ctypes.Structure):
         ("cross_q_proj", Linear),
         ("decay_bias", P), ("local_bias", P), ("rope", P), ("cross_state", P),
         ("state", P), ("state_out", P), ("k_cache", P), ("v_cache", P), ("y", P), ("new_state", P),
-        ("ld_u", I64),
+        ("ld_u", I64), ("step_pos", P), ("rope_rows", I64),
     ]
 
 

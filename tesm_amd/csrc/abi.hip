@@ -217,7 +217,8 @@ int check_desc_ptrs(const tesm_hip_siso_step& p) {
   if (int rc = check_ptrs("siso decode",
                           {{p.u, "u"}, {p.decay_bias, "decay_bias"}, {p.local_bias, "local_bias"}, {p.rope, "rope"},
                            {p.cross_state, "cross_state"}, {p.state, "state"}, {p.state_out, "state_out"},
-                           {p.k_cache, "k_cache"}, {p.v_cache, "v_cache"}, {p.y, "y"}, {p.new_state, "new_state"}}))
+                           {p.k_cache, "k_cache"}, {p.v_cache, "v_cache"}, {p.y, "y"}, {p.new_state, "new_state"},
+                           {p.step_pos, "step_pos"}}))
     return rc;
   for (const auto& w : {std::make_pair(&p.in_proj, "in_proj"), std::make_pair(&p.state_proj, "state_proj"),
                         std::make_pair(&p.ent_proj, "ent_proj"), std::make_pair(&p.out_proj, "out_proj"),
@@ -1153,8 +1154,11 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   hipStream_t st = static_cast<hipStream_t>(stream);
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso decode: dtype must be 0 or 1");
   TESM_REQUIRE(p.B >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.ent_rank >= 2 && p.ent_rank % 2 == 0 &&
-                   p.window >= 1 && p.window <= 64 && p.seq_pos >= 0 && p.cache_idx >= 0 && p.cache_idx < p.window,
-               kErrInvalidArg, "siso decode: bad sizes or ring position (need even ent_rank, 1 <= window <= 64)");
+                   p.window >= 1 && p.window <= 64 &&
+                   (p.step_pos ? p.rope_rows >= 1 : p.seq_pos >= 0 && p.cache_idx >= 0 && p.cache_idx < p.window),
+               kErrInvalidArg,
+               "siso decode: bad sizes or ring position (need even ent_rank, 1 <= window <= 64, rope_rows >= 1 with "
+               "step_pos)");
   TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.state && p.state_out && p.k_cache && p.v_cache &&
                    p.y,
                kErrInvalidArg, "siso decode: null pointer");
@@ -1219,10 +1223,19 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   da.R = R;
   da.D = D;
   da.W = p.window;
-  da.pos = p.seq_pos;
-  da.slot = p.cache_idx;
-  da.valid = std::min<int64_t>(p.seq_pos + 1, p.window);
-  da.full = da.valid >= p.window;
+  if (p.step_pos) {  // read on the device at run time; the host fields only have to pass the checks
+    da.step_pos = p.step_pos;
+    da.rope_rows = p.rope_rows;
+    da.pos = 0;
+    da.slot = 0;
+    da.valid = 1;
+    da.full = 0;
+  } else {
+    da.pos = p.seq_pos;
+    da.slot = p.cache_idx;
+    da.valid = std::min<int64_t>(p.seq_pos + 1, p.window);
+    da.full = da.valid >= p.window;
+  }
   da.proj = proj;
   da.ld_proj = n_in;
   da.o_sv = o_sv;
@@ -1286,7 +1299,8 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   op.ld = n_in;
   op.y = p.y;
   op.taps = tapping ? &tp : nullptr;
-  return run_output_path(op, st);
+  if ((rc = run_output_path(op, st))) return rc;
+  return p.step_pos ? launch_decode_advance(p.step_pos, p.window, st) : kOk;
 }
 
 int tesm_hip_siso_decode_noalloc(const tesm_hip_siso_step* p, void* stream) {

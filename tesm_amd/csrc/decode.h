@@ -48,10 +48,16 @@ struct DecodeArgs {
   int64_t ldq = 0;
   // optional (B, H, W) int8 ternary decisions at the padded window positions (reference read order)
   int8_t* tern = nullptr;
+  // optional device {seq_pos, cache_idx}: read at run time instead of pos / slot / valid / full (RoPE
+  // rows clamped to rope_rows - 1); launch_decode_advance moves it to the next step
+  const int64_t* step_pos = nullptr;
+  int64_t rope_rows = 0;
 };
 
 int64_t decode_lds_bytes(int64_t R, int64_t CW);
 int launch_decode_ent(const DecodeArgs& a, hipStream_t st);
+// step_pos = {seq_pos + 1, (cache_idx + 1) % W}: the device-side position of a graph-replayed step
+int launch_decode_advance(int64_t* step_pos, int64_t W, hipStream_t st);
 
 // Ring buffers after a prefill of L tokens: the last min(L, W) RoPE'd keys and states.
 struct CacheFillArgs {

@@ -94,9 +94,16 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   // ring element (b, s, h, i): keys at kbase + s*kstep + i, states at vbase + s*vstep + i
   const int64_t kbase = (b * a.W * H + h) * a.R, kstep = H * a.R;
   const int64_t vbase = (b * a.W * H + h) * a.D + c0, vstep = H * a.D;
-  const int slot = static_cast<int>(a.slot);
-  const int wlo = static_cast<int>(W - a.valid);  // padded positions below wlo hold no entry
-  const bool full = a.full != 0;
+  int64_t pos = a.pos;
+  int slot = static_cast<int>(a.slot), valid = static_cast<int>(a.valid);
+  if (a.step_pos) {  // position kept on the device (graph replay): read it here
+    const int64_t sp = a.step_pos[0] < 0 ? 0 : a.step_pos[0], si = a.step_pos[1] % W;
+    pos = sp < a.rope_rows ? sp : a.rope_rows - 1;
+    slot = static_cast<int>(si < 0 ? si + W : si);
+    valid = static_cast<int>(sp + 1 < W ? sp + 1 : W);
+  }
+  const int wlo = W - valid;  // padded positions below wlo hold no entry
+  const bool full = valid >= W;
   // ring slot read at padded window position w (w in [wlo, W)), in the reference's order
   auto slot_of = [&](int w) -> int {
     if (!full) return w - wlo;
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   }
   // 0b. RoPE inputs of element tid of each rank half (half <= 256)
   const int ir = tid < half ? tid : half - 1;
-  const float2 rcs = a.rope[a.pos * half + ir];
+  const float2 rcs = a.rope[pos * half + ir];
   const uint32_t bq1 = ld_bits<DT>(prow, o_q + ir), bq2 = ld_bits<DT>(prow, o_q + half + ir);
   const uint32_t bk1 = ld_bits<DT>(prow, o_k + ir), bk2 = ld_bits<DT>(prow, o_k + half + ir);
   const void* qadd = a.q_add ? a.q_add : a.proj;  // no cross query: a valid dummy address
@@ -409,7 +416,20 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(CacheFillArgs a) {
   }
 }
 
+__global__ void decode_advance_kernel(int64_t* __restrict__ sp, int64_t W) {
+  if (threadIdx.x == 0) {
+    sp[0] += 1;
+    sp[1] = (sp[1] + 1) % W;
+  }
+}
+
 }  // namespace
+
+int launch_decode_advance(int64_t* step_pos, int64_t W, hipStream_t st) {
+  TESM_REQUIRE(step_pos && W >= 1, kErrInvalidArg, "decode advance: bad arguments");
+  decode_advance_kernel<<<1, 64, 0, TESM_LOGGED(st, decode_advance_kernel)>>>(step_pos, W);
+  return check_launch("decode advance");
+}
 
 int64_t decode_lds_bytes(int64_t R, int64_t CW) { return (2 * R + 5 * CW + 64 + 16) * static_cast<int64_t>(sizeof(float)); }
 
