@@ -690,7 +690,8 @@ __device__ __forceinline__ void skinny_body(const LinearArgs& a, int64_t m0, int
     }
   skinny_loop<NW, TM, TN>(a.op[0], a.M, a.N, m0, n0, a.Kp, w, lane, acc0);
   if constexpr (epi_dual(EPI)) skinny_loop<NW, TM, TN>(a.op[1], a.M, a.N, m0, n0, a.Kp, w, lane, acc1);
-  if (w > 0) {
+  const int nblk = static_cast<int>((a.Kp + 255) / 256), nact = nblk < NW ? nblk : NW;  // waves with blocks
+  if (w > 0 && w < nact) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -701,7 +702,7 @@ __device__ __forceinline__ void skinny_body(const LinearArgs& a, int64_t m0, int
   }
   __syncthreads();
   if (w != 0) return;
-  for (int src = 0; src < NW - 1; ++src)
+  for (int src = 0; src < nact - 1; ++src)
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1560,7 +1561,8 @@ struct RowqLds {
 };
 
 inline int64_t rowq_lds_bytes(int64_t N, int64_t nks, int64_t ldq, int nw) {
-  return 2 * N * (16 * nks + 16) + 2 * 2 * 16 * (64 * nks + 16) + 16 * (ldq + 16) + 2 * 2 * 16 * nw * 4 + 2 * N * 4;
+  const int64_t stage = nks <= 4 ? 0 : 2 * N * (16 * nks + 16);  // register-resident weights for K <= 256
+  return stage + 2 * 2 * 16 * (64 * nks + 16) + 16 * (ldq + 16) + 2 * 2 * 16 * nw * 4 + 2 * N * 4;
 }
 
 template <int NCT, int AC, int RW>
@@ -1631,10 +1633,19 @@ struct RowqShared {
   const float* cwl;   // [2][N] output scale of every column (c_w, or its one scalar repeated)
 };
 
-template <int NW, int NCT, int DT, int NKS, int AC>
+// Packed-weight fragments of the lane's columns for the register-resident variant (NKS <= 4).  The
+// lanes of group q take the 16-code groups q NKS .. q NKS + NKS - 1 of their column (k-step ks: group
+// q NKS + ks, for weights and activation codes alike), so each lane's fragments are one contiguous
+// load and a column's four lanes read its packed row whole.
+template <int NCT, int NKS>
+struct RowqW {
+  uint32_t w0[NCT][NKS], w1[NCT][NKS];
+};
+
+template <int NW, int NCT, int DT, int NKS, int AC, bool RW = false>
 __device__ __forceinline__ void rowq_tile(const LinearArgs& a, const RowQuant& o, int64_t t,
                                           const RowqIn<NCT, AC, EpRaw<DT, true>::W>& in, const RowqShared& sh,
-                                          int tid) {
+                                          int tid, const RowqW<NCT, NKS>* rw = nullptr) {
   using L = RowqLds<NKS>;
   // all in-tile indices fit 32 bits: N <= 1024 and the LDS is 160 KB
   const int N = static_cast<int>(a.N);
@@ -1657,8 +1668,9 @@ __device__ __forceinline__ void rowq_tile(const LinearArgs& a, const RowQuant& o
   v4i x0[NKS], x1[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
-    x0[ks] = *reinterpret_cast<const v4i*>(sh.abuf + row * L::ARS + 64 * ks + 16 * q);
-    x1[ks] = *reinterpret_cast<const v4i*>(sh.abuf + (16 + row) * L::ARS + 64 * ks + 16 * q);
+    const int kb = RW ? 16 * (q * NKS + ks) : 64 * ks + 16 * q;  // the k-step's code group of lane group q
+    x0[ks] = *reinterpret_cast<const v4i*>(sh.abuf + row * L::ARS + kb);
+    x1[ks] = *reinterpret_cast<const v4i*>(sh.abuf + (16 + row) * L::ARS + kb);
   }
 
   // per 16-column tile: both products, then y = local + sigmoid(gate) * state_proj + ent_proj in the
@@ -1672,8 +1684,20 @@ __device__ __forceinline__ void rowq_tile(const LinearArgs& a, const RowQuant& o
     const int n = col0 + 16 * j + row;
     const int nc = n < N ? n : N - 1;
     uint32_t f0[NKS], f1[NKS];
-    lds_frag<NKS>(sh.wl + nc * L::RS + q * NKS * 4, f0);
-    lds_frag<NKS>(sh.wl + (N + nc) * L::RS + q * NKS * 4, f1);
+    if constexpr (RW) {
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        f0[ks] = rw->w0[j][ks];
+        f1[ks] = rw->w1[j][ks];
+        // opaque copies: the unpacking below stays per tile instead of being hoisted out of the tile
+        // loop as 4x as many live registers
+        asm volatile("" : "+v"(f0[ks]));
+        asm volatile("" : "+v"(f1[ks]));
+      }
+    } else {
+      lds_frag<NKS>(sh.wl + nc * L::RS + q * NKS * 4, f0);
+      lds_frag<NKS>(sh.wl + (N + nc) * L::RS + q * NKS * 4, f1);
+    }
     v4i acc0 = v4i{0, 0, 0, 0}, acc1 = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -1754,16 +1778,25 @@ __device__ __forceinline__ void rowq_tile(const LinearArgs& a, const RowQuant& o
   }
 }
 
+// NKS <= 4 (K <= 256): each wave's packed-weight fragments (its NCT column tiles of both products, 2 NCT
+// NKS dwords per lane) stay in registers for the whole kernel, read straight from global memory;
+// otherwise both weight matrices are staged once per workgroup in LDS.
+template <int NKS>
+constexpr bool rowq_reg_weights() {
+  return NKS <= 4;
+}
+
 template <int NW, int NCT, int DT, int NKS>
 __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, RowQuant o, int64_t ntiles) {
   using L = RowqLds<NKS>;
+  constexpr bool RW = rowq_reg_weights<NKS>();
   constexpr int NT = NW * 64;
-  constexpr int SB = (2 * NW * NCT * 16 * NKS + NT - 1) / NT;  // staged weight chunks per thread
-  constexpr int AC = (128 * NKS + NT - 1) / NT;                // activation chunks per thread per tile
+  constexpr int SB = RW ? 1 : (2 * NW * NCT * 16 * NKS + NT - 1) / NT;  // staged weight chunks per thread
+  constexpr int AC = (128 * NKS + NT - 1) / NT;                          // activation chunks per thread per tile
   using In = RowqIn<NCT, AC, EpRaw<DT, true>::W>;
   extern __shared__ __attribute__((aligned(16))) char lds_rowq[];
-  char* wl = lds_rowq;                                                    // [2][N][RS]
-  char* abuf = wl + 2 * a.N * L::RS;                                      // [2 tiles][2][16][ARS]
+  char* wl = lds_rowq;                                                    // [2][N][RS] (LDS weights only)
+  char* abuf = wl + (RW ? 0 : 2 * a.N * L::RS);                           // [2 tiles][2][16][ARS]
   int8_t* codes = reinterpret_cast<int8_t*>(abuf + 2 * L::ABUF);          // [16][ldq + 16]
   float* red = reinterpret_cast<float*>(codes + 16 * (o.ldq + 16));       // [2 tiles][16][NW]
   int32_t* redi = reinterpret_cast<int32_t*>(red + 2 * 16 * NW);         // [2 tiles][16][NW]
@@ -1771,16 +1804,40 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
   const int tid = threadIdx.x;
   const int64_t col0 = static_cast<int64_t>(tid >> 6) * NCT * 16;
 
-  // weights: every load of the stage first, then this workgroup's first tile, then the LDS writes
-  const int64_t total = 2 * a.N * NKS;
+  // weights: every load first (registers, or the LDS stage), then this workgroup's first tile, then
+  // the LDS writes
+  RowqW<NCT, NKS> rw;
   v4i sb[SB];
+  const int64_t total = 2 * a.N * NKS;
+  if constexpr (RW) {
+    // lane (q, row) of column tile j: column col0 + 16 j + row, dwords q NKS .. q NKS + NKS - 1 of its row
+    const int lane = tid & 63, q = lane >> 4, row = lane & 15;
 #pragma unroll
-  for (int b = 0; b < SB; ++b) {
-    const int64_t g = tid + static_cast<int64_t>(b) * NT;
-    const int64_t gc = g < total ? g : total - 1;
-    const int64_t pn = gc / NKS, c = gc - pn * NKS;  // pn = p * N + n
-    const uint8_t* wp = pn < a.N ? a.op[0].w + pn * a.op[0].ldw : a.op[1].w + (pn - a.N) * a.op[1].ldw;
-    sb[b] = *reinterpret_cast<const v4i*>(wp + 16 * c);
+    for (int j = 0; j < NCT; ++j) {
+      const int64_t n = col0 + 16 * j + row, nc = n < a.N ? n : a.N - 1;
+      const uint32_t* p0 = reinterpret_cast<const uint32_t*>(a.op[0].w + nc * a.op[0].ldw) + q * NKS;
+      const uint32_t* p1 = reinterpret_cast<const uint32_t*>(a.op[1].w + nc * a.op[1].ldw) + q * NKS;
+      if constexpr (NKS == 4) {
+        const uint4 v0 = *reinterpret_cast<const uint4*>(p0), v1 = *reinterpret_cast<const uint4*>(p1);
+        rw.w0[j][0] = v0.x, rw.w0[j][1] = v0.y, rw.w0[j][2] = v0.z, rw.w0[j][3] = v0.w;
+        rw.w1[j][0] = v1.x, rw.w1[j][1] = v1.y, rw.w1[j][2] = v1.z, rw.w1[j][3] = v1.w;
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          rw.w0[j][ks] = p0[ks];
+          rw.w1[j][ks] = p1[ks];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < SB; ++b) {
+      const int64_t g = tid + static_cast<int64_t>(b) * NT;
+      const int64_t gc = g < total ? g : total - 1;
+      const int64_t pn = gc / NKS, c = gc - pn * NKS;  // pn = p * N + n
+      const uint8_t* wp = pn < a.N ? a.op[0].w + pn * a.op[0].ldw : a.op[1].w + (pn - a.N) * a.op[1].ldw;
+      sb[b] = *reinterpret_cast<const v4i*>(wp + 16 * c);
+    }
   }
   RowqShared sh0, sh1;
   sh0.wl = sh1.wl = wl;
@@ -1796,14 +1853,16 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
   int64_t t = blockIdx.x;
   rowq_in_load<NW, NCT, NKS, DT, AC>(a, t, col0, tid, ta);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!RW) {
 #pragma unroll
-  for (int b = 0; b < SB; ++b) {
-    const int64_t g = tid + static_cast<int64_t>(b) * NT;
-    if (g >= total) continue;
-    const int64_t pn = g / NKS, c = g - pn * NKS;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(wl + pn * L::RS) + c;
+    for (int b = 0; b < SB; ++b) {
+      const int64_t g = tid + static_cast<int64_t>(b) * NT;
+      if (g >= total) continue;
+      const int64_t pn = g / NKS, c = g - pn * NKS;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(wl + pn * L::RS) + c;
 #pragma unroll
-    for (int qq = 0; qq < 4; ++qq) dst[qq * NKS] = static_cast<uint32_t>(sb[b][qq]);
+      for (int qq = 0; qq < 4; ++qq) dst[qq * NKS] = static_cast<uint32_t>(sb[b][qq]);
+    }
   }
   for (int64_t i = tid; i < a.N; i += NT) {
     cwl[i] = a.op[0].c_w_per_row ? a.op[0].c_w[i] : a.op[0].c_w[0];
@@ -1817,11 +1876,11 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
   for (;;) {
     const int64_t t1 = t + gridDim.x;
     rowq_in_load<NW, NCT, NKS, DT, AC>(a, t1 < ntiles ? t1 : t, col0, tid, tb);
-    rowq_tile<NW, NCT, DT, NKS, AC>(a, o, t, ta, sh0, tid);
+    rowq_tile<NW, NCT, DT, NKS, AC, RW>(a, o, t, ta, sh0, tid, &rw);
     if (t1 >= ntiles) break;
     const int64_t t2 = t1 + gridDim.x;
     rowq_in_load<NW, NCT, NKS, DT, AC>(a, t2 < ntiles ? t2 : t1, col0, tid, ta);
-    rowq_tile<NW, NCT, DT, NKS, AC>(a, o, t1, tb, sh1, tid);
+    rowq_tile<NW, NCT, DT, NKS, AC, RW>(a, o, t1, tb, sh1, tid, &rw);
     if (t2 >= ntiles) break;
     t = t2;
   }
@@ -1893,7 +1952,8 @@ inline bool host_vec4_ok(const void* p, int64_t ld, int dt) {
 
 template <int NW, int NCT, int NKS>
 void launch_rowq_lds(const LinearArgs& a, const RowQuant& o, int64_t ntiles, int64_t lds, int cus, hipStream_t st) {
-  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / lds));
+  // register-resident weights: one workgroup per CU (VGPR-bound), its tiles prefetched one ahead
+  const int64_t per_cu = rowq_reg_weights<NKS>() ? 1 : std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / lds));
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ntiles, cus * per_cu));
   if (a.out_dt == kBF16)
     gate_rowq_lds_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_lds_kernel<NW, NCT, kBF16, NKS>)>>>(a, o, ntiles);
@@ -1984,12 +2044,16 @@ int dispatch_dual(const LinearArgs& a, hipStream_t st) {
   return run_mfma32<1, 4, 2, 1, EPI>(a, st);
 }
 
+// Waves of a fused-quantization workgroup (16 waves, four per SIMD, were measured no faster at the
+// decode shapes: the quantization phase is bound by its dependent load / reduction / LDS steps).
+constexpr int kFqNW = 4;
+
 // LDS of one fused-quantization workgroup: 16 TM code rows of Kp + 16 bytes with their scales and sums
-// (dynamic), and skinny_body's static split-K reduction buffer (three waves' TM partial tiles, 16 bytes
-// per lane each).
+// (dynamic), and skinny_body's static split-K reduction buffer (kFqNW - 1 waves' TM partial tiles, 16
+// bytes per lane each).
 static int64_t linear_fq_lds_bytes(int64_t M, int64_t Kp) {
   const int64_t TM = M <= 16 ? 1 : 2;
-  return 16 * TM * (Kp + 16) + 16 * TM * 8 + 3 * TM * 64 * 16;
+  return 16 * TM * (Kp + 16) + 16 * TM * 8 + (kFqNW - 1) * TM * 64 * 16;
 }
 
 // Kp <= 1920 keeps a workgroup at most 68 KB of LDS; the device's per-workgroup limit is checked too (a
@@ -2008,15 +2072,15 @@ void run_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st) {
   const int64_t tiles = ((a.M + 16 * TM - 1) / (16 * TM)) * ((a.N + 15) / 16);
   const size_t lds = static_cast<size_t>(16 * TM * (a.Kp + 16) + 16 * TM * 8);
   if (a.out_dt == kBF16)
-    skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, TESM_LOGGED(st, skinny_fq_kernel<4, TM, 1, kBF16, DT, VEC, G>)>>>(a, f);
+    skinny_fq_kernel<kFqNW, TM, 1, kBF16, DT, VEC, G><<<static_cast<unsigned>(tiles), kFqNW * 64, lds, TESM_LOGGED(st, skinny_fq_kernel<kFqNW, TM, 1, kBF16, DT, VEC, G>)>>>(a, f);
   else
-    skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G><<<static_cast<unsigned>(tiles), 256, lds, TESM_LOGGED(st, skinny_fq_kernel<4, TM, 1, kF32, DT, VEC, G>)>>>(a, f);
+    skinny_fq_kernel<kFqNW, TM, 1, kF32, DT, VEC, G><<<static_cast<unsigned>(tiles), kFqNW * 64, lds, TESM_LOGGED(st, skinny_fq_kernel<kFqNW, TM, 1, kF32, DT, VEC, G>)>>>(a, f);
 }
 template <int TM>
 void dispatch_skinny_fq(const LinearArgs& a, const FusedQuantIn& f, bool vec, hipStream_t st) {
-  // groups per lane: Kp / 16 over 256 / (16 TM) lanes per row; the register-held variants (one read
+  // groups per lane: Kp / 16 over kFqNW * 64 / (16 TM) lanes per row; the register-held variants (one read
   // of the row, straight-line loads) need 16-byte aligned rows of whole 16-element groups
-  const int64_t gpl = (a.Kp / 16 + 256 / (16 * TM) - 1) / (256 / (16 * TM));
+  const int64_t lpr = kFqNW * 64 / (16 * TM), gpl = (a.Kp / 16 + lpr - 1) / lpr;
   const bool held = vec && f.K % 16 == 0;
   if (f.dt == kBF16) {
     if (held) {
