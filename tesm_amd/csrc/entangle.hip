@@ -620,7 +620,21 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
     float acc[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-    for (int w = 0; w < W; ++w) {
+    // four window rows' LDS reads in flight per step; each channel still sums w = 0, 1, .. in order
+    int w = 0;
+    for (; w + 4 <= W; w += 4) {
+      float x[4][16], wt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        lds_row16<DT>(sx + static_cast<int64_t>(p + w + u) * dp + 16 * g, x[u]);
+        wt[u] = wn[p * W + w + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += wt[u] * x[u][e];
+    }
+    for (; w < W; ++w) {
       float x[16];
       lds_row16<DT>(sx + static_cast<int64_t>(p + w) * dp + 16 * g, x);
       const float wt = wn[p * W + w];
