@@ -188,7 +188,7 @@ def measure_decode(torch, m, steps: int = 50, d_model: int = LAYER["d_model"]):
     ms = e0.elapsed_time(e1) / steps
     out = {"batch": Bd, "prefill": P, "ms_per_step": ms, "tokens_per_s": Bd / (ms * 1e-3),
            "note": "one decode step per sequence, host dispatch included (no graph capture)"}
-    if isinstance(m, TESM_SISO):
+    if type(m) is TESM_SISO:
         # the same steps replayed from captured graphs (position on the device); each step's token is
         # copied into the graph's input buffer inside the timed region
         t0 = P + 3 + steps

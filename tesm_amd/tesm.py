@@ -398,6 +398,8 @@ class SisoDecodeGraph:
     rows; no cross-layer query (``cross_layer_state`` is not supported here)."""
 
     def __init__(self, layer: "TESM_SISO", inference_params, max_positions: int, dtype: torch.dtype | None = None):
+        if type(layer) is not TESM_SISO:
+            raise TypeError(f"SisoDecodeGraph: takes a TESM_SISO layer, got {type(layer).__name__}")
         lib = _lib.load()
         cache = inference_params["state_cache"]
         self.cache = cache
