@@ -2155,9 +2155,13 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
     // long K loops over many tiles: direct-to-LDS loads into three stages (no staging registers)
     if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
-    // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768): 26.2 us vs 28.5 us
-    // for the register-staged 128x128 tiles
-    if (tiles256 >= 512 && a.Kp <= 1024) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
+    // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
+    // 151936 x 768): two direct-to-LDS stages, 48 KB, so three workgroups fit a CU's LDS: 23.6 us vs
+    // 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM head 74 us vs 82 us
+    if (tiles256 >= 512 && a.Kp <= 1024) return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
+    // fewer 128x256 tiles than CUs at short K (the SISO out_proj: 8192 x 768 x 768): 64x128 tiles, two
+    // direct-to-LDS stages: 10.1 us vs 10.7 us for 128x256 tiles
+    if (tiles256 < 256 && a.Kp <= 1024) return run_mfma32<1, 4, 2, 1, kEpiStore, 2>(a, st);
     if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
     if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
     return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
