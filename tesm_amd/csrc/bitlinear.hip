@@ -1132,7 +1132,7 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
   }
 }
 
-// NS == 0: register-staged main loop (two LDS stages); NS >= 3: direct-to-LDS loads into NS stages.
+// NS == 0: register-staged main loop (two LDS stages); NS >= 2: direct-to-LDS loads into NS stages.
 template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT, int NS = 0>
 __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   using C = Cfg32<WM, WN, TM, TN>;
@@ -2039,7 +2039,9 @@ int dispatch_dual(const LinearArgs& a, hipStream_t st) {
   if (a.M <= 16) return run_skinny<4, 1, 1, EPI>(a, st);
   if (a.M <= 32) return run_skinny<4, 2, 1, EPI>(a, st);
   const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, EPI, 3>(a, st);
+  // long K on many tiles (the MIMO output gate, K 2 x 8192): two direct-to-LDS stages, 694 us vs 766 us
+  // with three at M 8192
+  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);
   if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, EPI>(a, st);
   return run_mfma32<1, 4, 2, 1, EPI>(a, st);
 }
@@ -2153,8 +2155,9 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // out_proj / configs[1] / configs[4])
     const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
     const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-    // long K loops over many tiles: direct-to-LDS loads into three stages (no staging registers)
-    if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 3>(a, st);
+    // long K loops over many tiles: direct-to-LDS loads into two stages (no staging registers);
+    // MIMO in_proj at M 8192: 1048 us vs 1069 us with three stages
+    if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
     // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
     // 151936 x 768): two direct-to-LDS stages, 48 KB, so three workgroups fit a CU's LDS: 23.6 us vs
     // 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM head 74 us vs 82 us

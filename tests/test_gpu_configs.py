@@ -322,7 +322,7 @@ def test_cfg4_mimo_full_size():
             y, f = m(u.to(DEV))
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
-    for k in ("mfma32_kernel<2,4,2,2,0,1,3>", "mfma32_kernel<2,4,2,2,1,1,3>", "scan_lb_kernel<1,0,1,16,8,0>",
+    for k in ("mfma32_kernel<2,4,2,2,0,1,2>", "mfma32_kernel<2,4,2,2,1,1,2>", "scan_lb_kernel<1,0,1,16,8,0>",
               "mimo_mix_kernel<1,true,64>", "ent_scores_mimo_kernel<1>"):
         assert _has(log.kernels, k), (k, log.kernels)
     # the oracle on the causal prefix, fed the device's decisions (and, bf16, states and tanh(E) / C) for
