@@ -1180,9 +1180,12 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
   }
 
   const bool vout = vec4_ok<OUT_DT>(a.out, a.ldo);
-  if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
-    epi32_plain_staged<WM * WN, TM, TN, OUT_DT, SMEM>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
-    return;
+  // the staged epilogue needs one 32-column slab per wave in the tile's LDS (else the direct stores)
+  if constexpr (epi32_bytes<WM * WN, 1, OUT_DT>() <= SMEM) {
+    if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
+      epi32_plain_staged<WM * WN, TM, TN, OUT_DT, SMEM>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
+      return;
+    }
   }
   if (plain) {
     const int nrem = static_cast<int>(std::min<int64_t>(a.N - n0, C::BN));
@@ -2148,7 +2151,9 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // tiles to fill the chip (measured at M = 32: N = 768 .. 4096 faster split, N = 34816 staged)
     if (a.M <= 16 && a.N < 16384) return run_skinny<4, 1, 1, kEpiStore>(a, st);
     if (a.M <= 32 && a.N < 16384) return run_skinny<4, 2, 1, kEpiStore>(a, st);
-    if (a.M <= 32) return run_mfma<1, 4, 2, 1, kEpiStore>(a, st);
+    // decode-size batches over wide weights (MIMO decode in_proj, 32 x 34816 x 4096): 32x128 tiles on
+    // the 32x32x32 form, 16.5 us vs 19.3 us for 32x64 tiles on the 16x16x64 one
+    if (a.M <= 32) return run_mfma32<1, 4, 1, 1, kEpiStore>(a, st);
     // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
     // enough of them, 128x128 (4 waves of 64x64) when those still give two workgroups per CU,
     // else 64x128 (4 waves side by side along N); measured at the layer shapes (in_proj /
