@@ -215,9 +215,9 @@ def test_mimo_decode_vs_reference_fixture():
     _check_decode(got, want, meta["steps"], B, meta["H"], meta["D"], torch.float32, flips)
 
 
-def _mimo_dec(cls, seed, W, dtype):
+def _mimo_dec(cls, seed, W, dtype, D=24, H=3):
     torch.manual_seed(seed)
-    m = cls(d_model=96, d_state=24, n_heads=3, mimo_rank=2, ent_rank=8, entanglement_window=W,
+    m = cls(d_model=96, d_state=D, n_heads=H, mimo_rank=2, ent_rank=8, entanglement_window=W,
             entanglement_threshold=0.05, entanglement_scale=0.3, decay_init_bias=1.0, max_seq_len=64).eval()
     with torch.no_grad():
         gg = torch.Generator().manual_seed(seed + 7)
@@ -264,6 +264,20 @@ def test_mimo_decode_batch_tiles_vs_oracle(dtype, B):
         with hip_ops.launch_log() as log:
             m(u[:, P:P + 1].to(DEV), inference_params={"state_cache": cache})
     assert sum(k.startswith("skinny_fq_kernel<") for k in log.kernels) == 2, log.kernels
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [8, 32])
+def test_mimo_decode_wide_heads_vs_oracle(dtype, B):
+    """H * D = 4096 (long K for the output gate: sixteen 256-code blocks per product split over the
+    workgroup's waves, the configs[4] decode's shape class), call by call against the oracle."""
+    P, steps, W, H, D = 6, 3, 8, 2, 2048
+    ref = _mimo_dec(ot.TESMMIMO_Optimized, 91 + B, W, dtype, D=D, H=H)
+    m = _mimo_dec(TESMMIMO_Optimized, 91 + B, W, dtype, D=D, H=H).to(DEV)
+    gen = torch.Generator().manual_seed(B + 5)
+    u = torch.randn(B, P + steps, 96, generator=gen).to(dtype)
+    got, want, flips = _decode_lockstep(ref, m, u, None, P, steps, B, dtype)
+    _check_decode(got, want, steps, B, H, D, dtype, flips)
 
 
 def test_mimo_decode_rejects_bad_inputs():
