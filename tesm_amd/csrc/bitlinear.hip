@@ -976,8 +976,10 @@ __device__ __forceinline__ void mfma32d_mainloop(const LinearOperand& o, int64_t
                                                  int64_t Kp, v16i (&acc)[TM][TN], char* smem) {
   constexpr int NW = C::NT / 64;
   constexpr int NA = C::BM / 8, NB = C::BN / 32;  // 1 KB blocks per K tile
-  static_assert((NA + NB) % NW == 0, "DMA blocks must divide evenly over the waves");
-  constexpr int D = (NA + NB) / NW;
+  // deeper pipelines count each wave's loads in flight, so they need the same number per wave; two
+  // stages wait for all of a wave's loads, so the last blocks may leave some waves one short
+  static_assert(NS == 2 || (NA + NB) % NW == 0, "DMA blocks must divide evenly over the waves");
+  constexpr int D = (NA + NB + NW - 1) / NW;
   static_assert((NS - 2) * D < 64, "too many loads in flight for vmcnt");
   const int t = threadIdx.x;
   __builtin_assume(t < C::NT);
@@ -988,7 +990,7 @@ __device__ __forceinline__ void mfma32d_mainloop(const LinearOperand& o, int64_t
   int dst[D], adv[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
-    const int blk = w + i * NW;
+    const int blk = w + i * NW < NA + NB ? w + i * NW : NA + NB - 1;  // (blocks past the end are never issued)
     if (blk < NA) {
       const int row = blk * 8 + (lane >> 3);
       const int q = (lane & 7) ^ ((row >> 1) & 7);
@@ -1010,7 +1012,9 @@ __device__ __forceinline__ void mfma32d_mainloop(const LinearOperand& o, int64_t
     const int64_t k = kt < nk ? kt : nk - 1;
     char* stage = smem + static_cast<int>(kt % NS) * C::STAGE;
 #pragma unroll
-    for (int i = 0; i < D; ++i) lds_dma16(src[i] + k * adv[i], stage + dst[i]);
+    for (int i = 0; i < D; ++i)
+      if ((NA + NB) % NW == 0 || __builtin_amdgcn_readfirstlane(w) + i * NW < NA + NB)  // wave-uniform
+        lds_dma16(src[i] + k * adv[i], stage + dst[i]);
   };
   const int hq = 4 * (lane >> 5);
   int ar[4][TM], br[TN];
@@ -1133,15 +1137,11 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
 }
 
 // NS == 0: register-staged main loop (two LDS stages); NS >= 2: direct-to-LDS loads into NS stages.
-template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT, int NS = 0>
-__global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
+// One output tile at (m0, n0); smem holds SMEM bytes (at least the tile's stages).
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT, int NS, int SMEM>
+__device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int64_t n0, char* smem) {
   using C = Cfg32<WM, WN, TM, TN>;
-  constexpr int SMEM = (NS == 0 ? 2 : NS) * C::STAGE;
-  __shared__ __attribute__((aligned(16))) char smem[SMEM];
-  int64_t tm, tn;
-  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
-  const int64_t m0 = tm * C::BM;
-  const int64_t n0 = tn * C::BN;
+  static_assert((NS == 0 ? 2 : NS) * C::STAGE <= SMEM, "tile stages exceed the LDS given");
   v16i acc0[TM][TN], acc1[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -1294,6 +1294,37 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
         }
       }
     }
+  }
+}
+
+template <int WM, int WN, int TM, int TN, int EPI, int OUT_DT, int NS = 0>
+__global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
+  using C = Cfg32<WM, WN, TM, TN>;
+  constexpr int SMEM = (NS == 0 ? 2 : NS) * C::STAGE;
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  int64_t tm, tn;
+  xcd_tile((a.M + C::BM - 1) / C::BM, (a.N + C::BN - 1) / C::BN, tm, tn);
+  mfma32_tile<WM, WN, TM, TN, EPI, OUT_DT, NS, SMEM>(a, tm * C::BM, tn * C::BN, smem);
+}
+
+// Plain product whose 128x256 tiles would run in more rounds than the CUs hold (the SISO in_proj, 640
+// tiles): columns [0, nA) in 128x256 tiles, two per CU, and the remaining N - nA columns in 128x128
+// tiles launched after them, so the last round runs half-size tiles on more CUs.  Both use two
+// direct-to-LDS stages and eight waves.
+template <int OUT_DT>
+__global__ __launch_bounds__(512) void mfma32_split_kernel(LinearArgs a, int64_t nA) {
+  using CA = Cfg32<2, 4, 2, 2>;
+  using CB = Cfg32<2, 4, 2, 1>;
+  constexpr int SMEM = 2 * (CA::STAGE > CB::STAGE ? CA::STAGE : CB::STAGE);
+  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+  const int64_t ntm = (a.M + CA::BM - 1) / CA::BM, ntnA = nA / CA::BN, tilesA = ntm * ntnA;
+  int64_t tm, tn;
+  if (static_cast<int64_t>(blockIdx.x) < tilesA) {
+    xcd_tile_of(blockIdx.x, ntm, ntnA, tm, tn);
+    mfma32_tile<2, 4, 2, 2, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CA::BM, tn * CA::BN, smem);
+  } else {
+    xcd_tile_of(blockIdx.x - tilesA, ntm, (a.N - nA + CB::BN - 1) / CB::BN, tm, tn);
+    mfma32_tile<2, 4, 2, 1, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CB::BM, nA + tn * CB::BN, smem);
   }
 }
 
@@ -2166,7 +2197,23 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
     // 151936 x 768): two direct-to-LDS stages, 48 KB, so three workgroups fit a CU's LDS: 23.6 us vs
     // 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM head 74 us vs 82 us
-    if (tiles256 >= 512 && a.Kp <= 1024) return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
+    if (tiles256 >= 512 && a.Kp <= 1024) {
+      // more 128x256 tiles than two rounds of the CUs with a narrow remainder (the SISO in_proj: 640
+      // tiles): the columns past two tiles per CU go to 128x128 tiles (the split kernel)
+      const int cus = device_limits().cus;
+      const int64_t ntm = (a.M + 127) / 128;
+      const int64_t ntnA = cus > 0 ? std::min<int64_t>(a.N / 256, (2 * cus) / ntm) : 0;
+      const int64_t nA = ntnA * 256;
+      if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * (ntnA + (a.N - nA + 127) / 128) <= 0x7fffffff) {
+        const unsigned grid = static_cast<unsigned>(ntm * (ntnA + (a.N - nA + 127) / 128));
+        if (a.out_dt == kBF16)
+          mfma32_split_kernel<kBF16><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16>)>>>(a, nA);
+        else
+          mfma32_split_kernel<kF32><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32>)>>>(a, nA);
+        return check_launch("bitlinear mfma32 split");
+      }
+      return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
+    }
     // fewer 128x256 tiles than CUs at short K (the SISO out_proj: 8192 x 768 x 768): 64x128 tiles, two
     // direct-to-LDS stages: 10.1 us vs 10.7 us for 128x256 tiles
     if (tiles256 < 256 && a.Kp <= 1024) return run_mfma32<1, 4, 2, 1, kEpiStore, 2>(a, st);

@@ -193,10 +193,12 @@ def test_bitlinear_strict_errors():
 
 @pytest.mark.parametrize("M,K,N,ragged", [(16384, 2048, 4096, False), (16388, 2100, 4096, True), (2048, 768, 2432, False),
                                           (4096, 4096, 256, False), (4096, 2048, 1024, False),
-                                          (32, 2048, 34816, False), (20, 1000, 17000, True), (5, 4096, 16400, False)])
+                                          (32, 2048, 34816, False), (20, 1000, 17000, True), (5, 4096, 16400, False),
+                                          (8192, 768, 2432, False), (8000, 700, 2400, True)])
 def test_accumulators_bit_exact_large(M, K, N, ragged):
     """int32 accumulators of the large-tile GEMMs (direct-to-LDS main loop for K >= 2048 when N fills
-    256-wide tiles; register-staged otherwise; 32-row tiles for decode-size batches over wide weights)
+    256-wide tiles; register-staged otherwise; 32-row tiles for decode-size batches over wide weights;
+    128x256 then 128x128 tiles in one launch for the in_proj shape)
     vs the exact product: integer-valued float32 matrices multiply exactly on the device while |sums| <
     2^24 (here <= 127 * K)."""
     g = torch.Generator().manual_seed(M + K + N)
