@@ -1310,11 +1310,11 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
 // Plain product whose 128x256 tiles would run in more rounds than the CUs hold (the SISO in_proj, 640
 // tiles): columns [0, nA) in 128x256 tiles, two per CU, and the remaining N - nA columns in 128x128
 // tiles launched after them, so the last round runs half-size tiles on more CUs.  Both use two
-// direct-to-LDS stages and eight waves.
-template <int OUT_DT>
+// direct-to-LDS stages and eight waves; TMB = 32-row MFMA tiles per wave of a tail tile (2: 128 rows).
+template <int OUT_DT, int TMB>
 __global__ __launch_bounds__(512) void mfma32_split_kernel(LinearArgs a, int64_t nA) {
   using CA = Cfg32<2, 4, 2, 2>;
-  using CB = Cfg32<2, 4, 2, 1>;
+  using CB = Cfg32<2, 4, TMB, 1>;
   constexpr int SMEM = 2 * (CA::STAGE > CB::STAGE ? CA::STAGE : CB::STAGE);
   __shared__ __attribute__((aligned(16))) char smem[SMEM];
   const int64_t ntm = (a.M + CA::BM - 1) / CA::BM, ntnA = nA / CA::BN, tilesA = ntm * ntnA;
@@ -1323,8 +1323,8 @@ __global__ __launch_bounds__(512) void mfma32_split_kernel(LinearArgs a, int64_t
     xcd_tile_of(blockIdx.x, ntm, ntnA, tm, tn);
     mfma32_tile<2, 4, 2, 2, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CA::BM, tn * CA::BN, smem);
   } else {
-    xcd_tile_of(blockIdx.x - tilesA, ntm, (a.N - nA + CB::BN - 1) / CB::BN, tm, tn);
-    mfma32_tile<2, 4, 2, 1, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CB::BM, nA + tn * CB::BN, smem);
+    xcd_tile_of(blockIdx.x - tilesA, (a.M + CB::BM - 1) / CB::BM, (a.N - nA + CB::BN - 1) / CB::BN, tm, tn);
+    mfma32_tile<2, 4, TMB, 1, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CB::BM, nA + tn * CB::BN, smem);
   }
 }
 
@@ -2204,12 +2204,14 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
       const int64_t ntm = (a.M + 127) / 128;
       const int64_t ntnA = cus > 0 ? std::min<int64_t>(a.N / 256, (2 * cus) / ntm) : 0;
       const int64_t nA = ntnA * 256;
-      if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * (ntnA + (a.N - nA + 127) / 128) <= 0x7fffffff) {
-        const unsigned grid = static_cast<unsigned>(ntm * (ntnA + (a.N - nA + 127) / 128));
+      constexpr int TMB = 2;  // 128-row tail tiles (64-row ones: 26.7 against 26.1 us in the layer)
+      const int64_t ntmB = (a.M + 64 * TMB - 1) / (64 * TMB), ntnB = (a.N - nA + 127) / 128;
+      if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * ntnA + ntmB * ntnB <= 0x7fffffff) {
+        const unsigned grid = static_cast<unsigned>(ntm * ntnA + ntmB * ntnB);
         if (a.out_dt == kBF16)
-          mfma32_split_kernel<kBF16><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16>)>>>(a, nA);
+          mfma32_split_kernel<kBF16, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16, TMB>)>>>(a, nA);
         else
-          mfma32_split_kernel<kF32><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32>)>>>(a, nA);
+          mfma32_split_kernel<kF32, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32, TMB>)>>>(a, nA);
         return check_launch("bitlinear mfma32 split");
       }
       return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);

@@ -215,7 +215,7 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
         # the benchmarked in_proj instantiation (128x256 tiles for 2048 columns, 128x128 for the rest,
         # two direct-to-LDS stages), the out_proj one (64x128 tiles, two stages) and the single-pass
         # scan with the gates fused and eight sub-spans per workgroup
-        assert _has(log.kernels, f"mfma32_split_kernel<{dc}>"), log.kernels
+        assert _has(log.kernels, f"mfma32_split_kernel<{dc},2>"), log.kernels
         assert _has(log.kernels, f"mfma32_kernel<1,4,2,1,0,{dc},2>"), log.kernels
     assert _has(log.kernels, f"scan_lb_kernel<{dc},{dc},1,16,8,1>"), log.kernels
     assert _has(log.kernels, "ent_fused_kernel<") or _has(log.kernels, "ent_scores_kernel<"), log.kernels
