@@ -951,10 +951,10 @@ __device__ __forceinline__ void mfma32_mainloop(const LinearOperand& o, int64_t 
 // chunks (a row's 8 lanes read one 128-byte line, chunk q of row r lands in slot
 // r*8 + (q ^ ((r/2) % 8))), weights in blocks of 32 columns x 2 halves (half h of column n in slot
 // 2n + (h ^ ((n/8) % 2))); both make the fragment reads (16 lanes: consecutive rows or columns, one
-// chunk) hit 16 distinct 16-byte slots of 256 bytes.  Every wave issues the same number D of these
-// per K tile; the wait for tile kt is "at most (NS - 2) * D outstanding" (loads past the last K tile
-// re-read it, so the count never shrinks), then one barrier, then the refill of the stage the
-// previous tile used.
+// chunk) hit 16 distinct 16-byte slots of 256 bytes.  Each wave issues D of these per K tile (with two
+// stages the last blocks may leave some waves one short); the wait for tile kt is "at most (NS - 2) *
+// D outstanding" (loads past the last K tile re-read it, so the count never shrinks), then one
+// barrier, then the refill of the stage the previous tile used.
 template <int BM>
 __device__ __forceinline__ int a32d_off(int row, int q) { return 16 * (row * 8 + (q ^ ((row >> 1) & 7))); }
 __device__ __forceinline__ int b32d_off(int col, int h) { return 16 * (col * 2 + (h ^ ((col >> 3) & 1))); }
