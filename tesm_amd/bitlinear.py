@@ -86,7 +86,7 @@ class BitLinear(nn.Module):
     def cache_key(self):
         """Changes whenever the packed cache must be rebuilt: a new weight version, storage or dtype,
         or a new INT2 load."""
-        w = self.weight
+        w = self._parameters["weight"]
         return (w._version, w.data_ptr(), w.dtype, w.device, self._int2_gen)
 
     def packed_weight(self) -> PackedWeight:

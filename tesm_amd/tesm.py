@@ -283,8 +283,11 @@ class TESM_SISO(nn.Module):
     def _step_plan(self, B, dt, dev, cdt, W, cross):
         """The decode descriptor's fields that stay fixed from step to step, rebuilt when a shape, a
         dtype, a weight or a bias changes (the packed weights follow tesm.py:226-236's cache rule)."""
-        lins = (self.in_proj, self.state_proj, self.ent_proj, self.out_proj, self.cross_layer_q_proj)
-        db, lb = self.decay_bias, self.local_entanglement_bias
+        # modules and parameters read from their dicts: this runs once per decoded token, and
+        # nn.Module.__getattr__ costs a fraction of a microsecond per lookup
+        mods, params = self._modules, self._parameters
+        lins = (mods["in_proj"], mods["state_proj"], mods["ent_proj"], mods["out_proj"], mods["cross_layer_q_proj"])
+        db, lb = params["decay_bias"], params["local_entanglement_bias"]
         lb_key = (lb._version, lb.data_ptr()) if lb is not None else None
         key = (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
                db.data_ptr(), db.dtype, lb_key,
@@ -379,9 +382,9 @@ class TESM_SISO(nn.Module):
         cache["cache_idx"] = (slot + 1) % W
         cache["state"] = state_out
         cache["seq_pos"] = pos + 1
-        self._last_cross_layer_state = new
-        self._last_scan_state_f64 = state_out
-        self.last_entanglement_map = None
+        # plain attributes (never parameters, buffers or modules): set without nn.Module.__setattr__,
+        # which costs microseconds per call on this per-token path
+        self.__dict__.update(_last_cross_layer_state=new, _last_scan_state_f64=state_out, last_entanglement_map=None)
         return y, state_out
 
 
