@@ -219,3 +219,28 @@ def test_accumulators_bit_exact_large(M, K, N, ragged):
     # the plain (no dump) epilogue path writes the same values
     out2 = hip_ops.bitlinear(q, s, rs, packed, c_w, N, K, torch.float32)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("M,K,N", [(8192, 768, 2432), (32, 2048, 34816), (20, 1000, 3000), (2048, 4096, 4096),
+                                   (300, 768, 200)])
+def test_per_row_scale_and_bias_epilogue(M, K, N):
+    """Per-output-column weight scales (the grouped feed-forward's layout) and a bias through every
+    product family (split in_proj tiles, wide decode tiles, split-K, large tiles, small tiles): the
+    float32 output equals ((acc - rowsum) * (1 / s_x)) * c_w[n] + bias[n], each op one float32
+    rounding, computed from the kernel's own int32 accumulators (whose exactness the tests above pin)."""
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(DEV)
+    w = torch.randn(N, K, generator=g).to(DEV)
+    s_w = (1.0 / w.abs().mean(dim=1)).to(torch.float32)                 # one scale per output row of w
+    q, s, rs = hip_ops.quant_act(x)
+    packed = hip_ops.pack_weight(w, s_w, per_row=True)
+    c_w = (1.0 / s_w).contiguous()
+    bias = torch.randn(N, generator=g).to(DEV)
+    out, acc = hip_ops.bitlinear(q, s, rs, packed, c_w, N, K, torch.float32, bias=bias, c_w_per_row=True,
+                                 acc_dump=True)
+    inv = 1.0 / s                                                       # float32, as the kernels form it
+    ref = (acc.to(torch.float32) * inv[:, None]) * c_w[None, :] + bias[None, :]
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    out2 = hip_ops.bitlinear(q, s, rs, packed, c_w, N, K, torch.float32, bias=bias, c_w_per_row=True)
+    assert torch.equal(out, out2)
