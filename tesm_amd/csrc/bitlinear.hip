@@ -2195,8 +2195,9 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // MIMO in_proj at M 8192: 1048 us vs 1069 us with three stages
     if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
     // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
-    // 151936 x 768): two direct-to-LDS stages, 48 KB, so three workgroups fit a CU's LDS: 23.6 us vs
-    // 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM head 74 us vs 82 us
+    // 151936 x 768): two direct-to-LDS stages (48 KB; registers allow two workgroups per CU either
+    // way): 23.6 us vs 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM
+    // head 74 us vs 82 us
     if (tiles256 >= 512 && a.Kp <= 1024) {
       // more 128x256 tiles than two rounds of the CUs with a narrow remainder (the SISO in_proj: 640
       // tiles): the columns past two tiles per CU go to 128x128 tiles (the split kernel)
