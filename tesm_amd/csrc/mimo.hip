@@ -29,13 +29,12 @@ __global__ __launch_bounds__(256) void mimo_coef_kernel(const void* x, const voi
   x0sq[i] = x0 * x0;
 }
 
-constexpr int kMixTP = 128;          // positions per workgroup (the W - 1 halo rows re-read per 128, not 64: 0.88 against 1.01 ms at configs[4])
-constexpr int kMixNT = 512;          // threads per workgroup
+constexpr int kMixTP = 64;           // positions per workgroup
 constexpr int kMixDS = 32;           // channels per block
 constexpr int kMixSP = kMixDS + 8;   // state row pitch (floats): rows r and r + 4 fall in opposite bank halves
 constexpr int kMixWP = kMixTP + 4;   // weight row pitch (floats)
 constexpr int kMixCB = 16;           // channel blocks per workgroup
-constexpr int kMixLD = 3;            // float4 state loads per thread per block: (kMixTP + 63) * 8 <= 3 * kMixNT
+constexpr int kMixLD = 4;            // float4 state loads per thread per block: (kMixTP + 63) * 8 <= 4 * 256
 
 // Window mix for one (batch row, head) pair, kMixTP positions x kMixCB blocks of kMixDS channels.
 // Key position of window slot w is t - W + 1 + w (tesm_mimo.py:536-586); slots the reference drops
@@ -46,7 +45,7 @@ constexpr int kMixLD = 3;            // float4 state loads per thread per block:
 // one state and one weight read.  Sums run over w in increasing order.  WT is W when it is a
 // compile-time case (index math by shifts), else 0.
 template <int DT, bool VEC, int WT>
-__global__ __launch_bounds__(kMixNT) void mimo_mix_kernel(MimoMixArgs a) {
+__global__ __launch_bounds__(256) void mimo_mix_kernel(MimoMixArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_mimo[];
   const int W = WT > 0 ? WT : static_cast<int>(a.W);
   const int rows = kMixTP + W - 1;
@@ -69,7 +68,7 @@ __global__ __launch_bounds__(kMixNT) void mimo_mix_kernel(MimoMixArgs a) {
   auto prefetch = [&](int64_t cb) {
 #pragma unroll
     for (int k = 0; k < kMixLD; ++k) {
-      const int i = tid + k * kMixNT;
+      const int i = tid + k * 256;
       const int r = i >> 3, c4 = 4 * (i & 7);
       const int64_t t = tlo + r;
       const int64_t dc = cb * kMixDS + c4;
@@ -91,7 +90,7 @@ __global__ __launch_bounds__(kMixNT) void mimo_mix_kernel(MimoMixArgs a) {
   auto stage = [&]() {
 #pragma unroll
     for (int k = 0; k < kMixLD; ++k) {
-      const int i = tid + k * kMixNT;
+      const int i = tid + k * 256;
       const int r = i >> 3, c4 = 4 * (i & 7);
       if (r < rows) *reinterpret_cast<float4*>(srow + r * kMixSP + c4) = pre[k];
     }
@@ -99,7 +98,7 @@ __global__ __launch_bounds__(kMixNT) void mimo_mix_kernel(MimoMixArgs a) {
   prefetch(cb0);
   const float* wb = a.wts + ((b * a.L + t0) * a.H + h) * W;
   const int64_t wrow = a.H * W;  // floats between the weights of consecutive positions
-  for (int i = tid; i < kMixTP * W; i += kMixNT) {
+  for (int i = tid; i < kMixTP * W; i += 256) {
     const int p = i / W, w = i - p * W;
     wtT[w * kMixWP + p] = p < nvalid ? wb[p * wrow + w] : 0.0f;
   }
@@ -276,7 +275,7 @@ int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.S && a.wts && a.coef && a.te && a.cc, kErrInvalidArg, "mimo mix: null pointer");
   if (a.B == 0 || a.L == 0) return kOk;
   TESM_REQUIRE(a.B * a.H <= 65535 && (a.L + kMixTP - 1) / kMixTP <= 65535, kErrUnsupported, "mimo mix: grid too large");
-  static_assert((kMixTP + 63) * (kMixDS / 4) <= kMixLD * kMixNT, "state prefetch must cover the block and its halo");
+  static_assert((kMixTP + 63) * (kMixDS / 4) <= kMixLD * 256, "state prefetch must cover the block and its halo");
   const int64_t nblk = (a.D + kMixDS - 1) / kMixDS;
   const dim3 grid(static_cast<unsigned>((nblk + kMixCB - 1) / kMixCB), static_cast<unsigned>((a.L + kMixTP - 1) / kMixTP),
                   static_cast<unsigned>(a.B * a.H));
@@ -286,13 +285,13 @@ int launch_mimo_mix(const MimoMixArgs& a, hipStream_t st) {
                    reinterpret_cast<uintptr_t>(a.te) % (a.dt == kBF16 ? 8 : 16) == 0 &&
                    reinterpret_cast<uintptr_t>(a.cc) % (a.dt == kBF16 ? 8 : 16) == 0;
   if (a.dt == kBF16) {
-    if (vec && a.W == 64) mimo_mix_kernel<kBF16, true, 64><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 64>)>>>(a);
-    else if (vec) mimo_mix_kernel<kBF16, true, 0><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 0>)>>>(a);
-    else mimo_mix_kernel<kBF16, false, 0><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, false, 0>)>>>(a);
+    if (vec && a.W == 64) mimo_mix_kernel<kBF16, true, 64><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 64>)>>>(a);
+    else if (vec) mimo_mix_kernel<kBF16, true, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, true, 0>)>>>(a);
+    else mimo_mix_kernel<kBF16, false, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kBF16, false, 0>)>>>(a);
   } else {
-    if (vec && a.W == 64) mimo_mix_kernel<kF32, true, 64><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 64>)>>>(a);
-    else if (vec) mimo_mix_kernel<kF32, true, 0><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 0>)>>>(a);
-    else mimo_mix_kernel<kF32, false, 0><<<grid, kMixNT, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, false, 0>)>>>(a);
+    if (vec && a.W == 64) mimo_mix_kernel<kF32, true, 64><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 64>)>>>(a);
+    else if (vec) mimo_mix_kernel<kF32, true, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, true, 0>)>>>(a);
+    else mimo_mix_kernel<kF32, false, 0><<<grid, 256, lds, TESM_LOGGED(st, mimo_mix_kernel<kF32, false, 0>)>>>(a);
   }
   return check_launch("mimo mix");
 }
