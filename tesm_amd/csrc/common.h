@@ -33,7 +33,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// Two floats rounded to bf16 and packed low / high into one dword (a single conversion).
 // Workgroup barrier that orders LDS only: each wave waits for its own LDS operations, not for its
 // outstanding global loads and stores (which __syncthreads' workgroup fence would drain).
 __device__ __forceinline__ void lds_barrier() {
@@ -42,6 +41,7 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Two floats rounded to bf16 and packed low / high into one dword (a single conversion).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
