@@ -1142,23 +1142,31 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
   return run_output_path(op, st);
 }
 
-int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p) {
-  if (!p) return -1;
-  return plan_decode(*p, nullptr).total;
-}
-
-int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_bytes, void* stream) {
-  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso decode: null descriptor");
-  if (int rc = check_desc_ptrs(*pp)) return rc;
-  const tesm_hip_siso_step& p = *pp;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+// The dtype and size checks of a decode descriptor, made before any size is derived from it.
+static int validate_siso_step_sizes(const tesm_hip_siso_step& p) {
   TESM_REQUIRE(p.dt == kF32 || p.dt == kBF16, kErrInvalidArg, "siso decode: dtype must be 0 or 1");
+  // bounds that keep every size product of the step plan far inside int64
+  TESM_REQUIRE(p.B <= (int64_t(1) << 31) && p.d_model <= (int64_t(1) << 20) && p.d_state <= (int64_t(1) << 20) &&
+                   p.ent_rank <= (int64_t(1) << 20),
+               kErrInvalidArg, "siso decode: sizes out of range");
   TESM_REQUIRE(p.B >= 1 && p.d_model >= 1 && p.d_state >= 1 && p.ent_rank >= 2 && p.ent_rank % 2 == 0 &&
                    p.window >= 1 && p.window <= 64 &&
                    (p.step_pos ? p.rope_rows >= 1 : p.seq_pos >= 0 && p.cache_idx >= 0 && p.cache_idx < p.window),
                kErrInvalidArg,
                "siso decode: bad sizes or ring position (need even ent_rank, 1 <= window <= 64, rope_rows >= 1 with "
                "step_pos)");
+  return kOk;
+}
+
+int64_t tesm_hip_siso_decode_ws_bytes(const tesm_hip_siso_step* p) {
+  if (!p || validate_siso_step_sizes(*p) != kOk) return -1;
+  return plan_decode(*p, nullptr).total;
+}
+
+// Every check of a decode descriptor (shared by the entry points that run a step).
+static int validate_siso_step(const tesm_hip_siso_step& p) {
+  if (int rc = check_desc_ptrs(p)) return rc;
+  if (int rc = validate_siso_step_sizes(p)) return rc;
   TESM_REQUIRE(p.u && p.decay_bias && p.local_bias && p.rope && p.state && p.state_out && p.k_cache && p.v_cache &&
                    p.y,
                kErrInvalidArg, "siso decode: null pointer");
@@ -1168,6 +1176,14 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
   if (int rc = check_linear(p.out_proj, p.d_model, "out_proj")) return rc;
   if (p.cross_state)
     if (int rc = check_linear(p.cross_q_proj, p.d_state, "cross_q_proj")) return rc;
+  return kOk;
+}
+
+int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_bytes, void* stream) {
+  TESM_REQUIRE(pp != nullptr, kErrInvalidArg, "siso decode: null descriptor");
+  if (int rc = validate_siso_step(*pp)) return rc;
+  const tesm_hip_siso_step& p = *pp;
+  hipStream_t st = static_cast<hipStream_t>(stream);
   const DecodePlan s = plan_decode(p, ws);
   TESM_REQUIRE(ws && ws_bytes >= s.total, kErrWorkspace, "siso decode: workspace too small");
   tesm_hip_taps tp;
@@ -1305,6 +1321,8 @@ int tesm_hip_siso_decode(const tesm_hip_siso_step* pp, void* ws, int64_t ws_byte
 
 int tesm_hip_siso_decode_noalloc(const tesm_hip_siso_step* p, void* stream) {
   TESM_REQUIRE(p != nullptr, kErrInvalidArg, "no-alloc decode: null descriptor");
+  // the dtype and size errors of tesm_hip_siso_decode come before the scratch need is computed
+  if (int rc = validate_siso_step_sizes(*p)) return rc;
   const int64_t need = plan_decode(*p, nullptr).total;
   TESM_REQUIRE(need <= kNoAllocScratchBytes, kErrWorkspace,
                "no-alloc decode: the step needs " + std::to_string(need) + " bytes of scratch, more than the " +

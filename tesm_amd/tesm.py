@@ -280,18 +280,25 @@ class TESM_SISO(nn.Module):
             "cache_filled": False,
         }
 
-    def _step_plan(self, B, dt, dev, cdt, W, cross):
-        """The decode descriptor's fields that stay fixed from step to step, rebuilt when a shape, a
-        dtype, a weight or a bias changes (the packed weights follow tesm.py:226-236's cache rule)."""
+    def _step_key(self, B, dt, dev, cdt, W, cross):
+        """What the decode descriptor depends on: shapes, dtypes, thresholds, and the version and storage
+        of every weight and bias (the packed weights follow tesm.py:226-236's cache rule)."""
         # modules and parameters read from their dicts: this runs once per decoded token, and
         # nn.Module.__getattr__ costs a fraction of a microsecond per lookup
         mods, params = self._modules, self._parameters
         lins = (mods["in_proj"], mods["state_proj"], mods["ent_proj"], mods["out_proj"], mods["cross_layer_q_proj"])
         db, lb = params["decay_bias"], params["local_entanglement_bias"]
         lb_key = (lb._version, lb.data_ptr()) if lb is not None else None
-        key = (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
-               db.data_ptr(), db.dtype, lb_key,
-               tuple(p.cache_key() for p in lins))
+        return (B, dt, dev, cdt, W, cross, self.entanglement_threshold, float(self.entanglement_scale), db._version,
+                db.data_ptr(), db.dtype, lb_key, tuple(p.cache_key() for p in lins))
+
+    def _step_plan(self, B, dt, dev, cdt, W, cross):
+        """The decode descriptor's fields that stay fixed from step to step, rebuilt when a shape, a
+        dtype, a weight or a bias changes (``_step_key``)."""
+        mods, params = self._modules, self._parameters
+        lins = (mods["in_proj"], mods["state_proj"], mods["ent_proj"], mods["out_proj"], mods["cross_layer_q_proj"])
+        lb = params["local_entanglement_bias"]
+        key = self._step_key(B, dt, dev, cdt, W, cross)
         plan = self.__dict__.get("_decode_plan")
         if plan is not None and plan[0] == key:
             return plan[1]
@@ -398,7 +405,10 @@ class SisoDecodeGraph:
     read ``y`` (and ``new_state``, the next layer's cross-layer state).  ``sync_cache()`` hands state,
     position and slot back to the inference cache, after which eager steps may continue.  The graphs
     read the ring buffers of ``inference_params`` in place and need a RoPE table of ``max_positions``
-    rows; no cross-layer query (``cross_layer_state`` is not supported here)."""
+    rows; no cross-layer query (``cross_layer_state`` is not supported here).  The captured graphs hold
+    the packed weights and biases of the moment of capture: ``step()`` raises once a step would pass
+    ``max_positions`` or once a weight or bias of the layer has changed (load_state_dict, an INT2
+    load, an in-place update); build a new instance then."""
 
     def __init__(self, layer: "TESM_SISO", inference_params, max_positions: int, dtype: torch.dtype | None = None):
         if type(layer) is not TESM_SISO:
@@ -419,6 +429,9 @@ class SisoDecodeGraph:
         if max_positions <= pos:
             raise ValueError("SisoDecodeGraph: max_positions must exceed the cache's seq_pos")
         desc, nbytes, keep = layer._step_plan(B, dt, dev, kc.dtype, W, False)
+        self.layer, self._key_args = layer, (B, dt, dev, kc.dtype, W, False)
+        self._key = layer._step_key(*self._key_args)
+        self.start, self.max_positions = pos, max_positions
         dm = layer.d_model
         self.u = torch.zeros((B, 1, dm), dtype=dt, device=dev)
         self.y = torch.empty((B, 1, dm), dtype=dt, device=dev)
@@ -451,6 +464,12 @@ class SisoDecodeGraph:
 
     def step(self) -> torch.Tensor:
         """Replay one step on the current stream; returns ``y`` (B, 1, d_model), overwritten by the next."""
+        if self.start + self.k >= self.max_positions:
+            raise RuntimeError(f"SisoDecodeGraph: position {self.start + self.k} is past the RoPE table of "
+                               f"max_positions={self.max_positions}; build a new instance with more positions")
+        if self.layer._step_key(*self._key_args) != self._key:
+            raise RuntimeError("SisoDecodeGraph: the layer's weights or biases changed after capture; the graphs "
+                               "hold the old ones -- build a new instance")
         self.graphs[self.k % 2][0].replay()
         self.k += 1
         return self.y

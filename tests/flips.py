@@ -43,6 +43,10 @@ NEAR_SCORE = {torch.float32: (1e-5, 1e-4), torch.bfloat16: (2.0 ** -6, 4e-3)}
 # relative difference allowed between the two paths' per-token scales (the row's absmax)
 SCALE_REL = {torch.float32: 1e-5, torch.bfloat16: 2.0 ** -6}
 TOL = {torch.float32: 1e-3, torch.bfloat16: 2e-2}
+# bfloat16 without anything fed in: an end-to-end bound on how far the device's output drifts from the
+# oracle's own (decisions made independently), so that a bf16 regression cannot hide behind the fed
+# comparison -- rel. L2 within the north-star bf16 tolerance, the worst element within 5x it
+UNFED = {"rel_l2": 2e-2, "normwise": 1e-1, "state": 2e-2}
 
 
 class Taps:
@@ -337,7 +341,31 @@ def siso_lockstep(ref, m, u, cs, P, steps, B, dtype):
                 o[f"step{s}_vcache"] = c["ent_v_cache"].clone()
                 o[f"step{s}_cache_idx"] = c["cache_idx"]
                 o[f"step{s}_seq_pos"] = c["seq_pos"]
+    if dtype == torch.bfloat16:  # the oracle on its own, for the un-fed bound
+        free, cache = {}, ref.allocate_inference_cache(B, n)
+        with torch.no_grad():
+            if P:
+                free["prefill_y"] = ref(u[:, :P], inference_params={"state_cache": cache},
+                                        cross_layer_state=cs[:, :P] if cs is not None else None)[0]
+            for s in range(steps):
+                t = P + s
+                yr, str_ = ref(u[:, t:t + 1], inference_params={"state_cache": cache},
+                               cross_layer_state=cs[:, t] if cs is not None else None)
+                free[f"step{s}_y"], free[f"step{s}_state"] = yr.clone(), str_.clone()
+        outs[1]["unfed"] = free
     return outs[0], outs[1], flips
+
+
+def assert_unfed(y, y_ref, what, state=None, state_ref=None):
+    """bfloat16: the device output against the oracle's own, nothing fed in (``UNFED``)."""
+    a, b = np.asarray(to_np(y), np.float64), np.asarray(to_np(y_ref), np.float64)
+    r2 = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+    nw = normwise(a, b)
+    assert r2 <= UNFED["rel_l2"] and nw <= UNFED["normwise"], f"{what} un-fed: rel. L2 {r2:.3g}, normwise {nw:.3g}"
+    if state is not None:
+        ns = normwise(to_np(state), to_np(state_ref))
+        assert ns <= UNFED["state"], f"{what} un-fed final state: normwise {ns:.3g}"
+    return r2, nw
 
 
 def check_siso_steps(got, want, steps, B, dtype, flips):
@@ -364,6 +392,12 @@ def check_siso_steps(got, want, steps, B, dtype, flips):
     # decisions fed in are rare near-ties, not a systematic disagreement
     assert flips.code_flips <= max(4, 0.01 * flips.codes), flips.summary()
     assert flips.tern_flips <= max(4, 0.02 * flips.terns), flips.summary()
+    free = want.get("unfed")
+    if free is not None:
+        if "prefill_y" in got:
+            assert_unfed(got["prefill_y"], free["prefill_y"], "prefill")
+        for s in range(steps):
+            assert_unfed(got[f"step{s}_y"], free[f"step{s}_y"], f"step {s}", got[f"step{s}_state"], free[f"step{s}_state"])
 
 
 class ModelTaps:
@@ -450,6 +484,9 @@ def siso_prefill_check(ref, m, u, dtype, cs=None, h0=None):
         with Taps(B * L, D, dm, DEV, tern, d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV), cross_layer_state=cs.to(DEV) if cs is not None else None,
                      prev_state=h0.to(DEV) if h0 is not None else None)
+        if dtype == torch.bfloat16:
+            yr0, fr0 = ref(u, cross_layer_state=cs, prev_state=h0)
+            assert_unfed(y, yr0, "prefill", f, fr0)
         install(ref, flips, tp, "local" if W > 0 else "global", states=m._last_cross_layer_state)
         yr, fr = ref(u, cross_layer_state=cs, prev_state=h0)
         uninstall(ref)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from flips import Flips, Taps, assert_rows, check_siso_steps, install, siso_lockstep, uninstall
+from flips import Flips, Taps, assert_rows, assert_unfed, check_siso_steps, install, siso_lockstep, uninstall
 from hip_helpers import DEV, bf16_bits, need_gpu, normwise, to_np, unpermute_layout1
 from oracle import int_ref
 from oracle import tesm_torch as ot
@@ -53,6 +53,62 @@ def _exact_acc(q, codes):
     a = torch.from_numpy(q.astype(np.float32))
     b = torch.from_numpy(codes.astype(np.float32))
     return (a @ b.T).numpy().astype(np.int64)
+
+
+# ---------------------------------------------------------------------------------------------
+# TESMLMHeadModel(tiny()) at its stated size, B2 x L256, float32
+# ---------------------------------------------------------------------------------------------
+def test_cfg0_tiny_lm_at_size():
+    """configs[0] at B2 x L256: the model built from seed 0 (mixer_seq_simple.py:171-345), input ids
+    uniform over the vocabulary from a seed-0 generator, float32.  512 tokens run every layer product
+    on the 32x32 MFMA tiles (the fixture's 32 tokens take the split-K path).  The model takes the
+    oracle's ternary codes and scales through the INT2 export loader (the weight scale's reduction
+    order aside, bit-identical to the reference's quantization); every layer's mixer output and the
+    logits are compared with the oracle's, the device's int8 codes and ternary decisions fed in:
+    every row within 1e-3."""
+    from flips import ModelTaps
+    from oracle import int2_export
+    from tesm_amd import TESMConfig, TESMLMHeadModel
+    from tesm_amd.int2 import load_int2_weights_to_model
+    cfg = TESMConfig.tiny()
+    B, L = 2, 256
+    torch.manual_seed(0)
+    model = TESMLMHeadModel(cfg).eval()
+    torch.manual_seed(0)
+    ref = ot.TESMLMHeadModel(cfg).eval()
+    assert len(load_int2_weights_to_model(model, int2_export.export_model_to_int2(ref))) == cfg.n_layer * 8
+    model = model.to(DEV)
+    ids = torch.randint(0, cfg.vocab_size, (B, L), generator=torch.Generator().manual_seed(0))
+    flips = Flips(torch.float32)
+    outs, routs = [], []
+    with torch.no_grad():
+        hooks = [layer.mixer.register_forward_hook(lambda mod, a, out: outs.append(out[0].detach().clone()))
+                 for layer in model.backbone.layers]
+        mt = ModelTaps(model.backbone.layers, B, L)
+        with hip_ops.launch_log() as log:
+            res, finals = model(ids.to(DEV))
+            torch.cuda.synchronize()
+        mt.restore()
+        for hk in hooks:
+            hk.remove()
+        mt.install(ref.backbone.layers, flips)
+        hooks = [layer.mixer.register_forward_hook(lambda mod, a, out: routs.append(out[0].detach().clone()))
+                 for layer in ref.backbone.layers]
+        lr, _ = ref(ids)
+        for hk in hooks:
+            hk.remove()
+        uninstall(ref)
+    # the layer products at 512 rows: 64x128 MFMA tiles with two direct-to-LDS stages, f32 out
+    assert _has(log.kernels, "mfma32_kernel<1,4,2,1,0,0,2>"), log.kernels
+    assert not _has(log.kernels, "skinny"), log.kernels
+    assert len(outs) == cfg.n_layer and len(routs) == cfg.n_layer and len(finals) == cfg.n_layer
+    for i, (o, orf) in enumerate(zip(outs, routs)):
+        assert_rows(to_np(o), to_np(orf), torch.float32, f"configs[0] layer {i} mixer output ({flips.summary()})")
+    logits = res.logits
+    assert logits.shape == (B, L, cfg.vocab_size) and logits.dtype == torch.float32
+    err = assert_rows(to_np(logits), to_np(lr), torch.float32, f"configs[0] logits ({flips.summary()})")
+    print(f"configs[0] B2 x L256: worst logit row error {err:.3g}; {flips.summary()}")
+    assert flips.code_flips <= 0.01 * flips.codes and flips.tern_flips <= 0.01 * flips.terns, flips.summary()
 
 
 # ---------------------------------------------------------------------------------------------
@@ -207,6 +263,10 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
     with torch.no_grad():
         with hip_ops.launch_log() as log, Taps(B * L, D, cfg["d_model"], DEV, (B, L, W), d_state=D, dtype=dtype) as tp:
             y, f = m(u.to(DEV))
+        if dtype == torch.bfloat16:  # nothing fed in: the end-to-end drift from the oracle's own output
+            yr0, fr0 = ref(u)
+            r2, nw = assert_unfed(y, yr0, f"configs[3] {preset}", f, fr0)
+            print(f"configs[3] {preset} bf16 un-fed: rel. L2 {r2:.3g}, normwise {nw:.3g}")
         install(ref, flips, tp, "local", states=m._last_cross_layer_state)
         yr, fr = ref(u)
         uninstall(ref)
@@ -335,3 +395,49 @@ def test_cfg4_mimo_full_size():
     err = assert_rows(to_np(y[:, :Lp]), to_np(yr), dtype, f"configs[4] prefix rows ({flips.summary()})")
     print(f"configs[4] prefix: worst row error {err:.3g}; {flips.summary()}")
     assert flips.code_flips <= 0.01 * flips.codes and flips.tern_flips <= 0.01 * flips.terns, flips.summary()
+    _cfg4_states_full_length(m, tp, cfg, L)
+
+
+def _cfg4_states_full_length(m, tp, cfg, L):
+    """The rank-free states S of 64 channels (16 per head) at all 32768 positions against a float64
+    sequential recurrence on the CPU (tesm_mimo.py:375-392 with the ranks collapsed).  Its inputs are
+    rebuilt from the device run's own activation codes: the exact int32 products of the tapped in_proj
+    codes with those channels' ternary weight codes give the sv / decay / write columns, scaled and
+    rounded to bf16 as the product's epilogue does (acc * (1 / s_x) * c_w in float32), then the gates
+    in the reference's bf16 op order (tesm_mimo.py:957-975).  This covers every span of the
+    look-back chains, which the prefix comparison does not reach."""
+    H, D, dm = cfg["n_heads"], cfg["d_state"], cfg["d_model"]
+    HD = H * D
+    chans = np.array([h * D + d for h in range(H) for d in np.linspace(0, D - 1, 16).astype(int)])
+    cols = np.concatenate([dm + chans, dm + HD + chans, dm + 2 * HD + chans])  # sv, decay, write
+    pw = m.in_proj.packed_weight()
+    wc = int_ref.unpack_i2(pw.packed[torch.from_numpy(cols).to(DEV)].cpu().numpy(), dm)
+    q, sx = tp.codes("u")
+    acc = _exact_acc(q, wc)                                  # (L, 192) int64, exact
+    c_w = np.float32(pw.c_w.float().cpu()[0])
+    inv = np.float32(1.0) / sx.numpy().astype(np.float32)
+    raw = (acc.astype(np.float32) * inv[:, None]) * c_w      # float32, as the epilogue
+    raw = torch.from_numpy(raw).to(torch.bfloat16)
+    n = len(chans)
+    sv, dec, wr = raw[:, :n], raw[:, n:2 * n], raw[:, 2 * n:]
+    bias = m.decay_bias.detach().reshape(-1)[torch.from_numpy(chans).to(DEV)].cpu().to(torch.bfloat16)
+    decay = torch.sigmoid(dec + bias).double().numpy()
+    upd = (torch.sigmoid(wr).float() * torch.tanh(sv).float()).double().numpy()
+    S = np.empty((L, n))
+    h = np.zeros(n)
+    for t in range(L):
+        h = decay[t] * h + upd[t]
+        S[t] = h
+    got = tp.S[:, torch.from_numpy(chans).to(DEV)].double().cpu().numpy()
+    # per channel, normwise: a one-ulp gate difference (device vs torch transcendental at a bf16
+    # rounding boundary) moves a state by well under 1 %; a wrong carry moves it by its own size
+    den = np.abs(S).max(axis=0)
+    err = np.abs(got - S).max(axis=0) / np.maximum(den, 1e-30)
+    print(f"configs[4] states over L={L}: worst channel error {err.max():.3g}")
+    assert np.isfinite(got).all()
+    assert err.max() <= 2e-2, (err.max(), chans[err.argmax()])
+    # and position by position, past the prefix the oracle covers: every 4096-position block
+    for b0 in range(0, L, 4096):
+        blk = np.abs(got[b0:b0 + 4096] - S[b0:b0 + 4096]).max(axis=0) / np.maximum(
+            np.abs(S[b0:b0 + 4096]).max(axis=0), 1e-30)
+        assert blk.max() <= 2e-2, (b0, blk.max())

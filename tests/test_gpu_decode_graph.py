@@ -72,3 +72,26 @@ def test_graph_rejects_short_rope_table():
     ip = _prefilled(m, u, 4, 2)
     with pytest.raises(ValueError):
         SisoDecodeGraph(m, ip, max_positions=4)
+
+
+def test_graph_refuses_steps_past_table_and_stale_weights():
+    """A replay whose position would pass the RoPE table, or after the layer's weights changed, raises
+    instead of returning wrong outputs (the graphs hold the table and packed weights of capture)."""
+    m = _layer(torch.float32, 8, seed=2)
+    u = torch.randn(2, 10, 96, device=DEV)
+    ip = _prefilled(m, u, 6, 2)
+    gr = SisoDecodeGraph(m, ip, max_positions=8)   # positions 6 and 7 fit
+    for s in range(2):
+        gr.u.copy_(u[:, 6 + s:7 + s])
+        gr.step()
+    with pytest.raises(RuntimeError, match="past the RoPE table"):
+        gr.step()
+    ip2 = _prefilled(m, u, 6, 2)
+    gr2 = SisoDecodeGraph(m, ip2, max_positions=16)
+    gr2.u.copy_(u[:, 6:7])
+    gr2.step()
+    with torch.no_grad():
+        m.out_proj.weight.mul_(2.0)                # an in-place update bumps the weight version
+    with pytest.raises(RuntimeError, match="changed after capture"):
+        gr2.step()
+    torch.cuda.synchronize()

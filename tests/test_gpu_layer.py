@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from conftest import golden_meta, load_golden
-from flips import siso_prefill_check
+from flips import assert_unfed, siso_prefill_check
 from hip_helpers import DEV, TOL, need_gpu, normwise, to_np
 from oracle import tesm_torch as ot
 from tesm_amd import TESM_SISO
@@ -56,6 +56,9 @@ def test_siso_prefill_vs_reference_fixture(name):
     if dt == torch.float32:
         assert normwise(to_np(y), g["y"]) <= TOL[dt]
         np.testing.assert_allclose(fin.cpu().numpy(), g["final_state"], rtol=1e-4, atol=1e-5)
+    else:
+        # the reference's own bf16 output, nothing fed in: an end-to-end bound on the drift
+        assert_unfed(y, torch.from_numpy(g["y"]), name, fin, torch.from_numpy(g["final_state"]))
     states = m._last_cross_layer_state
     assert normwise(to_np(states), g["_parallel_state_scan/out#0"]) <= (1e-5 if dt == torch.float32 else TOL[dt])
     assert m.last_entanglement_map is None

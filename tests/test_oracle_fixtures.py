@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from conftest import golden_meta, load_golden
+from hip_helpers import bf16_bits
 from oracle import int_ref
 from oracle import tesm_torch as ot
 from tesm_amd.config import TESMConfig
@@ -241,6 +242,132 @@ def test_mimo_bf16_reference_raises_and_amendment_runs():
         y, _ = m(_t(g["u"], torch.bfloat16))
         _exact(m.in_proj(_t(g["u"], torch.bfloat16)), g["in_proj/y"], "in_proj")
     assert torch.isfinite(y.float()).all()
+
+
+def test_mimo_bf16_stage_values():
+    """The reference's own bf16 MIMO stages, recorded before its raise at tesm_mimo.py:1045: the
+    oracle's bf16 forward feeds the scan and the window entanglement exactly the reference's inputs
+    (in_proj, split and gates, RoPE: tesm_mimo.py:940-986), in the reference's dtypes (bf16 decay,
+    float32 rank update; bf16 q, k and bias against float32 states), and each stage returns exactly
+    the reference's output (tesm_mimo.py:375-392, 525-588), for every rank."""
+    g, meta = load_golden("mimo_bf16"), golden_meta("mimo_bf16")
+    m = build_mimo(meta).to(torch.bfloat16)
+    seen = {"scan": [], "ent": []}
+    scan0, ent0 = m._scan_mimo, m._local_ent_mimo
+    m._scan_mimo = lambda d, u: seen["scan"].append((d, u)) or scan0(d, u)
+    m._local_ent_mimo = lambda q, k, v, b: seen["ent"].append((q, k, v, b)) or ent0(q, k, v, b)
+    with torch.no_grad():
+        m(_t(g["u"], torch.bfloat16))
+    assert len(seen["scan"]) == len(seen["ent"]) == meta["Rm"]
+    scan_dt = (torch.bfloat16, torch.float32)
+    ent_dt = (torch.bfloat16, torch.bfloat16, torch.float32, torch.bfloat16)
+    for r in range(meta["Rm"]):
+        key = "_parallel_state_scan_mimo/{}#" + str(r)
+        for i, (a, dt) in enumerate(zip(seen["scan"][r], scan_dt)):
+            assert a.dtype == dt, (r, i, a.dtype)
+            _exact(a, g[key.format(f"arg{i}")], f"scan arg{i} rank {r}")
+        with torch.no_grad():
+            out = scan0(*(_t(g[key.format(f"arg{i}")], dt) for i, dt in enumerate(scan_dt)))
+        assert out.dtype == torch.float32
+        _exact(out, g[key.format("out")], f"scan rank {r}")
+        key = "_compute_local_entanglement_mimo/{}#" + str(r)
+        for i, (a, dt) in enumerate(zip(seen["ent"][r], ent_dt)):
+            assert a.dtype == dt, (r, i, a.dtype)
+            _exact(a, g[key.format(f"arg{i}")], f"entanglement arg{i} rank {r}")
+        with torch.no_grad():
+            out = ent0(*(_t(g[key.format(f"arg{i}")], dt) for i, dt in enumerate(ent_dt)))
+        assert out.dtype == torch.float32
+        _exact(out, g[key.format("out")], f"entanglement rank {r}")
+
+
+def _bf16_twins(make, seed):
+    """A float32 module whose parameters are bf16 values, and its bf16 copy."""
+    m32 = make(seed)
+    with torch.no_grad():
+        for p in m32.parameters():
+            p.copy_(p.bfloat16().float())
+    m16 = make(seed)
+    with torch.no_grad():
+        for p, p32 in zip(m16.parameters(), m32.parameters()):
+            p.copy_(p32)
+    return m32, m16.to(torch.bfloat16)
+
+
+def test_mimo_bf16_amendment_bounded():
+    """What ``amend_bf16`` adds where the reference raises (the merged float32 tanh(E) and C reach the
+    bf16 state_proj / ent_proj, tesm_mimo.py:1016-1045) is one round-to-nearest cast of each value to
+    bf16 -- checked exactly here -- and the amended bf16 layer stays as close to the float32 layer on
+    the same bf16-representable parameters and inputs as the reference's own SISO layer, which runs in
+    bf16 without amendment, stays to its float32 twin at the same widths and seeds (rel. L2 0.043 to
+    0.076 between the two dtypes here).  Bound: rel. L2 <= 0.08 and <= 1.5x the largest SISO gap."""
+    meta = golden_meta("mimo_bf16")
+
+    def mimo(seed):
+        return build_mimo(dict(meta, seed=seed))
+
+    def siso(seed):
+        torch.manual_seed(seed)
+        return ot.TESM_SISO(d_model=meta["dm"], d_state=meta["D"] * meta["H"], ent_rank=meta["R"],
+                            entanglement_window=meta["W"], entanglement_threshold=meta["thr"],
+                            entanglement_scale=0.2, decay_init_bias=meta["decay_bias"], max_seq_len=64).eval()
+
+    def rel_l2(a, b):
+        a, b = a.double(), b.double()
+        return float((a - b).norm() / b.norm())
+
+    gaps = {"mimo": [], "siso": []}
+    casts = []
+    for seed in (2, 5, 9):
+        u = torch.randn(meta["B"], meta["L"], meta["dm"], generator=torch.Generator().manual_seed(seed)).bfloat16()
+        for kind, make in (("mimo", mimo), ("siso", siso)):
+            m32, m16 = _bf16_twins(make, seed)
+            if kind == "mimo":
+                def hook(te, c, ent, states, where):
+                    # te / c as the amended path passes them on: one RNE cast of the float32 values
+                    assert te.dtype == c.dtype == torch.bfloat16 and ent.dtype == torch.float32
+                    assert torch.equal(te, torch.tanh(ent).to(torch.bfloat16))
+                    casts.append(where)
+                    return te, c
+                m16.mix_hook = hook
+            with torch.no_grad():
+                y32, _ = m32(u.float())
+                y16, _ = m16(u)
+            assert y16.dtype == torch.bfloat16 and torch.isfinite(y16.float()).all()
+            gaps[kind].append(rel_l2(y16, y32))
+    assert len(casts) == 3
+    assert max(gaps["mimo"]) <= min(0.08, 1.5 * max(gaps["siso"])), gaps
+
+
+def test_exact_products_vs_int_ref():
+    """``BitLinear.exact_products`` (the bf16 comparison basis of the GPU parity tests) equals the exact
+    int32 product of the C oracle's codes, scaled once: out = bf16(acc / s_x * fl(1/s_w)), with acc the
+    brute-force integer accumulator (int_ref.c), s_x the C oracle's per-token scale and fl(1/s_w) the
+    bf16 dequantized weight magnitude (tesm.py:211-215)."""
+    for M, K, N, seed in ((3, 64, 40, 0), (17, 700, 96, 1), (5, 4096, 64, 2)):
+        gen = torch.Generator().manual_seed(seed)
+        bl = ot.BitLinear(K, N).to(torch.bfloat16)
+        with torch.no_grad():
+            bl.weight.copy_(torch.randn(N, K, generator=gen).bfloat16())
+        x = (torch.randn(M, K, generator=gen) * 3).bfloat16()
+        x[0, :] = 0  # an all-zero row: eps-clamped scale, zero codes
+        bl.exact_products = True
+        with torch.no_grad():
+            y = bl(x)
+            s_w = bl.weight_scale()
+            cw = bl.quantized_weight().float().abs().max()
+        assert y.dtype == torch.bfloat16
+        wc = int_ref.weight_codes(bf16_bits(bl.weight.detach()), float(s_w.float()), bf16_bits=True)
+        q, sx = int_ref.quant_act(bf16_bits(x), bf16_bits=True)
+        acc = int_ref.bitlinear_acc(q, wc).astype(np.float64)
+        assert float(cw) == float((torch.ones((), dtype=torch.bfloat16) / s_w).float())
+        want = torch.from_numpy(acc / sx.astype(np.float64)[:, None] * float(cw)).to(torch.bfloat16)
+        _exact(y, want.float().numpy(), f"exact products M{M} K{K} N{N}")
+        # and F.linear of the dequantized bf16 operands (the reference's own arithmetic) is not exact:
+        # it differs from the exact product by rounding only
+        bl.exact_products = False
+        with torch.no_grad():
+            yf = bl(x).double()
+        assert float((yf - want.double()).abs().max()) <= 2 ** -6 * float(want.double().abs().max())
 
 
 def test_mimo_decode_fixture():

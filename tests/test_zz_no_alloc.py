@@ -82,3 +82,19 @@ def test_noalloc_decode_refuses_oversized_step():
     assert nbytes > _lib.NOALLOC_SCRATCH_BYTES
     rc = lib.tesm_hip_siso_decode_noalloc(ctypes.byref(desc), None)
     assert rc == 5 and b"scratch" in lib.tesm_hip_last_error()
+
+
+def test_noalloc_decode_rejects_bad_sizes_before_scratch():
+    """A descriptor with out-of-range sizes gets tesm_hip_siso_decode's invalid-argument error, not
+    a scratch-size one computed from overflowing products; the workspace query returns -1 for it."""
+    lib = _lib.load()
+    torch.manual_seed(0)
+    m = TESM_SISO(**CFG).to(DEV).eval()
+    for field, value in (("B", -3), ("d_model", 1 << 40), ("d_state", 0), ("window", 65)):
+        plan, _, _keep = m._step_plan(4, torch.float32, torch.device("cuda", 0), torch.float32, 16, False)
+        desc = _lib.SisoStep()  # a copy: the layer keeps its plan
+        ctypes.memmove(ctypes.byref(desc), ctypes.byref(plan), ctypes.sizeof(desc))
+        setattr(desc, field, value)
+        rc = lib.tesm_hip_siso_decode_noalloc(ctypes.byref(desc), None)
+        assert rc == 1 and b"siso decode" in lib.tesm_hip_last_error(), (field, rc, lib.tesm_hip_last_error())
+        assert lib.tesm_hip_siso_decode_ws_bytes(ctypes.byref(desc)) == -1
