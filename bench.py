@@ -50,6 +50,9 @@ def parse():
     p.add_argument("--workload", default="all",
                    choices=["all", "layer", "decode", "mimo", "global", "lm", "base", "kernels"],
                    help="run one measurement alone and print its JSON (for per-workload profiles)")
+    p.add_argument("--trace-summary", metavar="CSV", default="",
+                   help="summarize a rocprofv3 --kernel-trace CSV (per kernel and launch shape: calls, median, "
+                        "mean, min, max microseconds) as a markdown table, then exit")
     p.add_argument("--copy-calib", action="store_true",
                    help="run one 256 MiB device-to-device copy first (a known-size reference for "
                         "FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -520,8 +523,36 @@ def copy_bandwidth(torch):
     return 2 * (1 << 30) / t / 1e9, 2 * (1 << 30) / t_torch / 1e9
 
 
+def trace_summary(path: str) -> str:
+    """Per kernel and launch shape of a rocprofv3 kernel-trace CSV: calls and the median / mean / min / max
+    of end - start, in microseconds, as a markdown table sorted by total time."""
+    import csv
+    import statistics
+
+    rows = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            grid = "x".join(r[k] for k in ("Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z") if r.get(k, "1") != "1") or "1"
+            key = (r["Kernel_Name"], grid, r.get("Workgroup_Size_X", ""),
+                   f"{r.get('VGPR_Count', '')} / {r.get('Accum_VGPR_Count', '')} / {r.get('LDS_Block_Size', '')}")
+            rows.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in rows.values())
+    out = ["| kernel | grid | wg | VGPR / AGPR / LDS | calls | median us | mean us | min us | max us | % of time |",
+           "|---|---|---:|---|---:|---:|---:|---:|---:|---:|"]
+    for (name, grid, wg, regs), d in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        short = name.replace("(anonymous namespace)::", "").replace("tesm::", "")
+        short = short[5:] if short.startswith("void ") else short
+        short = short.split("(")[0][:90]
+        out.append(f"| `{short}` | {grid} | {wg} | {regs} | {len(d)} | {statistics.median(d):.2f} | "
+                   f"{statistics.fmean(d):.2f} | {min(d):.2f} | {max(d):.2f} | {100 * sum(d) / total:.1f} |")
+    return "\n".join(out)
+
+
 def main():
     args = parse()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary))
+        return
     if args.cpu_all:
         import torch
 

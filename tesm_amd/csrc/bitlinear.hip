@@ -15,6 +15,8 @@
 //   * mfma_kernel  (M > 4): LDS-tiled int8 MFMA (v_mfma_i32_16x16x64_i8).  Packed weight tiles
 //     are unpacked to int8 while being staged in LDS; A and B fragments are stored in MFMA
 //     lane order so every ds_read_b128 of a wave is one contiguous 1 KiB block.
+#include <cstdlib>
+
 #include "tesm_hip_internal.h"
 
 namespace tesm {
@@ -1920,6 +1922,302 @@ __global__ __launch_bounds__(NW * 64) void gate_rowq_lds_kernel(LinearArgs a, Ro
   }
 }
 
+// ---------------------------------------------------------------------------
+// Output gate on 32-row tiles (v_mfma_i32_32x32x32_i8).  A workgroup of NW waves owns 32 tokens and
+// all N = d_model columns (wave w: NCT 32-column tiles from 32 NCT w), so it can quantize y per
+// token for out_proj without writing y.  Per 32x32 product each unpacked weight dword serves 32
+// tokens (twice the 16-row kernel's reuse), and the epilogue is cut to the operations the reference
+// rounds (one conversion per bf16 rounding), codes written to LDS byte by byte in layout 1 (no VALU)
+// and their sums formed with v_dot4 while the tile is copied out.
+//
+// Operands: weights are the MFMA's A operand (D rows = output columns), activation codes the B
+// operand (D columns = tokens), so lane (t, h) holds token t and output columns 8 g + 4 h + r of each
+// 32-column tile.  Lane half h takes the 16-code groups h NKS .. h NKS + NKS - 1 of a row (K step ks:
+// group h NKS + ks, for both operands), so a lane's packed weight fragments are one contiguous read.
+// ---------------------------------------------------------------------------
+template <int NKS>
+struct G32 {
+  static constexpr int ARS = 32 * NKS + 16;  // staged activation row pitch: 16 rows span all banks
+};
+
+// bf16 local / gate are staged per wave in LDS (G32S: slab row pitch of NCT 32-column tiles)
+template <int NCT>
+struct G32S {
+  // 16 NCT + 2 words: an odd multiple of two words, so the 32 rows of an 8-byte read hit 64 distinct banks
+  static constexpr int SP = NCT * 64 + 8;
+};
+
+inline int64_t gate32_lds_bytes(int64_t Kp, int64_t ldq, int64_t nct, int nw, bool staged) {
+  const int64_t slab = staged ? nw * 2 * 32 * (nct * 64 + 8) : 0;
+  const int64_t codes = 32 * (ldq + 16);  // aliases the slabs when they are staged (used after them)
+  return 2 * 32 * (Kp + 16) + std::max(slab, codes) + 32 * nw * 4;
+}
+
+// a and b rounded to the layer dtype
+template <int DT>
+__device__ __forceinline__ void rnd2(float& a, float& b) {
+  a = rnd<DT>(a);
+  b = rnd<DT>(b);
+}
+
+template <int NW, int NCT, int DT, int NKS>
+__global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant o) {
+  constexpr int NT = NW * 64;
+  constexpr int ARS = G32<NKS>::ARS;
+  constexpr int ACH = 2 * 32 * 2 * NKS;        // 16-byte chunks of both operands' activation tiles
+  constexpr int AC = (ACH + NT - 1) / NT;
+  constexpr int RW = EpRaw<DT, true>::W;
+  static_assert(NKS % 4 == 0, "K steps come in 16-byte fragment loads");
+  // bf16: each wave stages its own columns of local and gate (32 rows x NCT 32-column tiles) in LDS
+  // through row-contiguous 16-byte loads, instead of one 8-byte load per lane and token row
+  constexpr bool STG = DT == kBF16;
+  constexpr int SP = G32S<NCT>::SP;
+  constexpr int SPL = 2 * 32 * NCT * 4 / 64;   // 16-byte slab chunks per lane: 4 per column tile
+  extern __shared__ __attribute__((aligned(16))) char lds_g32[];
+  char* abuf = lds_g32;                                                  // [2][32][ARS]
+  // in-tile indices fit 32 bits: N <= 1024
+  const int cp = static_cast<int>(o.ldq) + 16;                           // staged code row pitch
+  char* slabs = lds_g32 + 2 * 32 * ARS;                                  // [NW][2][32][SP] (bf16)
+  int8_t* codes = reinterpret_cast<int8_t*>(slabs);                      // [32][cp], after the slabs are read
+  const int region = STG ? NW * 2 * 32 * SP : 0;
+  float* red = reinterpret_cast<float*>(slabs + (region > 32 * cp ? region : 32 * cp));  // [NW][32]
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(tid < NT);
+  const int h = lane >> 5, row = lane & 31;
+  const int N = static_cast<int>(a.N);
+  const int col0 = w * NCT * 32;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int64_t m = m0 + row, mc = m < a.M ? m : a.M - 1;  // rows past M compute from row M - 1, never stored
+
+  // 1. every global load first, in straight-line code: packed weight fragments (lane (t, h) of column
+  //    tile c: column col0 + 32 c + t, dwords h NKS .. h NKS + NKS - 1), the activation tiles, the row
+  //    scales and sums, and the lane's local / gate values
+  uint32_t w0[NCT][NKS], w1[NCT][NKS];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int n = col0 + 32 * c + row, nc = n < N ? n : N - 1;
+    const uint4* p0 = reinterpret_cast<const uint4*>(a.op[0].w + nc * a.op[0].ldw + h * NKS * 4);
+    const uint4* p1 = reinterpret_cast<const uint4*>(a.op[1].w + nc * a.op[1].ldw + h * NKS * 4);
+#pragma unroll
+    for (int i = 0; i < NKS / 4; ++i) {
+      const uint4 v0 = p0[i], v1 = p1[i];
+      w0[c][4 * i] = v0.x, w0[c][4 * i + 1] = v0.y, w0[c][4 * i + 2] = v0.z, w0[c][4 * i + 3] = v0.w;
+      w1[c][4 * i] = v1.x, w1[c][4 * i + 1] = v1.y, w1[c][4 * i + 2] = v1.z, w1[c][4 * i + 3] = v1.w;
+    }
+  }
+  v4i ac[AC];
+#pragma unroll
+  for (int i = 0; i < AC; ++i) {
+    int g = tid + i * NT;
+    g = g < ACH ? g : ACH - 1;
+    const int p = g / (64 * NKS), rem = g - p * 64 * NKS;
+    const int r = rem / (2 * NKS), c = rem - r * 2 * NKS;
+    const int64_t mr = m0 + r < a.M ? m0 + r : a.M - 1;
+    // operand fields selected by value (a lane-dependent choice of the struct itself would be read
+    // from the kernel arguments with a vector load and a full wait)
+    const int8_t* q = p == 0 ? a.op[0].q : a.op[1].q;
+    const int64_t ldq = p == 0 ? a.op[0].ldq : a.op[1].ldq;
+    ac[i] = *reinterpret_cast<const v4i*>(q + mr * ldq + 16 * c);
+  }
+  // the loads above land first: the products wait for them only, the epilogue's below stay in flight
+  __builtin_amdgcn_sched_barrier(0);
+  const float sx0 = a.op[0].s_x[mc], sx1 = a.op[1].s_x[mc];
+  const int32_t rs0 = a.op[0].rowsum[mc], rs1 = a.op[1].rowsum[mc];
+  const float cw0 = a.op[0].c_w[0], cw1 = a.op[1].c_w[0];
+  uint32_t lr[NCT][4][RW], gr[NCT][4][RW];
+  uint4 sg[STG ? SPL : 1];
+  if constexpr (STG) {
+    // column tile by column tile (the epilogue of tile c needs only its own chunks): chunk i = 4 c + q
+    // of a lane is operand q / 2 (local, gate), row (lane + 64 (q % 2)) / 4, 16-byte chunk lane % 4
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const int c = i / 4, q = i % 4;
+      const int r = (lane >> 2) + 16 * (q & 1);
+      const int64_t mr = m0 + r < a.M ? m0 + r : a.M - 1;
+      const int cb = col0 + 32 * c + 8 * (lane & 3);
+      const int col = cb < N ? cb : N - 8;  // columns past N: never stored
+      if (q < 2)
+        sg[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.local) + mr * a.ld_local + col);
+      else
+        sg[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.gate) + mr * a.ld_gate + col);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t nb = col0 + 32 * c + 8 * g + 4 * h;
+        ep_load<DT, true>(a.local, a.ld_local, mc, nb, a.N, lr[c][g]);
+        ep_load<DT, true>(a.gate, a.ld_gate, mc, nb, a.N, gr[c][g]);
+      }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. activation tiles into LDS; the code tile's padding columns [N, ldq) are zero
+#pragma unroll
+  for (int i = 0; i < AC; ++i) {
+    const int g = tid + i * NT;
+    if (ACH % NT != 0 && g >= ACH) continue;
+    const int p = g / (64 * NKS), rem = g - p * 64 * NKS;
+    const int r = rem / (2 * NKS), c = rem - r * 2 * NKS;
+    *reinterpret_cast<v4i*>(abuf + (p * 32 + r) * ARS + 16 * c) = ac[i];
+  }
+  // LDS-only barriers throughout: the local / gate loads stay in flight under the products
+  lds_barrier();
+
+  // 3. both products: per K step, one B fragment per operand from LDS and NCT weight fragments each
+  v16i acc0[NCT], acc1[NCT];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    acc0[c] = v16i{};
+    acc1[c] = v16i{};
+  }
+  const char* xr0 = abuf + row * ARS + 16 * h * NKS;
+  const char* xr1 = abuf + (32 + row) * ARS + 16 * h * NKS;
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    const v4i x0 = *reinterpret_cast<const v4i*>(xr0 + 16 * ks);
+    const v4i x1 = *reinterpret_cast<const v4i*>(xr1 + 16 * ks);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      acc0[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w0[c][ks]), x0, acc0[c], 0, 0, 0);
+      acc1[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w1[c][ks]), x1, acc1[c], 0, 0, 0);
+    }
+  }
+
+  // the wave's local / gate slab into its own LDS region (read back by the same wave only: LDS
+  // operations of one wave complete in order, the wave barrier keeps the compiler from moving them)
+  char* slab = slabs + w * 2 * 32 * SP;
+
+  // 4. y = local + sigmoid(gate) * state_proj + ent_proj in the reference's op order (tesm.py:1256-1260),
+  //    every op rounded to the layer dtype; columns past N are 0
+  const float inv0 = 1.0f / sx0, inv1 = 1.0f / sx1;
+  float y[NCT][16];
+  float mx = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    if (col0 + 32 * c >= N) continue;  // N % 32 == 0: a column tile is all in range or all out (uniform)
+    if constexpr (STG) {
+      // this tile's local / gate chunks into the wave's own LDS slab, read back by the same wave only
+      // (LDS operations of one wave complete in order; the wave barriers keep the compiler from moving them)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = (lane >> 2) + 16 * (q & 1);
+        uint2* d = reinterpret_cast<uint2*>(slab + ((q >> 1) * 32 + r) * SP + 64 * c + 16 * (lane & 3));
+        d[0] = make_uint2(sg[4 * c + q].x, sg[4 * c + q].y);
+        d[1] = make_uint2(sg[4 * c + q].z, sg[4 * c + q].w);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if constexpr (STG) {
+        const int off = (32 * c + 8 * g + 4 * h) * 2;
+        const uint2 l2 = *reinterpret_cast<const uint2*>(slab + row * SP + off);
+        const uint2 g2 = *reinterpret_cast<const uint2*>(slab + (32 + row) * SP + off);
+        lr[c][g][0] = l2.x, lr[c][g][1] = l2.y, gr[c][g][0] = g2.x, gr[c][g][1] = g2.y;
+      }
+      float sp[4], ep[4], gv[4], v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        // (acc / s_x) * c_w as the tiled kernels form it, so that every output-gate kernel agrees bit for bit
+        sp[r] = (static_cast<float>(acc0[c][4 * g + r] - rs0) * inv0) * cw0;
+        ep[r] = (static_cast<float>(acc1[c][4 * g + r] - rs1) * inv1) * cw1;
+        gv[r] = sigmoidf_(ep_get<DT, true>(gr[c][g], r));
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        rnd2<DT>(sp[r], sp[r + 1]);
+        rnd2<DT>(ep[r], ep[r + 1]);
+        rnd2<DT>(gv[r], gv[r + 1]);
+        v[r] = gv[r] * sp[r];
+        v[r + 1] = gv[r + 1] * sp[r + 1];
+        rnd2<DT>(v[r], v[r + 1]);
+        v[r] = ep_get<DT, true>(lr[c][g], r) + v[r];
+        v[r + 1] = ep_get<DT, true>(lr[c][g], r + 1) + v[r + 1];
+        rnd2<DT>(v[r], v[r + 1]);
+        v[r] = v[r] + ep[r];
+        v[r + 1] = v[r + 1] + ep[r + 1];
+        rnd2<DT>(v[r], v[r + 1]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y[c][4 * g + r] = v[r];
+        mx = fmaxf(mx, fabsf(v[r]));
+      }
+    }
+  }
+  if (o.y && m < a.M) {  // the optional y itself (decision taps)
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nb = col0 + 32 * c + 8 * g + 4 * h;
+        if (nb < N) {
+          const float yy[4] = {y[c][4 * g], y[c][4 * g + 1], y[c][4 * g + 2], y[c][4 * g + 3]};
+          store4<DT>(o.y, m * o.ldy + nb, yy, vec4_ok<DT>(o.y, o.ldy));
+        }
+      }
+  }
+
+  // 5. per-token absmax over the workgroup's columns, then int8 codes into LDS in layout 1: column
+  //    n = 16 G + e sits at byte 16 G + 4 (e & 3) + (e >> 2); here e = 8 (g & 1) + 4 h + r
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (h == 0) red[w * 32 + row] = mx;
+  lds_barrier();  // every wave is past its slab reads: the code tile may overwrite them
+  const int padw = (static_cast<int>(o.ldq) - N) / 4;  // N % 32 == 0, ldq % 16 == 0
+  if (padw > 0)
+    for (int i = tid; i < 32 * padw; i += NT)
+      reinterpret_cast<uint32_t*>(codes + (i / padw) * cp + N)[i % padw] = 0u;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) amax = fmaxf(amax, red[i * 32 + row]);
+  const float sc = act_scale<DT>(amax, o.eps);
+  int8_t* crow = codes + row * cp + col0 + h;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    if (col0 + 32 * c >= N) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float t[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t[r] = y[c][4 * g + r] * sc;
+      rnd2<DT>(t[0], t[1]);
+      rnd2<DT>(t[2], t[3]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float q = fminf(fmaxf(rintf(t[r]), -128.0f), 127.0f);
+        crow[32 * c + 16 * (g >> 1) + 4 * r + 2 * (g & 1)] = static_cast<int8_t>(static_cast<int>(q));
+      }
+    }
+  }
+  lds_barrier();
+
+  // 6. the code tile out, row by row in 16-byte chunks; each row's code sum by v_dot4 over its chunks
+  constexpr int TPR = NT / 32;  // threads per row
+  const int r = tid / TPR, tr = tid % TPR;
+  const int chunks = static_cast<int>(o.ldq / 16);
+  const int64_t mr = m0 + r;
+  int sum = 0;
+  for (int ck = tr; ck < chunks; ck += TPR) {
+    const uint4 v = *reinterpret_cast<const uint4*>(codes + r * cp + 16 * ck);
+    sum = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, sum, false);
+    sum = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, sum, false);
+    sum = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, sum, false);
+    sum = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, sum, false);
+    if (mr < a.M) reinterpret_cast<uint4*>(o.q + mr * o.ldq)[ck] = v;
+  }
+#pragma unroll
+  for (int off = TPR / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  if (tr == 0 && mr < a.M) {
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) am = fmaxf(am, red[i * 32 + r]);
+    o.s[mr] = act_scale<DT>(am, o.eps);
+    o.rs[mr] = sum;
+  }
+}
+
 template <int WM, int WN, int TM, int TN, int EPI, int NS = 0>
 int run_mfma32(const LinearArgs& a, hipStream_t st) {
   using C = Cfg32<WM, WN, TM, TN>;
@@ -2029,6 +2327,57 @@ int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
       gate_rowq_kernel<NW, NCT, kF32, false, 0><<<grid, NW * 64, lds, TESM_LOGGED(st, gate_rowq_kernel<NW, NCT, kF32, false, 0>)>>>(a, o);
   }
   return check_launch("output gate rowq");
+}
+
+template <int NW, int NCT, int NKS>
+void launch_gate32(const LinearArgs& a, const RowQuant& o, int64_t lds, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>((a.M + 31) / 32);
+  if (a.out_dt == kBF16)
+    gate32_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kBF16, NKS>)>>>(a, o);
+  else
+    gate32_kernel<NW, NCT, kF32, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kF32, NKS>)>>>(a, o);
+}
+
+template <int NCT>
+void launch_gate32_k(const LinearArgs& a, const RowQuant& o, int64_t nks, int64_t lds, hipStream_t st) {
+  if (nks == 4)
+    launch_gate32<8, NCT, 4>(a, o, lds, st);
+  else if (nks == 8)
+    launch_gate32<8, NCT, 8>(a, o, lds, st);
+  else
+    launch_gate32<8, NCT, 12>(a, o, lds, st);
+}
+
+// The 32-row kernel when it applies: per-tensor weight scales, N a multiple of 32 up to 1024, K up to
+// 384 (register-resident weights), vector-aligned local / gate rows and an LDS budget that fits.
+int try_gate32(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
+  // TESM_HIP_NO_GATE32=1 keeps the 16-row kernel (a diagnostic switch for side-by-side timing)
+  static const bool off = [] {
+    const char* e = std::getenv("TESM_HIP_NO_GATE32");
+    return e != nullptr && e[0] == '1';
+  }();
+  const int64_t nks = a.Kp / 32;
+  if (off) return -1;
+  // bf16 slabs are read in 16-byte chunks: rows and bases 16-byte aligned
+  const bool a16 = a.out_dt != kBF16 || (reinterpret_cast<uintptr_t>(a.local) % 16 == 0 && a.ld_local % 8 == 0 &&
+                                        reinterpret_cast<uintptr_t>(a.gate) % 16 == 0 && a.ld_gate % 8 == 0);
+  if (a.op[0].c_w_per_row || a.op[1].c_w_per_row || a.N % 32 != 0 || a.N > 1024 ||
+      !(nks == 4 || nks == 8 || nks == 12) || !host_vec4_ok(a.local, a.ld_local, a.out_dt) ||
+      !host_vec4_ok(a.gate, a.ld_gate, a.out_dt) || !a16 || (o.y && !host_vec4_ok(o.y, o.ldy, a.out_dt)))
+    return -1;
+  const DeviceLimits dl = device_limits();
+  const int64_t nct = (a.N / 32 + 7) / 8;
+  const int64_t lds = gate32_lds_bytes(a.Kp, o.ldq, nct, 8, a.out_dt == kBF16);
+  if (dl.cus <= 0 || lds > dl.lds) return -1;
+  if (nct == 1)
+    launch_gate32_k<1>(a, o, nks, lds, st);
+  else if (nct == 2)
+    launch_gate32_k<2>(a, o, nks, lds, st);
+  else if (nct == 3)
+    launch_gate32_k<3>(a, o, nks, lds, st);
+  else
+    launch_gate32_k<4>(a, o, nks, lds, st);
+  return check_launch("output gate (32-row tiles)");
 }
 
 template <int LPR, int MR, int NCH, int RPG = 4>
@@ -2241,6 +2590,7 @@ int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
   TESM_REQUIRE(o.q && o.s && o.rs && o.ldq >= a.N && o.ldq % 16 == 0 && aligned(o.q, 16), kErrInvalidArg,
                "gate_rowq: bad code outputs");
   TESM_REQUIRE(!o.y || o.ldy >= a.N, kErrInvalidArg, "gate_rowq: bad y output");
+  if (const int rc = try_gate32(a, o, st); rc >= 0) return rc;
   const int64_t tiles = (a.N + 15) / 16;
   if (tiles <= 4) return run_rowq<4, 1>(a, o, st);
   if (tiles <= 8) return run_rowq<4, 2>(a, o, st);

@@ -46,11 +46,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
-// Round a float to the nearest value of the storage dtype (identity for f32).
+// Round a float to the nearest value of the storage dtype (identity for f32).  bf16: one
+// v_cvt_pk_bf16_f32 with f in the high half and 0 in the low half leaves the rounded value's float32
+// bit pattern in the register itself (no shift back).
 template <int DT>
 __device__ __forceinline__ float rnd(float f) {
   if constexpr (DT == kBF16) {
-    return bf16_to_f32(f32_to_bf16(f));
+    return __uint_as_float(pack_bf16x2(0.0f, f));
   } else {
     return f;
   }
