@@ -48,8 +48,9 @@ def parse():
                         "the affinity core count and on one thread, print their JSON and exit (slow)")
     p.add_argument("--only", default="", help="comma list of isolated kernels to run (profiling)")
     p.add_argument("--workload", default="all",
-                   choices=["all", "layer", "decode", "mimo", "global", "lm", "base", "kernels"],
+                   choices=["all", "layer", "decode", "mimo", "global", "lm", "base", "kernels", "in_proj"],
                    help="run one measurement alone and print its JSON (for per-workload profiles)")
+    p.add_argument("--mimo-reps", type=int, default=3, help="timed configs[4] forwards (profiles use more)")
     p.add_argument("--trace-summary", metavar="CSV", default="",
                    help="summarize a rocprofv3 --kernel-trace CSV (per kernel and launch shape: calls, median, "
                         "mean, min, max microseconds) as a markdown table, then exit")
@@ -125,8 +126,11 @@ def measure_kernels(torch, only):
         del packs
     # SISO scan + local entanglement at small() dims, W=16, B8 x L512, bf16
     Bs, Ls, D, R, W = 8, 512, 256, 48, 16
+    def rotation(set_bytes):  # distinct input sets covering >= 512 MiB, past the 256 MB Infinity Cache
+        return (512 << 20) // set_bytes + 1
+
     if sel("scan_small"):
-        nrot = 80
+        nrot = rotation(Bs * Ls * D * 2 * 3)  # decay, update in; states out
         sets = [(torch.sigmoid(torch.randn(Bs, Ls, D, device=dev, generator=gen)).to(torch.bfloat16),
                  torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
         t = time_back_to_back(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100)
@@ -135,7 +139,7 @@ def measure_kernels(torch, only):
                              "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
         del sets
     if sel("local_ent_small"):
-        nrot = 80
+        nrot = rotation(Bs * Ls * (2 * R + 2 * D) * 2)  # q, k, states in; window average out
         rope = hip_ops.rope_table(Ls, R, torch.bfloat16, dev)
         bias = torch.randn(W, device=dev, generator=gen) * 0.3
         sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
@@ -148,7 +152,7 @@ def measure_kernels(torch, only):
                                   "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
         del sets
     if sel("local_ent_quant_small"):
-        nrot = 80
+        nrot = rotation(Bs * Ls * (2 * R * 2 + D * 2 + 2 * (D + 8)))
         rope = hip_ops.rope_table(Ls, R, torch.bfloat16, dev)
         bias = torch.randn(W, device=dev, generator=gen) * 0.3
         sets = [(torch.randn(Bs, Ls, R, device=dev, generator=gen).to(torch.bfloat16),
@@ -298,6 +302,22 @@ def measure_global(torch, steps: int = 10):
     ms = e0.elapsed_time(e1) / steps
     return {"workload": "TESM_SISO prefill with entanglement_window=0 (global causal ternary entanglement), "
                         "configs[3] dims, B4 x L2048, bf16", "ms_per_forward": ms, "tokens_per_s": B * L / (ms * 1e-3)}
+
+
+def measure_in_proj(torch, m, u, n: int = 50):
+    """The layer's in_proj GEMM (M=8192, K=768, N=2432, bf16 out) launched n times back to back on the
+    stream it runs on, timed with one event pair: the roofline's per-launch figure."""
+    from tesm_amd import hip_ops
+
+    dev = torch.device("cuda:0")
+    M, K = B * L, LAYER["d_model"]
+    N = m.in_proj.out_features
+    pw = m.in_proj.packed_weight()
+    q, s, rs = hip_ops.quant_act(u.reshape(M, K))
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    t = time_back_to_back(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K, torch.bfloat16,
+                                                             out=out), n)
+    return t, 2 * M * N * K, M * K + N * (K // 4) + 8 * M + 2 * M * N
 
 
 def measure_mimo(torch, reps: int = 3):
@@ -594,7 +614,10 @@ def main():
             elif args.workload == "decode":
                 res = measure_decode(torch, m)
             elif args.workload == "mimo":
-                res = measure_mimo(torch)
+                res = measure_mimo(torch, reps=args.mimo_reps)
+            elif args.workload == "in_proj":
+                t, ops, nbytes = measure_in_proj(torch, m, u, n=args.steps)
+                res = {"us": t * 1e6, "TOP_per_s": ops / t / 1e12, "frac_of_int8_peak": ops / t / 1e12 / INT8_PEAK_TOPS}
             elif args.workload == "global":
                 res = measure_global(torch)
             elif args.workload == "base":
@@ -622,12 +645,7 @@ def main():
         # dominant kernel: the in_proj GEMM of the same layer on the same stream
         M, K = B * L, LAYER["d_model"]
         N = m.in_proj.out_features
-        pw = m.in_proj.packed_weight()
-        q, s, rs = hip_ops.quant_act(u.reshape(M, K))
-        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-        t_gemm = time_back_to_back(torch, lambda i: hip_ops.bitlinear(q, s, rs, pw.packed, pw.c_w, N, K,
-                                                                      torch.bfloat16, out=out), 50)
-        ops = 2 * M * N * K
+        t_gemm, ops, _ = measure_in_proj(torch, m, u, n=100)
         decode = measure_decode(torch, m)
         mimo = None if args.no_mimo else measure_mimo(torch)
         glob = measure_global(torch)
@@ -667,8 +685,10 @@ def main():
                      "achieved": ops / t_gemm / 1e12, "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                      "frac": ops / t_gemm / 1e12 / INT8_PEAK_TOPS, "traffic": gemm_traffic(), "us": t_gemm * 1e6,
                      "algorithmic_bytes": M * K + N * (K // 4) + 8 * M + 2 * M * N,
-                     "note": "int8 ops/s (TOP/s) against the 5.0 POP/s dense int8 MFMA peak; traffic = HBM bytes "
-                             "per launch from profiles/in_proj_gemm_traffic.json"},
+                     "note": "int8 ops/s (TOP/s) against the 5.0 POP/s dense int8 MFMA peak; us = 100 back-to-back "
+                             "launches between one event pair (rocprof medians: profiles/in_proj_gemm_isolated.md, and "
+                             "inside the layer: profiles/siso_layer_kernels_base_bf16.md); traffic = HBM bytes per "
+                             "launch from profiles/in_proj_gemm_traffic.json"},
         "decode": decode,
         "mimo_layer": mimo,
         "global_layer": glob,

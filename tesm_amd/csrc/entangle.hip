@@ -17,6 +17,8 @@
 //     applied on the fly from a (L, R/2) cos/sin table; writes normalised weights (B, L, H, W).
 //   * ent_mix_kernel: a workgroup per (row, 64 positions, 64 channels) stages the state halo
 //     (64 + W - 1 rows) in LDS and forms the window sums, the mix and tanh in one pass.
+#include <cstdlib>
+
 #include "entangle.h"
 #include "tesm_hip_internal.h"
 
@@ -710,6 +712,327 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
   }
 }
 
+// Fused SISO kernel, second form: 32 threads per position, each owning an 8-channel slice (D <= 512,
+// D % 8 == 0), 16 positions per workgroup of 512 threads -- twice the waves of ent_fused_kernel on the
+// same work.  The state halo is converted to float32 once while it is staged (instead of once per
+// window row that reads it), in chunk order (q, s): the 16-byte half q of slice s at chunk
+// q * nsl + s, so the 16 lanes of a read pass take 256 contiguous bytes.  The arithmetic and its
+// order are ent_fused_kernel's, so the two give the same bits.  Layout-1 codes of a 16-channel group
+// come from a lane pair (slices 2g, 2g + 1): each lane forms its two bytes of every dword, the pair
+// swaps them, the even lane stores the group.
+constexpr int kF2TP = 16;
+constexpr int kF2TPP = 32;
+constexpr int kF2MaxSPT = 2;
+
+struct Fused2Lds {
+  int64_t kr, qr, wn, sx, total;  // byte offsets
+  int64_t krs;                    // row stride of kr / qr in floats
+  int64_t nsl;                    // 8-channel slices per row
+};
+
+__host__ __device__ inline Fused2Lds fused2_lds(int64_t R, int64_t D, int64_t weff) {
+  Fused2Lds f;
+  const int64_t rows = kF2TP + weff - 1;
+  f.krs = R + 4;
+  f.nsl = D / 8;
+  f.kr = 0;
+  f.qr = f.kr + rows * f.krs * 4;
+  f.wn = f.qr + kF2TP * f.krs * 4;
+  f.sx = (f.wn + kF2TP * weff * 4 + 15) / 16 * 16;
+  f.total = f.sx + rows * f.nsl * 32;
+  return f;
+}
+
+template <int DT>
+__global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff, Fused2Lds f) {
+  using T = typename Elem<DT>::T;
+  extern __shared__ __attribute__((aligned(16))) char lds_f2[];
+  float* kr = reinterpret_cast<float*>(lds_f2 + f.kr);
+  float* qr = reinterpret_cast<float*>(lds_f2 + f.qr);
+  float* wn = reinterpret_cast<float*>(lds_f2 + f.wn);
+  float* sx = reinterpret_cast<float*>(lds_f2 + f.sx);
+  const int tid = threadIdx.x;
+  __builtin_assume(tid < 512);
+  const int64_t b = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kF2TP;
+  const int half = static_cast<int>(a.R / 2), D = static_cast<int>(a.D), W = static_cast<int>(weff);
+  const int krs = static_cast<int>(f.krs), nsl = static_cast<int>(f.nsl);
+  const int rows = kF2TP + W - 1;
+  const int64_t tk0 = t0 - (W - 1);  // position of key row 0
+  const int p = tid / kF2TPP, h8 = tid % kF2TPP;
+
+  // window bias of the thread's score slots w = h8, h8 + 32 (read first, used after the LDS phase)
+  float wbias[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int w = h8 + 32 * i;
+    wbias[i] = a.bias[a.W - W + (w < W ? w : W - 1)];
+  }
+
+  // 1. staging: keys and queries RoPE'd into float32 rows, the state halo converted to float32.  All of
+  //    a thread's loads are requested before any is used; rows outside [0, L) are zero.
+  const T* S = static_cast<const T*>(a.S);
+  {
+    constexpr int kSI = 4, kKI = 4, kQI = 2;  // items per thread (checked on the host)
+    v4i sv[kSI][DT == kBF16 ? 1 : 2];
+    int sr[kSI], ss[kSI];
+#pragma unroll
+    for (int k = 0; k < kSI; ++k) {
+      const int i = tid + 512 * k;
+      const int r = i / nsl, sl = i - r * nsl;
+      sr[k] = r;
+      ss[k] = sl;
+      int64_t tt = tk0 + (r < rows ? r : rows - 1);
+      tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
+      const T* src = S + (b * a.L + tt) * a.ld_s + 8 * sl;
+      sv[k][0] = *reinterpret_cast<const v4i*>(src);
+      if constexpr (DT != kBF16) sv[k][1] = *reinterpret_cast<const v4i*>(src + 4);
+    }
+    float kxa[kKI], kxb[kKI], qxa[kQI], qxb[kQI], qaa[kQI], qab[kQI];
+    float2 kcs[kKI], qcs[kQI];
+#pragma unroll
+    for (int k = 0; k < kKI; ++k) {
+      const int i = tid + 512 * k;
+      const int r = i / half, c = i - r * half;
+      int64_t tt = tk0 + (r < rows ? r : rows - 1);
+      tt = tt < 0 ? 0 : (tt >= a.L ? a.L - 1 : tt);
+      const int64_t ko = (b * a.L + tt) * a.ld_k;
+      kxa[k] = ld<DT>(a.k, ko + c);
+      kxb[k] = ld<DT>(a.k, ko + half + c);
+      kcs[k] = a.rope[tt * half + c];
+    }
+#pragma unroll
+    for (int k = 0; k < kQI; ++k) {
+      const int i = tid + 512 * k;
+      const int pp = i / half, c = i - pp * half;
+      const int64_t tt = (t0 + pp < a.L) ? t0 + pp : a.L - 1;
+      const int64_t qo = (b * a.L + tt) * a.ld_q;
+      qxa[k] = ld<DT>(a.q, qo + c);
+      qxb[k] = ld<DT>(a.q, qo + half + c);
+      qcs[k] = a.rope[tt * half + c];
+      qaa[k] = qab[k] = 0.0f;
+      if (a.q_add) {
+        const int64_t ao = (b * a.L + tt) * a.ld_qadd;
+        qaa[k] = ld<DT>(a.q_add, ao + c);
+        qab[k] = ld<DT>(a.q_add, ao + half + c);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSI; ++k) {
+      const int r = sr[k];
+      if (r >= rows) break;
+      const int64_t tt = tk0 + r;
+      const bool ok = tt >= 0 && tt < a.L;
+      float x[8];
+      if constexpr (DT == kBF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t wd = static_cast<uint32_t>(sv[k][0][i]);
+          x[2 * i] = ok ? __uint_as_float(wd << 16) : 0.0f;
+          x[2 * i + 1] = ok ? __uint_as_float(wd & 0xffff0000u) : 0.0f;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = ok ? __int_as_float(sv[k][i >> 2][i & 3]) : 0.0f;
+      }
+      float* row = sx + static_cast<int64_t>(r) * nsl * 8;
+      *reinterpret_cast<float4*>(row + 4 * ss[k]) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(row + 4 * (nsl + ss[k])) = make_float4(x[4], x[5], x[6], x[7]);
+    }
+#pragma unroll
+    for (int k = 0; k < kKI; ++k) {
+      const int i = tid + 512 * k;
+      const int r = i / half, c = i - r * half;
+      if (r >= rows) break;
+      const int64_t tt = tk0 + r;
+      float o1 = 0.0f, o2 = 0.0f;
+      if (tt >= 0 && tt < a.L) rope_pair<DT>(kxa[k], kxb[k], kcs[k], o1, o2);
+      kr[r * krs + c] = o1;
+      kr[r * krs + half + c] = o2;
+    }
+#pragma unroll
+    for (int k = 0; k < kQI; ++k) {
+      const int i = tid + 512 * k;
+      const int pp = i / half, c = i - pp * half;
+      if (pp >= kF2TP) break;
+      float o1 = 0.0f, o2 = 0.0f;
+      if (t0 + pp < a.L) {
+        rope_pair<DT>(qxa[k], qxb[k], qcs[k], o1, o2);
+        if (a.q_add) {
+          o1 = rnd<DT>(o1 + qaa[k]);
+          o2 = rnd<DT>(o2 + qab[k]);
+        }
+      }
+      qr[pp * krs + c] = o1;
+      qr[pp * krs + half + c] = o2;
+    }
+  }
+  __syncthreads();
+
+  const int64_t t = t0 + p;
+  const bool tok = t < a.L;
+  // 2. window scores, ternary decisions and their normalisation (ent_fused_kernel's arithmetic)
+  {
+    const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
+    const int half4 = (half % 4 == 0) ? half : 0;
+    float tern[2];
+    float n = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int w = h8 + 32 * i;
+      tern[i] = 0.0f;
+      if (w >= W) continue;
+      const int64_t j = t - (W - 1) + w;
+      if (tok && j >= 0) {
+        const float* qp = qr + p * krs;
+        const float* kp = kr + (p + w) * krs;
+        float dot = 0.0f;
+        for (int c = 0; c < half4; c += 4) {
+          const float4 qa = *reinterpret_cast<const float4*>(qp + c);
+          const float4 ka = *reinterpret_cast<const float4*>(kp + c);
+          const float4 qb = *reinterpret_cast<const float4*>(qp + half + c);
+          const float4 kb = *reinterpret_cast<const float4*>(kp + half + c);
+          dot += qa.x * ka.x;
+          dot += qb.x * kb.x;
+          dot += qa.y * ka.y;
+          dot += qb.y * kb.y;
+          dot += qa.z * ka.z;
+          dot += qb.z * kb.z;
+          dot += qa.w * ka.w;
+          dot += qb.w * kb.w;
+        }
+        for (int c = half4; c < half; ++c) {
+          dot += qp[c] * kp[c];
+          dot += qp[half + c] * kp[half + c];
+        }
+        float sc = rnd<DT>(rnd<DT>(dot) / sq);
+        sc = rnd<DT>(sc + wbias[i]);
+        tern[i] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);
+      }
+      n += fabsf(tern[i]);
+      if (a.tern && tok) a.tern[(b * a.L + t) * W + w] = static_cast<int8_t>(tern[i]);
+    }
+    n = wave_sum_f<kF2TPP>(n);
+    n = fmaxf(n, 1.0f);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int w = h8 + 32 * i;
+      if (w < W) wn[p * W + w] = rnd<DT>(tern[i] / n);
+    }
+  }
+  __syncthreads();
+
+  // 3. window sums, mix and tanh of the thread's slices
+  float tv[kF2MaxSPT][8], cv[kF2MaxSPT][8];
+  float mx_t = 0.0f, mx_c = 0.0f;
+#pragma unroll
+  for (int si = 0; si < kF2MaxSPT; ++si) {
+    const int sl = h8 + kF2TPP * si;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      tv[si][e] = 0.0f;
+      cv[si][e] = 0.0f;
+    }
+    if (sl >= nsl || !tok) continue;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    auto row8 = [&](int r, float (&x)[8]) {
+      const float* rp = sx + static_cast<int64_t>(r) * nsl * 8;
+      const float4 lo = *reinterpret_cast<const float4*>(rp + 4 * sl);
+      const float4 hi = *reinterpret_cast<const float4*>(rp + 4 * (nsl + sl));
+      x[0] = lo.x, x[1] = lo.y, x[2] = lo.z, x[3] = lo.w, x[4] = hi.x, x[5] = hi.y, x[6] = hi.z, x[7] = hi.w;
+    };
+    int w = 0;
+    for (; w + 4 <= W; w += 4) {  // four rows' reads in flight; each channel sums w = 0, 1, .. in order
+      float x[4][8], wt[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        row8(p + w + u, x[u]);
+        wt[u] = wn[p * W + w + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += wt[u] * x[u][e];
+    }
+    for (; w < W; ++w) {
+      float x[8];
+      row8(p + w, x);
+      const float wt = wn[p * W + w];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += wt * x[e];
+    }
+    float sv[8];
+    row8(p + W - 1, sv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = 8 * sl + e;
+      const float avg = rnd<DT>(acc[e]);
+      const float s0 = sv[e];
+      const float ev = rnd<DT>(s0 + rnd<DT>(a.ent_scale * rnd<DT>(avg - s0)));
+      cv[si][e] = rnd<DT>(ev - s0);
+      tv[si][e] = rnd<DT>(tanhf_(ev));
+      mx_t = fmaxf(mx_t, fabsf(tv[si][e]));
+      mx_c = fmaxf(mx_c, fabsf(cv[si][e]));
+      if (a.e_tanh || a.c_out) {
+        const int64_t o = (b * a.L + t) * a.ld_out + c;
+        if (a.c_out) st<DT>(a.c_out, o, cv[si][e]);
+        if (a.e_tanh) st<DT>(a.e_tanh, o, tv[si][e]);
+      }
+    }
+  }
+  // 4. per-token scales and codes (tesm.py:206-209); a position's 32 lanes share its row
+  mx_t = wave_max<kF2TPP>(mx_t);
+  mx_c = wave_max<kF2TPP>(mx_c);
+  const float sc_t = act_scale<DT>(mx_t, a.eps);
+  const float sc_c = act_scale<DT>(mx_c, a.eps);
+  int sum_t = 0, sum_c = 0;
+  const int64_t row = b * a.L + t;
+  const int ngq = static_cast<int>(a.ldq / 16), groups = D / 16;
+#pragma unroll
+  for (int si = 0; si < kF2MaxSPT; ++si) {
+    const int sl = h8 + kF2TPP * si, g = sl >> 1, hh = sl & 1;
+    if (2 * (kF2TPP * si) >= 2 * nsl) break;  // no thread of this round has a slice (uniform)
+    // layout 1: byte 4s + j of the group holds code 4j + s; this lane's codes e = 8 hh + i sit at
+    // bytes 4 (i & 3) + 2 hh + (i >> 2)
+    uint32_t pt[4] = {0, 0, 0, 0}, pc[4] = {0, 0, 0, 0};
+    if (sl < nsl && tok) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c1 = act_code<DT>(tv[si][i], sc_t), c2 = act_code<DT>(cv[si][i], sc_c);
+        sum_t += c1;
+        sum_c += c2;
+        const int sh = 8 * (2 * hh + (i >> 2));
+        pt[i & 3] |= (static_cast<uint32_t>(c1) & 0xffu) << sh;
+        pc[i & 3] |= (static_cast<uint32_t>(c2) & 0xffu) << sh;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pt[q] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(pt[q]), 1, 64));
+      pc[q] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(pc[q]), 1, 64));
+    }
+    if (tok && hh == 0 && g < ngq) {
+      reinterpret_cast<uint4*>(a.q_te + row * a.ldq)[g] = make_uint4(pt[0], pt[1], pt[2], pt[3]);
+      reinterpret_cast<uint4*>(a.q_c + row * a.ldq)[g] = make_uint4(pc[0], pc[1], pc[2], pc[3]);
+    }
+  }
+  // code groups of the padding (ldq > D) are zero
+  for (int g = groups + h8; tok && g < ngq; g += kF2TPP) {
+    reinterpret_cast<uint4*>(a.q_te + row * a.ldq)[g] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(a.q_c + row * a.ldq)[g] = make_uint4(0, 0, 0, 0);
+  }
+  sum_t = wave_sum_i<kF2TPP>(sum_t);
+  sum_c = wave_sum_i<kF2TPP>(sum_c);
+  if (tok && h8 == 0) {
+    a.s_te[row] = sc_t;
+    a.rs_te[row] = sum_t;
+    a.s_c[row] = sc_c;
+    a.rs_c[row] = sum_c;
+  }
+}
+
 template <int DT, int MIMO>
 int run_scores(const EntArgs& a, int64_t weff, hipStream_t st) {
   if (MIMO && a.q_add == nullptr) {
@@ -754,6 +1077,16 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
 
+// TESM_HIP_NO_ENT_FUSED2=1 keeps the 16-threads-per-position kernel (a diagnostic switch for
+// side-by-side timing and bit-for-bit comparison)
+static bool no_f2() {
+  static const bool off = [] {
+    const char* e = std::getenv("TESM_HIP_NO_ENT_FUSED2");
+    return e != nullptr && e[0] == '1';
+  }();
+  return off;
+}
+
 bool ent_fused_ok(const EntArgs& a) {
   if (a.mimo || a.H != 1 || a.D > 16 * 16 * kFusedMaxGPT) return false;
   const int64_t weff = eff_window(a);
@@ -794,6 +1127,23 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
       return rows * half <= 256 * si && kFusedTP * half <= 256 * (si / 2) && rows * nvec <= 256 * si;
     };
     const bool big = !fits(4) && fits(8);
+    // the 32-threads-per-position form: D % 16 == 0 up to 512, its load items within 4 / 4 / 2 per thread,
+    // 16-byte aligned state rows, LDS within 64 KB
+    {
+      const Fused2Lds f2 = fused2_lds(a.R, a.D, weff);
+      const int64_t nsl = a.D / 8;
+      const bool ok2 = a.D % 16 == 0 && a.D <= 512 && rows * nsl <= 512 * 4 && rows * half <= 512 * 4 &&
+                       kF2TP * half <= 512 * 2 && weff <= 64 && a.ld_s % 8 == 0 && aligned(a.S, 16) &&
+                       f2.total <= 64 * 1024 && !no_f2();
+      if (ok2) {
+        dim3 grid2(static_cast<unsigned>((a.L + kF2TP - 1) / kF2TP), static_cast<unsigned>(a.B));
+        if (a.dt == kBF16)
+          ent_fused2_kernel<kBF16><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kBF16>)>>>(a, weff, f2);
+        else
+          ent_fused2_kernel<kF32><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kF32>)>>>(a, weff, f2);
+        return check_launch("entanglement fused (32 threads per position)");
+      }
+    }
     if (a.dt == kBF16) {
       if (big)
         ent_fused_kernel<kBF16, 8><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16, 8>)>>>(a, weff, f);
