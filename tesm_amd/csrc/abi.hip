@@ -1568,10 +1568,32 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
                              scan_zero_n)))
     return rc;
   if (tapping && (rc = tap_codes(tp.q_u, tp.s_u, s.xu, M, st))) return rc;
-  if ((rc = run_linear(s.xu, p.in_proj, M, n_in, dm, proj, dt, n_in, st))) return rc;
-  // 2. gates + rank-free state scan: sequential float32 recurrence h = d h + w tanh(sv) per channel
+  // in_proj with the scan's gates applied in its epilogue (tesm_mimo.py:958-961) where its kernels
+  // allow it (M > 32 and 32-column aligned regions), so the scan only streams them; else the scan
+  // applies them to the raw slices.  TESM_HIP_NO_GATE_EPI=1 keeps the latter (a diagnostic switch,
+  // read per call, for side-by-side timing and bit-for-bit comparison: the values are the same).
+  const char* no_gate_epi = std::getenv("TESM_HIP_NO_GATE_EPI");
+  const bool gate_epi = M > 32 && dm % 32 == 0 && HD % 32 == 0 && !(no_gate_epi && no_gate_epi[0] == '1');
+  {
+    LinearArgs la;
+    la.op[0] = operand(s.xu, p.in_proj);
+    la.M = M;
+    la.N = n_in;
+    la.Kp = kpad(dm);
+    la.out = proj;
+    la.out_dt = dt;
+    la.ldo = n_in;
+    if (gate_epi) {
+      la.epilogue = kEpiGates;
+      la.act_n0 = o_sv;  // state value, then decay, then write (o_decay = o_sv + HD, o_write = o_sv + 2 HD)
+      la.act_w = HD;
+      la.act_bias = p.decay_bias;
+    }
+    if ((rc = launch_linear(la, st))) return rc;
+  }
+  // 2. rank-free state scan: sequential float32 recurrence h = d h + w tanh(sv) per channel
   ScanArgs sa;
-  sa.mode = 1;
+  sa.mode = gate_epi ? 2 : 1;
   sa.dt = dt;
   sa.out_dt = kF32;
   sa.clamp = 0;

@@ -357,6 +357,32 @@ __device__ __forceinline__ float dual_epi(float p0, float p1, float local, float
   }
 }
 
+// kEpiGates: the region of the 32-column tile that starts at column n (0: stored as is, 1: tanh,
+// 2: biased sigmoid, 3: sigmoid).  act_n0 and act_w are multiples of 32, so a tile lies in one region
+// and the region is uniform over the wave.
+__device__ __forceinline__ int gate_region(const LinearArgs& a, int64_t n) {
+  const int64_t r = n - a.act_n0;
+  return r < 0 ? 0 : r < a.act_w ? 1 : r < 2 * a.act_w ? 2 : r < 3 * a.act_w ? 3 : 0;
+}
+
+// The MIMO gates on four consecutive columns n .. n + 3 of one region (tesm_mimo.py:958-961), each
+// on the product rounded to the output dtype: the float ops a scan would apply to the stored
+// products, so the values it reads are the ones it would have computed.
+template <int DT>
+__device__ __forceinline__ void gate_act4(const LinearArgs& a, int kind, int64_t n, float (&v)[4]) {
+  if (kind == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = rnd<DT>(tanhf_(rnd<DT>(v[r])));
+  } else if (kind == 2) {
+    const int64_t c = n - a.act_n0 - a.act_w;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = rnd<DT>(sigmoidf_(rnd<DT>(rnd<DT>(v[r]) + ld<DT>(a.act_bias, c + r))));
+  } else if (kind == 3) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = rnd<DT>(sigmoidf_(rnd<DT>(v[r])));
+  }
+}
+
 // General epilogue of the 16 x 16 tiles of one wave (tile rows wm*TM.., columns wn*TN..): scale the
 // exact accumulators, optional bias / accumulator dump, or the output gate
 // y = local + sigmoid(gate) * state_proj + ent_proj in the module dtype's op order.
@@ -1077,7 +1103,7 @@ constexpr int epi32_bytes() {
   return NWV * 32 * (JU * 32 * (OUT_DT == kBF16 ? 2 : 4) + 16);
 }
 
-template <int NWV, int TM, int TN, int OUT_DT, int AVAIL>
+template <int NWV, int TM, int TN, int OUT_DT, int AVAIL, bool GATES>
 __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v16i (&acc)[TM][TN], const float (&sx)[TM],
                                                    const int32_t (&rsum)[TM], float cws, int64_t m0, int64_t n0,
                                                    int wm, int wn, char* smem) {
@@ -1100,11 +1126,14 @@ __device__ __forceinline__ void epi32_plain_staged(const LinearArgs& a, const v1
       lds_barrier();  // the buffer's previous contents (or the last K tile) are consumed
 #pragma unroll
       for (int jj = 0; jj < JU; ++jj) {
+        const int64_t nt = n0 + (wn * TN + jb + jj) * 32;  // the 32-column tile's first column
+        const int kind = GATES ? gate_region(a, nt) : 0;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc[i][jb + jj][4 * g + r] - rsum[i]) * inv) * cws;
+          if constexpr (GATES) gate_act4<OUT_DT>(a, kind, nt + 8 * g + 4 * (lane >> 5), v);
           char* p = wb + (lane & 31) * PITCH + (jj * 32 + 8 * g + 4 * (lane >> 5)) * ES;
           if constexpr (OUT_DT == kBF16)
             *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -1156,7 +1185,7 @@ __device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int
   const int wm = w / WN, wn = w % WN;
   const LinearOperand& o0 = a.op[0];
   const LinearOperand& o1 = a.op[1];
-  const bool plain = EPI == kEpiStore && !o0.c_w_per_row && !a.bias && !a.acc_dump;
+  const bool plain = (EPI == kEpiStore || EPI == kEpiGates) && !o0.c_w_per_row && !a.bias && !a.acc_dump;
   float sx[TM], sx1[TM];
   int32_t rsum[TM], rs1[TM];
 #pragma unroll
@@ -1185,7 +1214,8 @@ __device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int
   // the staged epilogue needs one 32-column slab per wave in the tile's LDS (else the direct stores)
   if constexpr (epi32_bytes<WM * WN, 1, OUT_DT>() <= SMEM) {
     if (plain && reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && (a.ldo * (OUT_DT == kBF16 ? 2 : 4)) % 16 == 0) {
-      epi32_plain_staged<WM * WN, TM, TN, OUT_DT, SMEM>(a, acc0, sx, rsum, cws, m0, n0, wm, wn, smem);
+      epi32_plain_staged<WM * WN, TM, TN, OUT_DT, SMEM, EPI == kEpiGates>(a, acc0, sx, rsum, cws, m0, n0, wm, wn,
+                                                                        smem);
       return;
     }
   }
@@ -1199,6 +1229,7 @@ __device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int
       char* orow = static_cast<char*>(a.out) + (m * a.ldo + n0) * (OUT_DT == kBF16 ? 2 : 4);
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
+        const int kind = EPI == kEpiGates ? gate_region(a, n0 + (wn * TN + j) * 32) : 0;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int nb = (wn * TN + j) * 32 + 8 * g + 4 * (lane >> 5);
@@ -1206,6 +1237,7 @@ __device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = (static_cast<float>(acc0[i][j][4 * g + r] - rsum[i]) * inv) * cws;
+          if constexpr (EPI == kEpiGates) gate_act4<OUT_DT>(a, kind, n0 + nb, v);
           if (vout && nb + 4 <= nrem) {
             store4<OUT_DT>(orow, nb, v, true);
           } else {
@@ -1270,7 +1302,7 @@ __device__ __forceinline__ void mfma32_tile(const LinearArgs& a, int64_t m0, int
           const int32_t a0 = acc0[i][j][4 * g + r] - rsum[i];
           if (a.acc_dump && n < a.N) a.acc_dump[m * a.N + n] = a0;
           const float v0 = (static_cast<float>(a0) * inv0) * cw0;
-          if constexpr (EPI == kEpiStore) {
+          if constexpr (!epi_dual(EPI)) {  // (kEpiGates is always plain)
             v[r] = a.bias ? v0 + ld<OUT_DT>(a.bias, n < a.N ? n : a.N - 1) : v0;
           } else {
             const float cw1 = o1.c_w_per_row ? o1.c_w[n < a.N ? n : a.N - 1] : cws1;
@@ -2504,15 +2536,67 @@ int launch_linear_fq(const LinearArgs& a, const FusedQuantIn& f, hipStream_t st)
   return check_launch("bitlinear skinny (fused quant)");
 }
 
+// Store-epilogue products of more than 32 rows on the 32x32x32 MFMA kernels (EPI kEpiStore or
+// kEpiGates).
+template <int EPI>
+int dispatch_store32(const LinearArgs& a, hipStream_t st) {
+  // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
+  // enough of them, 128x128 (4 waves of 64x64) when those still give two workgroups per CU,
+  // else 64x128 (4 waves side by side along N); measured at the layer shapes (in_proj /
+  // out_proj / configs[1] / configs[4])
+  const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
+  const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+  // long K loops over many tiles: direct-to-LDS loads into two stages (no staging registers);
+  // MIMO in_proj at M 8192: 1048 us vs 1069 us with three stages
+  if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);
+  // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
+  // 151936 x 768): two direct-to-LDS stages (48 KB; registers allow two workgroups per CU either
+  // way): 23.6 us vs 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM
+  // head 74 us vs 82 us
+  if (tiles256 >= 512 && a.Kp <= 1024) {
+    // more 128x256 tiles than two rounds of the CUs with a narrow remainder (the SISO in_proj: 640
+    // tiles): the columns past two tiles per CU go to 128x128 tiles (the split kernel)
+    if constexpr (EPI != kEpiStore) return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);
+    const int cus = device_limits().cus;
+    const int64_t ntm = (a.M + 127) / 128;
+    const int64_t ntnA = cus > 0 ? std::min<int64_t>(a.N / 256, (2 * cus) / ntm) : 0;
+    const int64_t nA = ntnA * 256;
+    constexpr int TMB = 2;  // 128-row tail tiles (64-row ones: 26.7 against 26.1 us in the layer)
+    const int64_t ntmB = (a.M + 64 * TMB - 1) / (64 * TMB), ntnB = (a.N - nA + 127) / 128;
+    if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * ntnA + ntmB * ntnB <= 0x7fffffff) {
+      const unsigned grid = static_cast<unsigned>(ntm * ntnA + ntmB * ntnB);
+      if (a.out_dt == kBF16)
+        mfma32_split_kernel<kBF16, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16, TMB>)>>>(a, nA);
+      else
+        mfma32_split_kernel<kF32, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32, TMB>)>>>(a, nA);
+      return check_launch("bitlinear mfma32 split");
+    }
+    return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);
+  }
+  // fewer 128x256 tiles than CUs at short K (the SISO out_proj: 8192 x 768 x 768): 64x128 tiles, two
+  // direct-to-LDS stages: 10.1 us vs 10.7 us for 128x256 tiles
+  if (tiles256 < 256 && a.Kp <= 1024) return run_mfma32<1, 4, 2, 1, EPI, 2>(a, st);
+  if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, EPI>(a, st);
+  if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, EPI>(a, st);
+  return run_mfma32<1, 4, 2, 1, EPI>(a, st);
+}
+
 int launch_linear(const LinearArgs& a, hipStream_t st) {
   TESM_REQUIRE(a.M >= 0 && a.N >= 0, kErrInvalidArg, "bitlinear: negative size");
   TESM_REQUIRE(a.Kp >= kKTile && a.Kp % kKTile == 0, kErrInvalidArg, "bitlinear: Kp must be a positive multiple of 128");
   TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "bitlinear: out dtype must be 0 or 1");
-  TESM_REQUIRE(a.epilogue == kEpiStore || a.epilogue == kEpiOutputGate || a.epilogue == kEpiSwiGLU, kErrInvalidArg,
-               "bitlinear: bad epilogue");
+  TESM_REQUIRE(a.epilogue == kEpiStore || a.epilogue == kEpiOutputGate || a.epilogue == kEpiSwiGLU ||
+                   a.epilogue == kEpiGates,
+               kErrInvalidArg, "bitlinear: bad epilogue");
   if (a.M == 0 || a.N == 0) return kOk;
   TESM_REQUIRE(a.out && a.ldo >= a.N, kErrInvalidArg, "bitlinear: need out and ldo >= N");
   if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
+  if (a.epilogue == kEpiGates) {
+    TESM_REQUIRE(a.M > 32 && !a.bias && !a.acc_dump && !a.op[0].c_w_per_row && a.act_bias && a.act_w > 0 &&
+                     a.act_n0 >= 0 && a.act_n0 % 32 == 0 && a.act_w % 32 == 0 && a.act_n0 + 3 * a.act_w <= a.N,
+                 kErrUnsupported, "bitlinear gates epilogue: needs M > 32, 32-aligned regions inside N, no bias");
+    return dispatch_store32<kEpiGates>(a, st);
+  }
   if (a.epilogue != kEpiStore) {
     if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
     TESM_REQUIRE(a.bias == nullptr, kErrInvalidArg, "bitlinear two-product epilogue: bias unsupported");
@@ -2534,44 +2618,7 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
     // decode-size batches over wide weights (MIMO decode in_proj, 32 x 34816 x 4096): 32x128 tiles on
     // the 32x32x32 form, 16.5 us vs 19.3 us for 32x64 tiles on the 16x16x64 one
     if (a.M <= 32) return run_mfma32<1, 4, 1, 1, kEpiStore>(a, st);
-    // 32x32x32 MFMA kernels: 128x256 tiles (8 waves of 64x64) when N fills them and there are
-    // enough of them, 128x128 (4 waves of 64x64) when those still give two workgroups per CU,
-    // else 64x128 (4 waves side by side along N); measured at the layer shapes (in_proj /
-    // out_proj / configs[1] / configs[4])
-    const int64_t tiles256 = ((a.M + 127) / 128) * ((a.N + 255) / 256);
-    const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-    // long K loops over many tiles: direct-to-LDS loads into two stages (no staging registers);
-    // MIMO in_proj at M 8192: 1048 us vs 1069 us with three stages
-    if (a.N % 256 == 0 && tiles256 >= 2048 && a.Kp >= 2048) return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
-    // short K on a few hundred 128x256 tiles (the SISO in_proj: 8192 x 2432 x 768; the LM head: 512 x
-    // 151936 x 768): two direct-to-LDS stages (48 KB; registers allow two workgroups per CU either
-    // way): 23.6 us vs 25.6 us with three stages and 27.6 us for register-staged 128x128 tiles; LM
-    // head 74 us vs 82 us
-    if (tiles256 >= 512 && a.Kp <= 1024) {
-      // more 128x256 tiles than two rounds of the CUs with a narrow remainder (the SISO in_proj: 640
-      // tiles): the columns past two tiles per CU go to 128x128 tiles (the split kernel)
-      const int cus = device_limits().cus;
-      const int64_t ntm = (a.M + 127) / 128;
-      const int64_t ntnA = cus > 0 ? std::min<int64_t>(a.N / 256, (2 * cus) / ntm) : 0;
-      const int64_t nA = ntnA * 256;
-      constexpr int TMB = 2;  // 128-row tail tiles (64-row ones: 26.7 against 26.1 us in the layer)
-      const int64_t ntmB = (a.M + 64 * TMB - 1) / (64 * TMB), ntnB = (a.N - nA + 127) / 128;
-      if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * ntnA + ntmB * ntnB <= 0x7fffffff) {
-        const unsigned grid = static_cast<unsigned>(ntm * ntnA + ntmB * ntnB);
-        if (a.out_dt == kBF16)
-          mfma32_split_kernel<kBF16, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16, TMB>)>>>(a, nA);
-        else
-          mfma32_split_kernel<kF32, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32, TMB>)>>>(a, nA);
-        return check_launch("bitlinear mfma32 split");
-      }
-      return run_mfma32<2, 4, 2, 2, kEpiStore, 2>(a, st);
-    }
-    // fewer 128x256 tiles than CUs at short K (the SISO out_proj: 8192 x 768 x 768): 64x128 tiles, two
-    // direct-to-LDS stages: 10.1 us vs 10.7 us for 128x256 tiles
-    if (tiles256 < 256 && a.Kp <= 1024) return run_mfma32<1, 4, 2, 1, kEpiStore, 2>(a, st);
-    if (a.N % 256 == 0 && tiles256 >= 128) return run_mfma32<2, 4, 2, 2, kEpiStore>(a, st);
-    if (tiles128 >= 512) return run_mfma32<2, 2, 2, 2, kEpiStore>(a, st);
-    return run_mfma32<1, 4, 2, 1, kEpiStore>(a, st);
+    return dispatch_store32<kEpiStore>(a, st);
   }
   if (a.epilogue == kEpiOutputGate) return dispatch_dual<kEpiOutputGate>(a, st);
   return dispatch_dual<kEpiSwiGLU>(a, st);

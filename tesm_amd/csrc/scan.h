@@ -7,20 +7,23 @@
 namespace tesm {
 
 struct ScanArgs {
-  int mode = 0;        // 0: decay/update given; 1: gates from raw projection slices
+  // 0: decay/update given; 1: gates from raw projection slices; 2: gates already applied by the
+  // producer (decay = sigmoid(x + bias), write = sigmoid, sv = tanh, each rounded to dt), so the scan
+  // forms only update = write * sv
+  int mode = 0;
   int dt = 0;          // input dtype (0 f32, 1 bf16)
   int out_dt = 0;      // states dtype
   int clamp = 1;       // 1: SISO closed-form clamp semantics (1e-12); 0: plain recurrence (MIMO)
-  int round_update = 1;  // mode 1: round write*tanh(sv) to dt (SISO) or keep fp32 (MIMO); in mode 1
-                         // clamp and round_update must agree (the SISO and MIMO semantics)
+  int round_update = 1;  // modes 1, 2: round write*tanh(sv) to dt (SISO) or keep fp32 (MIMO); in
+                         // these modes clamp and round_update must agree (the SISO and MIMO semantics)
   int64_t B = 0, L = 0, C = 0;
   int64_t cs = 16;     // reference chunk size (state_scan_chunk_size)
   // token-major inputs: element (b, t, c) at ptr[(b*L + t)*ld + c]
-  const void* decay = nullptr;   // mode 0: decay; mode 1: raw decay slice
+  const void* decay = nullptr;   // mode 0: decay; mode 1: raw decay slice; mode 2: decay gate
   int64_t ld_decay = 0;
-  const void* update = nullptr;  // mode 0: update; mode 1: raw write slice
+  const void* update = nullptr;  // mode 0: update; mode 1: raw write slice; mode 2: write gate
   int64_t ld_update = 0;
-  const void* sv = nullptr;      // mode 1: raw state_value slice
+  const void* sv = nullptr;      // mode 1: raw state_value slice; mode 2: tanh(state_value)
   int64_t ld_sv = 0;
   const void* decay_bias = nullptr;  // mode 1: (C) in dt
   const double* h0 = nullptr;    // (B, C) initial state or null

@@ -38,10 +38,15 @@ struct ScanIn {
     if constexpr (MODE == 0) {
       d = ld<DT>(a.decay, tok * a.ld_decay + ch);
       u = ld<DT>(a.update, tok * a.ld_update + ch);
-    } else {
+    } else if constexpr (MODE == 1) {
       const float sv = rnd<DT>(tanhf_(ld<DT>(a.sv, tok * a.ld_sv + ch)));
       d = rnd<DT>(sigmoidf_(rnd<DT>(ld<DT>(a.decay, tok * a.ld_decay + ch) + ld<DT>(a.decay_bias, ch))));
       const float w = rnd<DT>(sigmoidf_(ld<DT>(a.update, tok * a.ld_update + ch)));
+      u = a.round_update ? rnd<DT>(w * sv) : w * sv;
+    } else {  // gates applied by the producer
+      const float sv = ld<DT>(a.sv, tok * a.ld_sv + ch);
+      d = ld<DT>(a.decay, tok * a.ld_decay + ch);
+      const float w = ld<DT>(a.update, tok * a.ld_update + ch);
       u = a.round_update ? rnd<DT>(w * sv) : w * sv;
     }
   }
@@ -135,7 +140,7 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
     const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
     Vec<DT, CPT>::load(a.decay, tok * a.ld_decay + ch, x0[i]);
     Vec<DT, CPT>::load(a.update, tok * a.ld_update + ch, x1[i]);
-    if constexpr (MODE == 1) Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2[i]);
+    if constexpr (MODE >= 1) Vec<DT, CPT>::load(a.sv, tok * a.ld_sv + ch, x2[i]);
   }
   float d[TM][CPT], u[TM][CPT];
 #pragma unroll
@@ -145,11 +150,14 @@ __global__ __launch_bounds__(256) void scan_fast_kernel(ScanArgs a, int64_t T, i
       if constexpr (MODE == 0) {
         d[i][j] = x0[i][j];
         u[i][j] = x1[i][j];
-      } else {
+      } else if constexpr (MODE == 1) {
         const float sv = rnd<DT>(tanhf_(x2[i][j]));
         d[i][j] = rnd<DT>(sigmoidf_(rnd<DT>(x0[i][j] + bias[j])));
         const float w = rnd<DT>(sigmoidf_(x1[i][j]));
         u[i][j] = a.round_update ? rnd<DT>(w * sv) : w * sv;
+      } else {
+        d[i][j] = x0[i][j];
+        u[i][j] = a.round_update ? rnd<DT>(x1[i][j] * x2[i][j]) : x1[i][j] * x2[i][j];
       }
       if (i >= n) {
         d[i][j] = 1.0f;
@@ -353,7 +361,7 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
       const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
       x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
       x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
-      if constexpr (MODE == 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
+      if constexpr (MODE >= 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
     }
     const int cs = static_cast<int>(a.cs);
     float A = 1.0f;
@@ -363,11 +371,14 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
       if constexpr (MODE == 0) {
         dd = x0[i];
         uu = x1[i];
-      } else {
+      } else if constexpr (MODE == 1) {
         const float sv = rnd<DT>(tanhf_(x2[i]));
         dd = rnd<DT>(sigmoidf_(rnd<DT>(x0[i] + bias)));
         const float wr = rnd<DT>(sigmoidf_(x1[i]));
         uu = round_update ? rnd<DT>(wr * sv) : wr * sv;
+      } else {
+        dd = x0[i];
+        uu = round_update ? rnd<DT>(x1[i] * x2[i]) : x1[i] * x2[i];
       }
       if (clamp) {
         dd = fmaxf(dd, kScanEps);
@@ -562,11 +573,11 @@ int run_scan_lb_cr(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStr
   return check_launch("scan look-back");
 }
 
-// Gate mode fixes the clamp / rounding semantics at compile time (both or neither); the
+// Gate modes fix the clamp / rounding semantics at compile time (both or neither); the
 // decay / update mode reads them.
 template <int DT, int OUT_DT, int MODE>
 int run_scan_lb(const ScanArgs& a, int64_t T, float* summ, int* flags, hipStream_t st) {
-  if constexpr (MODE == 1) {
+  if constexpr (MODE >= 1) {
     if (a.clamp) return run_scan_lb_cr<DT, OUT_DT, MODE, 1>(a, T, summ, flags, st);
     return run_scan_lb_cr<DT, OUT_DT, MODE, 0>(a, T, summ, flags, st);
   } else {
@@ -659,15 +670,17 @@ int64_t scan_ws_bytes(int64_t B, int64_t L, int64_t C, int64_t cs) {
 int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   TESM_REQUIRE(a.dt == kF32 || a.dt == kBF16, kErrInvalidArg, "scan: input dtype must be 0 or 1");
   TESM_REQUIRE(a.out_dt == kF32 || a.out_dt == kBF16, kErrInvalidArg, "scan: output dtype must be 0 or 1");
-  TESM_REQUIRE(a.mode == 0 || a.mode == 1, kErrInvalidArg, "scan: mode must be 0 (decay/update) or 1 (gates)");
+  TESM_REQUIRE(a.mode >= 0 && a.mode <= 2, kErrInvalidArg,
+               "scan: mode must be 0 (decay/update), 1 (gates) or 2 (activated gates)");
   TESM_REQUIRE(a.B >= 0 && a.L >= 0 && a.C >= 1 && a.cs >= 1, kErrInvalidArg, "scan: bad sizes");
   if (a.B == 0 || a.L == 0) return kOk;
   TESM_REQUIRE(a.decay && a.update && a.states, kErrInvalidArg, "scan: null pointer");
   TESM_REQUIRE(a.ld_decay >= a.C && a.ld_update >= a.C && a.ld_states >= a.C, kErrInvalidArg, "scan: ld < C");
-  if (a.mode == 1) {
-    TESM_REQUIRE(a.sv && a.decay_bias && a.ld_sv >= a.C, kErrInvalidArg, "scan mode 1: need sv and decay_bias");
+  if (a.mode >= 1) {
+    TESM_REQUIRE(a.sv && (a.decay_bias || a.mode == 2) && a.ld_sv >= a.C, kErrInvalidArg,
+                 "scan gate modes: need sv (and decay_bias in mode 1)");
     TESM_REQUIRE((a.clamp != 0) == (a.round_update != 0), kErrUnsupported,
-                 "scan mode 1: clamp and round_update must agree (SISO: both, MIMO: neither)");
+                 "scan gate modes: clamp and round_update must agree (SISO: both, MIMO: neither)");
   }
   const int64_t need = scan_ws_bytes(a.B, a.L, a.C, a.cs);
   TESM_REQUIRE(ws && ws_bytes >= need, kErrWorkspace, "scan: workspace too small");
@@ -682,8 +695,8 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
   e.cs = std::max<int64_t>(1, std::min(a.cs, a.L));
   const bool pairs = a.dt == kBF16 && a.C % 2 == 0 && a.ld_decay % 2 == 0 && a.ld_update % 2 == 0 &&
                      (a.mode == 0 || a.ld_sv % 2 == 0) && a.ld_states % 2 == 0 && aligned(a.decay, 4) &&
-                     aligned(a.update, 4) && (a.mode == 0 || (aligned(a.sv, 4) && aligned(a.decay_bias, 4))) &&
-                     aligned(a.states, 4);
+                     aligned(a.update, 4) && (a.mode == 0 || aligned(a.sv, 4)) &&
+                     (a.mode != 1 || aligned(a.decay_bias, 4)) && aligned(a.states, 4);
   if (scan_lb_eligible(a.B, a.L, a.C, T, ws)) {
     // single pass with decoupled look-back
     const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
@@ -696,6 +709,10 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
       case 101: return run_scan_lb<kBF16, kF32, 1>(e, T, summ, flags, st);
       case 10: return run_scan_lb<kF32, kBF16, 0>(e, T, summ, flags, st);
       case 11: return run_scan_lb<kF32, kBF16, 1>(e, T, summ, flags, st);
+      case 2: return run_scan_lb<kF32, kF32, 2>(e, T, summ, flags, st);
+      case 112: return run_scan_lb<kBF16, kBF16, 2>(e, T, summ, flags, st);
+      case 102: return run_scan_lb<kBF16, kF32, 2>(e, T, summ, flags, st);
+      case 12: return run_scan_lb<kF32, kBF16, 2>(e, T, summ, flags, st);
       default: return fail(kErrInvalidArg, "scan: unsupported dtype combination");
     }
   }
@@ -703,14 +720,17 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
     if (a.dt == kBF16) {
       if (a.out_dt == kBF16) {
         if (a.mode == 0) return scan_fast_dispatch<kBF16, kBF16, 0>(e, T, nc, summ, carry, pairs, st);
-        return scan_fast_dispatch<kBF16, kBF16, 1>(e, T, nc, summ, carry, pairs, st);
+        if (a.mode == 1) return scan_fast_dispatch<kBF16, kBF16, 1>(e, T, nc, summ, carry, pairs, st);
+        return scan_fast_dispatch<kBF16, kBF16, 2>(e, T, nc, summ, carry, pairs, st);
       }
       if (a.mode == 0) return scan_fast_dispatch<kBF16, kF32, 0>(e, T, nc, summ, carry, pairs, st);
-      return scan_fast_dispatch<kBF16, kF32, 1>(e, T, nc, summ, carry, pairs, st);
+      if (a.mode == 1) return scan_fast_dispatch<kBF16, kF32, 1>(e, T, nc, summ, carry, pairs, st);
+      return scan_fast_dispatch<kBF16, kF32, 2>(e, T, nc, summ, carry, pairs, st);
     }
     if (a.out_dt == kF32) {
       if (a.mode == 0) return scan_fast_dispatch<kF32, kF32, 0>(e, T, nc, summ, carry, false, st);
-      return scan_fast_dispatch<kF32, kF32, 1>(e, T, nc, summ, carry, false, st);
+      if (a.mode == 1) return scan_fast_dispatch<kF32, kF32, 1>(e, T, nc, summ, carry, false, st);
+      return scan_fast_dispatch<kF32, kF32, 2>(e, T, nc, summ, carry, false, st);
     }
   }
   const int key = a.dt * 100 + a.out_dt * 10 + a.mode;
@@ -723,6 +743,10 @@ int launch_scan(const ScanArgs& a, void* ws, int64_t ws_bytes, hipStream_t st) {
     case 101: return run_scan<kBF16, kF32, 1>(e, T, nc, summ, carry, st);
     case 10: return run_scan<kF32, kBF16, 0>(e, T, nc, summ, carry, st);
     case 11: return run_scan<kF32, kBF16, 1>(e, T, nc, summ, carry, st);
+    case 2: return run_scan<kF32, kF32, 2>(e, T, nc, summ, carry, st);
+    case 112: return run_scan<kBF16, kBF16, 2>(e, T, nc, summ, carry, st);
+    case 102: return run_scan<kBF16, kF32, 2>(e, T, nc, summ, carry, st);
+    case 12: return run_scan<kF32, kBF16, 2>(e, T, nc, summ, carry, st);
     default: return fail(kErrInvalidArg, "scan: unsupported dtype combination");
   }
 }

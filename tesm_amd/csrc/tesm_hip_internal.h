@@ -37,10 +37,11 @@ enum Epilogue : int {
   kEpiStore = 0,       // out = rnd(v (+ bias))
   kEpiOutputGate = 1,  // out = rnd(rnd(local + rnd(sigmoid(gate) * sp)) + ep), two products (sp, ep)
   kEpiSwiGLU = 2,      // out = rnd(rnd(silu(rnd(g))) * rnd(u)), two products (g, u) of one activation
+  kEpiGates = 3,       // kEpiStore with the MIMO scan's gate activations on three column regions
 };
 
 // Epilogues that combine two products (op[0], op[1]) computed over the same output tile.
-constexpr bool epi_dual(int epi) { return epi != kEpiStore; }
+constexpr bool epi_dual(int epi) { return epi == kEpiOutputGate || epi == kEpiSwiGLU; }
 
 struct LinearArgs {
   LinearOperand op[2];  // op[1] used only by the two-product epilogues
@@ -55,6 +56,13 @@ struct LinearArgs {
   const void* gate = nullptr;
   int64_t ld_gate = 0;
   int32_t* acc_dump = nullptr;  // optional (M, N) signed int32 accumulators of op[0]
+  // kEpiGates (tesm_mimo.py:957-986, the gates of the MIMO state scan), on the rounded product p of
+  // column n: [act_n0, act_n0 + act_w) -> rnd(tanh(p)) (the state value), the next act_w columns ->
+  // rnd(sigmoid(rnd(p + act_bias[c]))) (the decay, c counted from that region's start), the next
+  // act_w -> rnd(sigmoid(p)) (the write gate); other columns are stored as kEpiStore stores them.
+  // act_n0 and act_w are multiples of 32, act_bias is (act_w) in the out dtype; M > 32, no bias.
+  int64_t act_n0 = 0, act_w = 0;
+  const void* act_bias = nullptr;
 };
 
 int launch_linear(const LinearArgs& a, hipStream_t st);

@@ -357,7 +357,9 @@ def test_cfg4_mimo_long_vs_oracle(dtype):
         yr, fr = ref(u)
         uninstall(ref)
     dc = DT_CODE[dtype]
-    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,1,16,8,0>"), log.kernels
+    # in_proj applies the scan's gates in its epilogue; the scan streams them (its activated-gate mode)
+    assert _has(log.kernels, f"mfma32_kernel<1,4,2,1,3,{dc},2>"), log.kernels
+    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,2,16,8,0>"), log.kernels
     assert _has(log.kernels, f"mimo_mix_kernel<{dc},true,64>"), log.kernels
     assert _has(log.kernels, f"ent_scores_mimo_kernel<{dc}>"), log.kernels
     assert_rows(to_np(y), to_np(yr), dtype, f"configs[4]-shaped MIMO L1100 ({flips.summary()})")
@@ -384,7 +386,8 @@ def test_cfg4_mimo_full_size():
             y, f = m(u.to(DEV))
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
-    for k in ("mfma32_kernel<2,4,2,2,0,1,2>", "mfma32_kernel<2,4,2,2,1,1,2>", "scan_lb_kernel<1,0,1,16,8,0>",
+    for k in ("mfma32_kernel<2,4,2,2,3,1,2>", "mfma32_kernel<2,4,2,2,0,1,2>", "mfma32_kernel<2,4,2,2,1,1,2>",
+              "scan_lb_kernel<1,0,2,16,8,0>",
               "mimo_mix_kernel<1,true,64>", "ent_scores_mimo_kernel<1>"):
         assert _has(log.kernels, k), (k, log.kernels)
     # the oracle on the causal prefix, fed the device's decisions (and, bf16, states and tanh(E) / C) for

@@ -8,7 +8,7 @@ from conftest import golden_meta, load_golden
 from flips import Flips, Taps, assert_rows, install, uninstall
 from hip_helpers import DEV, TOL, need_gpu, normwise, to_np
 from oracle import tesm_torch as ot
-from tesm_amd import TESMMIMO_Optimized
+from tesm_amd import TESMMIMO_Optimized, hip_ops
 
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +70,36 @@ def test_mimo_prefill_random_vs_oracle(dtype, B, L, H, Rm, D, R, W):
         np.testing.assert_allclose(f.cpu().numpy(), fr.numpy(), rtol=1e-4, atol=1e-5)
     else:
         assert normwise(f.cpu().numpy(), fr.numpy()) <= TOL[dtype]
+
+
+def _gates_kernels(kernels, dc):
+    """(in_proj with the gate epilogue, scan in its activated-gate mode) seen in a launch log."""
+    epi = [k for k in kernels if k.startswith("mfma32_kernel<") and k[len("mfma32_kernel<"):].split(",")[4] == "3"]
+    return bool(epi), any(k.startswith(f"scan_lb_kernel<{dc},0,2,") for k in kernels)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mimo_gate_epilogue_matches_scan_gates(dtype, monkeypatch):
+    """The scan's gates (tesm_mimo.py:958-961) applied in in_proj's epilogue, the scan only streaming
+    them, give the same bits as the scan applying them to the raw in_proj slices (the path taken with
+    TESM_HIP_NO_GATE_EPI=1, and by prefills of at most 32 tokens): output, final state, cross state."""
+    meta = dict(seed=9, dm=256, D=64, H=4, Rm=3, R=16, W=16, thr=0.05, decay_bias=2.0, max_seq_len=320)
+    m = build(TESMMIMO_Optimized, meta).to(DEV).to(dtype)
+    u = torch.randn(2, 300, 256, generator=torch.Generator().manual_seed(4)).to(dtype).to(DEV)
+    dc = 1 if dtype == torch.bfloat16 else 0
+    with torch.no_grad():
+        with hip_ops.launch_log() as log:
+            y, f = m(u)
+        s = m._last_cross_layer_state.clone()
+        monkeypatch.setenv("TESM_HIP_NO_GATE_EPI", "1")
+        with hip_ops.launch_log() as log1:
+            y1, f1 = m(u)
+        s1 = m._last_cross_layer_state.clone()
+    assert _gates_kernels(log.kernels, dc) == (True, True), log.kernels
+    assert _gates_kernels(log1.kernels, dc) == (False, False), log1.kernels
+    assert any(k.startswith(f"scan_lb_kernel<{dc},0,1,") for k in log1.kernels), log1.kernels
+    assert torch.isfinite(y.float()).all()
+    assert torch.equal(y, y1) and torch.equal(f, f1) and torch.equal(s, s1)
 
 
 def _prefill_lockstep(ref, m, u, dtype):
