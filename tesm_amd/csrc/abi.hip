@@ -526,6 +526,11 @@ struct MimoPlan {
   int64_t total;
 };
 
+// Thread-chunk length of the MIMO state scan.  Its recurrence has no clamp (tesm_mimo.py:375-392 is
+// the plain sequential h = d h + u), so the chunk only sets the scan's work split: 32 positions per
+// wave halve the look-back spans of 16 (configs[4]: 0.52 against 0.65 ms).
+constexpr int64_t kMimoScanChunk = 32;
+
 MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
   Carve c(base);
   MimoPlan s;
@@ -534,7 +539,7 @@ MimoPlan plan_mimo(const tesm_hip_mimo_layer& p, void* base) {
   const int es = esize(p.dt);
   s.xu = take_codes(c, M, p.d_model);
   s.proj = c.take<void>(M * n_in * es);
-  s.scan_bytes = scan_ws_bytes(p.B, p.L, HD, 16);
+  s.scan_bytes = scan_ws_bytes(p.B, p.L, HD, kMimoScanChunk);
   s.scan_ws = c.take<void>(s.scan_bytes);
   s.S = c.take<float>(M * HD * 4);
   s.wts = nullptr;
@@ -1563,7 +1568,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   // the u quantization also clears the single-pass scan's flags, saving the scan its reset launch
   int* scan_zero = nullptr;
   int64_t scan_zero_n = 0;
-  scan_lb_clear_range(p.B, p.L, HD, 16, s.scan_ws, &scan_zero, &scan_zero_n);
+  scan_lb_clear_range(p.B, p.L, HD, kMimoScanChunk, s.scan_ws, &scan_zero, &scan_zero_n);
   if ((rc = launch_quant_act(p.u, dt, M, dm, dm, p.bit_eps, 1, s.xu.q, s.xu.ldq, s.xu.s, s.xu.rs, st, scan_zero,
                              scan_zero_n)))
     return rc;
@@ -1601,7 +1606,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
   sa.B = p.B;
   sa.L = p.L;
   sa.C = HD;
-  sa.cs = 16;
+  sa.cs = kMimoScanChunk;
   sa.decay = proj + o_decay * es;
   sa.ld_decay = n_in;
   sa.update = proj + o_write * es;

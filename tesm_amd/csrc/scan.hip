@@ -326,6 +326,26 @@ __device__ __forceinline__ float scan_val_load(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Streaming (non-temporal) gate loads and state stores of the activated-gate mode: the MIMO scan
+// reads its gates once and writes float32 states that are read back only after the whole scan
+// (configs[4]: 1.6 GB and 1.07 GB), so caching either only evicts other lines.
+template <int DT>
+__device__ __forceinline__ float ld_stream(const void* p, int64_t i) {
+  if constexpr (DT == kBF16) {
+    const uint32_t h = __builtin_nontemporal_load(static_cast<const uint16_t*>(p) + i);
+    return __uint_as_float(h << 16);
+  } else {
+    return __builtin_nontemporal_load(static_cast<const float*>(p) + i);
+  }
+}
+template <int MODE, int OUT_DT>
+__device__ __forceinline__ void st_state(void* p, int64_t i, float v) {
+  if constexpr (MODE == 2 && OUT_DT == kF32)
+    __builtin_nontemporal_store(v, static_cast<float*>(p) + i);
+  else
+    st<OUT_DT>(p, i, v);
+}
+
 // CR: the clamp / update-rounding semantics, 1 = both (SISO), 0 = neither (MIMO), 2 = read from a.
 template <int DT, int OUT_DT, int MODE, int TM, int SUB, int CR>
 __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, int64_t T, int64_t nc, int64_t G,
@@ -359,9 +379,15 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int64_t tok = b * a.L + t0 + (i < n ? i : n - 1);
-      x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
-      x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
-      if constexpr (MODE >= 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
+      if constexpr (MODE == 2) {
+        x0[i] = ld_stream<DT>(a.decay, tok * a.ld_decay + chc);
+        x1[i] = ld_stream<DT>(a.update, tok * a.ld_update + chc);
+        x2[i] = ld_stream<DT>(a.sv, tok * a.ld_sv + chc);
+      } else {
+        x0[i] = ld<DT>(a.decay, tok * a.ld_decay + chc);
+        x1[i] = ld<DT>(a.update, tok * a.ld_update + chc);
+        if constexpr (MODE == 1) x2[i] = ld<DT>(a.sv, tok * a.ld_sv + chc);
+      }
     }
     const int cs = static_cast<int>(a.cs);
     float A = 1.0f;
@@ -525,7 +551,7 @@ __global__ __launch_bounds__(kScanLbCh * SUB) void scan_lb_kernel(ScanArgs a, in
   for (int i = 0; i < TM; ++i) {
     if (i < n) {
       hh = d[i] * hh + u[i];
-      st<OUT_DT>(a.states, (b * a.L + t0 + i) * a.ld_states + ch, hh);
+      st_state<MODE, OUT_DT>(a.states, (b * a.L + t0 + i) * a.ld_states + ch, hh);
     }
   }
 }

@@ -337,7 +337,7 @@ def _mimo_pair(cfg, dtype, seed=0, oracle_len=None):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_cfg4_mimo_long_vs_oracle(dtype):
-    """L = 1100 (> 1024: the scan's eight-sub-span workgroups) with window 64 (the window-64 mix
+    """L = 1100 (nine look-back spans of 4 x 32 positions per chain) with window 64 (the window-64 mix
     kernel) at reduced width, the whole output against the oracle, which runs the ranks uncollapsed."""
     cfg = dict(d_model=128, d_state=64, n_heads=2, mimo_rank=4, ent_rank=16, entanglement_window=64,
                entanglement_threshold=0.05, entanglement_scale=0.2, max_seq_len=1100)
@@ -359,7 +359,7 @@ def test_cfg4_mimo_long_vs_oracle(dtype):
     dc = DT_CODE[dtype]
     # in_proj applies the scan's gates in its epilogue; the scan streams them (its activated-gate mode)
     assert _has(log.kernels, f"mfma32_kernel<1,4,2,1,3,{dc},2>"), log.kernels
-    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,2,16,8,0>"), log.kernels
+    assert _has(log.kernels, f"scan_lb_kernel<{dc},0,2,32,4,0>"), log.kernels
     assert _has(log.kernels, f"mimo_mix_kernel<{dc},true,64>"), log.kernels
     assert _has(log.kernels, f"ent_scores_mimo_kernel<{dc}>"), log.kernels
     assert_rows(to_np(y), to_np(yr), dtype, f"configs[4]-shaped MIMO L1100 ({flips.summary()})")
@@ -387,7 +387,7 @@ def test_cfg4_mimo_full_size():
     assert hip_ops.device_status() == 0
     assert torch.isfinite(y.float()).all() and torch.isfinite(f).all()
     for k in ("mfma32_kernel<2,4,2,2,3,1,2>", "mfma32_kernel<2,4,2,2,0,1,2>", "mfma32_kernel<2,4,2,2,1,1,2>",
-              "scan_lb_kernel<1,0,2,16,8,0>",
+              "scan_lb_kernel<1,0,2,32,8,0>",
               "mimo_mix_kernel<1,true,64>", "ent_scores_mimo_kernel<1>"):
         assert _has(log.kernels, k), (k, log.kernels)
     # the oracle on the causal prefix, fed the device's decisions (and, bf16, states and tanh(E) / C) for
