@@ -51,6 +51,8 @@ def parse():
                    choices=["all", "layer", "decode", "mimo", "global", "lm", "base", "kernels", "in_proj"],
                    help="run one measurement alone and print its JSON (for per-workload profiles)")
     p.add_argument("--mimo-reps", type=int, default=3, help="timed configs[4] forwards (profiles use more)")
+    p.add_argument("--reps", type=int, default=0,
+                   help="timed repetitions of a single decode / lm / base / global workload (default: its own)")
     p.add_argument("--trace-summary", metavar="CSV", default="",
                    help="summarize a rocprofv3 --kernel-trace CSV (per kernel and launch shape: calls, median, "
                         "mean, min, max microseconds) as a markdown table, then exit")
@@ -612,20 +614,20 @@ def main():
                 torch.cuda.synchronize()
                 res = {"ms_per_forward": e0.elapsed_time(e1) / args.steps}
             elif args.workload == "decode":
-                res = measure_decode(torch, m)
+                res = measure_decode(torch, m, **({"steps": args.reps} if args.reps else {}))
             elif args.workload == "mimo":
                 res = measure_mimo(torch, reps=args.mimo_reps)
             elif args.workload == "in_proj":
                 t, ops, nbytes = measure_in_proj(torch, m, u, n=args.steps)
                 res = {"us": t * 1e6, "TOP_per_s": ops / t / 1e12, "frac_of_int8_peak": ops / t / 1e12 / INT8_PEAK_TOPS}
             elif args.workload == "global":
-                res = measure_global(torch)
+                res = measure_global(torch, **({"steps": args.reps} if args.reps else {}))
             elif args.workload == "base":
-                res = measure_true_base(torch)
+                res = measure_true_base(torch, **({"steps": args.reps} if args.reps else {}))
             elif args.workload == "kernels":
                 res = measure_kernels(torch, args.only)
             else:
-                res = measure_lm(torch)
+                res = measure_lm(torch, **({"steps": args.reps} if args.reps else {}))
         print(json.dumps({"workload": args.workload, "result": res}))
         return
     with torch.no_grad():
