@@ -743,7 +743,22 @@ __host__ __device__ inline Fused2Lds fused2_lds(int64_t R, int64_t D, int64_t we
   return f;
 }
 
+// Stores of a thread's 8 consecutive channels of one output: two 4-wide stores when the row and base allow.
 template <int DT>
+__device__ __forceinline__ void st8(void* p, int64_t o, const float (&v)[8], bool vec) {
+  if (vec) {
+    const float lo[4] = {v[0], v[1], v[2], v[3]}, hi[4] = {v[4], v[5], v[6], v[7]};
+    st4<DT>(p, o, lo);
+    st4<DT>(p, o + 4, hi);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) st<DT>(p, o + e, v[e]);
+  }
+}
+
+// QUANT: the layer's form (int8 codes of tanh(E) and C, optionally their float values too); otherwise
+// the float outputs alone (window average, E, tanh(E), C; each optional), as the unfused kernels give them.
+template <int DT, bool QUANT>
 __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff, Fused2Lds f) {
   using T = typename Elem<DT>::T;
   extern __shared__ __attribute__((aligned(16))) char lds_f2[];
@@ -923,6 +938,11 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
   __syncthreads();
 
   // 3. window sums, mix and tanh of the thread's slices
+  // 4-wide output stores when every requested output is 4-element aligned and rows are 4 elements apart
+  constexpr uintptr_t kAl = DT == kBF16 ? 8 : 16;
+  const bool vout = a.ld_out % 4 == 0 && reinterpret_cast<uintptr_t>(a.avg) % kAl == 0 &&
+                    reinterpret_cast<uintptr_t>(a.e_out) % kAl == 0 && reinterpret_cast<uintptr_t>(a.e_tanh) % kAl == 0 &&
+                    reinterpret_cast<uintptr_t>(a.c_out) % kAl == 0;
   float tv[kF2MaxSPT][8], cv[kF2MaxSPT][8];
   float mx_t = 0.0f, mx_c = 0.0f;
 #pragma unroll
@@ -963,25 +983,29 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += wt * x[e];
     }
-    float sv[8];
+    float sv[8], av[8], evs[8];
     row8(p + W - 1, sv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = 8 * sl + e;
       const float avg = rnd<DT>(acc[e]);
       const float s0 = sv[e];
       const float ev = rnd<DT>(s0 + rnd<DT>(a.ent_scale * rnd<DT>(avg - s0)));
+      av[e] = avg;
+      evs[e] = ev;
       cv[si][e] = rnd<DT>(ev - s0);
       tv[si][e] = rnd<DT>(tanhf_(ev));
       mx_t = fmaxf(mx_t, fabsf(tv[si][e]));
       mx_c = fmaxf(mx_c, fabsf(cv[si][e]));
-      if (a.e_tanh || a.c_out) {
-        const int64_t o = (b * a.L + t) * a.ld_out + c;
-        if (a.c_out) st<DT>(a.c_out, o, cv[si][e]);
-        if (a.e_tanh) st<DT>(a.e_tanh, o, tv[si][e]);
-      }
+    }
+    if (a.e_tanh || a.c_out || a.avg || a.e_out) {
+      const int64_t o = (b * a.L + t) * a.ld_out + 8 * sl;
+      if (a.c_out) st8<DT>(a.c_out, o, cv[si], vout);
+      if (a.e_tanh) st8<DT>(a.e_tanh, o, tv[si], vout);
+      if (a.avg) st8<DT>(a.avg, o, av, vout);
+      if (a.e_out) st8<DT>(a.e_out, o, evs, vout);
     }
   }
+  if constexpr (!QUANT) return;
   // 4. per-token scales and codes (tesm.py:206-209); a position's 32 lanes share its row
   mx_t = wave_max<kF2TPP>(mx_t);
   mx_c = wave_max<kF2TPP>(mx_c);
@@ -1077,6 +1101,17 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
 
+template <bool QUANT>
+static int run_fused2(const EntArgs& a, int64_t weff, hipStream_t st) {
+  const Fused2Lds f2 = fused2_lds(a.R, a.D, weff);
+  dim3 grid2(static_cast<unsigned>((a.L + kF2TP - 1) / kF2TP), static_cast<unsigned>(a.B));
+  if (a.dt == kBF16)
+    ent_fused2_kernel<kBF16, QUANT><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kBF16, QUANT>)>>>(a, weff, f2);
+  else
+    ent_fused2_kernel<kF32, QUANT><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kF32, QUANT>)>>>(a, weff, f2);
+  return check_launch("entanglement fused (32 threads per position)");
+}
+
 // TESM_HIP_NO_ENT_FUSED2=1 keeps the 16-threads-per-position kernel (a diagnostic switch for
 // side-by-side timing and bit-for-bit comparison)
 static bool no_f2() {
@@ -1085,6 +1120,23 @@ static bool no_f2() {
     return e != nullptr && e[0] == '1';
   }();
   return off;
+}
+
+// The 32-threads-per-position form (SISO): D % 16 == 0 up to 512, its load items within 4 / 4 / 2 per
+// thread, 16-byte aligned state rows, LDS within 64 KB.
+static bool fused2_fits(const EntArgs& a, int64_t weff) {
+  if (a.mimo || a.H != 1 || no_f2()) return false;
+  const Fused2Lds f2 = fused2_lds(a.R, a.D, weff);
+  const int64_t rows = kFusedTP + weff - 1, half = a.R / 2, nsl = a.D / 8;
+  return a.D % 16 == 0 && a.D <= 512 && rows * nsl <= 512 * 4 && rows * half <= 512 * 4 && kF2TP * half <= 512 * 2 &&
+         weff <= 64 && a.ld_s % 8 == 0 && aligned(a.S, 16) && f2.total <= 64 * 1024;
+}
+
+// TESM_HIP_ENT_UNFUSED=1 makes the float-output entry (no int8 codes) take the scores + mix kernels
+// instead of the 32-thread fused kernel (read per call: the tests compare the two bit for bit)
+static bool ent_unfused_requested() {
+  const char* e = std::getenv("TESM_HIP_ENT_UNFUSED");
+  return e != nullptr && e[0] == '1';
 }
 
 bool ent_fused_ok(const EntArgs& a) {
@@ -1127,23 +1179,7 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
       return rows * half <= 256 * si && kFusedTP * half <= 256 * (si / 2) && rows * nvec <= 256 * si;
     };
     const bool big = !fits(4) && fits(8);
-    // the 32-threads-per-position form: D % 16 == 0 up to 512, its load items within 4 / 4 / 2 per thread,
-    // 16-byte aligned state rows, LDS within 64 KB
-    {
-      const Fused2Lds f2 = fused2_lds(a.R, a.D, weff);
-      const int64_t nsl = a.D / 8;
-      const bool ok2 = a.D % 16 == 0 && a.D <= 512 && rows * nsl <= 512 * 4 && rows * half <= 512 * 4 &&
-                       kF2TP * half <= 512 * 2 && weff <= 64 && a.ld_s % 8 == 0 && aligned(a.S, 16) &&
-                       f2.total <= 64 * 1024 && !no_f2();
-      if (ok2) {
-        dim3 grid2(static_cast<unsigned>((a.L + kF2TP - 1) / kF2TP), static_cast<unsigned>(a.B));
-        if (a.dt == kBF16)
-          ent_fused2_kernel<kBF16><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kBF16>)>>>(a, weff, f2);
-        else
-          ent_fused2_kernel<kF32><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kF32>)>>>(a, weff, f2);
-        return check_launch("entanglement fused (32 threads per position)");
-      }
-    }
+    if (fused2_fits(a, weff)) return run_fused2<true>(a, weff, st);
     if (a.dt == kBF16) {
       if (big)
         ent_fused_kernel<kBF16, 8><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16, 8>)>>>(a, weff, f);
@@ -1157,6 +1193,8 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
     }
     return check_launch("entanglement fused");
   }
+  // float outputs only: the same 32-thread kernel without its quantization phase
+  if (fused2_fits(a, weff) && !ent_unfused_requested()) return run_fused2<false>(a, weff, st);
   int rc;
   if (a.dt == kBF16)
     rc = a.mimo ? run_scores<kBF16, 1>(a, weff, st) : run_scores<kBF16, 0>(a, weff, st);

@@ -36,7 +36,7 @@ def _case(B, L, R, D, W, dtype, seed, std=1.0):
 @pytest.mark.parametrize("B,L,R,D,W,cross", [(2, 40, 8, 32, 8, False), (1, 300, 64, 256, 16, True),
                                              (3, 17, 16, 48, 32, False), (1, 5, 8, 512, 8, True),
                                              (2, 130, 64, 384, 32, False)])
-def test_fused_entanglement_quant_matches_unfused(dtype, B, L, R, D, W, cross):
+def test_fused_entanglement_quant_matches_unfused(dtype, B, L, R, D, W, cross, monkeypatch):
     q, k, S, bias, cq = _case(B, L, R, D, W, dtype, seed=B * 100 + L + D)
     qa = cq if cross else None
     rope = hip_ops.rope_table(L, R, dtype, DEV)
@@ -47,8 +47,10 @@ def test_fused_entanglement_quant_matches_unfused(dtype, B, L, R, D, W, cross):
             hip_ops.local_ent_quant(q, k, rope, S, bias, W, 0.08, 0.2, q_add=qa)
         return
     weff = min(W, L)
+    monkeypatch.setenv("TESM_HIP_ENT_UNFUSED", "1")  # the float outputs from the scores + mix kernels
     ref = hip_ops.local_ent(q, k, rope, S, bias[-weff:], weff, 0.08, 0.2, q_add=qa,
                             outputs=("e_tanh", "c"), want_tern=True)
+    monkeypatch.delenv("TESM_HIP_ENT_UNFUSED")
     fz = hip_ops.local_ent_quant(q, k, rope, S, bias, W, 0.08, 0.2, q_add=qa, want_floats=True, want_tern=True)
     torch.cuda.synchronize()
     assert torch.equal(fz["tern"], ref["tern"][:, :, 0, :])
@@ -58,6 +60,41 @@ def test_fused_entanglement_quant_matches_unfused(dtype, B, L, R, D, W, cross):
         qf, sf, rf = fz[name]
         assert torch.equal(qf, qr), name
         assert torch.equal(sf, sr) and torch.equal(rf, rr), name
+
+
+def _fused2_fits(R, D, weff):
+    """The 32-threads-per-position kernel's limits as the library states them: 16-channel multiples up to
+    512, at most 4 staged key / state items and 2 query items per thread, its LDS within 64 KB."""
+    rows, half, nsl = 16 + weff - 1, R // 2, D // 8
+    lds = (rows * (R + 4) * 4 + 16 * (R + 4) * 4 + 16 * weff * 4 + 15) // 16 * 16 + rows * nsl * 32
+    return (D % 16 == 0 and D <= 512 and rows * nsl <= 2048 and rows * half <= 2048 and 16 * half <= 1024
+            and weff <= 64 and lds <= 65536)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,L,R,D,W,cross", [(2, 40, 8, 32, 8, False), (1, 300, 64, 256, 16, True),
+                                             (3, 17, 16, 48, 32, False), (1, 5, 8, 512, 8, True),
+                                             (2, 130, 64, 384, 32, False), (8, 512, 48, 256, 16, False)])
+def test_fused_entanglement_float_outputs_match_unfused(dtype, B, L, R, D, W, cross, monkeypatch):
+    """The float-output entry (window average, E, C, tanh(E); tesm.py:921-952, 1231-1232) on the
+    32-threads-per-position kernel equals the scores + mix kernels bit for bit, ternary map included."""
+    q, k, S, bias, cq = _case(B, L, R, D, W, dtype, seed=B * 100 + L + D + 7)
+    qa = cq if cross else None
+    rope = hip_ops.rope_table(L, R, dtype, DEV)
+    weff = min(W, L)
+    names = ("avg", "e", "c", "e_tanh")
+    with hip_ops.launch_log() as log:
+        got = hip_ops.local_ent(q, k, rope, S, bias[-weff:], weff, 0.08, 0.2, q_add=qa, outputs=names, want_tern=True)
+        torch.cuda.synchronize()
+    monkeypatch.setenv("TESM_HIP_ENT_UNFUSED", "1")
+    with hip_ops.launch_log() as log1:
+        ref = hip_ops.local_ent(q, k, rope, S, bias[-weff:], weff, 0.08, 0.2, q_add=qa, outputs=names, want_tern=True)
+        torch.cuda.synchronize()
+    fits = _fused2_fits(R, D, weff)
+    assert any(k_.startswith("ent_fused2_kernel<") for k_ in log.kernels) == fits, log.kernels
+    assert not any(k_.startswith("ent_fused2_kernel<") for k_ in log1.kernels), log1.kernels
+    for name in names + ("tern",):
+        assert torch.equal(got[name], ref[name]), name
 
 
 @pytest.mark.parametrize("name", ["siso_f32", "siso_bf16", "siso_f32_widerank"])
