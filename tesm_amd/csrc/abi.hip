@@ -443,6 +443,24 @@ int run_output_path(const OutputPath& o, hipStream_t st) {
       rq.y = o.taps->yv;
       rq.ldy = o.dm;
     }
+    // the gate and out_proj in one launch where the 32-row kernel takes both: y's codes stay in LDS
+    // (written out only for the decision taps).  TESM_HIP_NO_GATE_OUT=1 keeps the two launches (a
+    // diagnostic switch, read per call: the results are the same bits)
+    const char* no_fuse = std::getenv("TESM_HIP_NO_GATE_OUT");
+    if (!(no_fuse && no_fuse[0] == '1')) {
+      RowQuant rf = rq;
+      if (!o.taps) {
+        rf.q = nullptr;
+        rf.s = nullptr;
+        rf.rs = nullptr;
+      }
+      rc = launch_gate_out(ga, rf, operand(o.xy, *o.out_proj), o.y, o.dm, st);
+      if (rc == kOk) {
+        if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
+        return kOk;
+      }
+      if (rc > 0) return rc;
+    }
     if ((rc = launch_gate_rowq(ga, rq, st))) return rc;
     if (o.taps && (rc = tap_codes(o.taps->q_y, o.taps->s_y, o.xy, o.M, st))) return rc;
   } else {

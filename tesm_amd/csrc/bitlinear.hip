@@ -1982,7 +1982,7 @@ struct G32S {
 inline int64_t gate32_lds_bytes(int64_t Kp, int64_t ldq, int64_t nct, int nw, bool staged) {
   const int64_t slab = staged ? nw * 2 * 32 * (nct * 64 + 8) : 0;
   const int64_t codes = 32 * (ldq + 16);  // aliases the slabs when they are staged (used after them)
-  return 2 * 32 * (Kp + 16) + std::max(slab, codes) + 32 * nw * 4;
+  return 2 * 32 * (Kp + 16) + std::max(slab, codes) + 32 * nw * 4 + 32 * 4;
 }
 
 // a and b rounded to the layer dtype
@@ -1992,8 +1992,18 @@ __device__ __forceinline__ void rnd2(float& a, float& b) {
   b = rnd<DT>(b);
 }
 
-template <int NW, int NCT, int DT, int NKS>
-__global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant o) {
+// The out_proj a 32-row output-gate workgroup runs on its own rows' y codes (gate32_kernel with NKO > 0).
+struct G32Out {
+  const uint8_t* w = nullptr;  // (N, ldw) packed weights, K = N
+  int64_t ldw = 0;
+  const float* c_w = nullptr;  // per-tensor +1 value
+  void* out = nullptr;         // (M, ldo) in the output dtype
+  int64_t ldo = 0;
+};
+
+// NKO > 0: out_proj (NKO K steps of 32 over y's codes, K = N) follows the gate in the same workgroup.
+template <int NW, int NCT, int DT, int NKS, int NKO>
+__global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant o, G32Out op) {
   constexpr int NT = NW * 64;
   constexpr int ARS = G32<NKS>::ARS;
   constexpr int ACH = 2 * 32 * 2 * NKS;        // 16-byte chunks of both operands' activation tiles
@@ -2013,6 +2023,7 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
   int8_t* codes = reinterpret_cast<int8_t*>(slabs);                      // [32][cp], after the slabs are read
   const int region = STG ? NW * 2 * 32 * SP : 0;
   float* red = reinterpret_cast<float*>(slabs + (region > 32 * cp ? region : 32 * cp));  // [NW][32]
+  int32_t* rsl = reinterpret_cast<int32_t*>(red + NW * 32);                            // [32] y code sums
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   __builtin_assume(tid < NT);
   const int h = lane >> 5, row = lane & 31;
@@ -2114,6 +2125,22 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
     for (int c = 0; c < NCT; ++c) {
       acc0[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w0[c][ks]), x0, acc0[c], 0, 0, 0);
       acc1[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w1[c][ks]), x1, acc1[c], 0, 0, 0);
+    }
+  }
+
+  // out_proj's weight fragments (same lane assignment as the gate's: column col0 + 32 c + t, dwords
+  // h NKO .. h NKO + NKO - 1): requested now, they land under the gate's epilogue arithmetic
+  uint32_t w2[NKO > 0 ? NCT : 1][NKO > 0 ? NKO : 1];
+  if constexpr (NKO > 0) {
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      const int n = col0 + 32 * c + row, nc = n < N ? n : N - 1;
+      const uint4* p2 = reinterpret_cast<const uint4*>(op.w + nc * op.ldw + h * NKO * 4);
+#pragma unroll
+      for (int i = 0; i < NKO / 4; ++i) {
+        const uint4 v = p2[i];
+        w2[c][4 * i] = v.x, w2[c][4 * i + 1] = v.y, w2[c][4 * i + 2] = v.z, w2[c][4 * i + 3] = v.w;
+      }
     }
   }
 
@@ -2237,16 +2264,49 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
     sum = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, sum, false);
     sum = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, sum, false);
     sum = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, sum, false);
-    if (mr < a.M) reinterpret_cast<uint4*>(o.q + mr * o.ldq)[ck] = v;
+    if (o.q && mr < a.M) reinterpret_cast<uint4*>(o.q + mr * o.ldq)[ck] = v;
   }
 #pragma unroll
   for (int off = TPR / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-  if (tr == 0 && mr < a.M) {
+  if (tr == 0 && o.q && mr < a.M) {
     float am = 0.0f;
 #pragma unroll
     for (int i = 0; i < NW; ++i) am = fmaxf(am, red[i * 32 + r]);
     o.s[mr] = act_scale<DT>(am, o.eps);
     o.rs[mr] = sum;
+  }
+  if constexpr (NKO > 0) {
+    if (tr == 0) rsl[r] = sum;
+    lds_barrier();
+    // 7. out_proj on the workgroup's y codes (the B operand from the code tile, K split between the lane
+    //    halves as the gate's products split it), then its plain epilogue (acc - rowsum) / s_x * c_w, the
+    //    tiled kernels' op order, so the result equals a separate out_proj bit for bit
+    v16i acc2[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) acc2[c] = v16i{};
+    const char* xr = reinterpret_cast<const char*>(codes) + row * cp + 16 * h * NKO;
+#pragma unroll
+    for (int ks = 0; ks < NKO; ++ks) {
+      const v4i x = *reinterpret_cast<const v4i*>(xr + 16 * ks);
+#pragma unroll
+      for (int c = 0; c < NCT; ++c)
+        acc2[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w2[c][ks]), x, acc2[c], 0, 0, 0);
+    }
+    if (m >= a.M) return;
+    const int32_t rsy = rsl[row];
+    const float invy = 1.0f / sc, cwo = op.c_w[0];
+    const bool vo = vec4_ok<DT>(op.out, op.ldo);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nb = col0 + 32 * c + 8 * g + 4 * h;
+        if (nb >= N) continue;
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) v[rr] = (static_cast<float>(acc2[c][4 * g + rr] - rsy) * invy) * cwo;
+        store4<DT>(op.out, m * op.ldo + nb, v, vo);
+      }
   }
 }
 
@@ -2361,13 +2421,13 @@ int run_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {
   return check_launch("output gate rowq");
 }
 
-template <int NW, int NCT, int NKS>
-void launch_gate32(const LinearArgs& a, const RowQuant& o, int64_t lds, hipStream_t st) {
+template <int NW, int NCT, int NKS, int NKO = 0>
+void launch_gate32(const LinearArgs& a, const RowQuant& o, int64_t lds, hipStream_t st, const G32Out& op = G32Out{}) {
   const unsigned grid = static_cast<unsigned>((a.M + 31) / 32);
   if (a.out_dt == kBF16)
-    gate32_kernel<NW, NCT, kBF16, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kBF16, NKS>)>>>(a, o);
-  else
-    gate32_kernel<NW, NCT, kF32, NKS><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kF32, NKS>)>>>(a, o);
+    gate32_kernel<NW, NCT, kBF16, NKS, NKO><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kBF16, NKS, NKO>)>>>(a, o, op);
+  else if constexpr (NKO == 0)  // the fused out_proj is bf16 only (in float32 its registers would spill)
+    gate32_kernel<NW, NCT, kF32, NKS, NKO><<<grid, NW * 64, lds, TESM_LOGGED(st, gate32_kernel<NW, NCT, kF32, NKS, NKO>)>>>(a, o, op);
 }
 
 template <int NCT>
@@ -2622,6 +2682,45 @@ int launch_linear(const LinearArgs& a, hipStream_t st) {
   }
   if (a.epilogue == kEpiOutputGate) return dispatch_dual<kEpiOutputGate>(a, st);
   return dispatch_dual<kEpiSwiGLU>(a, st);
+}
+
+int launch_gate_out(const LinearArgs& a, const RowQuant& o, const LinearOperand& out_proj, void* out, int64_t ldout,
+                    hipStream_t st) {
+  static const bool off = [] {
+    const char* e = std::getenv("TESM_HIP_NO_GATE32");
+    return e != nullptr && e[0] == '1';
+  }();
+  if (off || a.epilogue != kEpiOutputGate || a.M <= 0 || a.N != 768 || a.out_dt != kBF16) return -1;
+  const int64_t nks = a.Kp / 32;
+  // out_proj over y's codes: K = N = 768 (24 K steps), per-tensor scale, rows of the code pitch
+  if (!out_proj.w || !out_proj.c_w || out_proj.c_w_per_row || o.ldq != kpad(a.N) || out_proj.ldw * 4 != o.ldq ||
+      !aligned(out_proj.w, 16) || !out || ldout < a.N)
+    return -1;
+  if (o.q && !(o.s && o.rs && o.ldq % 16 == 0 && aligned(o.q, 16))) return -1;
+  const bool a16 = a.out_dt != kBF16 || (reinterpret_cast<uintptr_t>(a.local) % 16 == 0 && a.ld_local % 8 == 0 &&
+                                        reinterpret_cast<uintptr_t>(a.gate) % 16 == 0 && a.ld_gate % 8 == 0);
+  if (a.op[0].c_w_per_row || a.op[1].c_w_per_row || !(nks == 4 || nks == 8 || nks == 12) ||
+      !host_vec4_ok(a.local, a.ld_local, a.out_dt) || !host_vec4_ok(a.gate, a.ld_gate, a.out_dt) || !a16 ||
+      (o.y && !host_vec4_ok(o.y, o.ldy, a.out_dt)))
+    return -1;
+  if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
+  if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
+  const DeviceLimits dl = device_limits();
+  const int64_t lds = gate32_lds_bytes(a.Kp, o.ldq, 3, 8, a.out_dt == kBF16);
+  if (dl.cus <= 0 || lds > dl.lds) return -1;
+  G32Out op;
+  op.w = out_proj.w;
+  op.ldw = out_proj.ldw;
+  op.c_w = out_proj.c_w;
+  op.out = out;
+  op.ldo = ldout;
+  if (nks == 4)
+    launch_gate32<8, 3, 4, 24>(a, o, lds, st, op);
+  else if (nks == 8)
+    launch_gate32<8, 3, 8, 24>(a, o, lds, st, op);
+  else
+    launch_gate32<8, 3, 12, 24>(a, o, lds, st, op);
+  return check_launch("output gate + out_proj (32-row tiles)");
 }
 
 int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st) {

@@ -94,4 +94,11 @@ struct RowQuant {
 // Output gate (kEpiOutputGate operands) with the whole row per workgroup; N <= 1024.
 int launch_gate_rowq(const LinearArgs& a, const RowQuant& o, hipStream_t st);
 
+// Output gate and out_proj in one launch: each 32-row workgroup quantizes its y rows into LDS and runs
+// out_proj (K = N = d_model) on them, writing out (M, ldout) in the output dtype.  o.q / o.s / o.rs are
+// written only when o.q is set (decision taps).  Returns -1 (nothing launched) where the sizes do not
+// allow it (bf16, per-tensor weight scales, d_model 768, the 32-row gate's other limits).
+int launch_gate_out(const LinearArgs& a, const RowQuant& o, const LinearOperand& out_proj, void* out, int64_t ldout,
+                    hipStream_t st);
+
 }  // namespace tesm

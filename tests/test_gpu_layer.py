@@ -104,6 +104,29 @@ def test_siso_prefill_properties_at_size():
     assert torch.isfinite(y.float()).all()
 
 
+def test_gate_out_one_launch_matches_two(monkeypatch):
+    """The output gate and out_proj in one launch (bf16, d_model 768, prefills of 4096+ tokens, which take the
+    row-complete gate: y's codes stay in the workgroup's LDS) give the same bits as the gate kernel writing
+    the codes and a separate out_proj (the path taken with TESM_HIP_NO_GATE_OUT=1, by float32 layers and by
+    other widths); tesm.py:1256-1261."""
+    from tesm_amd import hip_ops
+    torch.manual_seed(3)
+    m = TESM_SISO(d_model=768, d_state=256, ent_rank=64, entanglement_window=16, entanglement_threshold=0.08,
+                  entanglement_scale=0.2, decay_init_bias=2.0, max_seq_len=2048).to(DEV).to(torch.bfloat16).eval()
+    u = torch.randn(3, 1500, 768, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        with hip_ops.launch_log() as log:
+            y, f = m(u)
+        monkeypatch.setenv("TESM_HIP_NO_GATE_OUT", "1")
+        with hip_ops.launch_log() as log1:
+            y1, f1 = m(u)
+    assert any(k.startswith("gate32_kernel<8,3,1,8,24>") for k in log.kernels), log.kernels
+    assert not any(k.startswith("mfma32_kernel<1,4,2,1,0,") for k in log.kernels), log.kernels
+    assert any(k.startswith("gate32_kernel<8,3,1,8,0>") for k in log1.kernels), log1.kernels
+    assert torch.isfinite(y.float()).all()
+    assert torch.equal(y, y1) and torch.equal(f, f1)
+
+
 def test_siso_prefill_errors():
     m = TESM_SISO(d_model=64, d_state=32, ent_rank=8, entanglement_window=8, max_seq_len=16).to(DEV).eval()
     with torch.no_grad():
