@@ -2292,9 +2292,36 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
       for (int c = 0; c < NCT; ++c)
         acc2[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(unpack_frag(w2[c][ks]), x, acc2[c], 0, 0, 0);
     }
-    if (m >= a.M) return;
     const int32_t rsy = rsl[row];
     const float invy = 1.0f / sc, cwo = op.c_w[0];
+    if (DT == kBF16 && reinterpret_cast<uintptr_t>(op.out) % 16 == 0 && op.ldo % 8 == 0) {
+      // staged through the wave's own 32 x 80-byte LDS slab, one column tile at a time, so that a store
+      // instruction covers 16 rows x 64 contiguous bytes instead of 32 rows x 8
+      char* os = reinterpret_cast<char*>(rsl + 32) + w * 32 * 80;
+#pragma unroll
+      for (int c = 0; c < NCT; ++c) {
+        if (col0 + 32 * c >= N) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) v[rr] = (static_cast<float>(acc2[c][4 * g + rr] - rsy) * invy) * cwo;
+          *reinterpret_cast<uint2*>(os + row * 80 + (8 * g + 4 * h) * 2) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          const int idx = 64 * it + lane, rr = idx >> 2, ch = idx & 3;
+          const uint4 d = *reinterpret_cast<const uint4*>(os + rr * 80 + 16 * ch);
+          if (m0 + rr < a.M)
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(op.out) + (m0 + rr) * op.ldo + col0 + 32 * c + 8 * ch) = d;
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+      return;
+    }
+    if (m >= a.M) return;
     const bool vo = vec4_ok<DT>(op.out, op.ldo);
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
@@ -2706,7 +2733,8 @@ int launch_gate_out(const LinearArgs& a, const RowQuant& o, const LinearOperand&
   if (int rc = check_operand(a.op[0], a.Kp, "op0")) return rc;
   if (int rc = check_operand(a.op[1], a.Kp, "op1")) return rc;
   const DeviceLimits dl = device_limits();
-  const int64_t lds = gate32_lds_bytes(a.Kp, o.ldq, 3, 8, a.out_dt == kBF16);
+  // plus the out_proj output's staging slabs: 8 waves x 32 rows x 80 bytes
+  const int64_t lds = gate32_lds_bytes(a.Kp, o.ldq, 3, 8, a.out_dt == kBF16) + 8 * 32 * 80;
   if (dl.cus <= 0 || lds > dl.lds) return -1;
   G32Out op;
   op.w = out_proj.w;
