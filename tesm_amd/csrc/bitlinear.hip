@@ -1345,7 +1345,7 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma32_kernel(LinearArgs a) {
 // tiles): columns [0, nA) in 128x256 tiles, two per CU, and the remaining N - nA columns in 128x128
 // tiles launched after them, so the last round runs half-size tiles on more CUs.  Both use two
 // direct-to-LDS stages and eight waves; TMB = 32-row MFMA tiles per wave of a tail tile (2: 128 rows).
-template <int OUT_DT, int TMB>
+template <int OUT_DT, int TMB, int EPI>
 __global__ __launch_bounds__(512) void mfma32_split_kernel(LinearArgs a, int64_t nA) {
   using CA = Cfg32<2, 4, 2, 2>;
   using CB = Cfg32<2, 4, TMB, 1>;
@@ -1355,10 +1355,10 @@ __global__ __launch_bounds__(512) void mfma32_split_kernel(LinearArgs a, int64_t
   int64_t tm, tn;
   if (static_cast<int64_t>(blockIdx.x) < tilesA) {
     xcd_tile_of(blockIdx.x, ntm, ntnA, tm, tn);
-    mfma32_tile<2, 4, 2, 2, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CA::BM, tn * CA::BN, smem);
+    mfma32_tile<2, 4, 2, 2, EPI, OUT_DT, 2, SMEM>(a, tm * CA::BM, tn * CA::BN, smem);
   } else {
     xcd_tile_of(blockIdx.x - tilesA, (a.M + CB::BM - 1) / CB::BM, (a.N - nA + CB::BN - 1) / CB::BN, tm, tn);
-    mfma32_tile<2, 4, TMB, 1, kEpiStore, OUT_DT, 2, SMEM>(a, tm * CB::BM, nA + tn * CB::BN, smem);
+    mfma32_tile<2, 4, TMB, 1, EPI, OUT_DT, 2, SMEM>(a, tm * CB::BM, nA + tn * CB::BN, smem);
   }
 }
 
@@ -2643,7 +2643,6 @@ int dispatch_store32(const LinearArgs& a, hipStream_t st) {
   if (tiles256 >= 512 && a.Kp <= 1024) {
     // more 128x256 tiles than two rounds of the CUs with a narrow remainder (the SISO in_proj: 640
     // tiles): the columns past two tiles per CU go to 128x128 tiles (the split kernel)
-    if constexpr (EPI != kEpiStore) return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);
     const int cus = device_limits().cus;
     const int64_t ntm = (a.M + 127) / 128;
     const int64_t ntnA = cus > 0 ? std::min<int64_t>(a.N / 256, (2 * cus) / ntm) : 0;
@@ -2653,9 +2652,9 @@ int dispatch_store32(const LinearArgs& a, hipStream_t st) {
     if (ntnA >= 1 && a.N > nA && a.N - nA <= 512 && ntm * ntnA + ntmB * ntnB <= 0x7fffffff) {
       const unsigned grid = static_cast<unsigned>(ntm * ntnA + ntmB * ntnB);
       if (a.out_dt == kBF16)
-        mfma32_split_kernel<kBF16, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16, TMB>)>>>(a, nA);
+        mfma32_split_kernel<kBF16, TMB, EPI><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kBF16, TMB, EPI>)>>>(a, nA);
       else
-        mfma32_split_kernel<kF32, TMB><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32, TMB>)>>>(a, nA);
+        mfma32_split_kernel<kF32, TMB, EPI><<<grid, 512, 0, TESM_LOGGED(st, mfma32_split_kernel<kF32, TMB, EPI>)>>>(a, nA);
       return check_launch("bitlinear mfma32 split");
     }
     return run_mfma32<2, 4, 2, 2, EPI, 2>(a, st);

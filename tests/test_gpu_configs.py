@@ -276,7 +276,7 @@ def test_cfg3_siso_layer_at_size(dtype, preset):
         # the benchmarked in_proj instantiation (128x256 tiles for 2048 columns, 128x128 for the rest,
         # two direct-to-LDS stages), the out_proj one (64x128 tiles, two stages) and the single-pass
         # scan with the gates fused and eight sub-spans per workgroup
-        assert _has(log.kernels, f"mfma32_split_kernel<{dc},2>"), log.kernels
+        assert _has(log.kernels, f"mfma32_split_kernel<{dc},2,0>"), log.kernels
         if dtype == torch.bfloat16:  # the output gate and out_proj in one launch (32-row tiles, K 256 / 768)
             assert _has(log.kernels, "gate32_kernel<8,3,1,8,24>"), log.kernels
             assert not _has(log.kernels, "mfma32_kernel<1,4,2,1,0,"), log.kernels
