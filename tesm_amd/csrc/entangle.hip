@@ -115,7 +115,11 @@ __global__ __launch_bounds__(256) void ent_scores_kernel(EntArgs a, int64_t weff
 // ---------------------------------------------------------------------------
 constexpr int kScTP = 64;        // positions per workgroup
 constexpr int kScPairs = 32;     // RoPE pairs per LDS slice (64 values per row)
-constexpr int kScPitch = 2 * kScPairs + 1;
+constexpr int kScPitch = 2 * kScPairs;  // row pitch (floats); 16-byte chunks XOR-swizzled per 4 rows
+
+// LDS position of column c of staged row r: the row's 16 four-column chunks are permuted by (r / 4) % 16,
+// so the 16 lanes of a pass reading rows 4 apart (the window's key rows) hit 16 different bank groups
+__device__ __forceinline__ int sc_col(int r, int c) { return 4 * ((c >> 2) ^ ((r >> 2) & 15)) + (c & 3); }
 
 template <int DT>
 __global__ __launch_bounds__(256) void ent_scores_mimo_kernel(EntArgs a) {
@@ -180,21 +184,46 @@ __global__ __launch_bounds__(256) void ent_scores_mimo_kernel(EntArgs a) {
         const bool ok = i < np && tt_ >= 0 && tt_ < a.L;
         float o1 = 0.0f, o2 = 0.0f;
         if (ok) rope_pair<DT>(from_bits<DT>(xa[u]), from_bits<DT>(xb[u]), cs[u], o1, o2);
-        float* dst = (isq ? qs : ks) + rr * kScPitch + 2 * i;
-        dst[0] = o1;
-        dst[1] = o2;
+        *reinterpret_cast<float2*>((isq ? qs : ks) + rr * kScPitch + sc_col(rr, 2 * i)) = make_float2(o1, o2);
       }
     }
     __syncthreads();
     if (active) {
-      for (int c = 0; c < 2 * np; ++c) {
-        float qv[4], kv[7];
+      // four columns per step (16-byte reads); each product added in increasing column order as before
+      const int nc4 = (2 * np) >> 2;
+      for (int c4 = 0; c4 < nc4; ++c4) {
+        float4 qv[4], kv[7];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qv[i] = qs[(p0 + i) * kScPitch + c];
+        for (int i = 0; i < 4; ++i) {
+          const int r = p0 + i;
+          qv[i] = *reinterpret_cast<const float4*>(qs + r * kScPitch + sc_col(r, 4 * c4));
+        }
 #pragma unroll
         for (int i = 0; i < 7; ++i) {
-          const int r = p0 + w0 + i;
-          kv[i] = r < krows ? ks[r * kScPitch + c] : 0.0f;
+          const int r = p0 + w0 + i, rc = r < krows ? r : krows - 1;
+          const float4 v = *reinterpret_cast<const float4*>(ks + rc * kScPitch + sc_col(rc, 4 * c4));
+          kv[i] = r < krows ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float* qf = reinterpret_cast<const float*>(&qv[i]);
+              const float* kf = reinterpret_cast<const float*>(&kv[i + j]);
+              dot[i][j] += rnd<DT>(qf[e] * kf[e]);
+            }
+      }
+      for (int c = 4 * nc4; c < 2 * np; ++c) {
+        float qv[4], kv[7];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qv[i] = qs[(p0 + i) * kScPitch + sc_col(p0 + i, c)];
+#pragma unroll
+        for (int i = 0; i < 7; ++i) {
+          const int r = p0 + w0 + i, rc = r < krows ? r : krows - 1;
+          const float v = ks[rc * kScPitch + sc_col(rc, c)];
+          kv[i] = r < krows ? v : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
