@@ -268,17 +268,40 @@ __device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int
 // ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------
+// Lane exchanges for order-free reductions inside groups of WIDTH lanes: DPP quad permutes (lane ^ 1,
+// lane ^ 2), the half-row and row mirrors (a lane of the other 4- and 8-lane group, which is all a
+// butterfly needs once each group's lanes agree), a swizzle (lane ^ 16 within 32 lanes) and one
+// cross-half permute (lane ^ 32).  DPP moves are VALU operations; only the last two go through the LDS
+// crossbar, where every __shfl_xor step would.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i within 16
+constexpr int kSwzXor16 = 0x401F;      // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10
+
 template <int WIDTH = 64>
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, WIDTH));
+  if constexpr (WIDTH >= 2) v = fmaxf(v, __int_as_float(dpp_mov<kDppXor1>(__float_as_int(v))));
+  if constexpr (WIDTH >= 4) v = fmaxf(v, __int_as_float(dpp_mov<kDppXor2>(__float_as_int(v))));
+  if constexpr (WIDTH >= 8) v = fmaxf(v, __int_as_float(dpp_mov<kDppHalfMirror>(__float_as_int(v))));
+  if constexpr (WIDTH >= 16) v = fmaxf(v, __int_as_float(dpp_mov<kDppMirror>(__float_as_int(v))));
+  if constexpr (WIDTH >= 32) v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwzXor16)));
+  if constexpr (WIDTH >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
 }
 
 template <int WIDTH = 64>
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
+  if constexpr (WIDTH >= 2) v += dpp_mov<kDppXor1>(v);
+  if constexpr (WIDTH >= 4) v += dpp_mov<kDppXor2>(v);
+  if constexpr (WIDTH >= 8) v += dpp_mov<kDppHalfMirror>(v);
+  if constexpr (WIDTH >= 16) v += dpp_mov<kDppMirror>(v);
+  if constexpr (WIDTH >= 32) v += __builtin_amdgcn_ds_swizzle(v, kSwzXor16);
+  if constexpr (WIDTH >= 64) v += __shfl_xor(v, 32, 64);
   return v;
 }
 

@@ -787,7 +787,9 @@ __device__ __forceinline__ void st8(void* p, int64_t o, const float (&v)[8], boo
 
 // QUANT: the layer's form (int8 codes of tanh(E) and C, optionally their float values too); otherwise
 // the float outputs alone (window average, E, tanh(E), C; each optional), as the unfused kernels give them.
-template <int DT, bool QUANT>
+// KI: staging items per thread for the states and keys (the queries take KI / 2), 2 where the rows fit
+// (every item slot issues a load, so unused slots cost memory instructions), else 4.
+template <int DT, bool QUANT, int KI>
 __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff, Fused2Lds f) {
   using T = typename Elem<DT>::T;
   extern __shared__ __attribute__((aligned(16))) char lds_f2[];
@@ -817,7 +819,7 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
   //    a thread's loads are requested before any is used; rows outside [0, L) are zero.
   const T* S = static_cast<const T*>(a.S);
   {
-    constexpr int kSI = 4, kKI = 4, kQI = 2;  // items per thread (checked on the host)
+    constexpr int kSI = KI, kKI = KI, kQI = KI / 2;  // items per thread (checked on the host)
     v4i sv[kSI][DT == kBF16 ? 1 : 2];
     int sr[kSI], ss[kSI];
 #pragma unroll
@@ -956,7 +958,7 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
       n += fabsf(tern[i]);
       if (a.tern && tok) a.tern[(b * a.L + t) * W + w] = static_cast<int8_t>(tern[i]);
     }
-    n = wave_sum_f<kF2TPP>(n);
+    n = static_cast<float>(wave_sum_i<kF2TPP>(static_cast<int>(n)));  // a count: exact in any order
     n = fmaxf(n, 1.0f);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -1063,8 +1065,8 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      pt[q] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(pt[q]), 1, 64));
-      pc[q] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(pc[q]), 1, 64));
+      pt[q] |= static_cast<uint32_t>(dpp_mov<kDppXor1>(static_cast<int>(pt[q])));  // lane ^ 1
+      pc[q] |= static_cast<uint32_t>(dpp_mov<kDppXor1>(static_cast<int>(pc[q])));
     }
     if (tok && hh == 0 && g < ngq) {
       reinterpret_cast<uint4*>(a.q_te + row * a.ldq)[g] = make_uint4(pt[0], pt[1], pt[2], pt[3]);
@@ -1130,14 +1132,23 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
 
+template <bool QUANT, int KI>
+static void launch_fused2(const EntArgs& a, int64_t weff, const Fused2Lds& f2, hipStream_t st) {
+  dim3 grid2(static_cast<unsigned>((a.L + kF2TP - 1) / kF2TP), static_cast<unsigned>(a.B));
+  if (a.dt == kBF16)
+    ent_fused2_kernel<kBF16, QUANT, KI><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kBF16, QUANT, KI>)>>>(a, weff, f2);
+  else
+    ent_fused2_kernel<kF32, QUANT, KI><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kF32, QUANT, KI>)>>>(a, weff, f2);
+}
+
 template <bool QUANT>
 static int run_fused2(const EntArgs& a, int64_t weff, hipStream_t st) {
   const Fused2Lds f2 = fused2_lds(a.R, a.D, weff);
-  dim3 grid2(static_cast<unsigned>((a.L + kF2TP - 1) / kF2TP), static_cast<unsigned>(a.B));
-  if (a.dt == kBF16)
-    ent_fused2_kernel<kBF16, QUANT><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kBF16, QUANT>)>>>(a, weff, f2);
+  const int64_t rows = kF2TP + weff - 1, half = a.R / 2, nsl = a.D / 8;
+  if (rows * nsl <= 512 * 2 && rows * half <= 512 * 2 && kF2TP * half <= 512)
+    launch_fused2<QUANT, 2>(a, weff, f2, st);
   else
-    ent_fused2_kernel<kF32, QUANT><<<grid2, 512, f2.total, TESM_LOGGED(st, ent_fused2_kernel<kF32, QUANT>)>>>(a, weff, f2);
+    launch_fused2<QUANT, 4>(a, weff, f2, st);
   return check_launch("entanglement fused (32 threads per position)");
 }
 
