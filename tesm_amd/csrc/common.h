@@ -102,6 +102,17 @@ __device__ __forceinline__ float from_bits(uint32_t b) {
   return __uint_as_float(DT == kBF16 ? b << 16 : b);
 }
 
+// acc + a * b where the product of a and b is exact in float32 (values of the bf16 layer dtype: 8-bit
+// significands): one fused multiply-add then gives the bits of the separate multiply and add, which is what
+// float32 operands keep (the library is built with -ffp-contract=off).
+template <int DT>
+__device__ __forceinline__ float madd(float a, float b, float acc) {
+  if constexpr (DT == kBF16)
+    return __builtin_fmaf(a, b, acc);
+  else
+    return acc + a * b;
+}
+
 // Four consecutive elements at p[i .. i+3] in one store; needs i*size 8-byte (bf16) / 16-byte (f32) aligned.
 template <int DT>
 __device__ __forceinline__ void st4(void* p, int64_t i, const float (&v)[4]) {

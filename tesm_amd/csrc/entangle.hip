@@ -605,17 +605,17 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
           const float4 ka = *reinterpret_cast<const float4*>(kp + c);
           const float4 qb = *reinterpret_cast<const float4*>(qp + half + c);
           const float4 kb = *reinterpret_cast<const float4*>(kp + half + c);
-          dot += qa.x * ka.x;
-          dot += qb.x * kb.x;
-          dot += qa.y * ka.y;
-          dot += qb.y * kb.y;
-          dot += qa.z * ka.z;
-          dot += qb.z * kb.z;
-          dot += qa.w * ka.w;
-          dot += qb.w * kb.w;
+          dot = madd<DT>(qa.x, ka.x, dot);
+          dot = madd<DT>(qb.x, kb.x, dot);
+          dot = madd<DT>(qa.y, ka.y, dot);
+          dot = madd<DT>(qb.y, kb.y, dot);
+          dot = madd<DT>(qa.z, ka.z, dot);
+          dot = madd<DT>(qb.z, kb.z, dot);
+          dot = madd<DT>(qa.w, ka.w, dot);
+          dot = madd<DT>(qb.w, kb.w, dot);
         }
         for (int c = half4; c < half; ++c) {
-          dot += qp[c] * kp[c];
+          dot = madd<DT>(qp[c], kp[c], dot);
           dot += qp[half + c] * kp[half + c];
         }
         float sc = rnd<DT>(rnd<DT>(dot) / sq);
@@ -663,14 +663,14 @@ __global__ __launch_bounds__(256) void ent_fused_kernel(EntArgs a, int64_t weff,
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] += wt[u] * x[u][e];
+        for (int e = 0; e < 16; ++e) acc[e] = madd<DT>(wt[u], x[u][e], acc[e]);
     }
     for (; w < W; ++w) {
       float x[16];
       lds_row16<DT>(sx + static_cast<int64_t>(p + w) * dp + 16 * g, x);
       const float wt = wn[p * W + w];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[e] += wt * x[e];
+      for (int e = 0; e < 16; ++e) acc[e] = madd<DT>(wt, x[e], acc[e]);
     }
     float sv[16];
     lds_row16<DT>(sx + static_cast<int64_t>(p + W - 1) * dp + 16 * g, sv);
@@ -938,17 +938,17 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
           const float4 ka = *reinterpret_cast<const float4*>(kp + c);
           const float4 qb = *reinterpret_cast<const float4*>(qp + half + c);
           const float4 kb = *reinterpret_cast<const float4*>(kp + half + c);
-          dot += qa.x * ka.x;
-          dot += qb.x * kb.x;
-          dot += qa.y * ka.y;
-          dot += qb.y * kb.y;
-          dot += qa.z * ka.z;
-          dot += qb.z * kb.z;
-          dot += qa.w * ka.w;
-          dot += qb.w * kb.w;
+          dot = madd<DT>(qa.x, ka.x, dot);
+          dot = madd<DT>(qb.x, kb.x, dot);
+          dot = madd<DT>(qa.y, ka.y, dot);
+          dot = madd<DT>(qb.y, kb.y, dot);
+          dot = madd<DT>(qa.z, ka.z, dot);
+          dot = madd<DT>(qb.z, kb.z, dot);
+          dot = madd<DT>(qa.w, ka.w, dot);
+          dot = madd<DT>(qb.w, kb.w, dot);
         }
         for (int c = half4; c < half; ++c) {
-          dot += qp[c] * kp[c];
+          dot = madd<DT>(qp[c], kp[c], dot);
           dot += qp[half + c] * kp[half + c];
         }
         float sc = rnd<DT>(rnd<DT>(dot) / sq);
@@ -1005,14 +1005,14 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
 #pragma unroll
       for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += wt[u] * x[u][e];
+        for (int e = 0; e < 8; ++e) acc[e] = madd<DT>(wt[u], x[u][e], acc[e]);
     }
     for (; w < W; ++w) {
       float x[8];
       row8(p + w, x);
       const float wt = wn[p * W + w];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += wt * x[e];
+      for (int e = 0; e < 8; ++e) acc[e] = madd<DT>(wt, x[e], acc[e]);
     }
     float sv[8], av[8], evs[8];
     row8(p + W - 1, sv);
