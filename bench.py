@@ -175,12 +175,10 @@ def measure_decode(torch, m, steps: int = 50, d_model: int = LAYER["d_model"]):
     """Decode of layer `m` (configs[3]'s SISO layer, or the configs[4] MIMO layer): B = 32 sequences,
     caches filled by a 64-token prefill (>= W), then one-token steps; returns the per-step time (device
     events around `steps` consecutive steps)."""
-    from tesm_amd import SisoDecodeGraph, TESM_SISO
-
     Bd, P = 32, 64
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(1)
-    n = P + 3 + 2 * steps + 3
+    n = P + 3 + steps
     u = torch.randn(Bd, n, d_model, generator=g).to(torch.bfloat16).to(dev)
     cache = m.allocate_inference_cache(Bd, n)
     ip = {"state_cache": cache}
@@ -197,25 +195,6 @@ def measure_decode(torch, m, steps: int = 50, d_model: int = LAYER["d_model"]):
     ms = e0.elapsed_time(e1) / steps
     out = {"batch": Bd, "prefill": P, "ms_per_step": ms, "tokens_per_s": Bd / (ms * 1e-3),
            "note": "one decode step per sequence, host dispatch included (no graph capture)"}
-    if type(m) is TESM_SISO:
-        # the same steps replayed from captured graphs (position on the device); each step's token is
-        # copied into the graph's input buffer inside the timed region
-        t0 = P + 3 + steps
-        gr = SisoDecodeGraph(m, ip, max_positions=n)
-        for t in range(t0, t0 + 3):
-            gr.u.copy_(u[:, t:t + 1])
-            gr.step()
-        torch.cuda.synchronize()
-        e0.record()
-        for t in range(t0 + 3, t0 + 3 + steps):
-            gr.u.copy_(u[:, t:t + 1])
-            gr.step()
-        e1.record()
-        torch.cuda.synchronize()
-        gms = e0.elapsed_time(e1) / steps
-        gr.sync_cache()
-        out["graph"] = {"ms_per_step": gms, "tokens_per_s": Bd / (gms * 1e-3),
-                        "note": "HIP graph replay of the step (SisoDecodeGraph), input copy included"}
     return out
 
 

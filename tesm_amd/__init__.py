@@ -3,8 +3,7 @@
 Public API mirrors the reference package ``tesm_ssm`` for this path:
 ``BitLinear``, ``TESM_SISO`` (alias ``TESM``), ``TESMMIMO_Optimized`` and ``TESMConfig``, plus the
 block and model around the layers (``RMSNorm``, ``Block``, ``FeedForward``, ``MixerModel``,
-``TESMLMHeadModel``), the INT2 export format (``tesm_amd.int2``) and graph-replayed decode steps
-(``SisoDecodeGraph``).  Kernels live in
+``TESMLMHeadModel``) and the INT2 export format (``tesm_amd.int2``).  Kernels live in
 ``tesm_amd/csrc`` and are reached through the C-ABI library ``libtesm_hip.so``
 (``include/tesm_hip.h``).
 """
@@ -12,8 +11,8 @@ from .bitlinear import BitLinear
 from .block import Block, RMSNorm
 from .config import TESMConfig
 from .lm import FeedForward, MixerModel, TESMCausalLMOutput, TESMLMHeadModel
-from .tesm import TESM, TESM_SISO, SisoDecodeGraph
+from .tesm import TESM, TESM_SISO
 from .tesm_mimo import TESMMIMO_Optimized
 
-__all__ = ["BitLinear", "Block", "FeedForward", "MixerModel", "RMSNorm", "SisoDecodeGraph", "TESM",
-           "TESMCausalLMOutput", "TESMConfig", "TESMLMHeadModel", "TESM_SISO", "TESMMIMO_Optimized"]
+__all__ = ["BitLinear", "Block", "FeedForward", "MixerModel", "RMSNorm", "TESM", "TESMCausalLMOutput", "TESMConfig",
+           "TESMLMHeadModel", "TESM_SISO", "TESMMIMO_Optimized"]

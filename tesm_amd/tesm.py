@@ -395,96 +395,4 @@ class TESM_SISO(nn.Module):
         return y, state_out
 
 
-class SisoDecodeGraph:
-    """One-token decode steps of a TESM_SISO layer replayed from captured HIP graphs (the reference's
-    step, tesm.py:1274-1400, without per-step host dispatch).
-
-    The step's position and ring slot live in device memory (``tesm_hip_siso_step.step_pos``) and the
-    captured call advances them, so nothing on the host changes between replays; two graphs alternate
-    the float64 state buffers.  Per step: write the token into ``u`` (B, 1, d_model), call ``step()``,
-    read ``y`` (and ``new_state``, the next layer's cross-layer state).  ``sync_cache()`` hands state,
-    position and slot back to the inference cache, after which eager steps may continue.  The graphs
-    read the ring buffers of ``inference_params`` in place and need a RoPE table of ``max_positions``
-    rows; no cross-layer query (``cross_layer_state`` is not supported here).  The captured graphs hold
-    the packed weights and biases of the moment of capture: ``step()`` raises once a step would pass
-    ``max_positions`` or once a weight or bias of the layer has changed (load_state_dict, an INT2
-    load, an in-place update); build a new instance then."""
-
-    def __init__(self, layer: "TESM_SISO", inference_params, max_positions: int, dtype: torch.dtype | None = None):
-        if type(layer) is not TESM_SISO:
-            raise TypeError(f"SisoDecodeGraph: takes a TESM_SISO layer, got {type(layer).__name__}")
-        lib = _lib.load()
-        cache = inference_params["state_cache"]
-        self.cache = cache
-        kc, vc = cache["ent_k_cache"], cache["ent_v_cache"]
-        state = cache["state"]
-        dev = state.device
-        B, D = state.shape
-        W = kc.shape[1]
-        dt = dtype if dtype is not None else layer.in_proj.weight.dtype
-        layer._check_cache(kc, vc, B, dev)
-        if state.dtype != torch.float64:
-            raise RuntimeError("SisoDecodeGraph: cache['state'] must be float64")
-        pos = int(cache["seq_pos"])
-        if max_positions <= pos:
-            raise ValueError("SisoDecodeGraph: max_positions must exceed the cache's seq_pos")
-        desc, nbytes, keep = layer._step_plan(B, dt, dev, kc.dtype, W, False)
-        self.layer, self._key_args = layer, (B, dt, dev, kc.dtype, W, False)
-        self._key = layer._step_key(*self._key_args)
-        self.start, self.max_positions = pos, max_positions
-        dm = layer.d_model
-        self.u = torch.zeros((B, 1, dm), dtype=dt, device=dev)
-        self.y = torch.empty((B, 1, dm), dtype=dt, device=dev)
-        self.new_state = torch.empty((B, D), dtype=dt, device=dev)
-        self.states = [state.contiguous().clone(), torch.empty_like(state)]
-        self.step_pos = torch.tensor([pos, int(cache.get("cache_idx", 0))], dtype=torch.int64, device=dev)
-        self.rope = layer.rope_table(max_positions, dt, dev)
-        self.ws = torch.empty((max(nbytes, 256),), dtype=torch.uint8, device=dev)
-        self._keep = keep
-        self.window = W
-        self.k = 0
-        self.graphs = []
-        for i in range(2):
-            d = _lib.SisoStep()
-            ctypes.memmove(ctypes.byref(d), ctypes.byref(desc), ctypes.sizeof(d))
-            d.seq_pos, d.cache_idx = 0, 0  # not read: the position comes from step_pos
-            d.u, d.ld_u = self.u.data_ptr(), dm
-            d.cross_state = None
-            d.rope, d.rope_rows = self.rope.data_ptr(), self.rope.shape[0]
-            d.state, d.state_out = self.states[i].data_ptr(), self.states[1 - i].data_ptr()
-            d.k_cache, d.v_cache = kc.data_ptr(), vc.data_ptr()
-            d.y, d.new_state = self.y.data_ptr(), self.new_state.data_ptr()
-            d.step_pos = self.step_pos.data_ptr()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.device(dev), torch.cuda.graph(g, capture_error_mode="relaxed"):
-                rc = lib.tesm_hip_siso_decode(ctypes.byref(d), ctypes.c_void_p(self.ws.data_ptr()), self.ws.numel(),
-                                              ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
-            _lib.check(rc)
-            self.graphs.append((g, d))
-
-    def step(self) -> torch.Tensor:
-        """Replay one step on the current stream; returns ``y`` (B, 1, d_model), overwritten by the next."""
-        if self.start + self.k >= self.max_positions:
-            raise RuntimeError(f"SisoDecodeGraph: position {self.start + self.k} is past the RoPE table of "
-                               f"max_positions={self.max_positions}; build a new instance with more positions")
-        if self.layer._step_key(*self._key_args) != self._key:
-            raise RuntimeError("SisoDecodeGraph: the layer's weights or biases changed after capture; the graphs "
-                               "hold the old ones -- build a new instance")
-        self.graphs[self.k % 2][0].replay()
-        self.k += 1
-        return self.y
-
-    @property
-    def state(self) -> torch.Tensor:
-        """float64 state after the steps replayed so far."""
-        return self.states[self.k % 2]
-
-    def sync_cache(self):
-        """Write state, position and ring slot back into the inference cache (reads the position)."""
-        pos, idx = (int(v) for v in self.step_pos.cpu())
-        self.cache["state"] = self.state.clone()
-        self.cache["seq_pos"] = pos
-        self.cache["cache_idx"] = idx
-
-
 TESM = TESM_SISO

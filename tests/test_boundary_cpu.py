@@ -137,15 +137,6 @@ def test_host_tensors_are_rejected_before_any_launch():
         hip_ops.quant_act(torch.randn(2, 8))
 
 
-def test_decode_graph_takes_only_the_siso_layer():
-    """The MIMO layer subclasses the SISO layer but has another decode path: graph replay must refuse it."""
-    from tesm_amd import SisoDecodeGraph, TESMMIMO_Optimized
-    m = TESMMIMO_Optimized(d_model=32, d_state=8, n_heads=2, mimo_rank=2, ent_rank=4, entanglement_window=4,
-                           max_seq_len=8)
-    with pytest.raises(TypeError, match="TESM_SISO"):
-        SisoDecodeGraph(m, {"state_cache": {}}, max_positions=8)
-
-
 def test_lm_construction_matches_reference():
     """TESMLMHeadModel(tiny()) from seed 0 holds the reference's parameters (the fingerprints the
     reference wrote: shape, first values, sum), and a small model equals the oracle's state_dict."""
