@@ -1088,6 +1088,340 @@ __global__ __launch_bounds__(512) void ent_fused2_kernel(EntArgs a, int64_t weff
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused SISO kernel, third form: the window mix in registers, for the shapes whose state halo does not
+// fit ent_fused2_kernel's LDS (D 384-512 with window 32; D 384 with rank 96).  A workgroup owns (batch
+// row b, 2 TS positions) and all D channels (D % 64 == 0, D <= 512); thread (s, ch) owns channel ch of
+// the TS positions of half s.  A position's window mix reads its own channel's states only, so the thread
+// loads the W - 1 + 16 states of its channel it needs (as raw bits, all in flight at once, straight
+// from the state tensor) and forms its 16 window sums from registers, the window weights being the
+// same for all 64 lanes of a wave (broadcast LDS reads).  The weights come from one (position, window
+// slot) pair per thread over RoPE'd q / k rows staged in LDS; tanh(E) and C are staged in LDS and
+// quantized with one 16-channel group per thread.  Every value is the same sequence of float
+// operations as in ent_fused2_kernel, so the two give the same bits.
+// ---------------------------------------------------------------------------
+
+struct RegLds {
+  int64_t kr, qr, wn, stg, total;  // byte offsets
+  int64_t krs;                     // row pitch of the RoPE'd key / query rows, floats
+  int64_t nq;                      // quantities (tanh(E), C) staged per quantization pass
+};
+
+__host__ __device__ inline RegLds reg_lds(int64_t D, int64_t R, int64_t W, int wm, int es, int64_t tp) {
+  auto al = [](int64_t v) { return (v + 15) / 16 * 16; };
+  RegLds f;
+  f.krs = R + 4;
+  f.kr = 0;
+  f.qr = al(f.kr + (tp + W - 1) * f.krs * 4);
+  f.wn = al(f.qr + tp * f.krs * 4);
+  const int64_t end_wn = f.wn + tp * wm * 4;
+  // tanh(E) / C staging reuses the key rows onward once the mix has read the weights: both at once
+  // where that stays within 64 KB
+  f.stg = 0;
+  const int64_t e1 = tp * D * es, e2 = 2 * e1;
+  f.nq = (e2 <= end_wn || e2 <= 64 * 1024) ? 2 : 1;
+  const int64_t end_stg = f.nq == 2 ? e2 : e1;
+  f.total = end_wn > end_stg ? end_wn : end_stg;
+  return f;
+}
+
+// WM: window slots of the mix (16 or 32; a window W < WM is right-aligned, the first WM - W slots
+// weigh zero).  KI: key staging items per thread in the first round (queries: 2).
+template <int DT, int WM, int KI, int NTM, int TS>
+__global__ __launch_bounds__(NTM, 1) void ent_reg_kernel(EntArgs e, int64_t weff, RegLds f) {
+  using T = typename Elem<DT>::T;
+  constexpr int TP = 2 * TS, NX = WM - 1 + TS;
+  extern __shared__ __attribute__((aligned(16))) char lds_rg[];
+  float* kr = reinterpret_cast<float*>(lds_rg + f.kr);
+  float* qr = reinterpret_cast<float*>(lds_rg + f.qr);
+  float* wn = reinterpret_cast<float*>(lds_rg + f.wn);
+  T* stg = reinterpret_cast<T*>(lds_rg + f.stg);
+  const int tid = threadIdx.x;
+  const int D = static_cast<int>(e.D), W = static_cast<int>(weff), half = static_cast<int>(e.R / 2);
+  const int krs = static_cast<int>(f.krs), NT = 2 * D;
+  const int s = __builtin_amdgcn_readfirstlane(tid / D);  // D % 64 == 0: uniform per wave
+  const int ch = tid - s * D;
+  const int64_t L = e.L, b = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TP, ts = t0 + s * TS;
+  const int n = ts >= L ? 0 : static_cast<int>(ts + TS < L ? TS : L - ts);  // wave-uniform
+  const int rows = TP + W - 1;
+  const int64_t tk0 = t0 - (W - 1);
+  const int zs = WM - W;  // leading zero-weight slots
+
+  // 1. every load: the states of the thread's window rows (x[k] is position ts - (WM - 1) + k; rows
+  //    outside [0, L) and the zero-weight slots re-read a valid row and are zeroed), keys and queries
+  //    with their RoPE rows, the window bias of the thread's first score slot
+  uint32_t xb[NX];
+  {
+    const T* S = static_cast<const T*>(e.S);
+#pragma unroll
+    for (int k = 0; k < NX; ++k) {
+      int64_t pos = ts - (WM - 1) + k;
+      pos = pos < 0 ? 0 : (pos >= L ? L - 1 : pos);
+      xb[k] = ld_bits<DT>(S + (b * L + pos) * e.ld_s, ch);
+    }
+  }
+  constexpr int kQI = 2;
+  float kxa[KI], kxb[KI], qxa[kQI], qxb[kQI], qaa[kQI], qab[kQI];
+  float2 kcs[KI], qcs[kQI];
+#pragma unroll
+  for (int k = 0; k < KI; ++k) {
+    const int i = tid + NT * k;
+    const int r = i / half, cc = i - r * half;
+    int64_t tt = tk0 + (r < rows ? r : rows - 1);
+    tt = tt < 0 ? 0 : (tt >= L ? L - 1 : tt);
+    const int64_t ko = (b * L + tt) * e.ld_k;
+    kxa[k] = ld<DT>(e.k, ko + cc);
+    kxb[k] = ld<DT>(e.k, ko + half + cc);
+    kcs[k] = e.rope[tt * half + cc];
+  }
+#pragma unroll
+  for (int k = 0; k < kQI; ++k) {
+    const int i = tid + NT * k;
+    const int pp = i / half, cc = i - pp * half;
+    const int64_t tt = (t0 + pp < L && pp < TP) ? t0 + pp : L - 1;
+    const int64_t qo = (b * L + tt) * e.ld_q;
+    qxa[k] = ld<DT>(e.q, qo + cc);
+    qxb[k] = ld<DT>(e.q, qo + half + cc);
+    qcs[k] = e.rope[tt * half + cc];
+    qaa[k] = qab[k] = 0.0f;
+    if (e.q_add) {
+      const int64_t ao = (b * L + tt) * e.ld_qadd;
+      qaa[k] = ld<DT>(e.q_add, ao + cc);
+      qab[k] = ld<DT>(e.q_add, ao + half + cc);
+    }
+  }
+  float wbias0;
+  {
+    const int w = tid % WM;
+    wbias0 = e.bias[e.W - W + (w < W ? w : W - 1)];
+  }
+
+  // 2. RoPE'd keys and queries into LDS (rows outside [0, L) are zero); items beyond the first round
+  //    (small D with a wide rank) are loaded and rotated one at a time
+#pragma unroll
+  for (int k = 0; k < KI; ++k) {
+    const int i = tid + NT * k;
+    const int r = i / half, cc = i - r * half;
+    if (r >= rows) break;
+    const int64_t tt = tk0 + r;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (tt >= 0 && tt < L) rope_pair<DT>(kxa[k], kxb[k], kcs[k], o1, o2);
+    kr[r * krs + cc] = o1;
+    kr[r * krs + half + cc] = o2;
+  }
+#pragma unroll
+  for (int k = 0; k < kQI; ++k) {
+    const int i = tid + NT * k;
+    const int pp = i / half, cc = i - pp * half;
+    if (pp >= TP) break;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (t0 + pp < L) {
+      rope_pair<DT>(qxa[k], qxb[k], qcs[k], o1, o2);
+      if (e.q_add) {
+        o1 = rnd<DT>(o1 + qaa[k]);
+        o2 = rnd<DT>(o2 + qab[k]);
+      }
+    }
+    qr[pp * krs + cc] = o1;
+    qr[pp * krs + half + cc] = o2;
+  }
+  for (int i = tid + NT * KI; i < rows * half; i += NT) {
+    const int r = i / half, cc = i - r * half;
+    const int64_t tt = tk0 + r;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (tt >= 0 && tt < L) {
+      const int64_t ko = (b * L + tt) * e.ld_k;
+      rope_pair<DT>(ld<DT>(e.k, ko + cc), ld<DT>(e.k, ko + half + cc), e.rope[tt * half + cc], o1, o2);
+    }
+    kr[r * krs + cc] = o1;
+    kr[r * krs + half + cc] = o2;
+  }
+  for (int i = tid + NT * kQI; i < TP * half; i += NT) {
+    const int pp = i / half, cc = i - pp * half;
+    const int64_t tt = t0 + pp;
+    float o1 = 0.0f, o2 = 0.0f;
+    if (tt < L) {
+      const int64_t qo = (b * L + tt) * e.ld_q;
+      rope_pair<DT>(ld<DT>(e.q, qo + cc), ld<DT>(e.q, qo + half + cc), e.rope[tt * half + cc], o1, o2);
+      if (e.q_add) {
+        const int64_t ao = (b * L + tt) * e.ld_qadd;
+        o1 = rnd<DT>(o1 + ld<DT>(e.q_add, ao + cc));
+        o2 = rnd<DT>(o2 + ld<DT>(e.q_add, ao + half + cc));
+      }
+    }
+    qr[pp * krs + cc] = o1;
+    qr[pp * krs + half + cc] = o2;
+  }
+  __syncthreads();
+
+  // 3. window scores, ternary decisions and weights (ent_fused2_kernel's arithmetic); WM lanes per
+  //    position, slot w of the effective window at weight column WM - W + w
+  {
+    const float sq = static_cast<float>(sqrt(static_cast<double>(e.R)));
+    const int half4 = (half % 4 == 0) ? half : 0;
+    for (int item = tid; item < TP * WM; item += NT) {  // uniform per wave (TP * WM, NT multiples of 64)
+      const int p = item / WM, w = item % WM;
+      const int64_t t = t0 + p;
+      const bool tok = t < L;
+      float tern = 0.0f;
+      if (w < W) {
+        const int64_t j = t - (W - 1) + w;
+        if (tok && j >= 0) {
+          const float* qp = qr + p * krs;
+          const float* kp = kr + (p + w) * krs;
+          float dot = 0.0f;
+          for (int cc = 0; cc < half4; cc += 4) {
+            const float4 qa = *reinterpret_cast<const float4*>(qp + cc);
+            const float4 ka = *reinterpret_cast<const float4*>(kp + cc);
+            const float4 qb = *reinterpret_cast<const float4*>(qp + half + cc);
+            const float4 kb = *reinterpret_cast<const float4*>(kp + half + cc);
+            dot = madd<DT>(qa.x, ka.x, dot);
+            dot = madd<DT>(qb.x, kb.x, dot);
+            dot = madd<DT>(qa.y, ka.y, dot);
+            dot = madd<DT>(qb.y, kb.y, dot);
+            dot = madd<DT>(qa.z, ka.z, dot);
+            dot = madd<DT>(qb.z, kb.z, dot);
+            dot = madd<DT>(qa.w, ka.w, dot);
+            dot = madd<DT>(qb.w, kb.w, dot);
+          }
+          for (int cc = half4; cc < half; ++cc) {
+            dot = madd<DT>(qp[cc], kp[cc], dot);
+            dot = madd<DT>(qp[half + cc], kp[half + cc], dot);
+          }
+          float sc = rnd<DT>(rnd<DT>(dot) / sq);
+          const float wb = item == tid ? wbias0 : e.bias[e.W - W + w];
+          sc = rnd<DT>(sc + wb);
+          tern = sc > e.thr ? 1.0f : (sc < -e.thr ? -1.0f : 0.0f);
+        }
+        if (e.tern && tok) e.tern[(b * L + t) * W + w] = static_cast<int8_t>(tern);
+      }
+      float nn = static_cast<float>(wave_sum_i<WM>(static_cast<int>(fabsf(tern))));  // a count: exact
+      nn = fmaxf(nn, 1.0f);
+      if (w < W)
+        wn[p * WM + (WM - W) + w] = rnd<DT>(tern / nn);
+      else
+        wn[p * WM + (w - W)] = 0.0f;
+    }
+  }
+  __syncthreads();
+
+  // 4. window sums of the thread's TS positions (slots in order, as ent_fused2_kernel sums them), E,
+  //    tanh(E) and C
+  float x[NX];
+#pragma unroll
+  for (int k = 0; k < NX; ++k) {
+    const int64_t pos = ts - (WM - 1) + k;
+    const bool in = k >= zs && pos >= 0 && pos < L;
+    x[k] = in ? from_bits<DT>(xb[k]) : 0.0f;
+  }
+  float tv[TS], cv[TS];
+  {
+    float acc[TS];
+#pragma unroll
+    for (int i = 0; i < TS; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int w4 = 0; w4 < WM; w4 += 4) {
+#pragma unroll
+      for (int i = 0; i < TS; ++i) {
+        const float4 wt = *reinterpret_cast<const float4*>(wn + (s * TS + i) * WM + w4);
+        acc[i] = madd<DT>(wt.x, x[i + w4], acc[i]);
+        acc[i] = madd<DT>(wt.y, x[i + w4 + 1], acc[i]);
+        acc[i] = madd<DT>(wt.z, x[i + w4 + 2], acc[i]);
+        acc[i] = madd<DT>(wt.w, x[i + w4 + 3], acc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TS; ++i) {
+      const float s0 = x[WM - 1 + i];
+      const float avg = rnd<DT>(acc[i]);
+      const float ev = rnd<DT>(s0 + rnd<DT>(e.ent_scale * rnd<DT>(avg - s0)));
+      cv[i] = rnd<DT>(ev - s0);
+      tv[i] = rnd<DT>(tanhf_(ev));
+    }
+  }
+  if (e.e_tanh || e.c_out) {
+#pragma unroll
+    for (int i = 0; i < TS; ++i) {
+      if (i >= n) break;
+      const int64_t o = (b * L + ts + i) * e.ld_out + ch;
+      if (e.e_tanh) st<DT>(e.e_tanh, o, tv[i]);
+      if (e.c_out) st<DT>(e.c_out, o, cv[i]);
+    }
+  }
+
+  // 5. per-token codes of tanh(E) and of C: each thread's column staged in LDS (both quantities in one
+  //    pass where they fit, f.nq = 2, else one at a time), then one 16-channel group per thread, GQ
+  //    lanes per position (a power of two >= D / 16)
+  const int groups = D / 16, ngq = static_cast<int>(e.ldq / 16);
+  const int GQ = groups <= 4 ? 4 : (groups <= 8 ? 8 : (groups <= 16 ? 16 : 32));
+  const int nq = static_cast<int>(f.nq);
+  constexpr int NV = 16 * static_cast<int>(sizeof(T)) / 16;  // 16-byte LDS reads per group
+  for (int q0 = 0; q0 < 2; q0 += nq) {
+    __syncthreads();  // the mix's (or the previous pass's) LDS reads are done
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      if (q < q0 || q >= q0 + nq) continue;  // uniform
+      T* row0 = stg + ((q - q0) * TP + s * TS) * D + ch;
+#pragma unroll
+      for (int i = 0; i < TS; ++i) {
+        const float v = q == 0 ? tv[i] : cv[i];
+        if constexpr (DT == kBF16)
+          row0[i * D] = static_cast<T>(__float_as_uint(v) >> 16);
+        else
+          row0[i * D] = v;
+      }
+    }
+    __syncthreads();
+    for (int item = tid; item < nq * TP * GQ; item += NT) {  // uniform per wave (TP * GQ % 64 == 0)
+      const int ql = item / (TP * GQ), rem = item - ql * (TP * GQ), qn = q0 + ql;
+      const int p = rem / GQ, gi = rem % GQ;
+      const int64_t t = t0 + p, row = b * L + t;
+      const bool tok = t < L;
+      int8_t* qo = qn == 0 ? e.q_te : e.q_c;
+      float* so = qn == 0 ? e.s_te : e.s_c;
+      int32_t* ro = qn == 0 ? e.rs_te : e.rs_c;
+      const int gl = gi < groups ? gi : groups - 1;
+      const uint4* src = reinterpret_cast<const uint4*>(stg + (ql * TP + p) * D + 16 * gl);
+      uint4 raw[NV];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) raw[j] = src[j];
+      const uint32_t* wd = reinterpret_cast<const uint32_t*>(raw);
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float fv;
+        if constexpr (DT == kBF16)
+          fv = __uint_as_float(j % 2 == 0 ? wd[j / 2] << 16 : wd[j / 2] & 0xffff0000u);
+        else
+          fv = __uint_as_float(wd[j]);
+        v[j] = gi < groups ? fv : 0.0f;
+      }
+      float mx = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(v[j]));
+      if (GQ == 4) mx = wave_max<4>(mx);
+      else if (GQ == 8) mx = wave_max<8>(mx);
+      else if (GQ == 16) mx = wave_max<16>(mx);
+      else mx = wave_max<32>(mx);
+      const float sc = act_scale<DT>(mx, e.eps);
+      int32_t rs = 0;
+      const uint4 cw = group_codes<DT>(v, sc, 1, rs);
+      if (tok && gi < groups) reinterpret_cast<uint4*>(qo + row * e.ldq)[gi] = cw;
+      for (int gp = groups + gi; tok && gp < ngq; gp += GQ)
+        reinterpret_cast<uint4*>(qo + row * e.ldq)[gp] = make_uint4(0, 0, 0, 0);
+      if (GQ == 4) rs = wave_sum_i<4>(rs);
+      else if (GQ == 8) rs = wave_sum_i<8>(rs);
+      else if (GQ == 16) rs = wave_sum_i<16>(rs);
+      else rs = wave_sum_i<32>(rs);
+      if (tok && gi == 0) {
+        so[row] = sc;
+        ro[row] = rs;
+      }
+    }
+  }
+}
+
 template <int DT, int MIMO>
 int run_scores(const EntArgs& a, int64_t weff, hipStream_t st) {
   if (MIMO && a.q_add == nullptr) {
@@ -1131,6 +1465,51 @@ int launch_rope_table(float2* tab, int64_t L, int64_t R, int64_t pos_offset, dou
 }
 
 static int64_t eff_window(const EntArgs& a) { return a.mimo ? a.W : std::min(a.W, a.L); }
+
+constexpr int kRegTS = 8;  // positions per thread of the register-mix kernel (16 per workgroup)
+
+template <int DT, int WM, int KI>
+static void launch_reg_k(const EntArgs& a, int64_t weff, const RegLds& f, hipStream_t st) {
+  constexpr int TS = kRegTS;
+  dim3 grid(static_cast<unsigned>((a.L + 2 * TS - 1) / (2 * TS)), static_cast<unsigned>(a.B));
+  const unsigned nt = static_cast<unsigned>(2 * a.D);  // the register cap follows nt
+  if (nt > 768)
+    ent_reg_kernel<DT, WM, KI, 1024, TS><<<grid, nt, f.total, TESM_LOGGED(st, ent_reg_kernel<DT, WM, KI, 1024, TS>)>>>(a, weff, f);
+  else if (nt > 512)
+    ent_reg_kernel<DT, WM, KI, 768, TS><<<grid, nt, f.total, TESM_LOGGED(st, ent_reg_kernel<DT, WM, KI, 768, TS>)>>>(a, weff, f);
+  else
+    ent_reg_kernel<DT, WM, KI, 512, TS><<<grid, nt, f.total, TESM_LOGGED(st, ent_reg_kernel<DT, WM, KI, 512, TS>)>>>(a, weff, f);
+}
+
+template <int DT>
+static int run_reg(const EntArgs& a, int64_t weff, hipStream_t st) {
+  const int wm = weff <= 16 ? 16 : 32;
+  const RegLds f = reg_lds(a.D, a.R, weff, wm, DT == kBF16 ? 2 : 4, 2 * kRegTS);
+  const int64_t ki = ((2 * kRegTS + weff - 1) * (a.R / 2) + 2 * a.D - 1) / (2 * a.D);  // first-round key items
+  if (wm == 16) {
+    if (ki <= 2) launch_reg_k<DT, 16, 2>(a, weff, f, st);
+    else if (ki == 3) launch_reg_k<DT, 16, 3>(a, weff, f, st);
+    else launch_reg_k<DT, 16, 4>(a, weff, f, st);
+  } else {
+    if (ki <= 2) launch_reg_k<DT, 32, 2>(a, weff, f, st);
+    else if (ki == 3) launch_reg_k<DT, 32, 3>(a, weff, f, st);
+    else launch_reg_k<DT, 32, 4>(a, weff, f, st);
+  }
+  return check_launch("entanglement fused (window mix in registers)");
+}
+
+// The register-mix form (SISO, quantized outputs): D a multiple of 64 up to 512, an effective window of
+// at most 32, LDS within 64 KB.  It runs where neither of the other fused kernels fits (float32 rows of
+// 384+ channels, which otherwise take the scores + mix kernels and two activation quantizations: the
+// tiny() model's float32 forward 2.92 -> 2.51 ms); where they fit they are faster (configs[3] layer 11.6
+// against 14.6 us, the base() preset's own layer 107 against 109 us).  TESM_HIP_NO_ENT_REG=1 (read per
+// call) keeps the unfused kernels for those shapes (the tests compare the two bit for bit).
+static bool reg_fits(const EntArgs& a, int64_t weff) {
+  if (a.mimo || a.H != 1 || a.D % 64 != 0 || a.D > 512 || weff > 32) return false;
+  const char* off = std::getenv("TESM_HIP_NO_ENT_REG");
+  if (off != nullptr && off[0] == '1') return false;
+  return reg_lds(a.D, a.R, weff, weff <= 16 ? 16 : 32, a.dt == kBF16 ? 2 : 4, 2 * kRegTS).total <= 64 * 1024;
+}
 
 template <bool QUANT, int KI>
 static void launch_fused2(const EntArgs& a, int64_t weff, const Fused2Lds& f2, hipStream_t st) {
@@ -1179,10 +1558,16 @@ static bool ent_unfused_requested() {
   return e != nullptr && e[0] == '1';
 }
 
+// The 16-threads-per-position form: D up to 512, its LDS within 64 KB.
+static bool fused16_fits(const EntArgs& a, int64_t weff) {
+  return !a.mimo && a.H == 1 && a.D <= 16 * 16 * kFusedMaxGPT &&
+         fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4).total <= 64 * 1024;
+}
+
 bool ent_fused_ok(const EntArgs& a) {
-  if (a.mimo || a.H != 1 || a.D > 16 * 16 * kFusedMaxGPT) return false;
+  if (a.mimo || a.H != 1) return false;
   const int64_t weff = eff_window(a);
-  return fused_lds(a.R, a.D, weff, a.dt == kBF16 ? 2 : 4).total <= 64 * 1024;
+  return fused16_fits(a, weff) || reg_fits(a, weff);
 }
 
 int64_t ent_ws_bytes(int64_t B, int64_t L, int64_t H, int64_t W) {
@@ -1220,6 +1605,7 @@ int launch_local_ent(const EntArgs& a, hipStream_t st) {
     };
     const bool big = !fits(4) && fits(8);
     if (fused2_fits(a, weff)) return run_fused2<true>(a, weff, st);
+    if (!fused16_fits(a, weff)) return a.dt == kBF16 ? run_reg<kBF16>(a, weff, st) : run_reg<kF32>(a, weff, st);
     if (a.dt == kBF16) {
       if (big)
         ent_fused_kernel<kBF16, 8><<<grid, 256, f.total, TESM_LOGGED(st, ent_fused_kernel<kBF16, 8>)>>>(a, weff, f);

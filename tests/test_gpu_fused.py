@@ -40,12 +40,6 @@ def test_fused_entanglement_quant_matches_unfused(dtype, B, L, R, D, W, cross, m
     q, k, S, bias, cq = _case(B, L, R, D, W, dtype, seed=B * 100 + L + D)
     qa = cq if cross else None
     rope = hip_ops.rope_table(L, R, dtype, DEV)
-    if dtype == torch.float32 and D * W >= 384 * 32:
-        # 47 staged fp32 state rows of 384 channels do not fit the fused kernel's 64 KB of LDS:
-        # the entry point refuses (the layer then takes the unfused kernels)
-        with pytest.raises(RuntimeError, match="fused quantization needs"):
-            hip_ops.local_ent_quant(q, k, rope, S, bias, W, 0.08, 0.2, q_add=qa)
-        return
     weff = min(W, L)
     monkeypatch.setenv("TESM_HIP_ENT_UNFUSED", "1")  # the float outputs from the scores + mix kernels
     ref = hip_ops.local_ent(q, k, rope, S, bias[-weff:], weff, 0.08, 0.2, q_add=qa,
