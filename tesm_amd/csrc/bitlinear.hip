@@ -25,12 +25,6 @@ namespace {
 
 __device__ __forceinline__ uint32_t unpack_u(uint32_t w, int s) { return (w >> (2 * s)) & 0x03030303u; }
 
-template <int OUT_DT>
-__device__ __forceinline__ void store_plain(const LinearArgs& a, int64_t m, int64_t n, float v) {
-  if (a.bias) v = v + ld<OUT_DT>(a.bias, n);
-  st<OUT_DT>(a.out, m * a.ldo + n, v);
-}
-
 // ---------------------------------------------------------------------------
 // GEMV
 // ---------------------------------------------------------------------------
@@ -45,6 +39,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
   const int64_t n0 = group * RPG;
   if (n0 >= a.N) return;
   const int64_t nch = a.Kp / 64;
+
+  // the epilogue's operands first, from clamped indices (raw bits, converted where used): requested
+  // after the products they would each cost one more memory round trip at the end of the kernel
+  float sxv[MR];
+  int32_t rsv[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const int64_t mc = m < a.M ? m : a.M - 1;
+    sxv[m] = o.s_x[mc];
+    rsv[m] = o.rowsum[mc];
+  }
+  float cwv[RPG];
+  uint32_t bias_bits[RPG];
+  const void* bias_src = a.bias ? a.bias : static_cast<const void*>(o.c_w);  // a valid address either way
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    const int64_t nc = n0 + r < a.N ? n0 + r : a.N - 1;
+    cwv[r] = o.c_w[o.c_w_per_row ? nc : 0];
+    bias_bits[r] = ld_bits<OUT_DT>(bias_src, a.bias ? nc : 0);
+  }
 
   // unconditional loads from clamped rows / chunks (masked afterwards): all in flight at once
   uint4 W[RPG][NCH];
@@ -78,6 +92,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
       }
     }
   }
+  // the row scales and sums are wave-uniform (scalar loads): pinned here, while the vector loads above
+  // are in flight, so the compiler does not sink them past the products into the storing lanes' branch
+#pragma unroll
+  for (int m = 0; m < MR; ++m) asm volatile("" : "+s"(sxv[m]), "+s"(rsv[m]));
   int acc[RPG][MR];
 #pragma unroll
   for (int r = 0; r < RPG; ++r)
@@ -113,20 +131,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
       for (int mask = LPR / 2; mask > 0; mask >>= 1) v += __shfl_xor(v, mask, 64);
       acc[r][m] = v;
     }
+  // every lane forms the outputs (so the epilogue's loads are waited for here, not after the branch)
+  float outv[RPG][MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const float inv = 1.0f / sxv[m];
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) {
+      acc[r][m] -= rsv[m];
+      float v = (static_cast<float>(acc[r][m]) * inv) * cwv[r];
+      if (a.bias) v = v + from_bits<OUT_DT>(bias_bits[r]);
+      outv[r][m] = v;
+    }
+  }
   if (g != 0) return;
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m >= a.M) break;
-    const float inv = 1.0f / o.s_x[m];
-    const int32_t rs = o.rowsum[m];
 #pragma unroll
     for (int r = 0; r < RPG; ++r) {
       const int64_t n = n0 + r;
       if (n >= a.N) break;
-      const int32_t av = acc[r][m] - rs;
-      if (a.acc_dump) a.acc_dump[m * a.N + n] = av;
-      const float cw = o.c_w_per_row ? o.c_w[n] : o.c_w[0];
-      store_plain<OUT_DT>(a, m, n, (static_cast<float>(av) * inv) * cw);
+      if (a.acc_dump) a.acc_dump[m * a.N + n] = acc[r][m];
+      st<OUT_DT>(a.out, m * a.ldo + n, outv[r][m]);
     }
   }
 }

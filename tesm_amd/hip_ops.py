@@ -268,13 +268,29 @@ def rope_table(L: int, R: int, dtype: torch.dtype, device, base: float = 10000.0
     return tab
 
 
+def window_bias(bias, H: int, W: int, dt, device):
+    """The window bias as the entanglement kernels take it: float32 (H, W) on ``device``, each value rounded
+    to the layer dtype ``dt`` first (the reference adds the bias in that dtype)."""
+    return bias.reshape(H, W).to(device=device, dtype=dt).to(torch.float32).contiguous()
+
+
+def _ready_bias(bias, H: int, W: int, dt, device, bias_rounded: bool):
+    if not bias_rounded:
+        return window_bias(bias, H, W, dt, device)
+    if bias.dtype != torch.float32 or bias.numel() != H * W or not bias.is_contiguous() or bias.device != device:
+        raise ValueError("bias_rounded=True needs the float32 (H, W) contiguous tensor window_bias() returns, "
+                         "on the states' device")
+    return bias
+
+
 def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=None, mimo: bool = False, H: int = 1,
-              outputs=("avg",), want_tern: bool = False):
+              outputs=("avg",), want_tern: bool = False, bias_rounded: bool = False):
     """Window entanglement over (B, L, H*R) queries/keys and (B, L, H*D) states.
 
-    ``bias`` is (H, W) (or (W,)) in any float dtype; it is rounded to the states' dtype.
-    ``thr`` is rounded to that dtype too.  Returns a dict of the requested outputs
-    among ``avg``, ``e``, ``c``, ``e_tanh`` (and ``tern`` if ``want_tern``).
+    ``bias`` is (H, W) (or (W,)) in any float dtype; it is rounded to the states' dtype (with
+    ``bias_rounded`` it is already ``window_bias()``'s result and is passed as it is, so the call
+    launches no conversion).  ``thr`` is rounded to that dtype too.  Returns a dict of the requested
+    outputs among ``avg``, ``e``, ``c``, ``e_tanh`` (and ``tern`` if ``want_tern``).
     """
     lib = _lib.load()
     B, L, HR = q.shape
@@ -287,7 +303,7 @@ def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=N
     S2 = _rows(S.reshape(B * L, H * D))
     qa = _rows(q_add.reshape(B * L, HR)) if q_add is not None else None
     # small parameter: accepted from any device, copied next to the states
-    bias_f = bias.reshape(H, W).to(device=S.device, dtype=dt).to(torch.float32).contiguous()
+    bias_f = _ready_bias(bias, H, W, dt, S.device, bias_rounded)
     weff = W if mimo else min(W, L)
     outs = {name: torch.empty((B, L, H * D), dtype=dt, device=S.device) for name in outputs}
     tern = torch.empty((B, L, H, weff), dtype=torch.int8, device=S.device) if want_tern else None
@@ -307,8 +323,9 @@ def local_ent(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, q_add=N
 
 
 def local_ent_quant(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, eps: float = 1e-5, q_add=None,
-                    want_floats: bool = False, want_tern: bool = False):
+                    want_floats: bool = False, want_tern: bool = False, bias_rounded: bool = False):
     """Fused SISO entanglement + int8 codes of tanh(E) and C (the state_proj / ent_proj inputs).
+    ``bias`` as in ``local_ent`` (one head).
 
     Returns a dict with ``te`` and ``c`` = (codes (M, kpad(D)) layout 1, scales (M), rowsums (M)),
     plus ``e_tanh`` / ``c_float`` / ``tern`` when asked for.
@@ -320,7 +337,7 @@ def local_ent_quant(q, k, rope, S, bias, W: int, thr: float, ent_scale: float, e
     q2, k2 = _rows(q.reshape(B * L, R)), _rows(k.reshape(B * L, R))
     S2 = _rows(S.reshape(B * L, D))
     qa = _rows(q_add.reshape(B * L, R)) if q_add is not None else None
-    bias_f = bias.reshape(W).to(device=S.device, dtype=dt).to(torch.float32).contiguous()
+    bias_f = _ready_bias(bias, 1, W, dt, S.device, bias_rounded)
     M, ldq = B * L, kpad(D)
     dev = S.device
     te = (torch.empty((M, ldq), dtype=torch.int8, device=dev), torch.empty(M, device=dev),

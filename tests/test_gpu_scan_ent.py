@@ -256,3 +256,28 @@ def test_local_ent_cross_bias_and_thresholds():
     # huge threshold: every ternary weight is 0 -> avg == 0
     out0 = hip_ops.local_ent(q.to(DEV), k.to(DEV), rope, S.to(DEV), bias, W, 1e9, 0.2)
     assert float(out0["avg"].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_local_ent_prerounded_bias(dtype):
+    """A bias already in window_bias() form (float32, rounded to the layer dtype; what the bench's isolated
+    ops pass, so a call launches no conversion) gives the same bits as the raw bias, with and without codes."""
+    B, L, R, D, W = 2, 70, 16, 64, 16
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(B, L, R, generator=g).to(dtype).to(DEV)
+    k = torch.randn(B, L, R, generator=g).to(dtype).to(DEV)
+    S = torch.randn(B, L, D, generator=g).to(dtype).to(DEV)
+    bias = torch.randn(W, generator=g) * 0.3
+    rope = hip_ops.rope_table(L, R, dtype, DEV)
+    ready = hip_ops.window_bias(bias, 1, W, dtype, S.device)
+    a = hip_ops.local_ent(q, k, rope, S, bias, W, 0.08, 0.2, outputs=("avg", "c"))
+    b = hip_ops.local_ent(q, k, rope, S, ready, W, 0.08, 0.2, outputs=("avg", "c"), bias_rounded=True)
+    assert torch.equal(a["avg"], b["avg"]) and torch.equal(a["c"], b["c"])
+    qa = hip_ops.local_ent_quant(q, k, rope, S, bias, W, 0.08, 0.2)
+    qb = hip_ops.local_ent_quant(q, k, rope, S, ready, W, 0.08, 0.2, bias_rounded=True)
+    for name in ("te", "c"):
+        for x, y in zip(qa[name], qb[name]):
+            assert torch.equal(x, y), name
+    for bad in (bias, ready.to(torch.float64), ready.reshape(W, 1).t().contiguous()[:, : W - 1]):
+        with pytest.raises(ValueError):  # not window_bias()'s form: host memory, float64, wrong size
+            hip_ops.local_ent(q, k, rope, S, bad, W, 0.08, 0.2, bias_rounded=True)
