@@ -112,6 +112,16 @@ CodeBuf take_codes(Carve& c, int64_t M, int64_t K) {
   return b;
 }
 
+// Per-token codes of tanh(E) and C (both (M, K), row pitch K) in one launch where their code buffers
+// share a pitch, else one launch each.
+static int quant_te_c(const void* te, const void* cc, int dt, int64_t M, int64_t K, float eps, const CodeBuf& xe,
+                      const CodeBuf& xc, hipStream_t st) {
+  if (xe.ldq == xc.ldq)
+    return launch_quant_act2(te, cc, dt, M, K, K, eps, xe.q, xc.q, xe.ldq, xe.s, xc.s, xe.rs, xc.rs, st);
+  if (int rc = launch_quant_act(te, dt, M, K, K, eps, 1, xe.q, xe.ldq, xe.s, xe.rs, st)) return rc;
+  return launch_quant_act(cc, dt, M, K, K, eps, 1, xc.q, xc.ldq, xc.s, xc.rs, st);
+}
+
 LinearOperand operand(const CodeBuf& x, const tesm_hip_linear& w) {
   LinearOperand o;
   o.q = x.q;
@@ -1091,10 +1101,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     if (tapping && (rc = tap_copy(tp.tern, s.g_tern, M * global_tern_pitch(p.L), st))) return rc;
     if (tapping && (rc = tap_copy(tp.te, s.e_tanh, M * D * es, st))) return rc;
     if (tapping && (rc = tap_copy(tp.c, s.c_mix, M * D * es, st))) return rc;
-    if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
-      return rc;
-    if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
-      return rc;
+    if ((rc = quant_te_c(s.e_tanh, s.c_mix, dt, M, D, p.bit_eps, s.xe, s.xc, st))) return rc;
   } else if (s.fuse_ent) {
     ea.q_te = s.xe.q;
     ea.s_te = s.xe.s;
@@ -1117,10 +1124,7 @@ int tesm_hip_siso_prefill(const tesm_hip_siso_layer* pp, void* ws, int64_t ws_by
     if ((rc = launch_local_ent(ea, st))) return rc;
     if (tapping && (rc = tap_copy(tp.te, s.e_tanh, M * D * es, st))) return rc;
     if (tapping && (rc = tap_copy(tp.c, s.c_mix, M * D * es, st))) return rc;
-    if ((rc = launch_quant_act(s.e_tanh, dt, M, D, D, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st)))
-      return rc;
-    if ((rc = launch_quant_act(s.c_mix, dt, M, D, D, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st)))
-      return rc;
+    if ((rc = quant_te_c(s.e_tanh, s.c_mix, dt, M, D, p.bit_eps, s.xe, s.xc, st))) return rc;
   }
   if (tapping) {
     if ((rc = tap_codes(tp.q_te, tp.s_te, s.xe, M, st))) return rc;
@@ -1508,8 +1512,7 @@ int tesm_hip_mimo_decode(const tesm_hip_mimo_step* pp, void* ws, int64_t ws_byte
   if (tapping) da.tern = tp.tern;
   if ((rc = launch_decode_ent(da, st))) return rc;
   // 4. per-token codes of tanh(E) and C over the flattened heads (tesm_mimo.py:895-900)
-  if ((rc = launch_quant_act(s.te, dt, Bn, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
-  if ((rc = launch_quant_act(s.cc, dt, Bn, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  if ((rc = quant_te_c(s.te, s.cc, dt, Bn, HD, p.bit_eps, s.xe, s.xc, st))) return rc;
   if (tapping) {
     if ((rc = tap_copy(tp.te, s.te, Bn * HD * es, st))) return rc;
     if ((rc = tap_copy(tp.c, s.cc, Bn * HD * es, st))) return rc;
@@ -1737,8 +1740,7 @@ int tesm_hip_mimo_prefill(const tesm_hip_mimo_layer* pp, void* ws, int64_t ws_by
     sa2.counts = p.stats_counts;
     if ((rc = launch_mimo_stats(sa2, st))) return rc;
   }
-  if ((rc = launch_quant_act(s.te, dt, M, HD, HD, p.bit_eps, 1, s.xe.q, s.xe.ldq, s.xe.s, s.xe.rs, st))) return rc;
-  if ((rc = launch_quant_act(s.cc, dt, M, HD, HD, p.bit_eps, 1, s.xc.q, s.xc.ldq, s.xc.s, s.xc.rs, st))) return rc;
+  if ((rc = quant_te_c(s.te, s.cc, dt, M, HD, p.bit_eps, s.xe, s.xc, st))) return rc;
   if (tapping) {
     if ((rc = tap_copy(tp.te, s.te, M * HD * es, st))) return rc;
     if ((rc = tap_copy(tp.c, s.cc, M * HD * es, st))) return rc;

@@ -23,12 +23,19 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__
                                                         int64_t ldx, float eps, int layout, int8_t* __restrict__ q,
                                                         int64_t ldq, float* __restrict__ s_out,
                                                         int32_t* __restrict__ rowsum, int* __restrict__ zero_p,
-                                                        int64_t zero_n) {
+                                                        int64_t zero_n, QuantSet second) {
   constexpr int RPW = 64 / LPR;
-  // side job for a later kernel of the same stream: clear zero_n ints (a fill launch saved)
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < zero_n;
-       i += static_cast<int64_t>(gridDim.x) * 256)
-    zero_p[i] = 0;
+  if (blockIdx.y == 0) {
+    // side job for a later kernel of the same stream: clear zero_n ints (a fill launch saved)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < zero_n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+      zero_p[i] = 0;
+  } else {  // the second matrix of a two-matrix launch: same shape, its own codes, scales and sums
+    x = second.x;
+    q = second.q;
+    s_out = second.s;
+    rowsum = second.rs;
+  }
   const int lane = threadIdx.x & 63;
   const int g0 = lane & (LPR - 1);
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
@@ -88,41 +95,43 @@ __global__ __launch_bounds__(256) void quant_act_kernel(const void* __restrict__
 
 template <int DT, bool VEC, int LPR, int G>
 void run_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
-               float* s_x, int32_t* rowsum, int* zero_p, int64_t zero_n, hipStream_t st) {
+               float* s_x, int32_t* rowsum, int* zero_p, int64_t zero_n, const QuantSet& q2, hipStream_t st) {
   constexpr int RPB = 4 * (64 / LPR);
   const unsigned nb = static_cast<unsigned>(std::max<int64_t>((M + RPB - 1) / RPB, zero_n > 0 ? 1 : 0));
-  quant_act_kernel<DT, VEC, LPR, G><<<nb, 256, 0, TESM_LOGGED(st, quant_act_kernel<DT, VEC, LPR, G>)>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n);
+  const dim3 grid(nb, q2.x ? 2u : 1u);
+  quant_act_kernel<DT, VEC, LPR, G><<<grid, 256, 0, TESM_LOGGED(st, quant_act_kernel<DT, VEC, LPR, G>)>>>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, q2);
 }
 
 template <int DT, bool VEC>
 void dispatch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
-                    float* s_x, int32_t* rowsum, int* zp, int64_t zn, hipStream_t st) {
+                    float* s_x, int32_t* rowsum, int* zp, int64_t zn, const QuantSet& q2, hipStream_t st) {
   const int64_t ng = ldq / 16;
   // many rows of 24-64 groups (K 384-1024): 8 lanes per row with 3-8 groups each (measured at M 8192,
   // K 768: 5.2 us against 6.4 us for 64 lanes per row); short batches keep more lanes per row
   if (M >= 2048 && ng > 16 && ng <= 64) {
     switch ((ng + 7) / 8) {
-      case 3: return run_quant<DT, VEC, 8, 3>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-      case 4: return run_quant<DT, VEC, 8, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-      case 5: return run_quant<DT, VEC, 8, 5>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-      case 6: return run_quant<DT, VEC, 8, 6>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-      case 7: return run_quant<DT, VEC, 8, 7>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-      default: return run_quant<DT, VEC, 8, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+      case 3: return run_quant<DT, VEC, 8, 3>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      case 4: return run_quant<DT, VEC, 8, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      case 5: return run_quant<DT, VEC, 8, 5>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      case 6: return run_quant<DT, VEC, 8, 6>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      case 7: return run_quant<DT, VEC, 8, 7>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      default: return run_quant<DT, VEC, 8, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
     }
   }
-  if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 8) return run_quant<DT, VEC, 8, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 16) return run_quant<DT, VEC, 16, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 32) return run_quant<DT, VEC, 32, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 64) return run_quant<DT, VEC, 64, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 128) return run_quant<DT, VEC, 64, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 256) return run_quant<DT, VEC, 64, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  if (ng <= 512) return run_quant<DT, VEC, 64, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
-  return run_quant<DT, VEC, 64, 0>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, st);
+  if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 8) return run_quant<DT, VEC, 8, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 16) return run_quant<DT, VEC, 16, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 32) return run_quant<DT, VEC, 32, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 64) return run_quant<DT, VEC, 64, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 128) return run_quant<DT, VEC, 64, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 256) return run_quant<DT, VEC, 64, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  if (ng <= 512) return run_quant<DT, VEC, 64, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+  return run_quant<DT, VEC, 64, 0>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
 }
 
-int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
-                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p, int64_t zero_n) {
+static int quant_act_impl(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
+                          int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p, int64_t zero_n,
+                          const QuantSet& q2) {
   TESM_REQUIRE(dt == kF32 || dt == kBF16, kErrInvalidArg, "quant_act: dtype must be 0 (f32) or 1 (bf16)");
   TESM_REQUIRE(M >= 0 && K >= 1 && ldx >= K, kErrInvalidArg, "quant_act: need M >= 0, K >= 1, ldx >= K");
   TESM_REQUIRE(ldq >= K && ldq % 16 == 0, kErrInvalidArg, "quant_act: ldq must be >= K and a multiple of 16");
@@ -130,17 +139,36 @@ int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, f
   TESM_REQUIRE(M == 0 || (x && q && s_x), kErrInvalidArg, "quant_act: null pointer");
   TESM_REQUIRE(aligned(q, 16), kErrAlignment, "quant_act: code buffer must be 16-byte aligned");
   TESM_REQUIRE(zero_n == 0 || zero_p, kErrInvalidArg, "quant_act: null range to clear");
+  TESM_REQUIRE(!q2.x || M == 0 || (q2.q && q2.s && aligned(q2.q, 16)), kErrInvalidArg,
+               "quant_act: the second matrix needs 16-byte aligned codes and a scale buffer");
   if (M == 0 && zero_n == 0) return kOk;  // with M == 0 one workgroup still clears the side range
   const int esz = dt == kBF16 ? 2 : 4;
-  const bool vec = aligned(x, 16) && (ldx * esz) % 16 == 0;
+  const bool vec = aligned(x, 16) && (!q2.x || aligned(q2.x, 16)) && (ldx * esz) % 16 == 0;
   if (dt == kBF16) {
-    if (vec) dispatch_quant<kBF16, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
-    else dispatch_quant<kBF16, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
+    if (vec) dispatch_quant<kBF16, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, q2, st);
+    else dispatch_quant<kBF16, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, q2, st);
   } else {
-    if (vec) dispatch_quant<kF32, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
-    else dispatch_quant<kF32, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, st);
+    if (vec) dispatch_quant<kF32, true>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, q2, st);
+    else dispatch_quant<kF32, false>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zero_p, zero_n, q2, st);
   }
   return check_launch("quant_act");
+}
+
+int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
+                     int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p, int64_t zero_n) {
+  return quant_act_impl(x, dt, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, st, zero_p, zero_n, QuantSet{});
+}
+
+int launch_quant_act2(const void* x0, const void* x1, int dt, int64_t M, int64_t K, int64_t ldx, float eps,
+                      int8_t* q0, int8_t* q1, int64_t ldq, float* s0, float* s1, int32_t* rs0, int32_t* rs1,
+                      hipStream_t st) {
+  TESM_REQUIRE(x1 != nullptr, kErrInvalidArg, "quant_act: null second matrix");
+  QuantSet q2;
+  q2.x = x1;
+  q2.q = q1;
+  q2.s = s1;
+  q2.rs = rs1;
+  return quant_act_impl(x0, dt, M, K, ldx, eps, 1, q0, ldq, s0, rs0, st, nullptr, 0, q2);
 }
 
 // ---------------------------------------------------------------------------

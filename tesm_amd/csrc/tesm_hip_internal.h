@@ -13,6 +13,17 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 int launch_quant_act(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q,
                      int64_t ldq, float* s_x, int32_t* rowsum, hipStream_t st, int* zero_p = nullptr,
                      int64_t zero_n = 0);
+// The codes of a second matrix of the same shape and row pitch in the same launch (layout 1), e.g.
+// tanh(E) and C: one launch instead of two.
+struct QuantSet {
+  const void* x = nullptr;
+  int8_t* q = nullptr;
+  float* s = nullptr;
+  int32_t* rs = nullptr;
+};
+int launch_quant_act2(const void* x0, const void* x1, int dt, int64_t M, int64_t K, int64_t ldx, float eps,
+                      int8_t* q0, int8_t* q1, int64_t ldq, float* s0, float* s1, int32_t* rs0, int32_t* rs1,
+                      hipStream_t st);
 int launch_absmean(const void* w, int dt, int64_t n, float eps, double* ws, float* s_w, float* c_w, hipStream_t st);
 int launch_pack(const void* w, int dt, int64_t N, int64_t K, int64_t ldw, const float* s_w, int per_row,
                 uint8_t* packed, int64_t ldp, hipStream_t st);
