@@ -350,3 +350,33 @@ def test_mimo_entanglement_stats_vs_oracle(dtype, B, L, H, R, W):
     assert m.last_entanglement_stats is a
     m.last_entanglement_stats = None
     assert m.last_entanglement_stats is None
+
+
+def _codes_equal_single_launch(tp, rows, eps):
+    """The tapped codes of tanh(E) and C (one two-matrix launch in the layer) equal the single-matrix
+    quantization of the tapped values, bit for bit: codes, scales (row sums are not tapped)."""
+    for name in ("te", "c"):
+        x = getattr(tp, name)[:rows]
+        q, s, _ = hip_ops.quant_act(x, eps)
+        assert torch.equal(q, getattr(tp, "q_" + name)[:rows]), name
+        assert torch.equal(s, getattr(tp, "s_" + name)[:rows]), name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("W", [8, 0])
+def test_mimo_te_c_codes_match_single_launches(dtype, W):
+    """tanh(E) and C are quantized in one launch (the second matrix on grid y) in the MIMO prefill (local
+    and global entanglement) and decode step; each equals its own single-matrix quantization."""
+    B, P, H, D = 3, 40, 3, 24
+    m = _mimo_dec(TESMMIMO_Optimized, 17 + W, W, dtype).to(DEV)
+    u = torch.randn(B, P + 1, 96, generator=torch.Generator().manual_seed(W)).to(dtype).to(DEV)
+    cache = m.allocate_inference_cache(B, 64)
+    eps = m.in_proj.bit_eps
+    with torch.no_grad():
+        tern = (B, P, H, W) if W > 0 else (B, P, (P + 63) // 64 * 64)
+        with Taps(B * P, H * D, m.d_model, DEV, tern, dtype=dtype) as tp:
+            m(u[:, :P], inference_params={"state_cache": cache})
+        _codes_equal_single_launch(tp, B * P, eps)
+        with Taps(B, H * D, m.d_model, DEV, (B, H, max(W, 1)), dtype=dtype) as tp:
+            m(u[:, P:P + 1], inference_params={"state_cache": cache})
+        _codes_equal_single_launch(tp, B, eps)
