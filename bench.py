@@ -72,9 +72,10 @@ def busy(torch, ms: float = 20.0):
 def time_back_to_back(torch, fn, n: int, warm: int = 3):
     """Average device time per launch of n back-to-back fn() launches between one event pair on the
     current stream (the launches are queued behind a device-side wait first, so host launch latency
-    does not leave gaps)."""
-    for _ in range(warm):
-        fn(0)
+    does not leave gaps).  The warm-up calls fn(0 .. warm - 1): with rotating buffers, warm = their
+    count, so the first timed use of a buffer does not pay the library's one-time pointer check."""
+    for i in range(warm):
+        fn(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     busy(torch)
@@ -116,7 +117,7 @@ def measure_kernels(torch, only):
         c_w = torch.full((1,), 0.05, device=dev)
         out = torch.empty(M, N, device=dev)
         t = time_back_to_back(torch, lambda i: hip_ops.bitlinear(q, s, rs, packs[i % nrot], c_w, N, K, torch.float32,
-                                                             out=out), 200 if M == 1 else 50)
+                                                             out=out), 200 if M == 1 else 50, warm=max(3, nrot))
         if M == 1:
             nbytes = N * K // 4 + M * K + M * N * 4 + 8 * M + 4
             res[name] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
@@ -135,7 +136,7 @@ def measure_kernels(torch, only):
         nrot = rotation(Bs * Ls * D * 2 * 3)  # decay, update in; states out
         sets = [(torch.sigmoid(torch.randn(Bs, Ls, D, device=dev, generator=gen)).to(torch.bfloat16),
                  torch.randn(Bs, Ls, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nrot)]
-        t = time_back_to_back(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100)
+        t = time_back_to_back(torch, lambda i: hip_ops.scan(sets[i % nrot][0], sets[i % nrot][1], 16), 100, warm=nrot)
         nbytes = Bs * Ls * D * (2 + 2 + 2)
         res["scan_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
                              "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
@@ -150,7 +151,7 @@ def measure_kernels(torch, only):
         bias_r = hip_ops.window_bias(bias, 1, W, torch.bfloat16, dev)  # rounded once, as a layer keeps it
         t = time_back_to_back(torch, lambda i: hip_ops.local_ent(sets[i % nrot][0], sets[i % nrot][1], rope,
                                                              sets[i % nrot][2], bias_r, W, 0.08, 0.2,
-                                                             bias_rounded=True), 100)
+                                                             bias_rounded=True), 100, warm=nrot)
         nbytes = Bs * Ls * (2 * R + 2 * D) * 2
         res["local_ent_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",
                                   "frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "bytes": nbytes, "rotating_buffers": nrot}
@@ -165,7 +166,7 @@ def measure_kernels(torch, only):
         bias_r = hip_ops.window_bias(bias, 1, W, torch.bfloat16, dev)
         t = time_back_to_back(torch, lambda i: hip_ops.local_ent_quant(sets[i % nrot][0], sets[i % nrot][1], rope,
                                                                    sets[i % nrot][2], bias_r, W, 0.08, 0.2,
-                                                                   bias_rounded=True), 100)
+                                                                   bias_rounded=True), 100, warm=nrot)
         # q, k, states in; int8 codes + scale + rowsum of tanh(E) and C out
         nbytes = Bs * Ls * (2 * R * 2 + D * 2 + 2 * (D + 8))
         res["local_ent_quant_small"] = {"us": t * 1e6, "bound": "hbm", "achieved": nbytes / t / 1e9, "unit": "GB/s",

@@ -126,10 +126,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(LinearArgs a) {
   for (int r = 0; r < RPG; ++r)
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      int v = acc[r][m];
-#pragma unroll
-      for (int mask = LPR / 2; mask > 0; mask >>= 1) v += __shfl_xor(v, mask, 64);
-      acc[r][m] = v;
+      acc[r][m] = wave_sum_i<LPR>(acc[r][m]);  // DPP / swizzle steps (integer sums: any order is exact)
     }
   // every lane forms the outputs (so the epilogue's loads are waited for here, not after the branch)
   float outv[RPG][MR];
