@@ -2290,8 +2290,7 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
     sum = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, sum, false);
     if (o.q && mr < a.M) reinterpret_cast<uint4*>(o.q + mr * o.ldq)[ck] = v;
   }
-#pragma unroll
-  for (int off = TPR / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  sum = wave_sum_i<TPR>(sum);  // the row's TPR consecutive lanes; DPP steps, an integer sum in any order
   if (tr == 0 && o.q && mr < a.M) {
     float am = 0.0f;
 #pragma unroll
