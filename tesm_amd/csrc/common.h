@@ -281,9 +281,10 @@ __device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int
 // ---------------------------------------------------------------------------
 // Lane exchanges for order-free reductions inside groups of WIDTH lanes: DPP quad permutes (lane ^ 1,
 // lane ^ 2), the half-row and row mirrors (a lane of the other 4- and 8-lane group, which is all a
-// butterfly needs once each group's lanes agree), a swizzle (lane ^ 16 within 32 lanes) and one
-// cross-half permute (lane ^ 32).  DPP moves are VALU operations; only the last two go through the LDS
-// crossbar, where every __shfl_xor step would.
+// butterfly needs once each group's lanes agree), a swizzle (lane ^ 16 within 32 lanes), and for the
+// whole wave the two half-wave results read from lanes 0 and 32 (v_readlane: a uniform total).  DPP
+// moves and lane reads are VALU operations; only the swizzle goes through the LDS crossbar, where
+// every __shfl_xor step would.  Full-wave reductions need every lane active.
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
@@ -301,7 +302,9 @@ __device__ __forceinline__ float wave_max(float v) {
   if constexpr (WIDTH >= 8) v = fmaxf(v, __int_as_float(dpp_mov<kDppHalfMirror>(__float_as_int(v))));
   if constexpr (WIDTH >= 16) v = fmaxf(v, __int_as_float(dpp_mov<kDppMirror>(__float_as_int(v))));
   if constexpr (WIDTH >= 32) v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwzXor16)));
-  if constexpr (WIDTH >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  if constexpr (WIDTH >= 64)  // the two half-wave maxima, read from lanes 0 and 32
+    v = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
   return v;
 }
 
@@ -312,7 +315,7 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   if constexpr (WIDTH >= 8) v += dpp_mov<kDppHalfMirror>(v);
   if constexpr (WIDTH >= 16) v += dpp_mov<kDppMirror>(v);
   if constexpr (WIDTH >= 32) v += __builtin_amdgcn_ds_swizzle(v, kSwzXor16);
-  if constexpr (WIDTH >= 64) v += __shfl_xor(v, 32, 64);
+  if constexpr (WIDTH >= 64) v = __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
   return v;
 }
 
@@ -321,6 +324,28 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
   for (int m = WIDTH / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WIDTH);
   return v;
+}
+
+// Float sums of N values over the whole wave on wave_sum_i's exchanges (four DPP steps, the swizzle),
+// the two half-wave totals then read from lanes 0 and 32 and added: every lane receives each total.
+// The N chains are independent, so their exchanges overlap.  The addition tree differs from
+// wave_sum_f's butterfly: a kernel keeps one of the two wherever its sums must match another's.
+template <int N>
+__device__ __forceinline__ void wave_sum_fn(float (&v)[N]) {
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] += __int_as_float(dpp_mov<kDppXor1>(__float_as_int(v[n])));
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] += __int_as_float(dpp_mov<kDppXor2>(__float_as_int(v[n])));
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] += __int_as_float(dpp_mov<kDppHalfMirror>(__float_as_int(v[n])));
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] += __int_as_float(dpp_mov<kDppMirror>(__float_as_int(v[n])));
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[n]), kSwzXor16));
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+    v[n] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[n]), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[n]), 32));
 }
 
 template <int WIDTH = 64>

@@ -104,10 +104,10 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   }
   const int wlo = W - valid;  // padded positions below wlo hold no entry
   const bool full = valid >= W;
-  // ring slot read at padded window position w (w in [wlo, W)), in the reference's order
+  // ring slot read at padded window position w (w in [wlo, W)), in the reference's order; selects
+  // rather than branches (the value for other w is not used)
   auto slot_of = [&](int w) -> int {
-    if (!full) return w - wlo;
-    const int s = slot + w;
+    const int s = full ? slot + w : w - wlo;
     return s >= W ? s - W : s;
   };
 
@@ -116,8 +116,8 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   // slot, so the loads need no branch and, with W > 1, never read the slot this step writes.
   const int alt = W > 1 ? (slot + 1 == W ? 0 : slot + 1) : slot;
   auto read_slot = [&](int w) -> int {
-    const int s = (w >= wlo && w < W) ? slot_of(w) : alt;
-    return s == slot ? alt : s;
+    const int s = slot_of(w);
+    return ((w >= wlo) & (w < W) & (s != slot)) ? s : alt;
   };
 
   // 0. Every global read of steps 1-4 (the last batches of window keys and, with CPT > 1, of ring
@@ -223,43 +223,58 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
-  // 3. window scores (tesm.py:1338-1357): wave v scores windows v, v+4, ..; its lanes split the rank
+  // 3. window scores (tesm.py:1338-1357): wave v scores windows v, v+4, ..; its lanes split the rank.
+  //    A batch's four dot products are formed and reduced together (the next batch's keys requested
+  //    first), then lane jj turns window jj's sum into its ternary.  The step's own query and key
+  //    values come from LDS once; the fresh window picks the key by a select, lanes past the rank add
+  //    zero.
   const float sq = static_cast<float>(sqrt(static_cast<double>(a.R)));
+  float q1v[NI], q2v[NI], k1v[NI], k2v[NI];
+#pragma unroll
+  for (int t = 0; t < NI; ++t) {
+    const int i = min(lane + 64 * t, half - 1);
+    q1v[t] = qv[i];
+    q2v[t] = qv[half + i];
+    k1v[t] = kv[i];
+    k2v[t] = kv[half + i];
+  }
   for (int j0 = 0; j0 < 16; j0 += 4) {  // W <= 64: at most 16 windows per wave
     if (wave + 4 * j0 >= W) break;       // uniform in the wave
-    if (j0 > 0) load_keys(j0);
+    float dot[4];
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int w = wave + 4 * (j0 + jj);
-      const bool on = w < W && w >= wlo;
-      const bool fresh = on && slot_of(w) == slot;
-      float dot = 0.0f;
+      const bool fresh = slot_of(wave + 4 * (j0 + jj)) == slot;  // (value unused off the window)
+      float d = 0.0f;
 #pragma unroll
       for (int t = 0; t < NI; ++t) {
-        const int i = lane + 64 * t;
-        if (on && i < half) {
-          const float k1 = fresh ? kv[i] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t]));
-          const float k2 = fresh ? kv[half + i] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t + 1]));
-          dot += qv[i] * k1;
-          dot += qv[half + i] * k2;
-        }
+        const bool in = lane + 64 * t < half;
+        const float k1 = fresh ? k1v[t] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t]));
+        const float k2 = fresh ? k2v[t] : rnd<DT>(from_bits<CDT>(kb[jj][2 * t + 1]));
+        d += in ? q1v[t] * k1 : 0.0f;
+        d += in ? q2v[t] * k2 : 0.0f;
       }
-      dot = wave_sum_f<64>(dot);
-      if (lane == 0 && w < W) {
-        if (w < wlo) {
-          wn[w] = 0.0f;
-        } else {
-          float sc = rnd<DT>(rnd<DT>(dot) / sq);
-          sc = rnd<DT>(sc + wn[w]);  // wn[w] holds the window bias until here
-          wn[w] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);  // strict ternary (1359-1368)
-        }
+      dot[jj] = d;
+    }
+    if (j0 + 4 < 16 && wave + 4 * (j0 + 4) < W) load_keys(j0 + 4);  // uniform in the wave
+    wave_sum_fn<4>(dot);
+    const int w = wave + 4 * (j0 + (lane & 3));
+    if (lane < 4 && w < W) {
+      const float dsum = lane == 0 ? dot[0] : (lane == 1 ? dot[1] : (lane == 2 ? dot[2] : dot[3]));
+      if (w < wlo) {
+        wn[w] = 0.0f;
+      } else {
+        float sc = rnd<DT>(rnd<DT>(dsum) / sq);
+        sc = rnd<DT>(sc + wn[w]);  // wn[w] holds the window bias until here
+        wn[w] = sc > a.thr ? 1.0f : (sc < -a.thr ? -1.0f : 0.0f);  // strict ternary (1359-1368)
       }
     }
   }
   __syncthreads();
   if (wave == 0) {  // count normalisation (1370-1372)
     const float tern = lane < W ? wn[lane] : 0.0f;
-    const float n = fmaxf(wave_sum_f<64>(fabsf(tern)), 1.0f);
+    float cnt[1] = {fabsf(tern)};
+    wave_sum_fn<1>(cnt);  // a count: exact in any order
+    const float n = fmaxf(cnt[0], 1.0f);
     if (lane < W) wn[lane] = rnd<DT>(tern / n);
     if (a.tern && blockIdx.z == 0 && lane < W) a.tern[bh * a.W + lane] = static_cast<int8_t>(tern);
   }
@@ -271,6 +286,9 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
   for (int k = 0; k < CPT; ++k) acc[k] = 0.0f;
   if constexpr (CPT == 1) {
     float pm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float nvr[4];  // this step's states of the lane's channels (the fresh window), picked by a select
+#pragma unroll
+    for (int r = 0; r < 4; ++r) nvr[r] = nv[min(j4 + r, cn - 1)];  // channels past cn are not stored
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int w = wave + 4 * u;
@@ -280,7 +298,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
       const float wv = wn[w];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float x = fresh ? (j4 + r < cn ? nv[j4 + r] : 0.0f) : rnd<DT>(ring_val<CDT>(xr[u], r, vec));
+        const float x = fresh ? nvr[r] : rnd<DT>(ring_val<CDT>(xr[u], r, vec));
         pm[r] += wv * x;
       }
     }
@@ -291,6 +309,9 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
     if (tid < cn) acc[0] = ((mixp[tid] + mixp[CW + tid]) + mixp[2 * CW + tid]) + mixp[3 * CW + tid];
   } else {
     constexpr int kWB = 4;
+    float nvk[CPT];  // this step's states of the thread's channels (the fresh window)
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) nvk[k] = nv[min(tid + 256 * k, cn - 1)];  // channels past cn are not stored
     for (int w0 = wlo; w0 < W; w0 += kWB) {
       uint32_t xb[kWB][CPT];  // a batch's loads in straight-line code, all in flight together
 #pragma unroll
@@ -310,8 +331,7 @@ __global__ __launch_bounds__(256) void decode_ent_kernel(DecodeArgs a) {
         const float wv = wn[w];
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
-          const int j = tid + 256 * k;
-          const float x = j < cn ? (fresh ? nv[j] : rnd<DT>(from_bits<CDT>(xb[u][k]))) : 0.0f;
+          const float x = fresh ? nvk[k] : rnd<DT>(from_bits<CDT>(xb[u][k]));
           acc[k] += wv * x;
         }
       }
