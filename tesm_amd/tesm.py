@@ -25,11 +25,20 @@ from .bitlinear import BitLinear, backend_error, check_hip_call
 _WORKSPACES = {}
 
 
-def workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
-    """A per-(device, stream) scratch buffer, grown on demand; reused across calls on that stream."""
-    if stream is None:
-        stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+def raw_stream(index: int) -> int:
+    """The raw handle of device ``index``'s current stream (``torch.cuda.current_stream(..).cuda_stream``
+    without building a Stream object, which costs over a microsecond on the per-token decode path)."""
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
+def workspace(device: torch.device, nbytes: int, stream=None, raw=None) -> torch.Tensor:
+    """A per-(device, stream) scratch buffer, grown on demand; reused across calls on that stream.
+    ``raw``: the stream's raw handle, in place of ``stream``."""
+    if raw is None:
+        if stream is None:
+            stream = torch.cuda.current_stream(device)
+        raw = stream.cuda_stream
+    key = (device.index, raw)
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty((max(nbytes, 256),), dtype=torch.uint8, device=device)
@@ -354,9 +363,9 @@ class TESM_SISO(nn.Module):
         state = state.contiguous()
         pos = int(cache["seq_pos"])
         slot = int(cache.get("cache_idx", 0))
-        u2 = u.reshape(B, dm)  # a view for a one-token slice of a longer sequence
-        if u2.stride(1) != 1:
-            u2 = u2.contiguous()
+        if u.stride(2) != 1:
+            u = u.contiguous()
+        ld_u = u.stride(0) if B > 1 else dm  # rows of a one-token slice of a longer sequence, no view needed
         cs = None
         if cross_layer_state is not None:
             cs = cross_layer_state.reshape(B, D).to(dt).contiguous()
@@ -368,23 +377,23 @@ class TESM_SISO(nn.Module):
         new = torch.empty((B, D), dtype=dt, device=dev)
         rope = self.rope_table(pos + 1, dt, dev)
         desc.seq_pos, desc.cache_idx = pos, slot
-        desc.u, desc.ld_u = u2.data_ptr(), u2.stride(0)
+        desc.u, desc.ld_u = u.data_ptr(), ld_u
         desc.cross_state = cs.data_ptr() if cs is not None else None
         desc.rope = rope.data_ptr()
         desc.state, desc.state_out = state.data_ptr(), state_out.data_ptr()
         desc.k_cache, desc.v_cache = kc.data_ptr(), vc.data_ptr()
         desc.y = y.data_ptr()
         desc.new_state = new.data_ptr()
-        stream = torch.cuda.current_stream(dev)
+        raw = raw_stream(dev.index)
         if torch.cuda.current_device() == dev.index:
-            ws = workspace(dev, nbytes, stream)
+            ws = workspace(dev, nbytes, raw=raw)
             rc = lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                                          ctypes.c_void_p(stream.cuda_stream))
+                                          ctypes.c_void_p(raw))
         else:
             with torch.cuda.device(dev):
-                ws = workspace(dev, nbytes, stream)
+                ws = workspace(dev, nbytes, raw=raw)
                 rc = lib.tesm_hip_siso_decode(ctypes.byref(desc), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
-                                              ctypes.c_void_p(stream.cuda_stream))
+                                              ctypes.c_void_p(raw))
         _lib.check(rc)
         cache["cache_idx"] = (slot + 1) % W
         cache["state"] = state_out
