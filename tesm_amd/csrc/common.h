@@ -241,38 +241,57 @@ __device__ __forceinline__ void load_groups(const void* __restrict__ x, int64_t 
 #pragma unroll
   for (int gi = 0; gi < G; ++gi) {
     const bool in = g0 + LPR * gi < nfull;
-    const uint32_t* wd = reinterpret_cast<const uint32_t*>(&raw[gi][0]);
+    uint32_t wd[4 * NV];  // the group's words, zero past K (one select per word rather than per value)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float f = DT == kBF16 ? __uint_as_float(i % 2 == 0 ? wd[i / 2] << 16 : wd[i / 2] & 0xffff0000u)
-                                  : __uint_as_float(wd[i]);
-      v[gi][i] = in ? f : 0.0f;
+    for (int q = 0; q < NV; ++q) {
+      wd[4 * q] = in ? raw[gi][q].x : 0u;
+      wd[4 * q + 1] = in ? raw[gi][q].y : 0u;
+      wd[4 * q + 2] = in ? raw[gi][q].z : 0u;
+      wd[4 * q + 3] = in ? raw[gi][q].w : 0u;
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[gi][i] = DT == kBF16 ? __uint_as_float(i % 2 == 0 ? wd[i / 2] << 16 : wd[i / 2] & 0xffff0000u)
+                             : __uint_as_float(wd[i]);
   }
 }
 
-// Codes of one group, packed in the requested layout; adds the codes to rs.
+// Byte 0 of each of four words, gathered into one word (b0 lowest) by three v_perm_b32.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // b0.0, b1.0, 0, 0
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);  // b2.0, b3.0, 0, 0
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Codes of one group, packed in the requested layout; adds the codes to rs.  Each code is act_code's
+// clamp(rne(rnd(x * sc)), -128, 127) formed as clamp first (the bounds are integers, so clamping before or
+// after the rounding agrees; NaN gives -128 either way), then + 1.5 * 2^23: the addition rounds the value
+// to an integer, nearest even, held in the low mantissa bits, so the low byte of the sum's bits is the code
+// in two's complement.  The bytes are gathered by v_perm_b32 and summed by a four-byte dot product.
 template <int DT>
 __device__ __forceinline__ uint4 group_codes(const float (&v)[16], float sc, int layout, int32_t& rs) {
   uint32_t c[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int ci = act_code<DT>(v[i], sc);
-    rs += ci;
-    c[i] = static_cast<uint32_t>(ci) & 0xffu;
+    const float t = fminf(fmaxf(rnd<DT>(v[i] * sc), -128.0f), 127.0f);
+    c[i] = __float_as_uint(t + 12582912.0f);
   }
   uint4 out;
   if (layout == 1) {
-    out.x = c[0] | (c[4] << 8) | (c[8] << 16) | (c[12] << 24);
-    out.y = c[1] | (c[5] << 8) | (c[9] << 16) | (c[13] << 24);
-    out.z = c[2] | (c[6] << 8) | (c[10] << 16) | (c[14] << 24);
-    out.w = c[3] | (c[7] << 8) | (c[11] << 16) | (c[15] << 24);
+    out.x = pack_low_bytes(c[0], c[4], c[8], c[12]);
+    out.y = pack_low_bytes(c[1], c[5], c[9], c[13]);
+    out.z = pack_low_bytes(c[2], c[6], c[10], c[14]);
+    out.w = pack_low_bytes(c[3], c[7], c[11], c[15]);
   } else {
-    out.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    out.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    out.z = c[8] | (c[9] << 8) | (c[10] << 16) | (c[11] << 24);
-    out.w = c[12] | (c[13] << 8) | (c[14] << 16) | (c[15] << 24);
+    out.x = pack_low_bytes(c[0], c[1], c[2], c[3]);
+    out.y = pack_low_bytes(c[4], c[5], c[6], c[7]);
+    out.z = pack_low_bytes(c[8], c[9], c[10], c[11]);
+    out.w = pack_low_bytes(c[12], c[13], c[14], c[15]);
   }
+  rs = __builtin_amdgcn_sdot4(static_cast<int>(out.x), 0x01010101, rs, false);
+  rs = __builtin_amdgcn_sdot4(static_cast<int>(out.y), 0x01010101, rs, false);
+  rs = __builtin_amdgcn_sdot4(static_cast<int>(out.z), 0x01010101, rs, false);
+  rs = __builtin_amdgcn_sdot4(static_cast<int>(out.w), 0x01010101, rs, false);
   return out;
 }
 
