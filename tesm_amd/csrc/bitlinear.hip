@@ -2268,10 +2268,9 @@ __global__ __launch_bounds__(NW * 64) void gate32_kernel(LinearArgs a, RowQuant 
       rnd2<DT>(t[0], t[1]);
       rnd2<DT>(t[2], t[3]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float q = fminf(fmaxf(rintf(t[r]), -128.0f), 127.0f);
-        crow[32 * c + 16 * (g >> 1) + 4 * r + 2 * (g & 1)] = static_cast<int8_t>(static_cast<int>(q));
-      }
+      for (int r = 0; r < 4; ++r)  // clamp, then + 1.5 * 2^23 rounds to the code, left in the low byte (group_codes)
+        reinterpret_cast<uint8_t*>(crow)[32 * c + 16 * (g >> 1) + 4 * r + 2 * (g & 1)] =
+            static_cast<uint8_t>(__float_as_uint(fminf(fmaxf(t[r], -128.0f), 127.0f) + 12582912.0f));
     }
   }
   lds_barrier();
