@@ -106,16 +106,15 @@ template <int DT, bool VEC>
 void dispatch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, float eps, int layout, int8_t* q, int64_t ldq,
                     float* s_x, int32_t* rowsum, int* zp, int64_t zn, const QuantSet& q2, hipStream_t st) {
   const int64_t ng = ldq / 16;
-  // many rows of 24-64 groups (K 384-1024): 8 lanes per row with 3-8 groups each (measured at M 8192,
-  // K 768: 5.2 us against 6.4 us for 64 lanes per row); short batches keep more lanes per row
+  // many rows of 24-64 groups (K 384-1024): 16 lanes per row with 2-4 groups each, so that an 8192-row
+  // batch runs two waves per SIMD (measured at M 8192, K 768 on one box: 6.2 us against 6.8 us for 8 lanes
+  // per row with 6 groups each, which in turn had taken 5.2 against 6.4 us for 64 lanes per row); short
+  // batches keep more lanes per row
   if (M >= 2048 && ng > 16 && ng <= 64) {
-    switch ((ng + 7) / 8) {
-      case 3: return run_quant<DT, VEC, 8, 3>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
-      case 4: return run_quant<DT, VEC, 8, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
-      case 5: return run_quant<DT, VEC, 8, 5>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
-      case 6: return run_quant<DT, VEC, 8, 6>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
-      case 7: return run_quant<DT, VEC, 8, 7>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
-      default: return run_quant<DT, VEC, 8, 8>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+    switch ((ng + 15) / 16) {
+      case 2: return run_quant<DT, VEC, 16, 2>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      case 3: return run_quant<DT, VEC, 16, 3>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
+      default: return run_quant<DT, VEC, 16, 4>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);
     }
   }
   if (ng <= 4) return run_quant<DT, VEC, 4, 1>(x, M, K, ldx, eps, layout, q, ldq, s_x, rowsum, zp, zn, q2, st);

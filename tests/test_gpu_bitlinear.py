@@ -28,7 +28,8 @@ def _oracle_codes(x: torch.Tensor):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,K", [(1, 64), (3, 61), (5, 130), (17, 768), (2, 4096), (64, 256)])
+@pytest.mark.parametrize("M,K", [(1, 64), (3, 61), (5, 130), (17, 768), (2, 4096), (64, 256),
+                                 (2048, 384), (2048, 768), (2050, 1024)])  # last three: 16 lanes per row
 def test_quant_act_bit_exact(dtype, M, K):
     g = torch.Generator().manual_seed(M * 1000 + K)
     x = (torch.randn(M, K, generator=g) * 3).to(dtype)
