@@ -263,11 +263,13 @@ class TESM_SISO(nn.Module):
         return kc, vc
 
     def _check_cache(self, kc, vc, B, dev):
-        W = kc.shape[1] if kc.dim() == 3 else -1
-        ok = (kc.dim() == 3 and vc.dim() == 3 and tuple(kc.shape) == (B, W, self.ent_rank)
-              and tuple(vc.shape) == (B, W, self.d_state) and kc.dtype == vc.dtype
+        # sizes compared as torch.Size against tuples and devices by index: this runs once per decoded token
+        di = -1 if dev.index is None else dev.index
+        ks, vs = kc.size(), vc.size()
+        W = ks[1] if len(ks) == 3 else -1
+        ok = (len(ks) == 3 and ks == (B, W, self.ent_rank) and vs == (B, W, self.d_state) and kc.dtype == vc.dtype
               and kc.dtype in (torch.float32, torch.bfloat16) and kc.is_contiguous() and vc.is_contiguous()
-              and kc.device == dev and vc.device == dev and 1 <= W <= 64)
+              and kc.get_device() == di and vc.get_device() == di and 1 <= W <= 64)
         if not ok:
             raise RuntimeError("TESM hip decode: the inference cache must hold contiguous (B, W, ent_rank) and "
                                "(B, W, d_state) float32 or bfloat16 ring buffers on the layer's device, W <= 64")
@@ -357,7 +359,7 @@ class TESM_SISO(nn.Module):
         self._check_cache(kc, vc, B, dev)
         W = kc.shape[1]
         state = cache["state"]
-        if state.dtype != torch.float64 or tuple(state.shape) != (B, D) or state.device != dev:
+        if state.dtype != torch.float64 or state.size() != (B, D) or state.get_device() != (-1 if dev.index is None else dev.index):
             raise RuntimeError("TESM hip decode: cache['state'] must be a (B, d_state) float64 tensor on the layer's "
                                "device")
         state = state.contiguous()
